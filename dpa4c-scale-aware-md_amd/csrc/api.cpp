@@ -1,0 +1,828 @@
+// C ABI of libdpamd.so and the per-step pipeline that drives the kernels.
+//
+// One evaluation (standalone path):
+//   wrap + ghost images (count, scan, fill)          neighbor.hip
+//   cell binning (count, scan, scatter)              neighbor.hip
+//   sel-sorted neighbour list                        neighbor.hip
+//   env mat + embedding + contraction -> Tsec        embed.hip   (FP64 MFMA)
+//   descriptor T, D                                  embed.hip
+//   fitting forward + input gradient per type        fitting.hip (FP64 MFMA)
+//   dE/dD -> dE/dT                                   fitting.hip
+//   embedding backward -> edge gradients             embed.hip   (FP64 MFMA)
+//   reverse list + force / atom-virial gather        force.hip
+//   energy / virial reduction                        force.hip
+// The LAMMPS path replaces the first three stages with sel formatting of the
+// caller's candidate list and keeps ghost forces in ghost slots.
+//
+// This file is compiled with -ffp-contract=off: the box geometry (cutoff in
+// fractional units) must match the oracle's bit for bit because it decides
+// which ghost images exist.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <fstream>
+#include <iterator>
+#include <string>
+#include <vector>
+
+#include "../../include/dp_amd.h"
+#include "kernels.h"
+#include "model.h"
+
+using namespace dpamd;
+
+namespace {
+
+struct Buf {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+
+enum Stage {
+  kStGeom = 0,
+  kStNlist,
+  kStEmbFwd,
+  kStDescr,
+  kStFit,
+  kStDT,
+  kStEmbBwd,
+  kStForce,
+  kStReduce,
+  kNumStages
+};
+const char* kStageNames[kNumStages] = {"ghost+cells", "nlist",  "embed_fwd",
+                                       "descriptor",  "fitting", "dE_dT",
+                                       "embed_bwd",   "force",  "reduce"};
+
+}  // namespace
+
+struct dp_model {
+  int device = 0;
+  int precision = DP_PREC_FP64;
+  ModelHost host;
+  EmbLayout el{};
+  std::string err;
+  // device parameters
+  double* d_emb = nullptr;
+  double* d_envp = nullptr;
+  double* d_tpad = nullptr;
+  double* d_fit = nullptr;
+  FitOffsets fo{};
+  // workspace
+  std::vector<Buf*> bufs;
+  Buf coord_in, atype_in, sfrac, flags, gpos, ext, ext_type, mapping, cell_of, cell_count,
+      cell_start, cell_cursor, sorted, nlist, nreal, cand_off, cand, items, Tsec, T, D, dD, dT,
+      fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_cursor, rev, force_ws, av_ws,
+      ae_ws, partials, out10, status, scan_tmp;
+  size_t bytes_now = 0, bytes_peak = 0;
+  // type buckets
+  std::vector<int> atype_cache;
+  std::vector<int> items_h;
+  int type_off[kMaxTypes + 1] = {0};
+  int nbucket = 0;
+  bool buckets_valid = false;
+  // LAMMPS candidate cache
+  bool cand_valid = false;
+  int cand_nloc = -1;
+  // last evaluation sizes (debug copies)
+  int last_nloc = 0, last_nall = 0;
+  bool last_standalone = true;
+  // stage timers
+  bool timing = false;
+  hipEvent_t ev[kNumStages + 1] = {};
+  float stage_ms[kNumStages] = {0};
+
+  dp_model() {
+    bufs = {&coord_in, &atype_in, &sfrac,     &flags,    &gpos,       &ext,       &ext_type,
+            &mapping,  &cell_of,  &cell_count, &cell_start, &cell_cursor, &sorted,  &nlist,
+            &nreal,    &cand_off, &cand,      &items,    &Tsec,       &T,         &D,
+            &dD,       &dT,       &fitb,      &e_bucket, &edge_grad,  &cpart,     &rev_count,
+            &rev_off,  &rev_cursor, &rev,     &force_ws, &av_ws,      &ae_ws,     &partials,
+            &out10,    &status,   &scan_tmp};
+  }
+};
+
+namespace {
+
+template <class T>
+T* need(dp_model* M, Buf& b, size_t count) {
+  const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+  if (bytes > b.cap) {
+    if (b.p) {
+      DPAMD_HIP(hipFree(b.p));
+      M->bytes_now -= b.cap;
+    }
+    const size_t nb = bytes + bytes / 8;
+    b.p = nullptr;
+    b.cap = 0;
+    DPAMD_HIP(hipMalloc(&b.p, nb));
+    b.cap = nb;
+    M->bytes_now += nb;
+    M->bytes_peak = std::max(M->bytes_peak, M->bytes_now);
+  }
+  return static_cast<T*>(b.p);
+}
+
+// Grow while keeping the first `keep` bytes.
+template <class T>
+T* need_keep(dp_model* M, Buf& b, size_t count, size_t keep_count, hipStream_t st) {
+  const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+  if (bytes <= b.cap) return static_cast<T*>(b.p);
+  void* old = b.p;
+  const size_t old_cap = b.cap;
+  const size_t nb = bytes + bytes / 8;
+  void* np = nullptr;
+  DPAMD_HIP(hipMalloc(&np, nb));
+  M->bytes_now += nb;
+  M->bytes_peak = std::max(M->bytes_peak, M->bytes_now);
+  if (old && keep_count)
+    DPAMD_HIP(hipMemcpyAsync(np, old, keep_count * sizeof(T), hipMemcpyDeviceToDevice, st));
+  if (old) {
+    DPAMD_HIP(hipStreamSynchronize(st));
+    DPAMD_HIP(hipFree(old));
+    M->bytes_now -= old_cap;
+  }
+  b.p = np;
+  b.cap = nb;
+  return static_cast<T*>(np);
+}
+
+struct ApiError {
+  int code;
+  std::string msg;
+};
+
+// LAMMPS-shaped periodic box; formulas identical to the oracle's box_geometry.
+BoxParams make_box(const double* box, double rcut) {
+  BoxParams bp{};
+  for (int q = 0; q < 9; ++q) bp.h[q] = box[q];
+  const double xx = box[0], xy = box[3], yy = box[4], xz = box[6], yz = box[7], zz = box[8];
+  if (box[1] != 0.0 || box[2] != 0.0 || box[5] != 0.0)
+    throw ApiError{DP_ERR_ARG, "box must be lower-triangular (LAMMPS h: box[1]=box[2]=box[5]=0)"};
+  if (!(xx > 0.0 && yy > 0.0 && zz > 0.0))
+    throw ApiError{DP_ERR_ARG, "box diagonal must be positive"};
+  const double vol = xx * yy * zz;
+  const double bc0 = yy * zz, bc1 = xy * zz, bc2 = xy * yz - yy * xz;
+  const double ha = vol / std::sqrt(bc0 * bc0 + bc1 * bc1 + bc2 * bc2);
+  const double hb = (yy * zz) / std::sqrt(zz * zz + yz * yz);
+  const double hc = zz;
+  bp.rcf[0] = rcut / ha;
+  bp.rcf[1] = rcut / hb;
+  bp.rcf[2] = rcut / hc;
+  for (int d = 0; d < 3; ++d) {
+    bp.nrep[d] = (int)std::ceil(bp.rcf[d]);
+    bp.hi[d] = 1.0 + bp.rcf[d];
+    bp.origin[d] = 0.0;
+    bp.cell_lo[d] = -bp.rcf[d];
+    const double extent = 1.0 + 2.0 * bp.rcf[d];
+    int nc = (int)std::floor(extent / (bp.rcf[d] * (1.0 + 1e-6)));
+    nc = std::max(1, std::min(nc, 256));
+    bp.ncell[d] = nc;
+    bp.cw[d] = extent / nc;
+  }
+  bp.nshift = (2 * bp.nrep[0] + 1) * (2 * bp.nrep[1] + 1) * (2 * bp.nrep[2] + 1) - 1;
+  bp.periodic = 1;
+  return bp;
+}
+
+// Open system: a synthetic orthorhombic frame only for cell binning.
+BoxParams make_open_frame(int n, const double* coord, double rcut) {
+  BoxParams bp{};
+  double lo[3] = {0, 0, 0}, hi[3] = {0, 0, 0};
+  for (int d = 0; d < 3; ++d) {
+    lo[d] = n ? coord[d] : 0.0;
+    hi[d] = lo[d];
+  }
+  for (int k = 0; k < n; ++k)
+    for (int d = 0; d < 3; ++d) {
+      lo[d] = std::min(lo[d], coord[3 * k + d]);
+      hi[d] = std::max(hi[d], coord[3 * k + d]);
+    }
+  for (int d = 0; d < 3; ++d) {
+    const double L = (hi[d] - lo[d]) + 2.0;
+    bp.h[4 * d] = L;
+    bp.origin[d] = lo[d] - 1.0;
+    bp.rcf[d] = rcut / L;
+    bp.cell_lo[d] = 0.0;
+    int nc = (int)std::floor(1.0 / (bp.rcf[d] * (1.0 + 1e-6)));
+    nc = std::max(1, std::min(nc, 256));
+    bp.ncell[d] = nc;
+    bp.cw[d] = 1.0 / nc;
+  }
+  bp.nshift = 0;
+  bp.periodic = 0;
+  return bp;
+}
+
+void record(dp_model* M, hipStream_t st, int stage) {
+  if (M->timing) DPAMD_HIP(hipEventRecord(M->ev[stage], st));
+}
+
+// Group centres by type (stable) when the types change.
+void update_buckets(dp_model* M, int nloc, const int* atype_host, hipStream_t st) {
+  const int nt = M->host.ntypes;
+  if (M->buckets_valid && (int)M->atype_cache.size() == nloc &&
+      std::equal(atype_host, atype_host + nloc, M->atype_cache.begin()))
+    return;
+  M->atype_cache.assign(atype_host, atype_host + nloc);
+  M->items_h.clear();
+  M->items_h.reserve(nloc);
+  for (int t = 0; t < nt; ++t) {
+    M->type_off[t] = (int)M->items_h.size();
+    for (int k = 0; k < nloc; ++k)
+      if (atype_host[k] == t) M->items_h.push_back(k);
+  }
+  M->type_off[nt] = (int)M->items_h.size();
+  M->nbucket = M->type_off[nt];
+  int* d_items = need<int>(M, M->items, std::max(1, M->nbucket));
+  if (M->nbucket)
+    DPAMD_HIP(hipMemcpyAsync(d_items, M->items_h.data(), sizeof(int) * M->nbucket,
+                             hipMemcpyHostToDevice, st));
+  DPAMD_HIP(hipStreamSynchronize(st));
+  M->buckets_valid = true;
+}
+
+struct Outputs {
+  double* energy;       // device [1] or null
+  double* force;        // device [ntarget][3]
+  double* virial;       // device [9] or null
+  double* atom_energy;  // device [ntarget] or null
+  double* atom_virial;  // device [ntarget][9] or null
+};
+
+// Everything after the neighbour list; ext/ext_type/nlist/nreal/mapping ready.
+void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_mapping,
+               int ntarget, const Outputs& out) {
+  const ModelHost& m = M->host;
+  const int nt = m.ntypes, nnei = m.nnei, L3 = m.emb[2], axis = m.axis, Dn = L3 * axis;
+  const int nb = M->nbucket;
+  const double* ext = static_cast<const double*>(M->ext.p);
+  const int* nlist = static_cast<const int*>(M->nlist.p);
+  const int* nreal = static_cast<const int*>(M->nreal.p);
+  const int* items = static_cast<const int*>(M->items.p);
+  int* status = static_cast<int*>(M->status.p);
+
+  double* Tsec = need<double>(M, M->Tsec, (size_t)nloc * nt * 4 * L3);
+  double* T = need<double>(M, M->T, (size_t)nloc * 4 * L3);
+  double* D = need<double>(M, M->D, (size_t)std::max(nb, 1) * Dn);
+  double* dD = need<double>(M, M->dD, (size_t)std::max(nb, 1) * Dn);
+  double* dT = need<double>(M, M->dT, (size_t)nloc * 4 * L3);
+  const int Fmax = std::max(m.fit[0], std::max(m.fit[1], m.fit[2]));
+  double* fitb = need<double>(M, M->fitb, (size_t)8 * std::max(nb, 1) * Fmax);
+  double* e_bucket = need<double>(M, M->e_bucket, (size_t)std::max(nb, 1));
+  double* edge_grad = need<double>(M, M->edge_grad, (size_t)nloc * nnei * 3);
+  double* cpart = need<double>(M, M->cpart, (size_t)nloc * nt * 12);
+  DPAMD_HIP(hipMemsetAsync(cpart, 0, sizeof(double) * (size_t)nloc * nt * 12, st));
+
+  EmbArgs ea{};
+  ea.ntypes = nt;
+  ea.nnei = nnei;
+  ea.npair = nt * nt;
+  for (int t = 0; t < nt; ++t) ea.sel[t] = m.sel[t];
+  for (int t = 0; t <= nt; ++t) {
+    ea.sec[t] = m.sec[t];
+    ea.type_off[t] = M->type_off[t];
+  }
+  ea.stride = M->el.stride;
+  ea.rcut = m.rcut;
+  ea.rcut_smth = m.rcut_smth;
+  ea.inv_nnei = 1.0 / (double)nnei;
+  ea.emb = M->d_emb;
+  ea.envp = M->d_envp;
+  ea.ext = ext;
+  ea.nlist = nlist;
+  ea.nreal = nreal;
+  ea.items = items;
+  ea.Tsec = Tsec;
+  ea.dT = dT;
+  ea.edge_grad = edge_grad;
+  ea.cpart = cpart;
+  auto block_table = [&](int waves) {
+    int acc = 0;
+    for (int p = 0; p < nt * nt; ++p) {
+      ea.block_off[p] = acc;
+      const int ti = p / nt;
+      const int cnt = M->type_off[ti + 1] - M->type_off[ti];
+      acc += (cnt + waves - 1) / waves;
+    }
+    ea.block_off[nt * nt] = acc;
+    return acc;
+  };
+
+  int nblk = block_table(embed_waves_fwd(M->el));
+  launch_embed_fwd(st, M->el, ea, nblk);
+  record(M, st, kStEmbFwd + 1);
+
+  DescArgs da{};
+  da.ntypes = nt;
+  da.nloc = nb;
+  da.L3 = L3;
+  da.axis = axis;
+  da.nnei = nnei;
+  for (int t = 0; t < nt; ++t) da.sel[t] = m.sel[t];
+  da.inv_nnei = 1.0 / (double)nnei;
+  da.items = items;
+  da.ext_type = static_cast<const int*>(M->ext_type.p);
+  da.nreal = nreal;
+  da.Tsec = Tsec;
+  da.tpad = M->d_tpad;
+  da.T = T;
+  da.D = D;
+  launch_descriptor(st, da);
+  record(M, st, kStDescr + 1);
+
+  for (int t = 0; t < nt; ++t) {
+    const int rows = M->type_off[t + 1] - M->type_off[t];
+    if (rows <= 0) continue;
+    const double* P = M->d_fit + (size_t)t * m.fit_block;
+    FitNet net{};
+    const int ins[3] = {Dn, m.fit[0], m.fit[1]};
+    for (int k = 0; k < 3; ++k) {
+      net.L[k].W = P + M->fo.W[k];
+      net.L[k].b = P + M->fo.b[k];
+      net.L[k].idt = M->fo.idt[k] >= 0 ? P + M->fo.idt[k] : nullptr;
+      net.L[k].in = ins[k];
+      net.L[k].out = m.fit[k];
+    }
+    net.Wo = P + M->fo.Wo;
+    net.bo = m.fit_params[(size_t)t * m.fit_block + M->fo.bo];
+    net.bias = m.bias[t];
+    const size_t r0 = (size_t)M->type_off[t];
+    const size_t slab = (size_t)std::max(nb, 1) * Fmax;
+    FitBufs fb{};
+    double* base = fitb;
+    double** slots[8] = {&fb.H0, &fb.T1, &fb.H1, &fb.T2, &fb.H2, &fb.dZa, &fb.dZb, &fb.dH};
+    // slab q holds [rows][F] of every type back to back; F <= Fmax
+    for (int q = 0; q < 8; ++q) *slots[q] = base + q * slab + r0 * (size_t)Fmax;
+    launch_fitting(st, net, rows, D + r0 * Dn, fb, dD + r0 * Dn, e_bucket + r0);
+  }
+  record(M, st, kStFit + 1);
+
+  launch_dT(st, nb, L3, axis, items, T, dD, dT);
+  record(M, st, kStDT + 1);
+
+  nblk = block_table(embed_waves_bwd(M->el));
+  launch_embed_bwd(st, M->el, ea, nblk);
+  record(M, st, kStEmbBwd + 1);
+
+  // reverse list + gather
+  const long nedge = (long)nloc * nnei;
+  int* rcount = need<int>(M, M->rev_count, (size_t)ntarget + 1);
+  int* roff = need<int>(M, M->rev_off, (size_t)ntarget + 1);
+  int* rcur = need<int>(M, M->rev_cursor, (size_t)ntarget + 1);
+  int* rev = need<int>(M, M->rev, (size_t)std::max<long>(nedge, 1));
+  DPAMD_HIP(hipMemsetAsync(rcount, 0, sizeof(int) * ((size_t)ntarget + 1), st));
+  DPAMD_HIP(hipMemsetAsync(rcur, 0, sizeof(int) * ((size_t)ntarget + 1), st));
+  launch_rev_count(st, nedge, nnei, nlist, d_mapping, rcount);
+  {
+    const size_t tb = scan_temp_bytes(ntarget + 1);
+    void* tmp = need<char>(M, M->scan_tmp, tb);
+    exclusive_scan_int(st, rcount, roff, ntarget + 1, tmp, tb);
+  }
+  launch_rev_fill(st, nedge, nnei, nlist, d_mapping, roff, rcur, rev);
+  launch_force_gather(st, ntarget, nloc, nt, nnei, roff, rev, nlist, ext, edge_grad, cpart,
+                      out.force, out.atom_virial, status);
+  record(M, st, kStForce + 1);
+
+  double* partials = need<double>(M, M->partials, 256 * 10);
+  double* out10 = need<double>(M, M->out10, 10);
+  launch_reduce_ev(st, nb, nloc, nt, e_bucket, cpart, partials, out10);
+  if (out.energy) DPAMD_HIP(hipMemcpyAsync(out.energy, out10, 8, hipMemcpyDeviceToDevice, st));
+  if (out.virial)
+    DPAMD_HIP(hipMemcpyAsync(out.virial, out10 + 1, 72, hipMemcpyDeviceToDevice, st));
+  if (out.atom_energy) {
+    DPAMD_HIP(hipMemsetAsync(out.atom_energy, 0, sizeof(double) * (size_t)ntarget, st));
+    launch_scatter_energy(st, nb, items, e_bucket, out.atom_energy);
+  }
+  record(M, st, kStReduce + 1);
+  (void)nall;
+}
+
+// Ghosts + cells + nlist for the standalone path. Returns nall.
+int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* d_coord,
+                           const int* d_atype, const BoxParams& bp) {
+  const ModelHost& m = M->host;
+  double* sfrac = need<double>(M, M->sfrac, (size_t)nloc * 3);
+  double* ext = need<double>(M, M->ext, (size_t)nloc * 3 * 2);
+  int* ext_type = need<int>(M, M->ext_type, (size_t)nloc * 2);
+  int* mapping = need<int>(M, M->mapping, (size_t)nloc * 2);
+  launch_wrap(st, nloc, d_coord, d_atype, bp, ext, ext_type, mapping, sfrac);
+  int nall = nloc;
+  if (bp.nshift > 0 && nloc > 0) {
+    const long nf = (long)bp.nshift * nloc;
+    if (nf >= (1L << 31) - 1) throw ApiError{DP_ERR_CAPACITY, "too many ghost candidates"};
+    int* flags = need<int>(M, M->flags, (size_t)nf);
+    int* pos = need<int>(M, M->gpos, (size_t)nf);
+    launch_ghost_flags(st, nloc, bp, sfrac, flags);
+    const size_t tb = scan_temp_bytes((int)nf);
+    void* tmp = need<char>(M, M->scan_tmp, tb);
+    exclusive_scan_int(st, flags, pos, (int)nf, tmp, tb);
+    int last[2] = {0, 0};
+    DPAMD_HIP(hipMemcpyAsync(&last[0], pos + nf - 1, 4, hipMemcpyDeviceToHost, st));
+    DPAMD_HIP(hipMemcpyAsync(&last[1], flags + nf - 1, 4, hipMemcpyDeviceToHost, st));
+    DPAMD_HIP(hipStreamSynchronize(st));
+    nall = nloc + last[0] + last[1];
+    ext = need_keep<double>(M, M->ext, (size_t)nall * 3, (size_t)nloc * 3, st);
+    ext_type = need_keep<int>(M, M->ext_type, (size_t)nall, (size_t)nloc, st);
+    mapping = need_keep<int>(M, M->mapping, (size_t)nall, (size_t)nloc, st);
+    launch_ghost_fill(st, nloc, bp, flags, pos, ext, ext_type, mapping);
+  }
+  // cells
+  const int ncell = bp.ncell[0] * bp.ncell[1] * bp.ncell[2];
+  int* cell_of = need<int>(M, M->cell_of, (size_t)nall);
+  int* ccount = need<int>(M, M->cell_count, (size_t)ncell + 1);
+  int* cstart = need<int>(M, M->cell_start, (size_t)ncell + 1);
+  int* ccur = need<int>(M, M->cell_cursor, (size_t)ncell + 1);
+  CellAtom* sorted = need<CellAtom>(M, M->sorted, (size_t)nall);
+  DPAMD_HIP(hipMemsetAsync(ccount, 0, sizeof(int) * ((size_t)ncell + 1), st));
+  DPAMD_HIP(hipMemsetAsync(ccur, 0, sizeof(int) * ((size_t)ncell + 1), st));
+  launch_cell_assign(st, nall, bp, ext, cell_of, ccount);
+  {
+    const size_t tb = scan_temp_bytes(ncell + 1);
+    void* tmp = need<char>(M, M->scan_tmp, tb);
+    exclusive_scan_int(st, ccount, cstart, ncell + 1, tmp, tb);
+  }
+  launch_cell_scatter(st, nall, cell_of, cstart, ccur, ext, ext_type, sorted);
+  record(M, st, kStGeom + 1);
+  NlParams np{};
+  np.ntypes = m.ntypes;
+  np.nnei = m.nnei;
+  for (int t = 0; t < m.ntypes; ++t) np.sel[t] = m.sel[t];
+  for (int t = 0; t <= m.ntypes; ++t) np.sec[t] = m.sec[t];
+  np.rc2 = m.rcut * m.rcut;
+  int* nlist = need<int>(M, M->nlist, (size_t)std::max(nloc, 1) * m.nnei);
+  int* nreal = need<int>(M, M->nreal, (size_t)std::max(nloc, 1) * m.ntypes);
+  launch_nlist_cells(st, nloc, bp, np, ext, ext_type, cell_of, cstart, sorted, nlist, nreal,
+                     static_cast<int*>(M->status.p));
+  record(M, st, kStNlist + 1);
+  return nall;
+}
+
+void check_status(dp_model* M, hipStream_t st) {
+  int s = 0;
+  DPAMD_HIP(hipMemcpyAsync(&s, M->status.p, 4, hipMemcpyDeviceToHost, st));
+  DPAMD_HIP(hipStreamSynchronize(st));
+  if (s & kStatusNeighbourOverflow)
+    throw ApiError{DP_ERR_CAPACITY, "more than " + std::to_string(kMaxCand) +
+                                        " neighbours within rcut of one atom"};
+  if (s & kStatusReverseOverflow)
+    throw ApiError{DP_ERR_CAPACITY,
+                   "more than " + std::to_string(kMaxRev) + " edges point at one atom"};
+}
+
+void begin(dp_model* M, hipStream_t st) {
+  DPAMD_HIP(hipSetDevice(M->device));
+  need<int>(M, M->status, 1);
+  DPAMD_HIP(hipMemsetAsync(M->status.p, 0, 4, st));
+  if (M->timing) {
+    for (int q = 0; q <= kNumStages; ++q)
+      if (!M->ev[q]) DPAMD_HIP(hipEventCreate(&M->ev[q]));
+    DPAMD_HIP(hipEventRecord(M->ev[0], st));
+  }
+}
+
+void finish(dp_model* M, hipStream_t st) {
+  check_status(M, st);
+  if (M->timing) {
+    for (int q = 0; q < kNumStages; ++q) {
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, M->ev[q], M->ev[q + 1]) != hipSuccess) ms = 0.f;
+      M->stage_ms[q] = ms;
+    }
+  }
+}
+
+template <class F>
+int guarded(dp_model* M, F&& f) {
+  if (!M) return DP_ERR_ARG;
+  try {
+    M->err.clear();
+    f();
+    return DP_OK;
+  } catch (const ApiError& e) {
+    M->err = e.msg;
+    return e.code;
+  } catch (const HipError& e) {
+    M->err = std::string("HIP error ") + hipGetErrorString(e.code) + " in " + e.where;
+    return DP_ERR_HIP;
+  } catch (const std::exception& e) {
+    M->err = e.what();
+    return DP_ERR_ARG;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int dp_create(const char* path, int gpu_rank, const void* file_content, size_t content_len,
+              int precision, dp_model** out) {
+  if (!out) return DP_ERR_ARG;
+  *out = nullptr;
+  dp_model* M = new dp_model();
+  int rc = guarded(M, [&]() {
+    if (precision != DP_PREC_FP64)
+      throw ApiError{DP_ERR_ARG, "only DP_PREC_FP64 is implemented"};
+    M->precision = precision;
+    std::vector<unsigned char> buf;
+    if (file_content && content_len) {
+      const auto* b = static_cast<const unsigned char*>(file_content);
+      buf.assign(b, b + content_len);
+    } else {
+      if (!path) throw ApiError{DP_ERR_ARG, "no model path or content"};
+      std::ifstream f(path, std::ios::binary);
+      if (!f) throw ApiError{DP_ERR_MODEL, std::string("cannot open model file ") + path};
+      buf.assign(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
+    }
+    const std::string perr = parse_model(buf.data(), buf.size(), M->host);
+    if (!perr.empty()) throw ApiError{DP_ERR_MODEL, perr};
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+      throw ApiError{DP_ERR_NO_GPU, "no HIP device visible"};
+    if (gpu_rank < 0) gpu_rank = 0;
+    M->device = gpu_rank % ndev;
+    DPAMD_HIP(hipSetDevice(M->device));
+    hipDeviceProp_t prop;
+    DPAMD_HIP(hipGetDeviceProperties(&prop, M->device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+      throw ApiError{DP_ERR_NO_GPU, std::string("device is ") + prop.gcnArchName +
+                                        ", this library is built for gfx950"};
+    const ModelHost& m = M->host;
+    M->el = make_emb_layout(m.emb[0], m.emb[1], m.emb[2]);
+    std::vector<double> emb, envp, tpad;
+    pack_embedding(m, M->el, emb, envp, tpad);
+    auto upload = [&](double*& dst, const std::vector<double>& src) {
+      DPAMD_HIP(hipMalloc(&dst, std::max<size_t>(8, src.size() * 8)));
+      M->bytes_now += src.size() * 8;
+      DPAMD_HIP(hipMemcpy(dst, src.data(), src.size() * 8, hipMemcpyHostToDevice));
+    };
+    upload(M->d_emb, emb);
+    upload(M->d_envp, envp);
+    upload(M->d_tpad, tpad);
+    upload(M->d_fit, m.fit_params);
+    M->bytes_peak = M->bytes_now;
+    M->fo = fit_offsets(m);
+  });
+  if (rc != DP_OK) {
+    // keep the handle so the caller can read dp_last_error, unless nothing usable
+    *out = M;
+    return rc;
+  }
+  *out = M;
+  return DP_OK;
+}
+
+void dp_destroy(dp_model* M) {
+  if (!M) return;
+  hipSetDevice(M->device);
+  for (Buf* b : M->bufs)
+    if (b->p) hipFree(b->p);
+  for (double* p : {M->d_emb, M->d_envp, M->d_tpad, M->d_fit})
+    if (p) hipFree(p);
+  for (auto& e : M->ev)
+    if (e) hipEventDestroy(e);
+  delete M;
+}
+
+int dp_get_info(const dp_model* M, dp_model_info* info) {
+  if (!M || !info) return DP_ERR_ARG;
+  std::memset(info, 0, sizeof(*info));
+  const ModelHost& m = M->host;
+  info->ntypes = m.ntypes;
+  info->nnei = m.nnei;
+  for (int t = 0; t < m.ntypes; ++t) {
+    info->sel[t] = m.sel[t];
+    std::strncpy(info->type_map[t], m.type_map[t].c_str(), 15);
+  }
+  info->rcut = m.rcut;
+  info->rcut_smth = m.rcut_smth;
+  for (int k = 0; k < 3; ++k) {
+    info->emb[k] = m.emb[k];
+    info->fit[k] = m.fit[k];
+  }
+  info->axis = m.axis;
+  info->precision = M->precision;
+  return DP_OK;
+}
+
+const char* dp_last_error(const dp_model* M) { return M ? M->err.c_str() : "null handle"; }
+
+int dp_compute_device(dp_model* M, int natoms, const double* d_coord, const int* d_atype,
+                      const double* box, int ago, double* d_energy, double* d_force,
+                      double* d_virial, double* d_atom_energy, double* d_atom_virial,
+                      void* stream) {
+  return guarded(M, [&]() {
+    if (natoms < 0 || (natoms > 0 && (!d_coord || !d_atype || !d_force)))
+      throw ApiError{DP_ERR_ARG, "null device pointer"};
+    if (!box) throw ApiError{DP_ERR_ARG, "dp_compute_device needs a periodic box"};
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    begin(M, st);
+    if (ago == 0 || !M->buckets_valid || (int)M->atype_cache.size() != natoms) {
+      std::vector<int> at(natoms);
+      if (natoms)
+        DPAMD_HIP(hipMemcpyAsync(at.data(), d_atype, sizeof(int) * natoms, hipMemcpyDeviceToHost, st));
+      DPAMD_HIP(hipStreamSynchronize(st));
+      M->buckets_valid = false;
+      update_buckets(M, natoms, at.data(), st);
+    }
+    const BoxParams bp = make_box(box, M->host.rcut);
+    const int nall = build_standalone_nlist(M, st, natoms, d_coord, d_atype, bp);
+    Outputs o{d_energy, d_force, d_virial, d_atom_energy, d_atom_virial};
+    run_model(M, st, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o);
+    M->last_nloc = natoms;
+    M->last_nall = nall;
+    M->last_standalone = true;
+    finish(M, st);
+  });
+}
+
+int dp_compute(dp_model* M, int natoms, const double* coord, const int* atype, const double* box,
+               double* energy, double* force, double* virial, double* atom_energy,
+               double* atom_virial) {
+  return guarded(M, [&]() {
+    if (natoms < 0 || (natoms > 0 && (!coord || !atype)))
+      throw ApiError{DP_ERR_ARG, "null coord/atype"};
+    hipStream_t st = nullptr;
+    begin(M, st);
+    update_buckets(M, natoms, atype, st);
+    const BoxParams bp = box ? make_box(box, M->host.rcut)
+                             : make_open_frame(natoms, coord, M->host.rcut);
+    double* dc = need<double>(M, M->coord_in, (size_t)std::max(natoms, 1) * 3);
+    int* da = need<int>(M, M->atype_in, (size_t)std::max(natoms, 1));
+    if (natoms) {
+      DPAMD_HIP(hipMemcpyAsync(dc, coord, sizeof(double) * 3 * natoms, hipMemcpyHostToDevice, st));
+      DPAMD_HIP(hipMemcpyAsync(da, atype, sizeof(int) * natoms, hipMemcpyHostToDevice, st));
+    }
+    const int nall = build_standalone_nlist(M, st, natoms, dc, da, bp);
+    double* f = need<double>(M, M->force_ws, (size_t)std::max(natoms, 1) * 3);
+    double* av = atom_virial ? need<double>(M, M->av_ws, (size_t)std::max(natoms, 1) * 9) : nullptr;
+    double* ae = atom_energy ? need<double>(M, M->ae_ws, (size_t)std::max(natoms, 1)) : nullptr;
+    double* o10 = need<double>(M, M->out10, 10);
+    Outputs o{nullptr, f, nullptr, ae, av};
+    run_model(M, st, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o);
+    M->last_nloc = natoms;
+    M->last_nall = nall;
+    M->last_standalone = true;
+    finish(M, st);
+    double ev[10];
+    DPAMD_HIP(hipMemcpy(ev, o10, sizeof(ev), hipMemcpyDeviceToHost));
+    if (energy) *energy = ev[0];
+    if (virial) std::memcpy(virial, ev + 1, 72);
+    if (force && natoms) DPAMD_HIP(hipMemcpy(force, f, sizeof(double) * 3 * natoms, hipMemcpyDeviceToHost));
+    if (atom_energy && natoms)
+      DPAMD_HIP(hipMemcpy(atom_energy, ae, sizeof(double) * natoms, hipMemcpyDeviceToHost));
+    if (atom_virial && natoms)
+      DPAMD_HIP(hipMemcpy(atom_virial, av, sizeof(double) * 9 * natoms, hipMemcpyDeviceToHost));
+  });
+}
+
+int dp_compute_nlist(dp_model* M, int nall, int nghost, const double* coord, const int* atype,
+                     const double* box, int inum, const int* ilist, const int* numneigh,
+                     const int* const* firstneigh, int neigh_mask, int ago, double* energy,
+                     double* force, double* virial, double* atom_energy, double* atom_virial) {
+  return guarded(M, [&]() {
+    (void)box;
+    const int nloc = nall - nghost;
+    if (nall < 0 || nghost < 0 || nloc < 0) throw ApiError{DP_ERR_ARG, "bad nall/nghost"};
+    if (nall > 0 && (!coord || !atype)) throw ApiError{DP_ERR_ARG, "null coord/atype"};
+    if (inum > 0 && (!ilist || !numneigh || !firstneigh))
+      throw ApiError{DP_ERR_ARG, "null neighbour list"};
+    hipStream_t st = nullptr;
+    begin(M, st);
+    const ModelHost& m = M->host;
+    update_buckets(M, nloc, atype, st);
+    double* ext = need<double>(M, M->ext, (size_t)std::max(nall, 1) * 3);
+    int* ext_type = need<int>(M, M->ext_type, (size_t)std::max(nall, 1));
+    if (nall) {
+      DPAMD_HIP(hipMemcpyAsync(ext, coord, sizeof(double) * 3 * nall, hipMemcpyHostToDevice, st));
+      DPAMD_HIP(hipMemcpyAsync(ext_type, atype, sizeof(int) * nall, hipMemcpyHostToDevice, st));
+    }
+    if (ago == 0 || !M->cand_valid || M->cand_nloc != nloc) {
+      std::vector<long> off(nloc + 1, 0);
+      std::vector<int> cnt(nloc, 0);
+      for (int ii = 0; ii < inum; ++ii) {
+        const int i = ilist[ii];
+        if (i < 0 || i >= nloc) throw ApiError{DP_ERR_ARG, "ilist entry outside local atoms"};
+        cnt[i] = numneigh[ii];
+      }
+      for (int i = 0; i < nloc; ++i) off[i + 1] = off[i] + cnt[i];
+      std::vector<int> cand(std::max<long>(off[nloc], 1));
+      for (int ii = 0; ii < inum; ++ii) {
+        const int i = ilist[ii];
+        for (int q = 0; q < numneigh[ii]; ++q) {
+          int j = firstneigh[ii][q];
+          if (neigh_mask) j &= neigh_mask;
+          if (j < 0 || j >= nall) throw ApiError{DP_ERR_ARG, "neighbour index outside nall"};
+          cand[off[i] + q] = j;
+        }
+      }
+      long* d_off = need<long>(M, M->cand_off, (size_t)nloc + 1);
+      int* d_cand = need<int>(M, M->cand, cand.size());
+      DPAMD_HIP(hipMemcpyAsync(d_off, off.data(), sizeof(long) * (nloc + 1), hipMemcpyHostToDevice, st));
+      DPAMD_HIP(hipMemcpyAsync(d_cand, cand.data(), sizeof(int) * cand.size(), hipMemcpyHostToDevice, st));
+      DPAMD_HIP(hipStreamSynchronize(st));
+      M->cand_valid = true;
+      M->cand_nloc = nloc;
+    }
+    record(M, st, kStGeom + 1);
+    NlParams np{};
+    np.ntypes = m.ntypes;
+    np.nnei = m.nnei;
+    for (int t = 0; t < m.ntypes; ++t) np.sel[t] = m.sel[t];
+    for (int t = 0; t <= m.ntypes; ++t) np.sec[t] = m.sec[t];
+    np.rc2 = m.rcut * m.rcut;
+    int* nlist = need<int>(M, M->nlist, (size_t)std::max(nloc, 1) * m.nnei);
+    int* nreal = need<int>(M, M->nreal, (size_t)std::max(nloc, 1) * m.ntypes);
+    launch_nlist_csr(st, nloc, np, ext, ext_type, static_cast<const long*>(M->cand_off.p),
+                     static_cast<const int*>(M->cand.p), nlist, nreal,
+                     static_cast<int*>(M->status.p));
+    record(M, st, kStNlist + 1);
+    double* f = need<double>(M, M->force_ws, (size_t)std::max(nall, 1) * 3);
+    double* av = atom_virial ? need<double>(M, M->av_ws, (size_t)std::max(nall, 1) * 9) : nullptr;
+    double* ae = atom_energy ? need<double>(M, M->ae_ws, (size_t)std::max(nall, 1)) : nullptr;
+    double* o10 = need<double>(M, M->out10, 10);
+    Outputs o{nullptr, f, nullptr, ae, av};
+    run_model(M, st, nloc, nall, nullptr, nall, o);
+    M->last_nloc = nloc;
+    M->last_nall = nall;
+    M->last_standalone = false;
+    finish(M, st);
+    double ev[10];
+    DPAMD_HIP(hipMemcpy(ev, o10, sizeof(ev), hipMemcpyDeviceToHost));
+    if (energy) *energy = ev[0];
+    if (virial) std::memcpy(virial, ev + 1, 72);
+    if (force && nall) DPAMD_HIP(hipMemcpy(force, f, sizeof(double) * 3 * nall, hipMemcpyDeviceToHost));
+    if (atom_energy && nall)
+      DPAMD_HIP(hipMemcpy(atom_energy, ae, sizeof(double) * nall, hipMemcpyDeviceToHost));
+    if (atom_virial && nall)
+      DPAMD_HIP(hipMemcpy(atom_virial, av, sizeof(double) * 9 * nall, hipMemcpyDeviceToHost));
+  });
+}
+
+long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
+  if (!M) return DP_ERR_ARG;
+  long result = 0;
+  const int rc = guarded(M, [&]() {
+    const ModelHost& m = M->host;
+    const int nloc = M->last_nloc, nall = M->last_nall;
+    const int Dn = m.emb[2] * m.axis;
+    auto copy = [&](const void* src, size_t bytes) {
+      result = (long)bytes;
+      if (dst && capacity && src) {
+        DPAMD_HIP(hipDeviceSynchronize());
+        DPAMD_HIP(hipMemcpy(dst, src, std::min(bytes, capacity), hipMemcpyDeviceToHost));
+      }
+    };
+    // bucket-ordered arrays are returned in atom order
+    auto copy_bucket = [&](const void* src, size_t per_atom) {
+      const size_t bytes = (size_t)nloc * per_atom * sizeof(double);
+      result = (long)bytes;
+      if (!dst || !capacity || !src) return;
+      std::vector<double> tmp((size_t)M->nbucket * per_atom);
+      DPAMD_HIP(hipDeviceSynchronize());
+      if (!tmp.empty())
+        DPAMD_HIP(hipMemcpy(tmp.data(), src, tmp.size() * 8, hipMemcpyDeviceToHost));
+      std::vector<double> outv((size_t)nloc * per_atom, 0.0);
+      for (int p = 0; p < M->nbucket; ++p)
+        std::memcpy(&outv[(size_t)M->items_h[p] * per_atom], &tmp[(size_t)p * per_atom],
+                    per_atom * 8);
+      std::memcpy(dst, outv.data(), std::min(bytes, capacity));
+    };
+    switch (stage) {
+      case DP_STAGE_NLIST: copy(M->nlist.p, (size_t)nloc * m.nnei * 4); break;
+      case DP_STAGE_EXT_COORD: copy(M->ext.p, (size_t)nall * 24); break;
+      case DP_STAGE_EXT_TYPE: copy(M->ext_type.p, (size_t)nall * 4); break;
+      case DP_STAGE_MAPPING:
+        if (!M->last_standalone) throw ApiError{DP_ERR_ARG, "no mapping on the LAMMPS path"};
+        copy(M->mapping.p, (size_t)nall * 4);
+        break;
+      case DP_STAGE_DESCRPT: copy_bucket(M->D.p, Dn); break;
+      case DP_STAGE_DEDD: copy_bucket(M->dD.p, Dn); break;
+      case DP_STAGE_ATOM_ENERGY: copy_bucket(M->e_bucket.p, 1); break;
+      case DP_STAGE_EDGE_GRAD: copy(M->edge_grad.p, (size_t)nloc * m.nnei * 24); break;
+      default: throw ApiError{DP_ERR_ARG, "unknown stage"};
+    }
+  });
+  return rc == DP_OK ? result : rc;
+}
+
+int dp_stage_times(dp_model* M, int enable, double* times, int n, char* names, size_t names_len) {
+  if (!M) return DP_ERR_ARG;
+  M->timing = enable != 0;
+  for (int q = 0; q < std::min(n, (int)kNumStages); ++q) times[q] = M->stage_ms[q];
+  if (names && names_len) {
+    std::string all;
+    for (int q = 0; q < kNumStages; ++q) {
+      all += kStageNames[q];
+      all.push_back('\0');
+    }
+    std::memcpy(names, all.data(), std::min(names_len, all.size()));
+  }
+  return kNumStages;
+}
+
+size_t dp_device_bytes(const dp_model* M) { return M ? M->bytes_peak : 0; }
+
+}  // extern "C"

@@ -1,0 +1,68 @@
+// Padded layout of one embedding net (s -> L1 -> L2 -> L3) as the MFMA
+// kernels read it from LDS. Shared by the host packer and the kernels so the
+// two cannot drift.
+//
+//   w1[K2P] b1[K2P] | W2[K2P][L2P] b2[L2P] | W3[K3P][L3P] b3[L3P]
+//
+// K2P = 4*ceil(L1/4) (k-steps of layer 2), L2P = 16*ceil(L2/16) (16-row
+// output tiles of layer 2), K3P = 4*ceil(L2/4), L3P = 16*ceil(L3/16).
+// Padding entries are zero, so padded features evaluate to tanh(0) = 0.
+#pragma once
+
+namespace dpamd {
+
+struct EmbLayout {
+  int L1, L2, L3;
+  int NQ2, K2P, NT2, L2P, NQ3, K3P, NU3, L3P;
+  int off_w1, off_b1, off_w2, off_b2, off_w3, off_b3, size, stride;
+};
+
+inline EmbLayout make_emb_layout(int L1, int L2, int L3) {
+  EmbLayout e;
+  e.L1 = L1;
+  e.L2 = L2;
+  e.L3 = L3;
+  e.NQ2 = (L1 + 3) / 4;
+  e.K2P = 4 * e.NQ2;
+  e.NT2 = (L2 + 15) / 16;
+  e.L2P = 16 * e.NT2;
+  e.NQ3 = (L2 + 3) / 4;
+  e.K3P = 4 * e.NQ3;
+  e.NU3 = (L3 + 15) / 16;
+  e.L3P = 16 * e.NU3;
+  e.off_w1 = 0;
+  e.off_b1 = e.K2P;
+  e.off_w2 = 2 * e.K2P;
+  e.off_b2 = e.off_w2 + e.K2P * e.L2P;
+  e.off_w3 = e.off_b2 + e.L2P;
+  e.off_b3 = e.off_w3 + e.K3P * e.L3P;
+  e.size = e.off_b3 + e.L3P;
+  e.stride = (e.size + 31) / 32 * 32;
+  return e;
+}
+
+template <int L1_, int L2_, int L3_>
+struct EmbShape {
+  static constexpr int L1 = L1_, L2 = L2_, L3 = L3_;
+  static constexpr int NQ2 = (L1 + 3) / 4;
+  static constexpr int K2P = 4 * NQ2;
+  static constexpr int NT2 = (L2 + 15) / 16;
+  static constexpr int L2P = 16 * NT2;
+  static constexpr int NQ3 = (L2 + 3) / 4;
+  static constexpr int K3P = 4 * NQ3;
+  static constexpr int NU3 = (L3 + 15) / 16;
+  static constexpr int L3P = 16 * NU3;
+  static constexpr int OFF_W1 = 0;
+  static constexpr int OFF_B1 = K2P;
+  static constexpr int OFF_W2 = 2 * K2P;
+  static constexpr int OFF_B2 = OFF_W2 + K2P * L2P;
+  static constexpr int OFF_W3 = OFF_B2 + L2P;
+  static constexpr int OFF_B3 = OFF_W3 + K3P * L3P;
+  static constexpr int SIZE = OFF_B3 + L3P;
+  // residual kinds: 0 none, 1 identity, 2 concat [x, x]
+  static constexpr int RES2 = (L2 == L1) ? 1 : (L2 == 2 * L1 ? 2 : 0);
+  static constexpr int RES3 = (L3 == L2) ? 1 : (L3 == 2 * L2 ? 2 : 0);
+  static constexpr bool X1_ALIGNED = (L1 % 16) == 0;  // layer-2 residual is register-local
+};
+
+}  // namespace dpamd

@@ -1,0 +1,556 @@
+// Fused environment matrix + embedding net + descriptor contraction on
+// gfx950 FP64 MFMA (v_mfma_f64_16x16x4f64), and its backward.
+//
+// Work unit: one wave owns one (centre i, neighbour section tj) item and walks
+// its real slots in tiles of 16; a workgroup holds the padded weights of one
+// (ti, tj) net in LDS and serves WAVES items of that pair. G is never written
+// to HBM: the forward kernel contracts each tile into T on the fly and the
+// backward kernel recomputes it.
+//
+// Forward, per tile (lane = 16g + c, slot column c):
+//   env row R (fp64) -> s = R[0]
+//   layer 1 (elementwise) produced directly as the B operand of layer 2
+//   layer 2 transposed, Y2^T = W2^T X1^T: its D registers (row g+4r) are the
+//      natural-order B operand (k = feature 4q+g) of the next product
+//   layer 3 non-transposed, Y3 = X2 W3 (A operand = layer-2 registers), so
+//      each lane holds G[slot g+4r][feature 16u+c]; the [x,x] residual comes
+//      from an LDS copy of X2
+//   T[m][f] += sum_slots R[slot][m] G[slot][f] on VALU, lane-local, reduced
+//      over the 4 lane groups once per item.
+// Backward, per tile: layers 1-3 all transposed for the primal and the
+//   forward-mode tangent dG/ds (same weight fragments, two MFMA chains), then
+//   u = dT.G and v = dT.G' as lane-partial dot products; the layer-3 residual
+//   enters through a folded dT (dT[f'] + dT[f'+L2]) against X2 itself, so no
+//   residual is materialised. dE/dR = u/nnei, dE/ds = R.v/nnei, and the edge
+//   gradient g = sum_m dE/dR_m dR_m/dd is written per slot.
+//
+// Reference analogs: the tabulated radial + PairFiLM embedding analog
+// include/dpa_chain/graph_compress.cuh:91-154, the per-row moment accumulation
+// deepmd-op/overlays/op/pt/dpa4c/raw_kernel.cuh:71-120, the "reproduce the
+// amplitude instead of storing it" recompute backward
+// include/dpa_chain/graph_compress.cuh:9-10 and
+// deepmd-op/overlays/op/pt/dpa4c/graph_compress_kernel.cuh:1458-1466.
+#include "kernels.h"
+
+namespace dpamd {
+
+struct EnvOut {
+  double R[4];
+};
+
+// spline5 switch and the normalised env row [sw/r, sw x/r^2, sw y/r^2, sw z/r^2].
+__device__ __forceinline__ void env_value(double d0, double d1, double d2, double rs, double rc,
+                                          const double* avg, const double* sd, double* Rn) {
+  const double r2 = d0 * d0 + d1 * d1 + d2 * d2;
+  const double r = sqrt(r2);
+  double sw;
+  if (r < rs) {
+    sw = 1.0;
+  } else if (r >= rc) {
+    sw = 0.0;
+  } else {
+    const double u = (r - rs) / (rc - rs);
+    const double u2 = u * u, u3 = u2 * u;
+    sw = u3 * (-6.0 * u2 + 15.0 * u - 10.0) + 1.0;
+  }
+  const double inv_r = 1.0 / r;
+  const double inv_r2 = inv_r * inv_r;
+  Rn[0] = (sw * inv_r - avg[0]) / sd[0];
+  Rn[1] = (sw * d0 * inv_r2 - avg[1]) / sd[1];
+  Rn[2] = (sw * d1 * inv_r2 - avg[2]) / sd[2];
+  Rn[3] = (sw * d2 * inv_r2 - avg[3]) / sd[3];
+}
+
+// Edge gradient g = sum_m nd[m] * d(Rn_m)/dd for one slot.
+__device__ __forceinline__ void env_grad(double d0, double d1, double d2, double rs, double rc,
+                                         const double* sd, const double* nd, double* gv) {
+  const double d[3] = {d0, d1, d2};
+  const double r2 = d0 * d0 + d1 * d1 + d2 * d2;
+  const double r = sqrt(r2);
+  double sw, dsw;
+  if (r < rs) {
+    sw = 1.0;
+    dsw = 0.0;
+  } else if (r >= rc) {
+    sw = 0.0;
+    dsw = 0.0;
+  } else {
+    const double u = (r - rs) / (rc - rs);
+    const double u2 = u * u, u3 = u2 * u;
+    sw = u3 * (-6.0 * u2 + 15.0 * u - 10.0) + 1.0;
+    dsw = (3.0 * u2 * (-6.0 * u2 + 15.0 * u - 10.0) + u3 * (-12.0 * u + 15.0)) / (rc - rs);
+  }
+  const double inv_r = 1.0 / r;
+  const double inv_r2 = inv_r * inv_r;
+  const double dR0_dr = dsw * inv_r - sw * inv_r2;
+  const double q = sw * inv_r2;
+  const double dq_dr = dsw * inv_r2 - 2.0 * sw * inv_r2 * inv_r;
+  const double w0 = nd[0] / sd[0];
+  const double w[3] = {nd[1] / sd[1], nd[2] / sd[2], nd[3] / sd[3]};
+  // sum_c w_c d_c, used by the radial part of R_1..3
+  const double wd = w[0] * d[0] + w[1] * d[1] + w[2] * d[2];
+#pragma unroll
+  for (int mm = 0; mm < 3; ++mm) {
+    const double ur = d[mm] * inv_r;
+    gv[mm] = w0 * dR0_dr * ur + w[mm] * q + wd * dq_dr * ur;
+  }
+}
+
+__device__ __forceinline__ int find_pair(const EmbArgs& a) {
+  int p = 0;
+  while (p + 1 < a.npair && (int)blockIdx.x >= a.block_off[p + 1]) ++p;
+  return p;
+}
+
+template <class S>
+constexpr int fwd_lds_doubles(int waves) {
+  return (S::SIZE + 31) / 32 * 32 + waves * 16 * (S::L2P + 2) + waves * 64;
+}
+
+template <class S>
+constexpr int bwd_lds_doubles(int waves) {
+  return (S::SIZE + 31) / 32 * 32 + waves * 4 * (S::L3P + S::L2P);
+}
+
+template <class S, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
+  static_assert(S::L1 > 2, "layer-1 residual not supported");
+  extern __shared__ double lds[];
+  constexpr int PS = (S::SIZE + 31) / 32 * 32;
+  constexpr int X2LD = S::L2P + 2;
+  double* P = lds;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  double* X2s = lds + PS + w * 16 * X2LD;
+  double* Rs = lds + PS + WAVES * 16 * X2LD + w * 64;
+
+  const int p = find_pair(a);
+  const int ti = p / a.ntypes, tj = p % a.ntypes;
+  {
+    const double* src = a.emb + (long)p * a.stride;
+    for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
+  }
+  __syncthreads();
+  const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
+  if (item >= a.type_off[ti + 1] - a.type_off[ti]) return;
+  const int i = a.items[a.type_off[ti] + item];
+  const int nr = a.nreal[(long)i * a.ntypes + tj];
+  const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
+  const double* avg = a.envp + p * 8;
+  const double* sd = avg + 4;
+  const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
+
+  double Tacc[S::NU3 * 4];
+#pragma unroll
+  for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0;
+
+  for (int tile = 0; tile < nr; tile += 16) {
+    const int slot = tile + c;
+    double Rn[4] = {0.0, 0.0, 0.0, 0.0};
+    if (slot < nr) {
+      const long j = row[slot];
+      env_value(a.ext[3 * j] - xi, a.ext[3 * j + 1] - yi, a.ext[3 * j + 2] - zi, a.rcut_smth,
+                a.rcut, avg, sd, Rn);
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) Rs[c * 4 + m] = Rn[m];
+    }
+    const double s = Rn[0];
+
+    // layer 1 -> B operand of layer 2 (feature 4q+g of slot c)
+    double x1[S::NQ2];
+#pragma unroll
+    for (int q = 0; q < S::NQ2; ++q) {
+      const int f = 4 * q + g;
+      x1[q] = (f < S::L1) ? tanh(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
+    }
+    // layer 2, transposed
+    d4 acc2[S::NT2];
+#pragma unroll
+    for (int t = 0; t < S::NT2; ++t) acc2[t] = d4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int q = 0; q < S::NQ2; ++q) {
+#pragma unroll
+      for (int t = 0; t < S::NT2; ++t)
+        acc2[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1[q], acc2[t]);
+    }
+    double x2[S::NT2][4];
+#pragma unroll
+    for (int t = 0; t < S::NT2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int f = 16 * t + 4 * r + g;
+        const double th = tanh(acc2[t][r] + P[S::OFF_B2 + f]);
+        double res = 0.0;
+        if constexpr (S::RES2 != 0) {
+          if constexpr (S::X1_ALIGNED) {
+            res = x1[(S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r];
+          } else {
+            const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
+            res = (f1 < S::L1) ? tanh(s * P[S::OFF_W1 + f1] + P[S::OFF_B1 + f1]) : 0.0;
+          }
+        }
+        x2[t][r] = (f < S::L2) ? res + th : 0.0;
+      }
+    }
+    if constexpr (S::RES3 != 0) {
+#pragma unroll
+      for (int t = 0; t < S::NT2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) X2s[c * X2LD + 16 * t + 4 * r + g] = x2[t][r];
+    }
+    wave_lds_sync();
+    // layer 3, non-transposed, two output tiles at a time
+#pragma unroll
+    for (int u0 = 0; u0 < S::NU3; u0 += 2) {
+      d4 acc3[2] = {d4{0.0, 0.0, 0.0, 0.0}, d4{0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+      for (int q = 0; q < S::NQ3; ++q) {
+        const double av = x2[q / 4][q % 4];
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu)
+          if (u0 + uu < S::NU3)
+            acc3[uu] = mfma_f64(av, P[S::OFF_W3 + (4 * q + g) * S::L3P + 16 * (u0 + uu) + c],
+                                acc3[uu]);
+      }
+#pragma unroll
+      for (int uu = 0; uu < 2; ++uu) {
+        const int u = u0 + uu;
+        if (u < S::NU3) {
+          const int f = 16 * u + c;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int sl = g + 4 * r;
+            double G = tanh(acc3[uu][r] + P[S::OFF_B3 + f]);
+            if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
+            if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
+          }
+        }
+      }
+    }
+    wave_lds_sync();
+  }
+#pragma unroll
+  for (int q = 0; q < S::NU3 * 4; ++q) {
+    double v = Tacc[q];
+    v += shfl_xor_d(v, 16);
+    v += shfl_xor_d(v, 32);
+    Tacc[q] = v;
+  }
+  if (g == 0) {
+    double* out = a.Tsec + ((long)i * a.ntypes + tj) * 4 * S::L3;
+#pragma unroll
+    for (int u = 0; u < S::NU3; ++u) {
+      const int f = 16 * u + c;
+      if (f < S::L3) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) out[m * S::L3 + f] = Tacc[u * 4 + m];
+      }
+    }
+  }
+}
+
+template <class S, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
+  static_assert(S::L1 > 2, "layer-1 residual not supported");
+  extern __shared__ double lds[];
+  constexpr int PS = (S::SIZE + 31) / 32 * 32;
+  double* P = lds;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  double* dTs = lds + PS + w * 4 * (S::L3P + S::L2P);
+  double* dTf = dTs + 4 * S::L3P;
+
+  const int p = find_pair(a);
+  const int ti = p / a.ntypes, tj = p % a.ntypes;
+  {
+    const double* src = a.emb + (long)p * a.stride;
+    for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
+  }
+  __syncthreads();
+  const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
+  if (item >= a.type_off[ti + 1] - a.type_off[ti]) return;
+  const int i = a.items[a.type_off[ti] + item];
+  const int nr = a.nreal[(long)i * a.ntypes + tj];
+  const long ebase = (long)i * a.nnei + a.sec[tj];
+  const int* row = a.nlist + ebase;
+  const double* avg = a.envp + p * 8;
+  const double* sd = avg + 4;
+  const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
+
+  {
+    const double* dTi = a.dT + (long)i * 4 * S::L3;
+    for (int q = lane; q < 4 * S::L3P; q += 64) {
+      const int m = q / S::L3P, f = q % S::L3P;
+      dTs[q] = f < S::L3 ? dTi[m * S::L3 + f] : 0.0;
+    }
+    for (int q = lane; q < 4 * S::L2P; q += 64) {
+      const int m = q / S::L2P, f = q % S::L2P;
+      double v = 0.0;
+      if (f < S::L2) {
+        if constexpr (S::RES3 == 2) v = dTi[m * S::L3 + f] + dTi[m * S::L3 + f + S::L2];
+        if constexpr (S::RES3 == 1) v = dTi[m * S::L3 + f];
+      }
+      dTf[q] = v;
+    }
+  }
+  wave_lds_sync();
+
+  double fc[3] = {0.0, 0.0, 0.0};
+  double vc[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+
+  for (int tile = 0; tile < nr; tile += 16) {
+    const int slot = tile + c;
+    const bool valid = slot < nr;
+    double d0 = 0.0, d1 = 0.0, d2 = 0.0;
+    double Rn[4] = {0.0, 0.0, 0.0, 0.0};
+    if (valid) {
+      const long j = row[slot];
+      d0 = a.ext[3 * j] - xi;
+      d1 = a.ext[3 * j + 1] - yi;
+      d2 = a.ext[3 * j + 2] - zi;
+      env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
+    }
+    const double s = Rn[0];
+
+    // layer 1 and its tangent
+    double x1[S::NQ2], x1t[S::NQ2];
+#pragma unroll
+    for (int q = 0; q < S::NQ2; ++q) {
+      const int f = 4 * q + g;
+      if (f < S::L1) {
+        const double wv = P[S::OFF_W1 + f];
+        const double th = tanh(s * wv + P[S::OFF_B1 + f]);
+        x1[q] = th;
+        x1t[q] = (1.0 - th * th) * wv;
+      } else {
+        x1[q] = 0.0;
+        x1t[q] = 0.0;
+      }
+    }
+    // layer 2, transposed, primal + tangent sharing the weight fragment
+    d4 acc2[S::NT2], acc2t[S::NT2];
+#pragma unroll
+    for (int t = 0; t < S::NT2; ++t) {
+      acc2[t] = d4{0.0, 0.0, 0.0, 0.0};
+      acc2t[t] = d4{0.0, 0.0, 0.0, 0.0};
+    }
+#pragma unroll
+    for (int q = 0; q < S::NQ2; ++q) {
+#pragma unroll
+      for (int t = 0; t < S::NT2; ++t) {
+        const double wa = P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c];
+        acc2[t] = mfma_f64(wa, x1[q], acc2[t]);
+        acc2t[t] = mfma_f64(wa, x1t[q], acc2t[t]);
+      }
+    }
+    double x2[S::NT2][4], x2t[S::NT2][4];
+#pragma unroll
+    for (int t = 0; t < S::NT2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int f = 16 * t + 4 * r + g;
+        const double th = tanh(acc2[t][r] + P[S::OFF_B2 + f]);
+        double res = 0.0, rest = 0.0;
+        if constexpr (S::RES2 != 0) {
+          if constexpr (S::X1_ALIGNED) {
+            const int q1 = (S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r;
+            res = x1[q1];
+            rest = x1t[q1];
+          } else {
+            const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
+            if (f1 < S::L1) {
+              const double wv = P[S::OFF_W1 + f1];
+              const double y = tanh(s * wv + P[S::OFF_B1 + f1]);
+              res = y;
+              rest = (1.0 - y * y) * wv;
+            }
+          }
+        }
+        const bool live = f < S::L2;
+        x2[t][r] = live ? res + th : 0.0;
+        x2t[t][r] = live ? rest + (1.0 - th * th) * acc2t[t][r] : 0.0;
+      }
+    }
+    // u = dT.G, v = dT.G' : residual part through the folded dT against X2
+    double up[4] = {0.0, 0.0, 0.0, 0.0}, vp[4] = {0.0, 0.0, 0.0, 0.0};
+    if constexpr (S::RES3 != 0) {
+#pragma unroll
+      for (int t = 0; t < S::NT2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int f = 16 * t + 4 * r + g;
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const double wv = dTf[m * S::L2P + f];
+            up[m] += wv * x2[t][r];
+            vp[m] += wv * x2t[t][r];
+          }
+        }
+    }
+    // layer 3, transposed; tanh part of G and of G'
+#pragma unroll 1
+    for (int u0 = 0; u0 < S::NU3; u0 += 2) {
+      d4 acc3[2] = {d4{0.0, 0.0, 0.0, 0.0}, d4{0.0, 0.0, 0.0, 0.0}};
+      d4 acc3t[2] = {d4{0.0, 0.0, 0.0, 0.0}, d4{0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+      for (int q = 0; q < S::NQ3; ++q) {
+#pragma unroll
+        for (int uu = 0; uu < 2; ++uu)
+          if (u0 + uu < S::NU3) {
+            const double wa = P[S::OFF_W3 + (4 * q + g) * S::L3P + 16 * (u0 + uu) + c];
+            acc3[uu] = mfma_f64(wa, x2[q / 4][q % 4], acc3[uu]);
+            acc3t[uu] = mfma_f64(wa, x2t[q / 4][q % 4], acc3t[uu]);
+          }
+      }
+#pragma unroll
+      for (int uu = 0; uu < 2; ++uu) {
+        const int u = u0 + uu;
+        if (u < S::NU3) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int f = 16 * u + 4 * r + g;
+            const double th = tanh(acc3[uu][r] + P[S::OFF_B3 + f]);
+            const double tt = (1.0 - th * th) * acc3t[uu][r];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              const double wv = dTs[m * S::L3P + f];
+              up[m] += wv * th;
+              vp[m] += wv * tt;
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      up[m] += shfl_xor_d(up[m], 16);
+      up[m] += shfl_xor_d(up[m], 32);
+      vp[m] += shfl_xor_d(vp[m], 16);
+      vp[m] += shfl_xor_d(vp[m], 32);
+    }
+    if (valid && g == 0) {
+      double nd[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) nd[m] = up[m] * a.inv_nnei;
+      nd[0] += (Rn[0] * vp[0] + Rn[1] * vp[1] + Rn[2] * vp[2] + Rn[3] * vp[3]) * a.inv_nnei;
+      double gv[3];
+      env_grad(d0, d1, d2, a.rcut_smth, a.rcut, sd, nd, gv);
+      double* eg = a.edge_grad + (ebase + slot) * 3;
+      eg[0] = gv[0];
+      eg[1] = gv[1];
+      eg[2] = gv[2];
+      const double dd[3] = {d0, d1, d2};
+#pragma unroll
+      for (int cc = 0; cc < 3; ++cc) {
+        fc[cc] += gv[cc];
+#pragma unroll
+        for (int e = 0; e < 3; ++e) vc[3 * cc + e] -= gv[cc] * dd[e];
+      }
+    }
+  }
+  // padded slots carry no gradient
+  for (int sl = nr + lane; sl < a.sel[tj]; sl += 64) {
+    double* eg = a.edge_grad + (ebase + sl) * 3;
+    eg[0] = 0.0;
+    eg[1] = 0.0;
+    eg[2] = 0.0;
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) fc[q] += shfl_xor_d(fc[q], off);
+#pragma unroll
+    for (int q = 0; q < 9; ++q) vc[q] += shfl_xor_d(vc[q], off);
+  }
+  if (lane == 0) {
+    double* out = a.cpart + ((long)i * a.ntypes + tj) * 12;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) out[q] = fc[q];
+#pragma unroll
+    for (int q = 0; q < 9; ++q) out[3 + q] = vc[q];
+  }
+}
+
+// T = (sum over sections of Tsec + padded-slot constant) / nnei, and
+// D = T^T T[:, :axis], written in bucket order for the fitting GEMMs.
+__global__ __launch_bounds__(256) void k_descriptor(DescArgs a) {
+  extern __shared__ double Ts[];
+  const int pos = blockIdx.x;
+  const int i = a.items[pos];
+  const int ti = a.ext_type[i];
+  const int L3 = a.L3;
+  for (int q = threadIdx.x; q < 4 * L3; q += blockDim.x) {
+    double v = 0.0;
+    for (int tj = 0; tj < a.ntypes; ++tj) {
+      const long sec = (long)i * a.ntypes + tj;
+      const double npad = (double)(a.sel[tj] - a.nreal[sec]);
+      v += a.Tsec[sec * 4 * L3 + q] + npad * a.tpad[((long)(ti * a.ntypes + tj)) * 4 * L3 + q];
+    }
+    v *= a.inv_nnei;
+    Ts[q] = v;
+    a.T[(long)i * 4 * L3 + q] = v;
+  }
+  __syncthreads();
+  const int nd = L3 * a.axis;
+  double* D = a.D + (long)pos * nd;
+  for (int q = threadIdx.x; q < nd; q += blockDim.x) {
+    const int ai = q / a.axis, bi = q % a.axis;
+    D[q] = Ts[ai] * Ts[bi] + Ts[L3 + ai] * Ts[L3 + bi] + Ts[2 * L3 + ai] * Ts[2 * L3 + bi] +
+           Ts[3 * L3 + ai] * Ts[3 * L3 + bi];
+  }
+}
+
+// ---------------------------------------------------------------------------
+using ShapeWater = EmbShape<25, 50, 100>;
+using ShapeMetal = EmbShape<32, 64, 128>;
+constexpr int kFwdWaves = 8;
+constexpr int kBwdWaves = 4;
+
+bool emb_supported(int L1, int L2, int L3) {
+  return (L1 == 25 && L2 == 50 && L3 == 100) || (L1 == 32 && L2 == 64 && L3 == 128);
+}
+
+int embed_waves_fwd(const EmbLayout&) { return kFwdWaves; }
+int embed_waves_bwd(const EmbLayout&) { return kBwdWaves; }
+
+template <class S>
+static void fwd_impl(hipStream_t st, const EmbArgs& a, int nblocks) {
+  const size_t bytes = sizeof(double) * fwd_lds_doubles<S>(kFwdWaves);
+  auto kern = k_embed_fwd<S, kFwdWaves>;
+  DPAMD_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)bytes));
+  hipLaunchKernelGGL(kern, dim3(nblocks), dim3(kFwdWaves * 64), bytes, st, a);
+  DPAMD_LAUNCH_CHECK();
+}
+
+template <class S>
+static void bwd_impl(hipStream_t st, const EmbArgs& a, int nblocks) {
+  const size_t bytes = sizeof(double) * bwd_lds_doubles<S>(kBwdWaves);
+  auto kern = k_embed_bwd<S, kBwdWaves>;
+  DPAMD_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)bytes));
+  hipLaunchKernelGGL(kern, dim3(nblocks), dim3(kBwdWaves * 64), bytes, st, a);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_embed_fwd(hipStream_t st, const EmbLayout& e, const EmbArgs& a, int nblocks) {
+  if (nblocks <= 0) return;
+  if (e.L1 == 25) fwd_impl<ShapeWater>(st, a, nblocks);
+  else fwd_impl<ShapeMetal>(st, a, nblocks);
+}
+
+void launch_embed_bwd(hipStream_t st, const EmbLayout& e, const EmbArgs& a, int nblocks) {
+  if (nblocks <= 0) return;
+  if (e.L1 == 25) bwd_impl<ShapeWater>(st, a, nblocks);
+  else bwd_impl<ShapeMetal>(st, a, nblocks);
+}
+
+void launch_descriptor(hipStream_t st, const DescArgs& a) {
+  if (a.nloc <= 0) return;
+  hipLaunchKernelGGL(k_descriptor, dim3(a.nloc), dim3(256), sizeof(double) * 4 * a.L3, st, a);
+  DPAMD_LAUNCH_CHECK();
+}
+
+}  // namespace dpamd

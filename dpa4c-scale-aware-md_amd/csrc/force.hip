@@ -1,0 +1,202 @@
+// ProdForce / ProdVirial as a gather over the transposed neighbour list, plus
+// the deterministic energy / virial reduction.
+//
+// Every edge e = (centre i, slot) with neighbour j contributes +g_e to the
+// centre (summed inside the backward kernel, cpart) and -g_e to the target
+// atom t = mapping[j] (standalone: ghost images folded onto owners) or t = j
+// (LAMMPS path: ghost slots kept for reverse communication). The reverse list
+// is built by count / scan / fill; each target's edges are then ranked by edge
+// id in LDS so the sum order is fixed and the result bit-reproducible, with
+// no floating-point atomics. Atom virial -g (x) (x_j - x_i) is charged to the
+// target, as in deepmd-op/overlays/op/pt/edge_force_virial.cu:1-14, :138-146
+// (dual-CSR gather, one warp per node there, one 64-lane wave here). The frame
+// sums follow the fixed two-stage fp64 reduction of edge_force_virial.cu:187-256.
+#include "kernels.h"
+
+namespace dpamd {
+
+__global__ void k_rev_count(long nedge, const int* __restrict__ nlist,
+                            const int* __restrict__ mapping, int* __restrict__ count) {
+  const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= nedge) return;
+  const int j = nlist[e];
+  if (j < 0) return;
+  atomicAdd(&count[mapping ? mapping[j] : j], 1);
+}
+
+__global__ void k_rev_fill(long nedge, const int* __restrict__ nlist,
+                           const int* __restrict__ mapping, const int* __restrict__ off,
+                           int* __restrict__ cursor, int* __restrict__ rev) {
+  const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= nedge) return;
+  const int j = nlist[e];
+  if (j < 0) return;
+  const int t = mapping ? mapping[j] : j;
+  rev[off[t] + atomicAdd(&cursor[t], 1)] = (int)e;
+}
+
+constexpr int kGatherWaves = 4;
+
+__global__ __launch_bounds__(kGatherWaves * 64) void k_force_gather(
+    int ntarget, int nloc, int ntypes, int nnei, const int* __restrict__ rev_off,
+    const int* __restrict__ rev, const int* __restrict__ nlist, const double* __restrict__ ext,
+    const double* __restrict__ edge_grad, const double* __restrict__ cpart,
+    double* __restrict__ force, double* __restrict__ atom_virial, int* __restrict__ status) {
+  __shared__ int s_in[kGatherWaves][kMaxRev];
+  __shared__ int s_sorted[kGatherWaves][kMaxRev];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kGatherWaves + w;
+  if (t >= ntarget) return;
+  const int beg = rev_off[t];
+  int n = rev_off[t + 1] - beg;
+  if (n > kMaxRev) {
+    if (lane == 0) atomicOr(status, kStatusReverseOverflow);
+    n = kMaxRev;
+  }
+  for (int q = lane; q < n; q += 64) s_in[w][q] = rev[beg + q];
+  wave_lds_sync();
+  for (int q = lane; q < n; q += 64) {
+    const int eq = s_in[w][q];
+    int rank = 0;
+    for (int p = 0; p < n; ++p) rank += (s_in[w][p] < eq) ? 1 : 0;
+    s_sorted[w][rank] = eq;
+  }
+  wave_lds_sync();
+  double f[3] = {0.0, 0.0, 0.0};
+  double v[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  for (int q = lane; q < n; q += 64) {
+    const long e = s_sorted[w][q];
+    const double g0 = edge_grad[3 * e], g1 = edge_grad[3 * e + 1], g2 = edge_grad[3 * e + 2];
+    f[0] -= g0;
+    f[1] -= g1;
+    f[2] -= g2;
+    if (atom_virial) {
+      const long i = e / nnei;
+      const long j = nlist[e];
+      const double d[3] = {ext[3 * j] - ext[3 * i], ext[3 * j + 1] - ext[3 * i + 1],
+                           ext[3 * j + 2] - ext[3 * i + 2]};
+      const double g[3] = {g0, g1, g2};
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int b = 0; b < 3; ++b) v[3 * a + b] -= g[a] * d[b];
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) f[q] += shfl_xor_d(f[q], off);
+    if (atom_virial) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) v[q] += shfl_xor_d(v[q], off);
+    }
+  }
+  if (lane == 0) {
+    if (t < nloc) {
+      for (int tj = 0; tj < ntypes; ++tj) {
+        const double* cp = cpart + ((long)t * ntypes + tj) * 12;
+        f[0] += cp[0];
+        f[1] += cp[1];
+        f[2] += cp[2];
+      }
+    }
+    force[3 * (long)t] = f[0];
+    force[3 * (long)t + 1] = f[1];
+    force[3 * (long)t + 2] = f[2];
+    if (atom_virial)
+      for (int q = 0; q < 9; ++q) atom_virial[9 * (long)t + q] = v[q];
+  }
+}
+
+constexpr int kRedBlocks = 256;
+
+// Stage 1: block b sums energies of bucket positions and centre virials of
+// sections b, b + 256, ...; stage 2 (one block) adds the 256 partials in order.
+__global__ __launch_bounds__(256) void k_reduce_ev1(int nbucket, int nloc, int ntypes,
+                                                    const double* __restrict__ e_bucket,
+                                                    const double* __restrict__ cpart,
+                                                    double* __restrict__ partials) {
+  __shared__ double sm[10][256];
+  double acc[10];
+#pragma unroll
+  for (int q = 0; q < 10; ++q) acc[q] = 0.0;
+  const long stride = (long)kRedBlocks * 256;
+  for (long p = (long)blockIdx.x * 256 + threadIdx.x; p < nbucket; p += stride) acc[0] += e_bucket[p];
+  const long nsec = (long)nloc * ntypes;
+  for (long s = (long)blockIdx.x * 256 + threadIdx.x; s < nsec; s += stride)
+    for (int q = 0; q < 9; ++q) acc[1 + q] += cpart[s * 12 + 3 + q];
+  for (int q = 0; q < 10; ++q) sm[q][threadIdx.x] = acc[q];
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if ((int)threadIdx.x < h)
+      for (int q = 0; q < 10; ++q) sm[q][threadIdx.x] += sm[q][threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x < 10) partials[blockIdx.x * 10 + threadIdx.x] = sm[threadIdx.x][0];
+}
+
+__global__ __launch_bounds__(256) void k_reduce_ev2(const double* __restrict__ partials,
+                                                    double* __restrict__ out10) {
+  __shared__ double sm[10][256];
+  for (int q = 0; q < 10; ++q) sm[q][threadIdx.x] = partials[threadIdx.x * 10 + q];
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if ((int)threadIdx.x < h)
+      for (int q = 0; q < 10; ++q) sm[q][threadIdx.x] += sm[q][threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x < 10) out10[threadIdx.x] = sm[threadIdx.x][0];
+}
+
+__global__ void k_scatter_energy(int n, const int* __restrict__ items,
+                                 const double* __restrict__ e_bucket,
+                                 double* __restrict__ atom_energy) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p < n) atom_energy[items[p]] = e_bucket[p];
+}
+
+void launch_rev_count(hipStream_t st, long nedge, int, const int* nlist, const int* mapping,
+                      int* count) {
+  if (nedge <= 0) return;
+  hipLaunchKernelGGL(k_rev_count, dim3((unsigned)((nedge + 255) / 256)), dim3(256), 0, st, nedge,
+                     nlist, mapping, count);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_rev_fill(hipStream_t st, long nedge, int, const int* nlist, const int* mapping,
+                     const int* off, int* cursor, int* rev) {
+  if (nedge <= 0) return;
+  hipLaunchKernelGGL(k_rev_fill, dim3((unsigned)((nedge + 255) / 256)), dim3(256), 0, st, nedge,
+                     nlist, mapping, off, cursor, rev);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_force_gather(hipStream_t st, int ntarget, int nloc, int ntypes, int nnei,
+                         const int* rev_off, const int* rev, const int* nlist, const double* ext,
+                         const double* edge_grad, const double* cpart, double* force,
+                         double* atom_virial, int* status) {
+  if (ntarget <= 0) return;
+  hipLaunchKernelGGL(k_force_gather, dim3((ntarget + kGatherWaves - 1) / kGatherWaves),
+                     dim3(kGatherWaves * 64), 0, st, ntarget, nloc, ntypes, nnei, rev_off, rev,
+                     nlist, ext, edge_grad, cpart, force, atom_virial, status);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_reduce_ev(hipStream_t st, int nbucket, int nloc, int ntypes, const double* e_bucket,
+                      const double* cpart, double* partials, double* out10) {
+  hipLaunchKernelGGL(k_reduce_ev1, dim3(kRedBlocks), dim3(256), 0, st, nbucket, nloc, ntypes,
+                     e_bucket, cpart, partials);
+  DPAMD_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_reduce_ev2, dim3(1), dim3(256), 0, st, partials, out10);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_scatter_energy(hipStream_t st, int n, const int* items, const double* e_bucket,
+                           double* atom_energy) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_scatter_energy, dim3((n + 255) / 256), dim3(256), 0, st, n, items, e_bucket,
+                     atom_energy);
+  DPAMD_LAUNCH_CHECK();
+}
+
+}  // namespace dpamd

@@ -1,0 +1,195 @@
+// Model file parsing, validation and packing into the kernels' layouts.
+// The metadata read here mirrors what the reference's model API reads from a
+// model (rcut, type_map/ntypes, sel; deepmd-op/overlays/api_cc/src/DeepPotPTExpt.cc:368-478).
+#include "model.h"
+
+#include <cmath>
+#include <cstring>
+
+namespace dpamd {
+
+namespace {
+
+struct Reader {
+  const unsigned char* p;
+  size_t n, off = 0;
+  bool ok = true;
+  template <class T>
+  T get() {
+    T v{};
+    if (off + sizeof(T) > n) {
+      ok = false;
+      return v;
+    }
+    std::memcpy(&v, p + off, sizeof(T));
+    off += sizeof(T);
+    return v;
+  }
+  void doubles(std::vector<double>& out, size_t count) {
+    out.resize(count);
+    if (off + count * 8 > n) {
+      ok = false;
+      return;
+    }
+    std::memcpy(out.data(), p + off, count * 8);
+    off += count * 8;
+  }
+};
+
+}  // namespace
+
+std::string parse_model(const unsigned char* buf, size_t len, ModelHost& m) {
+  if (len < 8 || std::memcmp(buf, "DPAMDSEA", 8) != 0) return "not a DPAMDSEA se_e2_a model file";
+  Reader r{buf, len, 8};
+  const uint32_t ver = r.get<uint32_t>();
+  if (ver != 1) return "unsupported model file version " + std::to_string(ver);
+  const uint32_t nt = r.get<uint32_t>();
+  if (nt < 1 || nt > (uint32_t)kMaxTypes) return "ntypes must be in [1, 8]";
+  m.ntypes = (int)nt;
+  m.nnei = 0;
+  for (int t = 0; t < m.ntypes; ++t) {
+    m.sel[t] = (int)r.get<uint32_t>();
+    m.sec[t] = m.nnei;
+    m.nnei += m.sel[t];
+  }
+  m.sec[m.ntypes] = m.nnei;
+  m.rcut = r.get<double>();
+  m.rcut_smth = r.get<double>();
+  for (int k = 0; k < 3; ++k) m.emb[k] = (int)r.get<uint32_t>();
+  m.axis = (int)r.get<uint32_t>();
+  for (int k = 0; k < 3; ++k) m.fit[k] = (int)r.get<uint32_t>();
+  (void)r.get<uint32_t>();
+  m.type_map.clear();
+  for (int t = 0; t < m.ntypes; ++t) {
+    char name[17] = {0};
+    for (int q = 0; q < 16; ++q) name[q] = (char)r.get<uint8_t>();
+    m.type_map.emplace_back(name);
+  }
+  if (!r.ok) return "model file truncated in header";
+  if (!(m.rcut > 0) || !(m.rcut_smth >= 0) || !(m.rcut_smth < m.rcut))
+    return "need 0 <= rcut_smth < rcut";
+  for (int t = 0; t < m.ntypes; ++t)
+    if (m.sel[t] <= 0) return "sel entries must be positive";
+  const int L1 = m.emb[0], L2 = m.emb[1], L3 = m.emb[2];
+  if (!emb_supported(L1, L2, L3))
+    return "embedding widths " + std::to_string(L1) + "-" + std::to_string(L2) + "-" +
+           std::to_string(L3) + " not compiled (supported: 25-50-100, 32-64-128)";
+  if (m.axis < 1 || m.axis > L3) return "axis must be in [1, L3]";
+  const int Dn = L3 * m.axis;
+  for (int k = 0; k < 3; ++k)
+    if (m.fit[k] <= 0 || m.fit[k] % 16 != 0) return "fitting widths must be multiples of 16";
+  if (Dn % 16 != 0) return "descriptor width L3*axis must be a multiple of 16";
+  if (m.fit[0] == Dn) return "a residual first fitting layer is not supported";
+  m.emb_block = (long)L1 + L1 + (long)L1 * L2 + L2 + (long)L2 * L3 + L3;
+  const int ins[3] = {Dn, m.fit[0], m.fit[1]};
+  m.fit_block = 0;
+  for (int k = 0; k < 3; ++k)
+    m.fit_block += (long)ins[k] * m.fit[k] + m.fit[k] + (m.fit[k] == ins[k] ? m.fit[k] : 0);
+  m.fit_block += m.fit[2] + 1;
+  const size_t nt2 = (size_t)m.ntypes * m.ntypes;
+  r.doubles(m.davg, nt2 * 4);
+  r.doubles(m.dstd, nt2 * 4);
+  r.doubles(m.emb_params, nt2 * m.emb_block);
+  r.doubles(m.fit_params, (size_t)m.ntypes * m.fit_block);
+  r.doubles(m.bias, (size_t)m.ntypes);
+  if (!r.ok) return "model file truncated in parameters";
+  if (r.off != len) return "trailing bytes after model parameters";
+  for (double s : m.dstd)
+    if (!(s != 0.0)) return "dstd entries must be non-zero";
+  return "";
+}
+
+FitOffsets fit_offsets(const ModelHost& m) {
+  FitOffsets o{};
+  const int ins[3] = {m.emb[2] * m.axis, m.fit[0], m.fit[1]};
+  long p = 0;
+  for (int k = 0; k < 3; ++k) {
+    o.W[k] = p;
+    p += (long)ins[k] * m.fit[k];
+    o.b[k] = p;
+    p += m.fit[k];
+    if (m.fit[k] == ins[k]) {
+      o.idt[k] = p;
+      p += m.fit[k];
+    } else {
+      o.idt[k] = -1;
+    }
+  }
+  o.Wo = p;
+  o.bo = p + m.fit[2];
+  return o;
+}
+
+namespace {
+
+// Host fp64 evaluation of one embedding net at s (padded-slot constant).
+void embed_host(const ModelHost& m, const double* P, double s, std::vector<double>& out) {
+  const int L1 = m.emb[0], L2 = m.emb[1], L3 = m.emb[2];
+  const double* W1 = P;
+  const double* b1 = W1 + L1;
+  const double* W2 = b1 + L1;
+  const double* b2 = W2 + (long)L1 * L2;
+  const double* W3 = b2 + L2;
+  const double* b3 = W3 + (long)L2 * L3;
+  auto layer = [](const std::vector<double>& x, const double* W, const double* b, int out_n) {
+    const int in = (int)x.size();
+    std::vector<double> y(out_n);
+    for (int f = 0; f < out_n; ++f) {
+      double z = 0.0;
+      for (int k = 0; k < in; ++k) z += x[k] * W[(long)k * out_n + f];
+      const double t = std::tanh(z + b[f]);
+      double res = 0.0;
+      if (out_n == in) res = x[f];
+      else if (out_n == 2 * in) res = x[f % in];
+      y[f] = res + t;
+    }
+    return y;
+  };
+  std::vector<double> x{s};
+  x = layer(x, W1, b1, L1);
+  x = layer(x, W2, b2, L2);
+  out = layer(x, W3, b3, L3);
+}
+
+}  // namespace
+
+void pack_embedding(const ModelHost& m, const EmbLayout& e, std::vector<double>& emb,
+                    std::vector<double>& envp, std::vector<double>& tpad) {
+  const int nt = m.ntypes, np = nt * nt;
+  const int L1 = m.emb[0], L2 = m.emb[1], L3 = m.emb[2];
+  emb.assign((size_t)np * e.stride, 0.0);
+  envp.assign((size_t)np * 8, 0.0);
+  tpad.assign((size_t)np * 4 * L3, 0.0);
+  for (int p = 0; p < np; ++p) {
+    const double* P = m.emb_params.data() + (size_t)p * m.emb_block;
+    const double* W1 = P;
+    const double* b1 = W1 + L1;
+    const double* W2 = b1 + L1;
+    const double* b2 = W2 + (long)L1 * L2;
+    const double* W3 = b2 + L2;
+    const double* b3 = W3 + (long)L2 * L3;
+    double* Q = emb.data() + (size_t)p * e.stride;
+    for (int f = 0; f < L1; ++f) {
+      Q[e.off_w1 + f] = W1[f];
+      Q[e.off_b1 + f] = b1[f];
+    }
+    for (int k = 0; k < L1; ++k)
+      for (int n = 0; n < L2; ++n) Q[e.off_w2 + k * e.L2P + n] = W2[(long)k * L2 + n];
+    for (int n = 0; n < L2; ++n) Q[e.off_b2 + n] = b2[n];
+    for (int k = 0; k < L2; ++k)
+      for (int n = 0; n < L3; ++n) Q[e.off_w3 + k * e.L3P + n] = W3[(long)k * L3 + n];
+    for (int n = 0; n < L3; ++n) Q[e.off_b3 + n] = b3[n];
+    for (int q = 0; q < 4; ++q) {
+      envp[(size_t)p * 8 + q] = m.davg[(size_t)p * 4 + q];
+      envp[(size_t)p * 8 + 4 + q] = m.dstd[(size_t)p * 4 + q];
+    }
+    double Rpad[4];
+    for (int q = 0; q < 4; ++q) Rpad[q] = (0.0 - m.davg[(size_t)p * 4 + q]) / m.dstd[(size_t)p * 4 + q];
+    std::vector<double> G;
+    embed_host(m, P, Rpad[0], G);
+    for (int q = 0; q < 4; ++q)
+      for (int f = 0; f < L3; ++f) tpad[((size_t)p * 4 + q) * L3 + f] = Rpad[q] * G[f];
+  }
+}
+
+}  // namespace dpamd

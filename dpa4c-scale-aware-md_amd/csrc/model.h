@@ -1,0 +1,42 @@
+// Host representation of an se_e2_a model file (layout documented in the
+// package's model.py) and the device-side packing the kernels read.
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+
+namespace dpamd {
+
+struct ModelHost {
+  int ntypes = 0, nnei = 0;
+  int sel[kMaxTypes] = {0};
+  int sec[kMaxTypes + 1] = {0};
+  double rcut = 0, rcut_smth = 0;
+  int emb[3] = {0, 0, 0};
+  int axis = 0;
+  int fit[3] = {0, 0, 0};
+  std::vector<std::string> type_map;
+  std::vector<double> davg, dstd;  // [nt][nt][4]
+  std::vector<double> emb_params;  // [nt*nt][emb_block]
+  std::vector<double> fit_params;  // [nt][fit_block]
+  std::vector<double> bias;        // [nt]
+  long emb_block = 0, fit_block = 0;
+};
+
+// Parse and validate; returns "" on success or a message.
+std::string parse_model(const unsigned char* buf, size_t len, ModelHost& m);
+
+// Padded embedding nets [npair][layout.stride], env stats [npair][8],
+// padded-slot constants tpad[npair][4][L3] = Rpad[m] * G(s_pad)[f].
+void pack_embedding(const ModelHost& m, const EmbLayout& e, std::vector<double>& emb,
+                    std::vector<double>& envp, std::vector<double>& tpad);
+
+// Offsets (in doubles) of each fitting layer inside a type's block.
+struct FitOffsets {
+  long W[3], b[3], idt[3], Wo, bo;
+};
+FitOffsets fit_offsets(const ModelHost& m);
+
+}  // namespace dpamd

@@ -1,0 +1,359 @@
+// Neighbour stage on gfx950: periodic ghost images, cell binning over the
+// extended atoms, and the per-type sel-sorted neighbour list.
+//
+// This file is compiled with -ffp-contract=off: every squared distance is the
+// plain IEEE sequence dx = xj - xi, r2 = dx*dx + dy*dy + dz*dz, and ghost
+// coordinates are x + na*a + nb*b + nc*c evaluated left to right, so the list
+// (which depends on exact comparisons of r2 at the sel truncation) is
+// bit-identical to the CPU oracle's.
+//
+// Reference analogs: the warp-per-centre binned build
+// lammps/overlays/src/KOKKOS/npair_kokkos.cpp:281-356 (here a 64-lane wave per
+// centre with ballot compaction), the ballot/prefix compaction of
+// lammps-deepmd-plugin/src/compact_canonical_graph_kokkos.h:447-491 and
+// :643-745, and the exact-cut predicate include/dpa_chain/exact_cut.cuh:10-20.
+// The sel formatting itself (upstream format_nlist) is absent from the
+// reference: candidates with r2 <= rcut^2 are ranked by (type, r2, j) and the
+// first sel[t] of type t fill section t, the rest -1.
+#include "kernels.h"
+
+namespace dpamd {
+
+__device__ __forceinline__ void to_frac(const BoxParams& bp, double x0, double x1, double x2,
+                                        double* s) {
+  s[2] = x2 / bp.h[8];
+  s[1] = (x1 - s[2] * bp.h[7]) / bp.h[4];
+  s[0] = (x0 - s[1] * bp.h[3] - s[2] * bp.h[6]) / bp.h[0];
+}
+
+__global__ void k_wrap(int nloc, const double* __restrict__ coord, const int* __restrict__ atype,
+                       BoxParams bp, double* __restrict__ ext, int* __restrict__ ext_type,
+                       int* __restrict__ mapping, double* __restrict__ sfrac) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= nloc) return;
+  const double x0 = coord[3 * k], x1 = coord[3 * k + 1], x2 = coord[3 * k + 2];
+  double w0 = x0, w1 = x1, w2 = x2;
+  if (bp.periodic) {
+    double s[3];
+    to_frac(bp, x0, x1, x2, s);
+    const double n0 = floor(s[0]), n1 = floor(s[1]), n2 = floor(s[2]);
+    w0 = x0 - n0 * bp.h[0] - n1 * bp.h[3] - n2 * bp.h[6];
+    w1 = x1 - n1 * bp.h[4] - n2 * bp.h[7];
+    w2 = x2 - n2 * bp.h[8];
+    double sw[3];
+    to_frac(bp, w0, w1, w2, sw);
+    sfrac[3 * k] = sw[0];
+    sfrac[3 * k + 1] = sw[1];
+    sfrac[3 * k + 2] = sw[2];
+  }
+  ext[3 * k] = w0;
+  ext[3 * k + 1] = w1;
+  ext[3 * k + 2] = w2;
+  ext_type[k] = atype[k];
+  mapping[k] = k;
+}
+
+__device__ __forceinline__ void decode_shift(const BoxParams& bp, int s, int* n) {
+  const int wa = 2 * bp.nrep[0] + 1, wb = 2 * bp.nrep[1] + 1;
+  const int q0 = (bp.nrep[2] * wb + bp.nrep[1]) * wa + bp.nrep[0];
+  const int q = s < q0 ? s : s + 1;
+  n[0] = q % wa - bp.nrep[0];
+  n[1] = (q / wa) % wb - bp.nrep[1];
+  n[2] = q / (wa * wb) - bp.nrep[2];
+}
+
+// flags[s*nloc + k] = 1 when image s of atom k lies in the extended region.
+__global__ void k_ghost_flags(int nloc, BoxParams bp, const double* __restrict__ sfrac,
+                              int* __restrict__ flags) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)bp.nshift * nloc) return;
+  const int s = (int)(idx / nloc), k = (int)(idx % nloc);
+  int n[3];
+  decode_shift(bp, s, n);
+  const double f0 = sfrac[3 * k] + (double)n[0];
+  const double f1 = sfrac[3 * k + 1] + (double)n[1];
+  const double f2 = sfrac[3 * k + 2] + (double)n[2];
+  const bool in = f0 >= -bp.rcf[0] && f0 < bp.hi[0] && f1 >= -bp.rcf[1] && f1 < bp.hi[1] &&
+                  f2 >= -bp.rcf[2] && f2 < bp.hi[2];
+  flags[idx] = in ? 1 : 0;
+}
+
+__global__ void k_ghost_fill(int nloc, BoxParams bp, const int* __restrict__ flags,
+                             const int* __restrict__ pos, double* __restrict__ ext,
+                             int* __restrict__ ext_type, int* __restrict__ mapping) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)bp.nshift * nloc || !flags[idx]) return;
+  const int s = (int)(idx / nloc), k = (int)(idx % nloc);
+  int n[3];
+  decode_shift(bp, s, n);
+  const int o = nloc + pos[idx];
+  const double na = (double)n[0], nb = (double)n[1], nc = (double)n[2];
+  ext[3 * o] = ext[3 * k] + na * bp.h[0] + nb * bp.h[3] + nc * bp.h[6];
+  ext[3 * o + 1] = ext[3 * k + 1] + nb * bp.h[4] + nc * bp.h[7];
+  ext[3 * o + 2] = ext[3 * k + 2] + nc * bp.h[8];
+  ext_type[o] = ext_type[k];
+  mapping[o] = k;
+}
+
+__device__ __forceinline__ int cell_of_point(const BoxParams& bp, double x0, double x1, double x2) {
+  double s[3];
+  to_frac(bp, x0 - bp.origin[0], x1 - bp.origin[1], x2 - bp.origin[2], s);
+  int c[3];
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    int v = (int)floor((s[d] - bp.cell_lo[d]) / bp.cw[d]);
+    v = v < 0 ? 0 : (v >= bp.ncell[d] ? bp.ncell[d] - 1 : v);
+    c[d] = v;
+  }
+  return (c[2] * bp.ncell[1] + c[1]) * bp.ncell[0] + c[0];
+}
+
+__global__ void k_cell_assign(int nall, BoxParams bp, const double* __restrict__ ext,
+                              int* __restrict__ cell_of, int* __restrict__ cell_count) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= nall) return;
+  const int c = cell_of_point(bp, ext[3 * n], ext[3 * n + 1], ext[3 * n + 2]);
+  cell_of[n] = c;
+  atomicAdd(&cell_count[c], 1);
+}
+
+__global__ void k_cell_scatter(int nall, const int* __restrict__ cell_of,
+                               const int* __restrict__ cell_start, int* __restrict__ cursor,
+                               const double* __restrict__ ext, const int* __restrict__ ext_type,
+                               CellAtom* __restrict__ sorted) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= nall) return;
+  const int c = cell_of[n];
+  const int p = cell_start[c] + atomicAdd(&cursor[c], 1);
+  CellAtom a;
+  a.x = ext[3 * n];
+  a.y = ext[3 * n + 1];
+  a.z = ext[3 * n + 2];
+  a.idx = n;
+  a.type = ext_type[n];
+  sorted[p] = a;
+}
+
+// ---------------------------------------------------------------------------
+// sel formatting shared by the cell and the CSR front ends. One wave per
+// centre; candidates within rcut are compacted into LDS, ranked by
+// (type, r2, j) and placed in their type section.
+constexpr int kNlWaves = 4;
+
+struct NlLds {
+  double r2[kNlWaves][kMaxCand];
+  int j[kNlWaves][kMaxCand];
+  int t[kNlWaves][kMaxCand];
+};
+
+__device__ __forceinline__ void nl_push(bool keep, double r2, int j, int t, int& n, double* s_r2,
+                                        int* s_j, int* s_t) {
+  const unsigned long long m = __ballot(keep);
+  const int lane = threadIdx.x & 63;
+  const int before = __popcll(m & ((1ull << lane) - 1ull));
+  if (keep) {
+    const int q = n + before;
+    if (q < kMaxCand) {
+      s_r2[q] = r2;
+      s_j[q] = j;
+      s_t[q] = t;
+    }
+  }
+  n += __popcll(m);
+}
+
+__device__ void nl_place(const NlParams& np, int i, int n, const double* s_r2, const int* s_j,
+                         const int* s_t, int* __restrict__ nlist, int* __restrict__ nreal,
+                         int* __restrict__ status) {
+  const int lane = threadIdx.x & 63;
+  if (n > kMaxCand) {
+    if (lane == 0) atomicOr(status, kStatusNeighbourOverflow);
+    n = kMaxCand;
+  }
+  wave_lds_sync();
+  int* row = nlist + (long)i * np.nnei;
+  int cnt[kMaxTypes];
+#pragma unroll
+  for (int t = 0; t < kMaxTypes; ++t) cnt[t] = 0;
+  for (int base = 0; base < n; base += kWave) {
+    const int q = base + lane;
+    const int tq = q < n ? s_t[q] : -1;
+#pragma unroll
+    for (int t = 0; t < kMaxTypes; ++t) cnt[t] += __popcll(__ballot(tq == t));
+  }
+  for (int q = lane; q < n; q += kWave) {
+    const int tq = s_t[q], jq = s_j[q];
+    const double rq = s_r2[q];
+    int rank = 0;
+    for (int p = 0; p < n; ++p) {
+      const double rp = s_r2[p];
+      const bool before = (s_t[p] == tq) && (rp < rq || (rp == rq && s_j[p] < jq));
+      rank += before ? 1 : 0;
+    }
+    if (rank < np.sel[tq]) row[np.sec[tq] + rank] = jq;
+  }
+  for (int t = 0; t < np.ntypes; ++t) {
+    const int kept = cnt[t] < np.sel[t] ? cnt[t] : np.sel[t];
+    for (int s = np.sec[t] + kept + lane; s < np.sec[t + 1]; s += kWave) row[s] = -1;
+    if (lane == 0) nreal[(long)i * np.ntypes + t] = kept;
+  }
+}
+
+__device__ __forceinline__ void nl_empty_row(const NlParams& np, int i, int* __restrict__ nlist,
+                                             int* __restrict__ nreal) {
+  const int lane = threadIdx.x & 63;
+  for (int s = lane; s < np.nnei; s += kWave) nlist[(long)i * np.nnei + s] = -1;
+  if (lane < np.ntypes) nreal[(long)i * np.ntypes + lane] = 0;
+}
+
+__global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells(
+    int nloc, BoxParams bp, NlParams np, const double* __restrict__ ext,
+    const int* __restrict__ ext_type, const int* __restrict__ cell_of,
+    const int* __restrict__ cell_start, const CellAtom* __restrict__ sorted,
+    int* __restrict__ nlist, int* __restrict__ nreal, int* __restrict__ status) {
+  __shared__ NlLds lds;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = blockIdx.x * kNlWaves + w;
+  if (i >= nloc) return;
+  const int ti = ext_type[i];
+  if (ti < 0 || ti >= np.ntypes) {
+    nl_empty_row(np, i, nlist, nreal);
+    return;
+  }
+  const double xi = ext[3 * i], yi = ext[3 * i + 1], zi = ext[3 * i + 2];
+  const int ci = cell_of[i];
+  const int c0 = ci % bp.ncell[0], c1 = (ci / bp.ncell[0]) % bp.ncell[1];
+  const int c2 = ci / (bp.ncell[0] * bp.ncell[1]);
+  int n = 0;
+  for (int z = c2 - 1; z <= c2 + 1; ++z) {
+    if (z < 0 || z >= bp.ncell[2]) continue;
+    for (int y = c1 - 1; y <= c1 + 1; ++y) {
+      if (y < 0 || y >= bp.ncell[1]) continue;
+      for (int x = c0 - 1; x <= c0 + 1; ++x) {
+        if (x < 0 || x >= bp.ncell[0]) continue;
+        const int cc = (z * bp.ncell[1] + y) * bp.ncell[0] + x;
+        const int beg = cell_start[cc], end = cell_start[cc + 1];
+        for (int base = beg; base < end; base += kWave) {
+          const int p = base + lane;
+          bool keep = false;
+          double r2 = 0.0;
+          int j = -1, t = -1;
+          if (p < end) {
+            const CellAtom a = sorted[p];
+            j = a.idx;
+            t = a.type;
+            const double dx = a.x - xi;
+            const double dy = a.y - yi;
+            const double dz = a.z - zi;
+            r2 = dx * dx + dy * dy + dz * dz;
+            keep = (j != i) && t >= 0 && t < np.ntypes && r2 <= np.rc2;
+          }
+          nl_push(keep, r2, j, t, n, lds.r2[w], lds.j[w], lds.t[w]);
+        }
+      }
+    }
+  }
+  nl_place(np, i, n, lds.r2[w], lds.j[w], lds.t[w], nlist, nreal, status);
+}
+
+// LAMMPS front end: candidates come from the caller's full list (CSR by centre).
+__global__ __launch_bounds__(kNlWaves * 64) void k_nlist_csr(
+    int nloc, NlParams np, const double* __restrict__ ext, const int* __restrict__ ext_type,
+    const long* __restrict__ cand_off, const int* __restrict__ cand, int* __restrict__ nlist,
+    int* __restrict__ nreal, int* __restrict__ status) {
+  __shared__ NlLds lds;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = blockIdx.x * kNlWaves + w;
+  if (i >= nloc) return;
+  const int ti = ext_type[i];
+  if (ti < 0 || ti >= np.ntypes) {
+    nl_empty_row(np, i, nlist, nreal);
+    return;
+  }
+  const double xi = ext[3 * i], yi = ext[3 * i + 1], zi = ext[3 * i + 2];
+  const long beg = cand_off[i], end = cand_off[i + 1];
+  int n = 0;
+  for (long base = beg; base < end; base += kWave) {
+    const long p = base + lane;
+    bool keep = false;
+    double r2 = 0.0;
+    int j = -1, t = -1;
+    if (p < end) {
+      j = cand[p];
+      t = ext_type[j];
+      const double dx = ext[3 * (long)j] - xi;
+      const double dy = ext[3 * (long)j + 1] - yi;
+      const double dz = ext[3 * (long)j + 2] - zi;
+      r2 = dx * dx + dy * dy + dz * dz;
+      keep = (j != i) && t >= 0 && t < np.ntypes && r2 <= np.rc2;
+    }
+    nl_push(keep, r2, j, t, n, lds.r2[w], lds.j[w], lds.t[w]);
+  }
+  nl_place(np, i, n, lds.r2[w], lds.j[w], lds.t[w], nlist, nreal, status);
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+void launch_wrap(hipStream_t st, int nloc, const double* coord, const int* atype,
+                 const BoxParams& bp, double* ext, int* ext_type, int* mapping, double* sfrac) {
+  if (nloc <= 0) return;
+  hipLaunchKernelGGL(k_wrap, dim3((nloc + 255) / 256), dim3(256), 0, st, nloc, coord, atype, bp,
+                     ext, ext_type, mapping, sfrac);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_ghost_flags(hipStream_t st, int nloc, const BoxParams& bp, const double* sfrac,
+                        int* flags) {
+  const long n = (long)bp.nshift * nloc;
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_ghost_flags, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, nloc, bp,
+                     sfrac, flags);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_ghost_fill(hipStream_t st, int nloc, const BoxParams& bp, const int* flags,
+                       const int* pos, double* ext, int* ext_type, int* mapping) {
+  const long n = (long)bp.nshift * nloc;
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_ghost_fill, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, nloc, bp,
+                     flags, pos, ext, ext_type, mapping);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_cell_assign(hipStream_t st, int nall, const BoxParams& bp, const double* ext,
+                        int* cell_of, int* cell_count) {
+  if (nall <= 0) return;
+  hipLaunchKernelGGL(k_cell_assign, dim3((nall + 255) / 256), dim3(256), 0, st, nall, bp, ext,
+                     cell_of, cell_count);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_cell_scatter(hipStream_t st, int nall, const int* cell_of, const int* cell_start,
+                         int* cursor, const double* ext, const int* ext_type, CellAtom* sorted) {
+  if (nall <= 0) return;
+  hipLaunchKernelGGL(k_cell_scatter, dim3((nall + 255) / 256), dim3(256), 0, st, nall, cell_of,
+                     cell_start, cursor, ext, ext_type, sorted);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_nlist_cells(hipStream_t st, int nloc, const BoxParams& bp, const NlParams& np,
+                        const double* ext, const int* ext_type, const int* cell_of,
+                        const int* cell_start, const CellAtom* sorted, int* nlist, int* nreal,
+                        int* status) {
+  if (nloc <= 0) return;
+  hipLaunchKernelGGL(k_nlist_cells, dim3((nloc + kNlWaves - 1) / kNlWaves), dim3(kNlWaves * 64),
+                     0, st, nloc, bp, np, ext, ext_type, cell_of, cell_start, sorted, nlist, nreal,
+                     status);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_nlist_csr(hipStream_t st, int nloc, const NlParams& np, const double* ext,
+                      const int* ext_type, const long* cand_off, const int* cand, int* nlist,
+                      int* nreal, int* status) {
+  if (nloc <= 0) return;
+  hipLaunchKernelGGL(k_nlist_csr, dim3((nloc + kNlWaves - 1) / kNlWaves), dim3(kNlWaves * 64), 0,
+                     st, nloc, np, ext, ext_type, cand_off, cand, nlist, nreal, status);
+  DPAMD_LAUNCH_CHECK();
+}
+
+}  // namespace dpamd

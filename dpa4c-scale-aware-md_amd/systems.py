@@ -1,0 +1,125 @@
+"""Seeded synthetic systems and the counter-based PRNG they are built from.
+
+The PRNG is splitmix64 used counter-style: value(seed, stream, i) is the
+splitmix64 finaliser of (key + (i + 1) * golden), key = finaliser of
+(seed + stream * 0xD1B54A32D192ED03). Uniforms take the top 53 bits; normals
+use Box-Muller on the uniform pair (2i, 2i+1). Everything is vectorised numpy
+with wrapping uint64 arithmetic, so the same seed gives the same system on
+any host.
+
+The five workloads follow the benchmark configurations: 192-atom water
+(64 H2O, 12.42 A), 12,288-atom water (49.68 A), 131,072-atom FCC Cu
+(32^3 cells, a = 3.615 A), 128,000-atom BCC high-entropy alloy (40^3 cells,
+a = 3.2 A, four species at exactly 25 %) and 393,216-atom water (51^3 sites
+with 1,579 seeded vacancies, 157.5 A). Boxes use LAMMPS' row-major
+h = [xx,0,0, xy,yy,0, xz,yz,zz] (lammps-deepmd-plugin/src/pair_deepmd.cpp:293-299).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+_GOLDEN = np.uint64(0x9E3779B97F4A7C15)
+_STREAM = np.uint64(0xD1B54A32D192ED03)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+
+
+def _mix(z: np.ndarray) -> np.ndarray:
+    z = (z ^ (z >> np.uint64(30))) * _M1
+    z = (z ^ (z >> np.uint64(27))) * _M2
+    return z ^ (z >> np.uint64(31))
+
+
+class Stream:
+    """Counter-based splitmix64 stream: draws are pure functions of (seed, stream, i)."""
+
+    def __init__(self, seed: int, stream: int = 0):
+        with np.errstate(over="ignore"):
+            k = np.array([seed], dtype=np.uint64) + np.array([stream], dtype=np.uint64) * _STREAM
+            self.key = _mix(k + _GOLDEN)[0]
+        self.pos = 0
+
+    def bits(self, n: int) -> np.ndarray:
+        i = np.arange(self.pos, self.pos + n, dtype=np.uint64)
+        self.pos += n
+        with np.errstate(over="ignore"):
+            return _mix(self.key + (i + np.uint64(1)) * _GOLDEN)
+
+    def uniform(self, n: int) -> np.ndarray:
+        return (self.bits(n) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+
+    def normal(self, n: int) -> np.ndarray:
+        u = self.uniform(2 * n).reshape(n, 2)
+        return np.sqrt(-2.0 * np.log1p(-u[:, 0])) * np.cos(2.0 * np.pi * u[:, 1])
+
+    def permutation(self, n: int) -> np.ndarray:
+        return np.argsort(self.bits(n), kind="stable")
+
+
+def cubic_box(edge: float) -> np.ndarray:
+    return np.array([edge, 0, 0, 0, edge, 0, 0, 0, edge], dtype=np.float64)
+
+
+def water(n_side: int, edge: float, seed: int, n_vacancies: int = 0, sigma: float = 0.1,
+          r_oh: float = 0.96, angle_deg: float = 104.52):
+    """Jittered-lattice water: O = site + N(0, sigma^2); H = O + r_oh * unit vectors
+    at the H-O-H angle `angle_deg`. Atom order: all O, then H1/H2 per molecule.
+    Types: O = 0, H = 1."""
+    st_sites, st_o, st_h = Stream(seed, 1), Stream(seed, 2), Stream(seed, 3)
+    a = edge / n_side
+    g = np.arange(n_side, dtype=np.float64)
+    sites = np.stack(np.meshgrid(g, g, g, indexing="ij"), axis=-1).reshape(-1, 3)
+    if n_vacancies:
+        keep = np.sort(st_sites.permutation(len(sites))[n_vacancies:])
+        sites = sites[keep]
+    nmol = len(sites)
+    o = (sites + 0.5) * a + sigma * st_o.normal(3 * nmol).reshape(nmol, 3)
+    v = st_h.normal(6 * nmol).reshape(nmol, 2, 3)
+    u1 = v[:, 0] / np.linalg.norm(v[:, 0], axis=1, keepdims=True)
+    p = v[:, 1] - np.sum(v[:, 1] * u1, axis=1, keepdims=True) * u1
+    p /= np.linalg.norm(p, axis=1, keepdims=True)
+    th = np.deg2rad(angle_deg)
+    u2 = np.cos(th) * u1 + np.sin(th) * p
+    h = np.stack([o + r_oh * u1, o + r_oh * u2], axis=1).reshape(-1, 3)
+    coord = np.concatenate([o, h], axis=0)
+    atype = np.concatenate([np.zeros(nmol, np.int32), np.ones(2 * nmol, np.int32)])
+    return coord, atype, cubic_box(edge)
+
+
+def fcc(n_cells: int, a: float, seed: int, sigma: float = 0.05):
+    """FCC lattice (4-atom conventional cell) + N(0, sigma^2) displacements, one type."""
+    basis = np.array([[0, 0, 0], [0.5, 0.5, 0], [0.5, 0, 0.5], [0, 0.5, 0.5]])
+    g = np.arange(n_cells, dtype=np.float64)
+    cells = np.stack(np.meshgrid(g, g, g, indexing="ij"), axis=-1).reshape(-1, 1, 3)
+    coord = ((cells + basis[None]) * a).reshape(-1, 3)
+    coord = coord + sigma * Stream(seed, 1).normal(coord.size).reshape(-1, 3)
+    return coord, np.zeros(len(coord), np.int32), cubic_box(n_cells * a)
+
+
+def bcc_hea(n_cells: int, a: float, seed: int, ntypes: int = 4, sigma: float = 0.05):
+    """BCC lattice, species at exactly 1/ntypes each by a seeded permutation."""
+    basis = np.array([[0, 0, 0], [0.5, 0.5, 0.5]])
+    g = np.arange(n_cells, dtype=np.float64)
+    cells = np.stack(np.meshgrid(g, g, g, indexing="ij"), axis=-1).reshape(-1, 1, 3)
+    coord = ((cells + basis[None]) * a).reshape(-1, 3)
+    n = len(coord)
+    coord = coord + sigma * Stream(seed, 1).normal(coord.size).reshape(-1, 3)
+    atype = np.repeat(np.arange(ntypes, dtype=np.int32), n // ntypes)
+    atype = np.concatenate([atype, np.arange(n - len(atype), dtype=np.int32)])
+    atype = atype[Stream(seed, 2).permutation(n)].astype(np.int32)
+    return coord, atype, cubic_box(n_cells * a)
+
+
+# (system builder, model kind) per benchmark configuration
+CONFIGS = {
+    0: dict(name="water192", kind="water", build=lambda: water(4, 12.42, seed=0)),
+    1: dict(name="water12k", kind="water", build=lambda: water(16, 49.68, seed=1)),
+    2: dict(name="cu131k", kind="cu", build=lambda: fcc(32, 3.615, seed=2)),
+    3: dict(name="hea128k", kind="hea", build=lambda: bcc_hea(40, 3.2, seed=3)),
+    4: dict(name="water393k", kind="water", build=lambda: water(51, 157.5, seed=4, n_vacancies=1579)),
+}
+
+
+def build(config: int):
+    """(coord [n,3] f64, atype [n] i32, box [9] f64) of benchmark configuration `config`."""
+    return CONFIGS[config]["build"]()

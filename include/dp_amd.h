@@ -1,0 +1,170 @@
+/*
+ * dp_amd.h — C ABI of the MI355X-native DeePMD se_e2_a evaluator (libdpamd.so).
+ *
+ * This is the drop-in boundary for the per-step energy / force / virial call
+ * that `pair_style deepmd` makes through the DeePMD C++ model API. Every entry
+ * point takes plain pointers and sizes; no torch or C++ types cross it.
+ * Return value: 0 on success, a negative DP_ERR_* code on failure, with the
+ * message available from dp_last_error(). The C++ façade in
+ * include/deepmd_amd/DeepPot.h turns failures into deepmd::deepmd_exception,
+ * as the reference does (deepmd-op/overlays/api_cc/src/DeepPotPTExpt.cc:295-309,
+ * caught by lammps-deepmd-plugin/src/pair_deepmd.cpp:372-374).
+ *
+ * Conventions (lammps-deepmd-plugin/src/pair_deepmd.cpp:293-307, :603-621):
+ *   coord  [natoms][3] Angstrom, row-major;  atype [natoms] model type index,
+ *          negative = virtual atom (no energy, no force, not a neighbour);
+ *   box    [9] row-major h = [xx,0,0, xy,yy,0, xz,yz,zz] (lower-triangular,
+ *          LAMMPS shape), or NULL for an open (non-periodic) system;
+ *   energy [1] eV;  force [natoms][3] eV/A;  virial [9] eV, row-major
+ *          W[3c+d] = -sum_edges g_c (x_j - x_i)_d;
+ *   atom_energy [natoms];  atom_virial [natoms][9], charged to the neighbour
+ *          (source) atom as in deepmd-op/overlays/op/pt/edge_force_virial.cu:1-14.
+ * Any optional output pointer may be NULL.
+ *
+ * Threading: one handle per host thread; calls on one handle are serialised
+ * by the caller (the reference keeps thread_local caches per model,
+ * DeepPotPTExpt.cc:138).
+ */
+#ifndef DP_AMD_H
+#define DP_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DP_MAX_TYPES 8
+
+enum {
+  DP_OK = 0,
+  DP_ERR_ARG = -1,      /* bad argument (null pointer, bad size, bad box) */
+  DP_ERR_MODEL = -2,    /* model file missing, malformed or unsupported */
+  DP_ERR_HIP = -3,      /* HIP runtime failure (allocation, launch, copy) */
+  DP_ERR_CAPACITY = -4, /* a neighbour count exceeded a fixed kernel capacity */
+  DP_ERR_NO_GPU = -5    /* no usable gfx950 device */
+};
+
+enum { DP_PREC_FP64 = 0, DP_PREC_MIXED = 1 };
+
+typedef struct dp_model dp_model;
+
+typedef struct {
+  int ntypes;
+  int nnei;
+  int sel[DP_MAX_TYPES];
+  double rcut;
+  double rcut_smth;
+  int emb[3];
+  int axis;
+  int fit[3];
+  int dim_fparam;   /* always 0 for se_e2_a energy models here */
+  int dim_aparam;   /* always 0 */
+  int precision;    /* DP_PREC_* in use */
+  char type_map[DP_MAX_TYPES][16];
+} dp_model_info;
+
+/* Stage buffers of the last evaluation that dp_debug_copy can read back. */
+enum {
+  DP_STAGE_NLIST = 0,      /* int32 [nloc][nnei] (extended-atom indices, -1 pad) */
+  DP_STAGE_EXT_COORD = 1,  /* f64 [nall][3] extended coordinates */
+  DP_STAGE_MAPPING = 2,    /* int32 [nall] owner of each extended atom */
+  DP_STAGE_DESCRPT = 3,    /* f64 [nloc][M1*axis] descriptor D */
+  DP_STAGE_ATOM_ENERGY = 4,/* f64 [nloc] */
+  DP_STAGE_EDGE_GRAD = 5,  /* f64 [nloc][nnei][3] dE/d(x_j - x_i) */
+  DP_STAGE_DEDD = 6,       /* f64 [nloc][M1*axis] dE/dD */
+  DP_STAGE_EXT_TYPE = 7    /* int32 [nall] */
+};
+
+/*
+ * Load a model and bind it to device `gpu_rank`.
+ * Replaces deepmd::DeepPot::init(model, gpu_rank, file_content)
+ * (deepmd-op/overlays/api_cc/include/DeepPot.h:475-477; called at
+ * lammps-deepmd-plugin/src/pair_deepmd.cpp:668). If `file_content` is non-NULL
+ * the model is read from those `content_len` bytes instead of `path`.
+ */
+int dp_create(const char* path, int gpu_rank, const void* file_content, size_t content_len,
+              int precision, dp_model** out);
+
+/* Release the handle and every device buffer it owns. */
+void dp_destroy(dp_model* model);
+
+/*
+ * Model metadata: cutoff(), numb_types(), dim_fparam(), dim_aparam(),
+ * get_type_map() of the reference model API
+ * (deepmd-op/overlays/api_cc/include/DeepPotPTExpt.h:103-154; used at
+ * lammps-deepmd-plugin/src/pair_deepmd.cpp:672-677, :1000).
+ */
+int dp_get_info(const dp_model* model, dp_model_info* info);
+
+/* Message of the last failure on this handle ("" if none). */
+const char* dp_last_error(const dp_model* model);
+
+/*
+ * Standalone evaluation from coordinates and box: ghost images, neighbour
+ * list and evaluation are built on the GPU; ghost forces / virials are folded
+ * onto their owners. Replaces DeepPot::compute(ener, force, virial,
+ * [atom_energy, atom_virial,] coord, atype, box)
+ * (deepmd-op/overlays/api_cc/include/DeepPot.h:503-522, :605-628;
+ * backend path DeepPotPTExpt.cc:1643-1957). Host pointers.
+ */
+int dp_compute(dp_model* model, int natoms, const double* coord, const int* atype,
+               const double* box, double* energy, double* force, double* virial,
+               double* atom_energy, double* atom_virial);
+
+/*
+ * LAMMPS neighbour-list evaluation. coord/atype cover nall = nloc + nghost
+ * atoms; the neighbour list (inum, ilist, numneigh, firstneigh) is LAMMPS'
+ * full list with skin, indices into the nall atoms (masked with `neigh_mask`,
+ * pass 0x1FFFFFFF for LAMMPS' NEIGHMASK, or 0 for no mask). force and
+ * atom_virial cover all nall atoms; ghost contributions stay in ghost slots for
+ * LAMMPS' reverse communication. `ago == 0` means the list was rebuilt and is
+ * re-uploaded; otherwise the cached list is reused and only re-filtered.
+ * Replaces DeepPot::compute(ener, force, virial, [atom_energy, atom_virial,]
+ * coord, atype, box, nghost, lmp_list, ago)
+ * (deepmd-op/overlays/api_cc/include/DeepPot.h:551-576, :661-690; called at
+ * lammps-deepmd-plugin/src/pair_deepmd.cpp:370-371, :381-383). Host pointers.
+ */
+int dp_compute_nlist(dp_model* model, int nall, int nghost, const double* coord,
+                     const int* atype, const double* box, int inum, const int* ilist,
+                     const int* numneigh, const int* const* firstneigh, int neigh_mask, int ago,
+                     double* energy, double* force, double* virial, double* atom_energy,
+                     double* atom_virial);
+
+/*
+ * Device-resident standalone evaluation: every array pointer is device memory
+ * on the handle's GPU except `box` (host, 9 doubles); work is ordered on
+ * `stream` (a hipStream_t, NULL = default stream) and the call returns after
+ * the outputs are complete on that stream. `ago == 0` refreshes the per-type
+ * bucketing of atype (read back once); otherwise the previous one is reused.
+ * Device analog of DeepPot::compute_canonical_graph_gpu / compute_edges_gpu
+ * (deepmd-op/overlays/api_cc/include/DeepPot.h:395-445), which also write in
+ * place into caller-owned device buffers (DeepPotPTExpt.cc:2843-2847).
+ */
+int dp_compute_device(dp_model* model, int natoms, const double* d_coord, const int* d_atype,
+                      const double* box, int ago, double* d_energy, double* d_force,
+                      double* d_virial, double* d_atom_energy, double* d_atom_virial,
+                      void* stream);
+
+/* Copy a stage buffer of the last evaluation (DP_STAGE_*) to host memory.
+ * Returns the buffer's size in bytes (copies min(size, capacity) bytes);
+ * negative on error. No counterpart in the reference: parity tests use it to
+ * compare each pipeline stage with the CPU oracle (the reference's own
+ * analogue is its DPA_DUMP_FRAME hook, graph_compress.cu:1354-1378). */
+long dp_debug_copy(dp_model* model, int stage, void* dst, size_t capacity);
+
+/* Per-stage GPU time of the last evaluation in milliseconds (hipEvent pairs),
+ * filled into times[0..n-1] in pipeline order; returns the number of stages
+ * and writes their names into names (NUL separated) when non-NULL. The
+ * reference's analogue is its DPA_KTIME stage timer (graph_compress.cu:1394-1427). */
+int dp_stage_times(dp_model* model, int enable, double* times, int n, char* names, size_t names_len);
+
+/* Peak device bytes allocated by this handle so far (memory high-water mark). */
+size_t dp_device_bytes(const dp_model* model);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DP_AMD_H */

@@ -1,0 +1,53 @@
+"""Seeded systems + models shared by the parity tests (small enough for the
+CPU oracle to finish in seconds)."""
+import numpy as np
+
+from _pkg import load_pkg
+
+dp = load_pkg()
+
+
+def water192():
+    return dp.systems.build(0), dp.model.random_model("water", seed=1000)
+
+
+def cu_small(n=6):
+    # 864 atoms, box 21.69 A > 2*rcut: every atom has 176 neighbours within 8 A
+    # and keeps 138 (sel overflow by 38)
+    return dp.systems.fcc(n, 3.615, seed=22), dp.model.random_model("cu", seed=1002)
+
+
+def hea_small(n=8):
+    return dp.systems.bcc_hea(n, 3.2, seed=33), dp.model.random_model("hea", seed=1003)
+
+
+def water_small_box():
+    # 8 molecules in 6.21 A: box < 2*rcut, many images of each atom
+    return dp.systems.water(2, 6.21, seed=44), dp.model.random_model("water", seed=1004)
+
+
+CASES = {"water192": water192, "cu864": cu_small, "hea1024": hea_small,
+         "water24_smallbox": water_small_box}
+
+
+def model_bytes(m):
+    return dp.model.to_bytes(m)
+
+
+def lammps_inputs(orc_obj, coord, atype, box, skin=1.0):
+    """Extended system + full neighbour list with skin, shaped like LAMMPS'
+    (ilist, numneigh, firstneigh) with ghosts after the local atoms."""
+    ext, et, mp = orc_obj.ghosts(coord, atype, box, orc_obj.m["rcut"] + skin)
+    nloc = len(atype)
+    off, cand = orc_obj.candidates(nloc, ext, et, orc_obj.m["rcut"] + skin, "cell")
+    # shuffle each list: LAMMPS order is arbitrary
+    rng = np.random.default_rng(5)
+    firstneigh = []
+    for i in range(nloc):
+        row = cand[off[i]:off[i + 1]].copy()
+        rng.shuffle(row)
+        firstneigh.append(row)
+    ilist = np.arange(nloc, dtype=np.int32)[::-1].copy()
+    firstneigh = [firstneigh[i] for i in ilist]
+    numneigh = np.array([len(r) for r in firstneigh], np.int32)
+    return ext, et, mp, ilist, numneigh, firstneigh

@@ -1,0 +1,119 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle.
+
+Tolerances (fp64, from the benchmark definition): neighbour lists and types
+bit-exact; energy per atom <= 1e-10 eV; forces <= 1e-8 eV/A; virial <= 1e-8 eV
+(max abs).
+"""
+import numpy as np
+import pytest
+
+from cases import CASES, lammps_inputs, model_bytes
+
+pytestmark = pytest.mark.gpu
+
+E_TOL = 1e-10   # eV per atom
+F_TOL = 1e-8    # eV/A
+V_TOL = 1e-8    # eV
+
+
+def _run(dp, orc, case):
+    (coord, atype, box), m = CASES[case]()
+    mb = model_bytes(m)
+    O = orc.Oracle(mb)
+    ref = O.compute(coord, atype, box, want_internals=True)
+    pot = dp.DeepPot(file_content=mb)
+    e, f, v, ae, av = pot.compute(coord, atype, box, atomic=True)
+    return O, ref, pot, (e, f, v, ae, av), (coord, atype, box)
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_nlist_bit_exact(dp, orc, case):
+    O, ref, pot, _, (coord, atype, box) = _run(dp, orc, case)
+    nall = len(ref["ext_type"])
+    ext = pot.stage(dp.STAGE_EXT_COORD, np.float64, (nall, 3))
+    assert ext.tobytes() == ref["ext_coord"].tobytes(), "extended coordinates differ"
+    mp = pot.stage(dp.STAGE_MAPPING, np.int32, (nall,))
+    assert np.array_equal(mp, ref["mapping"])
+    et = pot.stage(dp.STAGE_EXT_TYPE, np.int32, (nall,))
+    assert np.array_equal(et, ref["ext_type"])
+    nl = pot.stage(dp.STAGE_NLIST, np.int32, ref["nlist"].shape)
+    assert np.array_equal(nl, ref["nlist"])
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_energy_force_virial(dp, orc, case):
+    O, ref, pot, (e, f, v, ae, av), (coord, atype, box) = _run(dp, orc, case)
+    n = len(atype)
+    assert abs(e - ref["energy"]) / n <= E_TOL
+    assert np.abs(ae - ref["atom_energy"]).max() <= E_TOL
+    assert np.abs(f - ref["force"]).max() <= F_TOL
+    assert np.abs(v - ref["virial"]).max() <= V_TOL
+    assert np.abs(av - ref["atom_virial"]).max() <= V_TOL
+
+
+@pytest.mark.parametrize("case", ["water192", "cu864"])
+def test_stage_parity(dp, orc, case):
+    O, ref, pot, _, (coord, atype, box) = _run(dp, orc, case)
+    n = len(atype)
+    d = pot.stage(dp.STAGE_DESCRPT, np.float64, (n, O.ndescrpt))
+    np.testing.assert_allclose(d, ref["descrpt"], rtol=0, atol=1e-12)
+    dd = pot.stage(dp.STAGE_DEDD, np.float64, (n, O.ndescrpt))
+    np.testing.assert_allclose(dd, ref["dE_dD"], rtol=0, atol=1e-11)
+    eg = pot.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))
+    np.testing.assert_allclose(eg, ref["edge_grad"], rtol=0, atol=1e-11)
+
+
+@pytest.mark.parametrize("case", ["water192", "hea1024"])
+def test_lammps_path(dp, orc, case):
+    (coord, atype, box), m = CASES[case]()
+    mb = model_bytes(m)
+    O = orc.Oracle(mb)
+    ext, et, mp, ilist, numneigh, firstneigh = lammps_inputs(O, coord, atype, box)
+    nloc = len(atype)
+    nall = len(et)
+    off = np.zeros(nloc + 1, np.int64)
+    order = np.argsort(ilist)
+    rows = [np.sort(firstneigh[k]) for k in order]
+    off[1:] = np.cumsum([len(r) for r in rows])
+    cand = np.concatenate(rows).astype(np.int32)
+    nl = O.format_nlist(nloc, ext, et, off, cand)
+    ref = O.eval_ext(nloc, ext, et, nl)
+    pot = dp.DeepPot(file_content=mb)
+    e, f, v, ae, av = pot.compute_nlist(ext, et, box, nall - nloc, ilist, numneigh, firstneigh,
+                                        ago=0, atomic=True)
+    assert np.array_equal(pot.stage(dp.STAGE_NLIST, np.int32, nl.shape), nl)
+    assert abs(e - ref["energy"]) / nloc <= E_TOL
+    assert np.abs(f - ref["force"]).max() <= F_TOL
+    assert np.abs(v - ref["virial"]).max() <= V_TOL
+    assert np.abs(av - ref["atom_virial"]).max() <= V_TOL
+    # ago > 0 reuses the cached list, re-filtered on new positions
+    ext2 = ext + 0.01 * np.random.default_rng(1).standard_normal(ext.shape)
+    nl2 = O.format_nlist(nloc, ext2, et, off, cand)
+    ref2 = O.eval_ext(nloc, ext2, et, nl2)
+    e2, f2, v2 = pot.compute_nlist(ext2, et, box, nall - nloc, ilist, numneigh, firstneigh, ago=3)
+    assert np.array_equal(pot.stage(dp.STAGE_NLIST, np.int32, nl.shape), nl2)
+    assert abs(e2 - ref2["energy"]) / nloc <= E_TOL
+    assert np.abs(f2 - ref2["force"]).max() <= F_TOL
+
+
+def test_virtual_atoms(dp, orc):
+    (coord, atype, box), m = CASES["water192"]()
+    atype = atype.copy()
+    atype[[3, 70, 150]] = -1
+    mb = model_bytes(m)
+    ref = orc.Oracle(mb).compute(coord, atype, box)
+    pot = dp.DeepPot(file_content=mb)
+    e, f, v, ae, av = pot.compute(coord, atype, box, atomic=True)
+    assert abs(e - ref["energy"]) / len(atype) <= E_TOL
+    assert np.abs(f - ref["force"]).max() <= F_TOL
+    assert np.all(f[[3, 70, 150]] == 0.0) and np.all(ae[[3, 70, 150]] == 0.0)
+
+
+def test_bitwise_reproducible(dp):
+    (coord, atype, box), m = CASES["cu864"]()
+    pot = dp.DeepPot(file_content=model_bytes(m))
+    r1 = pot.compute(coord, atype, box, atomic=True)
+    r2 = pot.compute(coord, atype, box, atomic=True)
+    assert r1[0] == r2[0]
+    for a, b in zip(r1[1:], r2[1:]):
+        assert a.tobytes() == b.tobytes()
