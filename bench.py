@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Benchmark: one DeePMD se_e2_a energy / force / virial evaluation per step on
+one MI355X, device-resident inputs, seeded synthetic system and random-init
+weights of the benchmark architecture.
+
+A step is one full pass of the hot path: ghost images, cell list, sel-sorted
+neighbour list, env matrix + embedding + descriptor, fitting net forward and
+input gradient, embedding backward, force / virial gather and reductions.
+
+Prints ONE JSON line. `value` is microseconds per step per atom on the
+131,072-atom FCC Cu system (config 2) unless --config says otherwise; the
+12,288-atom water system (config 1) is measured in the same run and reported
+under "secondary". The roofline object describes the dominant kernel, timed
+with HIP events on the stream it runs on; the CPU baseline is the repository's
+fp64 CPU restatement (oracle/) timed on a bounded sample of centres.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+PEAK_FP64_MFMA = 78.6e12   # FLOP/s, MI355X dense FP64 matrix
+PEAK_HBM = 8.0e12          # B/s
+DT_FS = {0: 0.5, 1: 0.5, 2: 1.0, 3: 1.0, 4: 0.5}
+KIND = {0: "water", 1: "water", 2: "cu", 3: "hea", 4: "water"}
+
+
+def flops_bytes(pot, n_real, nloc, nb_edges):
+    """Algorithmic FLOPs / bytes of each stage for one step (real slots only;
+    padded slots are a per-(type, type) constant and not evaluated)."""
+    L1, L2, L3 = (pot.info.emb[k] for k in range(3))
+    M2 = pot.info.axis
+    F0, F1, F2 = (pot.info.fit[k] for k in range(3))
+    Dn = L3 * M2
+    nt = pot.numb_types()
+    emb_fwd = 2.0 * (L1 + L1 * L2 + L2 * L3) + 2.0 * 4 * L3
+    emb_vjp = 2.0 * (L1 * L2 + L2 * L3) + 2.0 * L1 + 2.0 * (2 * 4 * L3)
+    fit = 2.0 * (Dn * F0 + F0 * F1 + F1 * F2 + F2) + 2.0 * (F2 * F1 + F1 * F0 + F0 * Dn)
+    return {
+        "embed_fwd": ("flop", emb_fwd * n_real),
+        "embed_bwd": ("flop", emb_vjp * n_real),
+        "fitting": ("flop", fit * nloc),
+        "descriptor": ("byte", 8.0 * nloc * (nt * 4 * L3 + 4 * L3 + Dn)),
+        "dE_dT": ("byte", 8.0 * nloc * (Dn + 4 * L3 + 4 * L3)),
+        # edge gradient (24 B) + reverse index (4 B) per edge, force 24 B per atom
+        "force": ("byte", 28.0 * nb_edges + 24.0 * nloc),
+        "nlist": ("byte", 4.0 * nloc * pot.nnei + 24.0 * nloc),
+    }
+
+
+def run_config(dp, hip, config, steps, warmup):
+    coord, atype, box = dp.systems.build(config)
+    n = len(atype)
+    mb = dp.model.to_bytes(dp.model.random_model(KIND[config], seed=1000 + config))
+    pot = dp.DeepPot(file_content=mb, gpu_rank=0)
+    d_coord = hip.DeviceArray(coord.astype("float64"))
+    d_atype = hip.DeviceArray(atype.astype("int32"))
+    d_e = hip.DeviceArray(nbytes=8)
+    d_f = hip.DeviceArray(nbytes=24 * n)
+    d_v = hip.DeviceArray(nbytes=72)
+
+    def step(ago):
+        pot.compute_device(d_coord.ptr, d_atype.ptr, n, box, d_e.ptr, d_f.ptr, d_v.ptr, ago=ago)
+
+    for w in range(max(warmup, 1)):
+        step(0 if w == 0 else 1)
+    hip.synchronize()
+    import numpy as np
+    nl = pot.stage(dp.STAGE_NLIST, np.int32, (n, pot.nnei))
+    n_real = int((nl >= 0).sum())
+
+    pot.enable_stage_timing(True)
+    stage_sum = {}
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(1)
+        for k, v in pot.stage_times().items():
+            stage_sum[k] = stage_sum.get(k, 0.0) + v
+    hip.synchronize()
+    t1 = time.perf_counter()
+    pot.enable_stage_timing(False)
+    ms = (t1 - t0) * 1e3 / steps
+    stage_ms = {k: v / steps for k, v in stage_sum.items()}
+    energy = d_e.to_host(np.float64, (1,))[0]
+    force = d_f.to_host(np.float64, (n, 3))
+    work = flops_bytes(pot, n_real, n, n_real)
+    stages = {}
+    for k, t in stage_ms.items():
+        entry = {"ms": round(t, 4)}
+        if k in work and t > 0:
+            kind, amount = work[k]
+            if kind == "flop":
+                entry.update(tflops=round(amount / (t * 1e-3) / 1e12, 3),
+                             frac=round(amount / (t * 1e-3) / PEAK_FP64_MFMA, 4))
+            else:
+                entry.update(gbs=round(amount / (t * 1e-3) / 1e9, 1),
+                             frac=round(amount / (t * 1e-3) / PEAK_HBM, 4))
+        stages[k] = entry
+    return dict(n=n, ms=ms, stage_ms=stage_ms, stages=stages, work=work, n_real=n_real,
+                energy=float(energy), max_abs_fsum=float(abs(force.sum(0)).max()),
+                device_bytes=pot.device_bytes(), mb=mb, coord=coord, atype=atype, box=box)
+
+
+def cpu_baseline(mb, coord, atype, box, target_s=12.0):
+    """fp64 CPU restatement (oracle/) on a bounded sample of centres: ghosts for
+    the whole box, then neighbour list + full evaluation of the first K centres."""
+    from _pkg import load_oracle
+    orc = load_oracle()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    O = orc.Oracle(mb)
+
+    def sample(K):
+        t0 = time.perf_counter()
+        ext, et, _ = O.ghosts(coord, atype, box, O.m["rcut"])
+        off, cand = O.candidates(K, ext, et, O.m["rcut"], "cell")
+        nl = O.format_nlist(K, ext, et, off, cand)
+        O.eval_ext(K, ext, et, nl, nthreads=threads, want_atomic=False)
+        return time.perf_counter() - t0
+
+    n = len(atype)
+    k0 = min(n, 256)
+    t0 = sample(k0)
+    K = int(min(n, max(k0, k0 * target_s / max(t0, 1e-6))))
+    t = sample(K)
+    return {"value": round(t * 1e6 / K, 3), "unit": "us/step/atom", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle fp64 se_e2_a: ghosts of all {n} atoms + nlist and full "
+                      f"evaluation of the first {K} centres ({t:.1f} s), per centre"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3, 4])
+    ap.add_argument("--secondary", type=int, default=1, help="second config reported alongside (-1: none)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build evaluates on one GPU; --gpus above 1 is not "
+                                   "supported (every GPU box here has one GPU)"}))
+        sys.exit(2)
+    from _pkg import load_pkg
+    dp = load_pkg()
+    import importlib
+    hip = importlib.import_module("dpamd.hip")
+    if hip.device_count() < 1:
+        print(json.dumps({"error": "no HIP device visible"}))
+        sys.exit(1)
+
+    main_r = run_config(dp, hip, args.config, args.steps, args.warmup)
+    n = main_r["n"]
+    us_atom = main_r["ms"] * 1e3 / n
+    ns_day = DT_FS[args.config] * 1e-6 * 86400.0 / (main_r["ms"] * 1e-3)
+    # dominant single-launch kernel
+    kernel_stages = ["embed_bwd", "embed_fwd", "descriptor", "dE_dT", "nlist"]
+    dom = max(kernel_stages, key=lambda k: main_r["stage_ms"].get(k, 0.0))
+    kind, amount = main_r["work"][dom]
+    t_dom = main_r["stage_ms"][dom] * 1e-3
+    if kind == "flop":
+        ach = amount / t_dom / 1e12
+        roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
+                "peak": PEAK_FP64_MFMA / 1e12, "unit": "TFLOP/s",
+                "frac": round(ach * 1e12 / PEAK_FP64_MFMA, 4), "traffic": None,
+                "algorithmic_per_launch": amount, "avg_launch_ms": round(t_dom * 1e3, 4)}
+    else:
+        ach = amount / t_dom / 1e9
+        roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": 8000.0,
+                "unit": "GB/s", "frac": round(ach * 1e9 / PEAK_HBM, 4), "traffic": None,
+                "algorithmic_per_launch": amount, "avg_launch_ms": round(t_dom * 1e3, 4)}
+    out = {
+        "metric": "us/step/atom (1 MI355X, se_e2_a fp64 energy+force+virial)",
+        "value": round(us_atom, 5),
+        "unit": "us/step/atom",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_r["ms"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic (seeded lattice + jitter, seeded random-init weights)",
+        "config": {"workload": {2: "cu131k FCC Cu 131,072 atoms, rcut 8, sel 138, 32-64-128/240x3",
+                                1: "water12k 12,288 atoms, rcut 6, sel [46,92], 25-50-100/240x3",
+                                0: "water192", 3: "hea128k", 4: "water393k"}[args.config],
+                   "atoms": n, "dt_fs": DT_FS[args.config]},
+        "ns_per_day": round(ns_day, 4),
+        "roofline": roof,
+        "stages": main_r["stages"],
+        "device_bytes_peak": main_r["device_bytes"],
+    }
+    if args.secondary >= 0 and args.secondary != args.config:
+        s = run_config(dp, hip, args.secondary, args.steps, args.warmup)
+        out["secondary"] = {"config": args.secondary, "atoms": s["n"],
+                            "us_per_step_atom": round(s["ms"] * 1e3 / s["n"], 5),
+                            "ms_per_step": round(s["ms"], 4),
+                            "ns_per_day": round(DT_FS[args.secondary] * 1e-6 * 86400.0 /
+                                                (s["ms"] * 1e-3), 4),
+                            "stages": s["stages"]}
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(main_r["mb"], main_r["coord"], main_r["atype"], main_r["box"])
+        cb["gpu_speedup"] = round(cb["value"] / us_atom, 1)
+        out["cpu_baseline"] = cb
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
