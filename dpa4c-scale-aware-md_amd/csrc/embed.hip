@@ -30,6 +30,7 @@
 // amplitude instead of storing it" recompute backward
 // include/dpa_chain/graph_compress.cuh:9-10 and
 // deepmd-op/overlays/op/pt/dpa4c/graph_compress_kernel.cuh:1458-1466.
+#include "fastmath.h"
 #include "kernels.h"
 
 namespace dpamd {
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
 #pragma unroll
     for (int q = 0; q < S::NQ2; ++q) {
       const int f = 4 * q + g;
-      x1[q] = (f < S::L1) ? tanh(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
+      x1[q] = (f < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
     }
     // layer 2, transposed
     d4 acc2[S::NT2];
@@ -180,14 +181,14 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int f = 16 * t + 4 * r + g;
-        const double th = tanh(acc2[t][r] + P[S::OFF_B2 + f]);
+        const double th = tanh_fast(acc2[t][r] + P[S::OFF_B2 + f]);
         double res = 0.0;
         if constexpr (S::RES2 != 0) {
           if constexpr (S::X1_ALIGNED) {
             res = x1[(S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r];
           } else {
             const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
-            res = (f1 < S::L1) ? tanh(s * P[S::OFF_W1 + f1] + P[S::OFF_B1 + f1]) : 0.0;
+            res = (f1 < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f1] + P[S::OFF_B1 + f1]) : 0.0;
           }
         }
         x2[t][r] = (f < S::L2) ? res + th : 0.0;
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int sl = g + 4 * r;
-            double G = tanh(acc3[uu][r] + P[S::OFF_B3 + f]);
+            double G = tanh_fast(acc3[uu][r] + P[S::OFF_B3 + f]);
             if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
             if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
 #pragma unroll
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       const int f = 4 * q + g;
       if (f < S::L1) {
         const double wv = P[S::OFF_W1 + f];
-        const double th = tanh(s * wv + P[S::OFF_B1 + f]);
+        const double th = tanh_fast(s * wv + P[S::OFF_B1 + f]);
         x1[q] = th;
         x1t[q] = (1.0 - th * th) * wv;
       } else {
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int f = 16 * t + 4 * r + g;
-        const double th = tanh(acc2[t][r] + P[S::OFF_B2 + f]);
+        const double th = tanh_fast(acc2[t][r] + P[S::OFF_B2 + f]);
         double res = 0.0, rest = 0.0;
         if constexpr (S::RES2 != 0) {
           if constexpr (S::X1_ALIGNED) {
@@ -362,7 +363,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
             const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
             if (f1 < S::L1) {
               const double wv = P[S::OFF_W1 + f1];
-              const double y = tanh(s * wv + P[S::OFF_B1 + f1]);
+              const double y = tanh_fast(s * wv + P[S::OFF_B1 + f1]);
               res = y;
               rest = (1.0 - y * y) * wv;
             }
@@ -411,7 +412,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int f = 16 * u + 4 * r + g;
-            const double th = tanh(acc3[uu][r] + P[S::OFF_B3 + f]);
+            const double th = tanh_fast(acc3[uu][r] + P[S::OFF_B3 + f]);
             const double tt = (1.0 - th * th) * acc3t[uu][r];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {

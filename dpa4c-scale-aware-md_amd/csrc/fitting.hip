@@ -9,6 +9,7 @@
 // e = h.w_head + b_head + bias_atom_e[type]
 // (deepmd-op/overlays/op/pt/graph_fitting.cu:1-25, :614-719); the reference's
 // fused tile analog is deepmd-op/overlays/op/pt/tiled_fitting.cuh:4-60.
+#include "fastmath.h"
 #include "kernels.h"
 
 namespace dpamd {
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
       if (a.epi == 0) {
         a.C[o] = v;
       } else if (a.epi == 1) {
-        const double t = tanh(v + a.bias[col]);
+        const double t = tanh_fast(v + a.bias[col]);
         if (a.T_out) a.T_out[o] = t;
         a.C[o] = a.idt ? a.A[(long)row * a.lda + col] + a.idt[col] * t : t;
       } else {

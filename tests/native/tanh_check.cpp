@@ -1,0 +1,34 @@
+// Accuracy of dpamd::tanh_fast (host build of the same source) against libm
+// tanh over a dense grid and random points; prints max error in ulp of the
+// result and max absolute error.
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <random>
+
+#include "../../dpa4c-scale-aware-md_amd/csrc/fastmath.h"
+
+static double ulp_err(double a, double b) {
+  if (a == b) return 0.0;
+  const double u = std::fabs(std::nextafter(b, INFINITY) - b);
+  return std::fabs(a - b) / (u > 0 ? u : 1e-300);
+}
+
+int main() {
+  double max_ulp = 0, max_abs = 0, worst = 0;
+  std::mt19937_64 g(7);
+  std::uniform_real_distribution<double> U(-25.0, 25.0);
+  auto check = [&](double x) {
+    const double a = dpamd::tanh_fast(x), b = std::tanh(x);
+    const double e = ulp_err(a, b);
+    if (e > max_ulp) { max_ulp = e; worst = x; }
+    if (std::fabs(a - b) > max_abs) max_abs = std::fabs(a - b);
+  };
+  for (int i = -2000000; i <= 2000000; ++i) check(i * 1e-5);
+  for (int i = 0; i < 2000000; ++i) check(U(g));
+  for (int k = -300; k < 3; ++k) { check(std::ldexp(1.0, k)); check(-std::ldexp(1.3, k)); }
+  check(0.0);
+  std::printf("max_ulp %.3f at x=%.17g max_abs %.3e\n", max_ulp, worst, max_abs);
+  return (max_ulp <= 4.0 && max_abs <= 4e-16) ? 0 : 1;
+}
