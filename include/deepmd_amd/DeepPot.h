@@ -1,0 +1,241 @@
+// deepmd_amd/DeepPot.h — header-only C++ façade over dp_amd.h that keeps the
+// surface `pair_style deepmd` calls on the reference's deepmd::DeepPot
+// (deepmd-op/overlays/api_cc/include/DeepPot.h:451-926) and the upstream
+// InputNlist type (fields evidenced at lammps-deepmd-plugin/src/pair_deepmd.cpp:355-364).
+// Failures throw deepmd::deepmd_exception, which the pair style turns into
+// error->one (pair_deepmd.cpp:372-374).
+//
+// Link with -ldpamd. Only double precision is evaluated on the GPU; the float
+// overloads convert at the boundary, as the reference's compute<float> does.
+#pragma once
+
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../dp_amd.h"
+
+namespace deepmd {
+
+typedef double ENERGYTYPE;
+
+class deepmd_exception : public std::runtime_error {
+ public:
+  explicit deepmd_exception(const std::string& msg) : std::runtime_error(msg) {}
+};
+
+// LAMMPS neighbour list handed to the model (full list, with skin). The
+// communication fields are carried for source compatibility; this build is
+// single-rank and does not read them.
+struct InputNlist {
+  int inum = 0;
+  int* ilist = nullptr;
+  int* numneigh = nullptr;
+  int** firstneigh = nullptr;
+  int nswap = 0;
+  int* sendnum = nullptr;
+  int* recvnum = nullptr;
+  int* firstrecv = nullptr;
+  int** sendlist = nullptr;
+  int* sendproc = nullptr;
+  int* recvproc = nullptr;
+  void* world = nullptr;
+  int nprocs = 1;
+  int mask = 0;
+  int* mapping = nullptr;
+  InputNlist() = default;
+  InputNlist(int inum_, int* ilist_, int* numneigh_, int** firstneigh_)
+      : inum(inum_), ilist(ilist_), numneigh(numneigh_), firstneigh(firstneigh_) {}
+  InputNlist(int inum_, int* ilist_, int* numneigh_, int** firstneigh_, int nswap_,
+             int* sendnum_, int* recvnum_, int* firstrecv_, int** sendlist_, int* sendproc_,
+             int* recvproc_, void* world_, int nprocs_ = 1)
+      : inum(inum_), ilist(ilist_), numneigh(numneigh_), firstneigh(firstneigh_),
+        nswap(nswap_), sendnum(sendnum_), recvnum(recvnum_), firstrecv(firstrecv_),
+        sendlist(sendlist_), sendproc(sendproc_), recvproc(recvproc_), world(world_),
+        nprocs(nprocs_) {}
+  void set_mask(int m) { mask = m; }
+  void set_mapping(int* m) { mapping = m; }
+};
+
+class DeepPot {
+ public:
+  DeepPot() = default;
+  DeepPot(const std::string& model, const int& gpu_rank = 0,
+          const std::string& file_content = "") {
+    init(model, gpu_rank, file_content);
+  }
+  ~DeepPot() {
+    if (h_) dp_destroy(h_);
+  }
+  DeepPot(const DeepPot&) = delete;
+  DeepPot& operator=(const DeepPot&) = delete;
+
+  void init(const std::string& model, const int& gpu_rank = 0,
+            const std::string& file_content = "") {
+    if (h_) {
+      dp_destroy(h_);
+      h_ = nullptr;
+    }
+    dp_model* h = nullptr;
+    const int rc = dp_create(model.c_str(), gpu_rank,
+                             file_content.empty() ? nullptr : file_content.data(),
+                             file_content.size(), DP_PREC_FP64, &h);
+    if (rc != DP_OK) {
+      const std::string msg = h ? dp_last_error(h) : "dp_create failed";
+      if (h) dp_destroy(h);
+      throw deepmd_exception("DeePMD-kit (MI355X) init: " + msg);
+    }
+    h_ = h;
+    dp_get_info(h_, &info_);
+  }
+
+  double cutoff() const { return info_.rcut; }
+  int numb_types() const { return info_.ntypes; }
+  int numb_types_spin() const { return 0; }
+  int dim_fparam() const { return info_.dim_fparam; }
+  int dim_aparam() const { return info_.dim_aparam; }
+  int dim_chg_spin() const { return 0; }
+  void get_type_map(std::string& type_map) const {
+    type_map.clear();
+    for (int t = 0; t < info_.ntypes; ++t) {
+      if (t) type_map += " ";
+      type_map += info_.type_map[t];
+    }
+  }
+
+  // compute(ener, force, virial, coord, atype, box[, fparam, aparam, charge_spin])
+  template <typename VALUETYPE>
+  void compute(ENERGYTYPE& ener, std::vector<VALUETYPE>& force, std::vector<VALUETYPE>& virial,
+               const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+               const std::vector<VALUETYPE>& box,
+               const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    std::vector<VALUETYPE> ae, av;
+    compute_impl(ener, force, virial, ae, av, false, coord, atype, box, fparam, aparam,
+                 charge_spin);
+  }
+  // compute(ener, force, virial, atom_energy, atom_virial, coord, atype, box[, ...])
+  template <typename VALUETYPE>
+  void compute(ENERGYTYPE& ener, std::vector<VALUETYPE>& force, std::vector<VALUETYPE>& virial,
+               std::vector<VALUETYPE>& atom_energy, std::vector<VALUETYPE>& atom_virial,
+               const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+               const std::vector<VALUETYPE>& box,
+               const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    compute_impl(ener, force, virial, atom_energy, atom_virial, true, coord, atype, box, fparam,
+                 aparam, charge_spin);
+  }
+  // compute(ener, force, virial, coord, atype, box, nghost, lmp_list, ago[, ...])
+  template <typename VALUETYPE>
+  void compute(ENERGYTYPE& ener, std::vector<VALUETYPE>& force, std::vector<VALUETYPE>& virial,
+               const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+               const std::vector<VALUETYPE>& box, const int nghost, const InputNlist& lmp_list,
+               const int& ago, const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    std::vector<VALUETYPE> ae, av;
+    compute_nlist_impl(ener, force, virial, ae, av, false, coord, atype, box, nghost, lmp_list,
+                       ago, fparam, aparam, charge_spin);
+  }
+  // compute(ener, force, virial, atom_energy, atom_virial, coord, atype, box, nghost, lmp_list, ago[, ...])
+  template <typename VALUETYPE>
+  void compute(ENERGYTYPE& ener, std::vector<VALUETYPE>& force, std::vector<VALUETYPE>& virial,
+               std::vector<VALUETYPE>& atom_energy, std::vector<VALUETYPE>& atom_virial,
+               const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+               const std::vector<VALUETYPE>& box, const int nghost, const InputNlist& lmp_list,
+               const int& ago, const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    compute_nlist_impl(ener, force, virial, atom_energy, atom_virial, true, coord, atype, box,
+                       nghost, lmp_list, ago, fparam, aparam, charge_spin);
+  }
+
+  dp_model* handle() const { return h_; }
+
+ private:
+  dp_model* h_ = nullptr;
+  dp_model_info info_{};
+
+  void check(int rc) const {
+    if (rc != DP_OK) throw deepmd_exception(std::string("DeePMD-kit (MI355X): ") + dp_last_error(h_));
+  }
+  void require_init() const {
+    if (!h_) throw deepmd_exception("DeePMD-kit (MI355X): model not initialised");
+  }
+  template <typename V>
+  static void no_params(const std::vector<V>& fparam, const std::vector<V>& aparam,
+                        const std::vector<double>& cs) {
+    if (!fparam.empty() || !aparam.empty() || !cs.empty())
+      throw deepmd_exception("se_e2_a model takes no fparam / aparam / charge_spin");
+  }
+  template <typename V>
+  static std::vector<double> to_double(const std::vector<V>& v) {
+    return std::vector<double>(v.begin(), v.end());
+  }
+  template <typename V>
+  static void from_double(std::vector<V>& out, const std::vector<double>& v) {
+    out.assign(v.begin(), v.end());
+  }
+
+  template <typename V>
+  void compute_impl(ENERGYTYPE& ener, std::vector<V>& force, std::vector<V>& virial,
+                    std::vector<V>& atom_energy, std::vector<V>& atom_virial, bool atomic,
+                    const std::vector<V>& coord, const std::vector<int>& atype,
+                    const std::vector<V>& box, const std::vector<V>& fparam,
+                    const std::vector<V>& aparam, const std::vector<double>& cs) {
+    require_init();
+    no_params(fparam, aparam, cs);
+    const int n = (int)atype.size();
+    if ((int)coord.size() != 3 * n) throw deepmd_exception("coord size must be 3 * natoms");
+    if (!box.empty() && box.size() != 9) throw deepmd_exception("box must have 9 entries");
+    const std::vector<double> c = to_double(coord), b = to_double(box);
+    std::vector<double> f(3 * (size_t)n), v(9), ae, av;
+    if (atomic) {
+      ae.resize(n);
+      av.resize(9 * (size_t)n);
+    }
+    check(dp_compute(h_, n, c.data(), atype.data(), b.empty() ? nullptr : b.data(), &ener,
+                     f.data(), v.data(), atomic ? ae.data() : nullptr,
+                     atomic ? av.data() : nullptr));
+    from_double(force, f);
+    from_double(virial, v);
+    if (atomic) {
+      from_double(atom_energy, ae);
+      from_double(atom_virial, av);
+    }
+  }
+
+  template <typename V>
+  void compute_nlist_impl(ENERGYTYPE& ener, std::vector<V>& force, std::vector<V>& virial,
+                          std::vector<V>& atom_energy, std::vector<V>& atom_virial, bool atomic,
+                          const std::vector<V>& coord, const std::vector<int>& atype,
+                          const std::vector<V>& box, int nghost, const InputNlist& nl, int ago,
+                          const std::vector<V>& fparam, const std::vector<V>& aparam,
+                          const std::vector<double>& cs) {
+    require_init();
+    no_params(fparam, aparam, cs);
+    const int nall = (int)atype.size();
+    if ((int)coord.size() != 3 * nall) throw deepmd_exception("coord size must be 3 * nall");
+    const std::vector<double> c = to_double(coord), b = to_double(box);
+    std::vector<double> f(3 * (size_t)nall), v(9), ae, av;
+    if (atomic) {
+      ae.resize(nall);
+      av.resize(9 * (size_t)nall);
+    }
+    check(dp_compute_nlist(h_, nall, nghost, c.data(), atype.data(),
+                           b.empty() ? nullptr : b.data(), nl.inum, nl.ilist, nl.numneigh,
+                           nl.firstneigh, nl.mask, ago, &ener, f.data(), v.data(),
+                           atomic ? ae.data() : nullptr, atomic ? av.data() : nullptr));
+    from_double(force, f);
+    from_double(virial, v);
+    if (atomic) {
+      from_double(atom_energy, ae);
+      from_double(atom_virial, av);
+    }
+  }
+};
+
+}  // namespace deepmd

@@ -1,0 +1,166 @@
+"""Native pieces that need no GPU: the C ABI library loads and exports every
+symbol include/dp_amd.h declares, fails cleanly without a GPU or with a bad
+model, the C++ façade compiles and links, the device tanh (host build) is
+accurate, and the oracle is clean under ASan/UBSan."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from _pkg import PKG_DIR, ROOT
+
+HEADER = os.path.join(ROOT, "include", "dp_amd.h")
+
+
+def declared_symbols():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|void|long|size_t|const char\*)\s+(dp_\w+)\(", txt, re.M)))
+
+
+def test_library_exports_declared_symbols(dp):
+    syms = declared_symbols()
+    assert len(syms) >= 10
+    L = dp.lib()
+    for s in syms:
+        assert hasattr(L, s), f"{s} not exported by libdpamd.so"
+    assert set(syms) == set(dp.EXPORTED)
+
+
+def test_bad_model_is_reported(dp):
+    L = dp.lib()
+    h = ctypes.c_void_p()
+    junk = b"NOTAMODEL" * 10
+    rc = L.dp_create(None, 0, junk, len(junk), 0, ctypes.byref(h))
+    assert rc == -2
+    assert b"DPAMDSEA" in L.dp_last_error(h)
+    L.dp_destroy(h)
+    with pytest.raises(dp.DeepmdException):
+        dp.DeepPot(file_content=junk)
+
+
+def test_unsupported_shape_is_reported(dp):
+    m = dp.model.random_model("water", seed=1, emb=[8, 16, 32])
+    with pytest.raises(dp.DeepmdException, match="not compiled"):
+        dp.DeepPot(file_content=dp.model.to_bytes(m))
+
+
+def _gpu_visible(dp):
+    import importlib
+    hip = importlib.import_module("dpamd.hip")
+    try:
+        return hip.device_count() > 0
+    except Exception:
+        return False
+
+
+def test_no_gpu_fails_loudly(dp):
+    if _gpu_visible(dp):
+        pytest.skip("a GPU is visible")
+    mb = dp.model.to_bytes(dp.model.random_model("water", seed=1))
+    with pytest.raises(dp.DeepmdException, match="HIP device|gfx950"):
+        dp.DeepPot(file_content=mb)
+
+
+def test_tanh_fast_accuracy(tmp_path):
+    exe = tmp_path / "tanh_check"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-o", str(exe),
+                    os.path.join(ROOT, "tests", "native", "tanh_check.cpp")], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+def build_facade(tmp_path):
+    exe = tmp_path / "facade_check"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "native", "facade_check.cpp"), "-o", str(exe),
+                    "-L", PKG_DIR, "-ldpamd", f"-Wl,-rpath,{PKG_DIR}"], check=True)
+    return exe
+
+
+def write_input(path, coord, atype, box):
+    with open(path, "wb") as f:
+        f.write(np.int32(len(atype)).tobytes())
+        f.write(np.ascontiguousarray(coord, np.float64).tobytes())
+        f.write(np.ascontiguousarray(atype, np.int32).tobytes())
+        f.write(np.ascontiguousarray(box, np.float64).tobytes())
+
+
+def test_facade_builds_and_throws_without_gpu(dp, tmp_path):
+    exe = build_facade(tmp_path)
+    if _gpu_visible(dp):
+        pytest.skip("a GPU is visible (the GPU test runs the façade)")
+    mpath = tmp_path / "m.dp"
+    dp.model.write_model(str(mpath), dp.model.random_model("water", seed=1))
+    coord, atype, box = dp.systems.build(0)
+    write_input(tmp_path / "in.bin", coord, atype, box)
+    r = subprocess.run([str(exe), str(mpath), str(tmp_path / "in.bin")], capture_output=True, text=True)
+    assert r.returncode == 3 and "EXC" in r.stdout
+
+
+def test_oracle_sanitizers(dp, tmp_path):
+    """Build the oracle with ASan + UBSan and evaluate the 192-atom water box."""
+    src = os.path.join(ROOT, "oracle")
+    drv = tmp_path / "drv.c"
+    drv.write_text(r'''
+#include <stdio.h>
+#include <stdlib.h>
+#include "se_e2_a.h"
+int main(int argc, char** argv) {
+  FILE* f = fopen(argv[1], "rb"); int n, nt, sel[8], emb[3], fit[3], axis; double rc, rs;
+  if (fread(&n, 4, 1, f) != 1) return 2;
+  double* coord = malloc(24 * n); int* at = malloc(4 * n); double box[9];
+  fread(coord, 8, 3 * n, f); fread(at, 4, n, f); fread(box, 8, 9, f);
+  fread(&nt, 4, 1, f); fread(sel, 4, nt, f); fread(&rc, 8, 1, f); fread(&rs, 8, 1, f);
+  fread(emb, 4, 3, f); fread(&axis, 4, 1, f); fread(fit, 4, 3, f);
+  long nd, ne, nf; fread(&nd, 8, 1, f); fread(&ne, 8, 1, f); fread(&nf, 8, 1, f);
+  double* davg = malloc(8 * nd); double* dstd = malloc(8 * nd); double* ep = malloc(8 * ne);
+  double* fp = malloc(8 * nf); double bias[8];
+  fread(davg, 8, nd, f); fread(dstd, 8, nd, f); fread(ep, 8, ne, f); fread(fp, 8, nf, f);
+  fread(bias, 8, nt, f); fclose(f);
+  orc_model m = {0}; m.ntypes = nt; int acc = 0;
+  for (int t = 0; t < nt; ++t) { m.sel[t] = sel[t]; m.sec[t] = acc; acc += sel[t]; }
+  m.sec[nt] = acc; m.nnei = acc; m.rcut = rc; m.rcut_smth = rs; m.axis = axis;
+  for (int k = 0; k < 3; ++k) { m.emb[k] = emb[k]; m.fit[k] = fit[k]; }
+  m.davg = davg; m.dstd = dstd; m.emb_params = ep; m.fit_params = fp; m.bias_atom_e = bias;
+  int nall = orc_ghost_count(n, coord, box, rc);
+  double* ext = malloc(24 * nall); int* et = malloc(4 * nall); int* mp = malloc(4 * nall);
+  orc_build_ghosts(n, coord, at, box, rc, nall, ext, et, mp);
+  long* off = malloc(8 * (n + 1));
+  long nc = orc_candidates_cell(n, nall, ext, et, NULL, rc, 0, off, NULL);
+  int* cand = malloc(4 * (nc + 1));
+  orc_candidates_cell(n, nall, ext, et, NULL, rc, nc, off, cand);
+  int* nl = malloc(4 * n * m.nnei);
+  orc_format_nlist(&m, n, ext, et, off, cand, nl);
+  double* ae = malloc(8 * n); double* frc = malloc(24 * nall); double v[9];
+  double* av = malloc(72 * nall);
+  orc_eval(&m, n, nall, ext, et, nl, 1, ae, NULL, NULL, NULL, NULL, frc, v, av);
+  double e = 0; for (int i = 0; i < n; ++i) e += ae[i];
+  printf("%.17g\n", e);
+  free(coord); free(at); free(davg); free(dstd); free(ep); free(fp); free(ext); free(et);
+  free(mp); free(off); free(cand); free(nl); free(ae); free(frc); free(av);
+  return 0;
+}
+''')
+    exe = tmp_path / "drv"
+    subprocess.run(["gcc", "-O1", "-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+                    "-I", src, str(drv), os.path.join(src, "orc_geom.c"), os.path.join(src, "se_e2_a.c"),
+                    "-o", str(exe), "-lm"], check=True)
+    coord, atype, box = dp.systems.build(0)
+    m = dp.model.random_model("water", seed=1000)
+    with open(tmp_path / "in.bin", "wb") as f:
+        f.write(np.int32(len(atype)).tobytes())
+        f.write(coord.tobytes()); f.write(atype.astype(np.int32).tobytes()); f.write(box.tobytes())
+        f.write(np.int32(2).tobytes()); f.write(np.array(m["sel"], np.int32).tobytes())
+        f.write(np.array([m["rcut"], m["rcut_smth"]]).tobytes())
+        f.write(np.array(m["emb"], np.int32).tobytes()); f.write(np.int32(m["axis"]).tobytes())
+        f.write(np.array(m["fit"], np.int32).tobytes())
+        f.write(np.array([m["davg"].size, m["emb_params"].size, m["fit_params"].size], np.int64).tobytes())
+        for k in ("davg", "dstd", "emb_params", "fit_params", "bias_atom_e"):
+            f.write(np.ascontiguousarray(m[k], np.float64).tobytes())
+    r = subprocess.run([str(exe), str(tmp_path / "in.bin")], capture_output=True, text=True,
+                       env={**os.environ, "ASAN_OPTIONS": "detect_leaks=1"})
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert float(r.stdout) == pytest.approx(367.6157183243399, abs=1e-9)

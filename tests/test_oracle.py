@@ -1,0 +1,244 @@
+"""Pins of the CPU oracle (no GPU): what fixes each function besides its own
+formula — closed forms, brute force, finite differences, invariances, and an
+independent torch fp64 autograd restatement (test_torch_crosscheck.py)."""
+import numpy as np
+import pytest
+
+from cases import CASES, model_bytes
+
+
+@pytest.fixture(scope="module")
+def water(dp, orc):
+    (coord, atype, box), m = CASES["water192"]()
+    O = orc.Oracle(model_bytes(m))
+    return O, coord, atype, box
+
+
+# ---- switching function -------------------------------------------------
+def test_switch_closed_forms(dp, orc):
+    O = orc.Oracle(model_bytes(dp.model.random_model("cu", seed=1)))
+    rs, rc = O.m["rcut_smth"], O.m["rcut"]
+    assert O.switch(rs - 1e-9) == (1.0, 0.0)
+    assert O.switch(0.5 * rs) == (1.0, 0.0)
+    assert O.switch(rc) == (0.0, 0.0)
+    assert O.switch(rc + 1.0) == (0.0, 0.0)
+    # smoothstep symmetry: sw(mid) = 1/2 and sw(mid + t) + sw(mid - t) = 1
+    mid = 0.5 * (rs + rc)
+    assert O.switch(mid)[0] == pytest.approx(0.5, abs=1e-15)
+    for t in np.linspace(0.01, 0.49, 9) * (rc - rs):
+        assert O.switch(mid + t)[0] + O.switch(mid - t)[0] == pytest.approx(1.0, abs=1e-14)
+    # derivative against central differences, and C1/C2 at both ends
+    h = 1e-6
+    for r in np.linspace(rs + 0.01, rc - 0.01, 25):
+        fd = (O.switch(r + h)[0] - O.switch(r - h)[0]) / (2 * h)
+        assert O.switch(r)[1] == pytest.approx(fd, abs=1e-8)
+    for edge in (rs, rc):
+        d_in = O.switch(edge - 1e-7 if edge == rc else edge + 1e-7)[1]
+        assert abs(d_in) < 1e-9
+    # second derivative vanishes at the ends: dsw changes like (r-rs)^2
+    e = 1e-3
+    assert abs(O.switch(rs + e)[1]) < 40.0 * e * e / (rc - rs) ** 3 * (rc - rs)
+
+
+def test_env_mat_single_neighbour(dp, orc):
+    """Two atoms in an open system: the env row is the closed form and its
+    derivative the central difference."""
+    m = dp.model.random_model("water", seed=3)
+    O = orc.Oracle(model_bytes(m))
+    d = np.array([1.3, -0.7, 2.1])
+    ext = np.array([[0.0, 0.0, 0.0], d])
+    et = np.array([0, 1], np.int32)
+    nl = np.full((1, O.nnei), -1, np.int32)
+    nl[0, O.sec[1]] = 1
+    env, envd, rij = O.env_mat(1, ext, et, nl)
+    r = np.linalg.norm(d)
+    sw, dsw = O.switch(r)
+    avg = m["davg"][0, 1]
+    std = m["dstd"][0, 1]
+    raw = np.array([sw / r, sw * d[0] / r**2, sw * d[1] / r**2, sw * d[2] / r**2])
+    np.testing.assert_allclose(env[0, O.sec[1]], (raw - avg) / std, rtol=1e-14, atol=1e-14)
+    np.testing.assert_allclose(rij[0, O.sec[1]], d, rtol=0, atol=0)
+    # padded slot of section 0: (0 - avg)/std, derivative 0
+    np.testing.assert_allclose(env[0, 0], (0.0 - m["davg"][0, 0]) / m["dstd"][0, 0], rtol=1e-15)
+    assert np.all(envd[0, 0] == 0.0)
+    h = 1e-6
+    for c in range(3):
+        ep = ext.copy(); ep[1, c] += h
+        em = ext.copy(); em[1, c] -= h
+        fd = (O.env_mat(1, ep, et, nl)[0] - O.env_mat(1, em, et, nl)[0])[0, O.sec[1]] / (2 * h)
+        np.testing.assert_allclose(envd[0, O.sec[1], :, c], fd, rtol=1e-6, atol=1e-8)
+
+
+# ---- neighbour lists ------------------------------------------------------
+@pytest.mark.parametrize("case", list(CASES))
+def test_candidates_brute_equals_cell(orc, case):
+    (coord, atype, box), m = CASES[case]()
+    O = orc.Oracle(model_bytes(m))
+    ext, et, mp = O.ghosts(coord, atype, box, O.m["rcut"])
+    nloc = len(atype)
+    ob, cb = O.candidates(nloc, ext, et, O.m["rcut"], "brute")
+    oc, cc = O.candidates(nloc, ext, et, O.m["rcut"], "cell")
+    assert np.array_equal(ob, oc) and np.array_equal(cb, cc)
+
+
+def test_ghosts_cover_every_image_within_rcut(orc, dp):
+    """Every periodic image within rcut of a local atom is present exactly once."""
+    (coord, atype, box), m = CASES["water24_smallbox"]()
+    O = orc.Oracle(model_bytes(m))
+    rc = O.m["rcut"]
+    ext, et, mp = O.ghosts(coord, atype, box, rc)
+    nloc = len(atype)
+    assert np.array_equal(mp[:nloc], np.arange(nloc))
+    L = box[0]
+    wrapped = ext[:nloc]
+    for i in range(nloc):
+        # brute force over images of every atom
+        cnt = 0
+        for k in range(nloc):
+            for sh in np.stack(np.meshgrid(*[np.arange(-2, 3)] * 3, indexing="ij"), -1).reshape(-1, 3):
+                if k == i and not sh.any():
+                    continue
+                if np.sum((wrapped[k] + L * sh - wrapped[i]) ** 2) <= rc * rc:
+                    cnt += 1
+        d2 = np.sum((ext - ext[i]) ** 2, axis=1)
+        d2[i] = np.inf
+        assert (d2 <= rc * rc).sum() == cnt
+    # each ghost is its owner shifted by an integer lattice vector
+    shift = (ext - ext[mp]) / L
+    assert np.abs(shift - np.rint(shift)).max() < 1e-12
+
+
+def _nlist_of(O, ext, et):
+    nloc = 1
+    off = np.array([0, len(et) - 1], np.int64)
+    cand = np.arange(1, len(et), dtype=np.int32)
+    return O.format_nlist(nloc, ext, et, off, cand)[0]
+
+
+def test_format_nlist_rules(dp, orc):
+    m = dp.model.random_model("water", seed=5, sel=[3, 2])
+    O = orc.Oracle(model_bytes(m))
+    rc = O.m["rcut"]
+    # centre 0 (type 0); candidates 1..: type, position
+    pts = [(0, [0, 0, 0]),
+           (1, [1.0, 0, 0]),     # j=1, H r=1
+           (0, [0, 2.0, 0]),     # j=2, O r=2
+           (0, [0, 0, 2.0]),     # j=3, O r=2 (tie with j=2 -> j order)
+           (1, [0, 0.5, 0]),     # j=4, H r=0.5
+           (0, [rc, 0, 0]),      # j=5, O at exactly rcut: kept (r2 <= rc^2)
+           (0, [0, rc + 1e-9, 0]),  # j=6, just outside
+           (1, [3.0, 0, 0]),     # j=7, H r=3 -> third H, dropped (sel 2)
+           (0, [1.5, 0, 0]),     # j=8, O r=1.5
+           ]
+    ext = np.array([p for _, p in pts], float)
+    et = np.array([t for t, _ in pts], np.int32)
+    row = _nlist_of(O, ext, et)
+    # O section (sel 3): r=1.5 (j8), r=2 (j2), r=2 (j3); j5 at rcut is 4th -> dropped
+    assert list(row[:3]) == [8, 2, 3]
+    # H section (sel 2): r=0.5 (j4), r=1 (j1); j7 dropped
+    assert list(row[3:5]) == [4, 1]
+    # with a larger O sel the rcut atom is kept and padding follows
+    m2 = dp.model.random_model("water", seed=5, sel=[6, 4])
+    O2 = orc.Oracle(model_bytes(m2))
+    row2 = _nlist_of(O2, ext, et)
+    assert list(row2[:6]) == [8, 2, 3, 5, -1, -1]
+    assert list(row2[6:]) == [4, 1, 7, -1]
+
+
+def test_nlist_sorted_and_within_cutoff(water, orc):
+    O, coord, atype, box = water
+    ext, et, mp, nl = O.neighbor_list(coord, atype, box)
+    rc2 = O.m["rcut"] ** 2
+    for i in range(len(atype)):
+        for t in range(2):
+            sec = nl[i, O.sec[t]:O.sec[t + 1]]
+            real = sec[sec >= 0]
+            assert np.all(sec[len(real):] == -1)
+            assert np.all(et[real] == t)
+            d2 = np.sum((ext[real] - ext[i]) ** 2, axis=1)
+            assert np.all(d2 <= rc2)
+            keys = list(zip(d2, real))
+            assert keys == sorted(keys)
+
+
+# ---- energy, force, virial -------------------------------------------------
+@pytest.mark.parametrize("case", ["water192", "hea1024"])
+def test_force_is_minus_gradient(orc, case):
+    (coord, atype, box), m = CASES[case]()
+    O = orc.Oracle(model_bytes(m))
+    out = O.compute(coord, atype, box)
+    h = 1e-5
+    rng = np.random.default_rng(0)
+    for a in rng.choice(len(atype), 4, replace=False):
+        for c in range(3):
+            cp = coord.copy(); cp[a, c] += h
+            cm = coord.copy(); cm[a, c] -= h
+            fd = -(O.compute(cp, atype, box)["energy"] - O.compute(cm, atype, box)["energy"]) / (2 * h)
+            assert out["force"][a, c] == pytest.approx(fd, abs=2e-7)
+
+
+@pytest.mark.parametrize("case", ["water192", "cu864"])
+def test_virial_is_minus_strain_derivative(orc, case):
+    (coord, atype, box), m = CASES[case]()
+    O = orc.Oracle(model_bytes(m))
+    out = O.compute(coord, atype, box)
+    W = out["virial"].reshape(3, 3)
+    h = 1e-6
+    for a in range(3):
+        for b in range(a + 1):
+            e = np.zeros((3, 3)); e[a, b] = h
+            def en(G):
+                return O.compute(coord @ G, atype, (box.reshape(3, 3) @ G).reshape(9))["energy"]
+            fd = -(en(np.eye(3) + e) - en(np.eye(3) - e)) / (2 * h)
+            assert W[a, b] == pytest.approx(fd, abs=2e-5 * max(1.0, abs(fd)))
+    assert np.abs(W - W.T).max() < 1e-10
+    np.testing.assert_allclose(out["atom_virial"].sum(0), out["virial"], rtol=0, atol=1e-10)
+    assert np.abs(out["force"].sum(0)).max() < 1e-10
+
+
+def test_invariances(dp, orc, water):
+    O, coord, atype, box = water
+    e0 = O.compute(coord, atype, box)
+    # translation (periodic: rewrapping changes coordinates, not the energy)
+    e1 = O.compute(coord + np.array([3.1, -7.7, 40.2]), atype, box)
+    assert e1["energy"] == pytest.approx(e0["energy"], abs=1e-10)
+    np.testing.assert_allclose(e1["force"], e0["force"], atol=1e-10)
+    # permutation of atoms
+    perm = np.random.default_rng(1).permutation(len(atype))
+    e2 = O.compute(coord[perm], atype[perm], box)
+    assert e2["energy"] == pytest.approx(e0["energy"], abs=1e-10)
+    np.testing.assert_allclose(e2["force"], e0["force"][perm], atol=1e-10)
+    # rotation of an open cluster
+    sub = coord[:24]
+    ts = atype[:24]
+    th = 0.7
+    R = np.array([[np.cos(th), -np.sin(th), 0], [np.sin(th), np.cos(th), 0], [0, 0, 1.0]])
+    R = R @ np.array([[1, 0, 0], [0, np.cos(0.3), -np.sin(0.3)], [0, np.sin(0.3), np.cos(0.3)]])
+    ext = sub.copy()
+    off, cand = O.candidates(24, ext, ts, O.m["rcut"], "brute")
+    nl = O.format_nlist(24, ext, ts, off, cand)
+    a = O.eval_ext(24, ext, ts, nl)
+    ext2 = sub @ R.T
+    off2, cand2 = O.candidates(24, ext2, ts, O.m["rcut"], "brute")
+    b = O.eval_ext(24, ext2, ts, O.format_nlist(24, ext2, ts, off2, cand2))
+    assert b["energy"] == pytest.approx(a["energy"], abs=1e-10)
+    np.testing.assert_allclose(b["force"], a["force"] @ R.T, atol=1e-10)
+
+
+def test_padded_slots_use_net_at_s_pad(dp, orc):
+    """An isolated atom has only padded slots: T = R_pad^T G(s_pad) per section."""
+    m = dp.model.random_model("water", seed=9)
+    O = orc.Oracle(model_bytes(m))
+    ext = np.zeros((1, 3))
+    et = np.zeros(1, np.int32)
+    nl = np.full((1, O.nnei), -1, np.int32)
+    out = O.eval_ext(1, ext, et, nl, want_internals=True)
+    L3, M2 = m["emb"][2], m["axis"]
+    T = np.zeros((4, L3))
+    for t in range(2):
+        rpad = (0.0 - m["davg"][0, t]) / m["dstd"][0, t]
+        T += O.m["sel"][t] * np.outer(rpad, O.embed(0, t, rpad[0]))
+    T /= O.nnei
+    D = T.T @ T[:, :M2]
+    np.testing.assert_allclose(out["descrpt"][0], D.reshape(-1), rtol=1e-13, atol=1e-15)
+    assert np.all(out["force"] == 0.0)
