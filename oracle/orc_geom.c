@@ -12,7 +12,7 @@
  *    (lammps-deepmd-plugin/src/pair_deepmd.cpp:293-299);
  *  - neighbours are kept when r2 <= rcut*rcut and sorted by the key
  *    (type_j, r2, j); section t holds the first sel[t] of type t, padded -1
- *    (reference analog: the exact-cut predicate
+ *    (DeepPot-SE neighbour formatting; reference analog: the exact-cut predicate
  *    production/dpa4c-runtime/include/dpa_chain/exact_cut.cuh:10-20).
  */
 #include <math.h>
