@@ -33,39 +33,76 @@ struct GemmArgs {
 };
 
 // C = epi(A[MxK] B[KxN]); B(k,n) = TRANSB ? B[n*ldb + k] : B[k*ldb + n].
-// 64 x BN block tile, K staged through LDS 16 at a time; wave w owns rows
-// 16w..16w+15 and all BN columns (BN/16 MFMA tiles sharing one A fragment).
-template <int BN, bool TRANSB>
+// Block tile 64 x 16*NT: wave w owns rows 16w..16w+15 and all NT column tiles,
+// so one A fragment feeds NT MFMAs. K advances 16 at a time through two LDS
+// buffers: the next chunk is fetched into registers while the current one is
+// multiplied, then stored into the other buffer (one barrier per chunk).
+template <int NT, bool TRANSB>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
-  constexpr int BM = 64, BK = 16, NT = BN / 16;
-  __shared__ double As[BM][BK + 1];
-  __shared__ double Bs[BK][BN + 1];
+  constexpr int BM = 64, BK = 16, BN = 16 * NT;
+  constexpr int ALD = BK + 1, BLD = BN + 1;
+  constexpr int NA = BM * BK / 256, NB = (BK * BN + 255) / 256;
+  __shared__ double As[2][BM * ALD];
+  __shared__ double Bs[2][BK * BLD];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+  double ra[NA], rb[NB];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+      const int q = tid + 256 * u, r = q / BK, kk = q % BK, gr = row0 + r;
+      ra[u] = gr < a.M ? a.A[(long)gr * a.lda + k0 + kk] : 0.0;
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int q = tid + 256 * u;
+      double v = 0.0;
+      if (q < BK * BN) {
+        if (!TRANSB) {
+          const int kk = q / BN, n = q % BN;
+          v = a.B[(long)(k0 + kk) * a.ldb + col0 + n];
+        } else {
+          const int n = q / BK, kk = q % BK;
+          v = a.B[(long)(col0 + n) * a.ldb + k0 + kk];
+        }
+      }
+      rb[u] = v;
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+      const int q = tid + 256 * u;
+      As[buf][(q / BK) * ALD + q % BK] = ra[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int q = tid + 256 * u;
+      if (q < BK * BN) {
+        if (!TRANSB) Bs[buf][(q / BN) * BLD + q % BN] = rb[u];
+        else Bs[buf][(q % BK) * BLD + q / BK] = rb[u];
+      }
+    }
+  };
   d4 acc[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) acc[n] = d4{0.0, 0.0, 0.0, 0.0};
-  for (int k0 = 0; k0 < a.K; k0 += BK) {
-    for (int q = tid; q < BM * BK; q += 256) {
-      const int r = q / BK, kk = q % BK, gr = row0 + r;
-      As[r][kk] = gr < a.M ? a.A[(long)gr * a.lda + k0 + kk] : 0.0;
-    }
-    for (int q = tid; q < BK * BN; q += 256) {
-      if (!TRANSB) {
-        const int kk = q / BN, n = q % BN;
-        Bs[kk][n] = a.B[(long)(k0 + kk) * a.ldb + col0 + n];
-      } else {
-        const int n = q / BK, kk = q % BK;
-        Bs[kk][n] = a.B[(long)(col0 + n) * a.ldb + k0 + kk];
-      }
-    }
-    __syncthreads();
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  const int nk = a.K / BK;
+  for (int kc = 0; kc < nk; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < nk) fetch((kc + 1) * BK);
+    const double* Ab = As[buf] + (16 * w + c) * ALD;
+    const double* Bb = Bs[buf];
 #pragma unroll
     for (int q = 0; q < BK / 4; ++q) {
-      const double av = As[16 * w + c][4 * q + g];
+      const double av = Ab[4 * q + g];
 #pragma unroll
-      for (int n = 0; n < NT; ++n) acc[n] = mfma_f64(av, Bs[4 * q + g][16 * n + c], acc[n]);
+      for (int n = 0; n < NT; ++n) acc[n] = mfma_f64(av, Bb[(4 * q + g) * BLD + 16 * n + c], acc[n]);
     }
+    if (kc + 1 < nk) stash(buf ^ 1);
     __syncthreads();
   }
 #pragma unroll
@@ -116,42 +153,96 @@ __global__ __launch_bounds__(256) void k_head(int rows, int F2, const double* __
 }
 
 // dT[m][a] = sum_b dD[a][b] T[m][b] + (a < axis) sum_a' dD[a'][a] T[m][a'].
-__global__ __launch_bounds__(256) void k_dT(int L3, int axis, const int* __restrict__ items,
-                                            const double* __restrict__ T,
-                                            const double* __restrict__ dD,
-                                            double* __restrict__ dT) {
-  extern __shared__ double sm[];
-  const int pos = blockIdx.x, i = items[pos];
-  double* Ts = sm;
-  double* dDs = sm + 4 * L3;
-  const int nd = L3 * axis;
-  for (int q = threadIdx.x; q < 4 * L3; q += blockDim.x) Ts[q] = T[(long)i * 4 * L3 + q];
-  for (int q = threadIdx.x; q < nd; q += blockDim.x) dDs[q] = dD[(long)pos * nd + q];
-  __syncthreads();
-  for (int q = threadIdx.x; q < 4 * L3; q += blockDim.x) {
-    const int m = q / L3, ai = q % L3;
-    const double* Tm = Ts + m * L3;
-    double v = 0.0;
-    for (int b = 0; b < axis; ++b) v += dDs[ai * axis + b] * Tm[b];
-    if (ai < axis)
-      for (int a2 = 0; a2 < L3; ++a2) v += dDs[a2 * axis + ai] * Tm[a2];
-    dT[(long)i * 4 * L3 + q] = v;
+// One wave per atom, axis == 16: dD is read coalesced, element e = 64k + lane
+// being (a, b) = (4k + g, c) for lane = 16g + c. First term: lane products
+// dD[a][c] T[m][c] summed over the 16 lanes of a row (xor 1..8). Second term:
+// lane (g, c) accumulates dD[a][c] T[m][a] over its rows, then the 4 row groups
+// are folded (xor 16, 32); lane c then holds column c.
+constexpr int kDtWaves = 4;
+__global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
+                                                     const int* __restrict__ items,
+                                                     const double* __restrict__ T,
+                                                     const double* __restrict__ dD,
+                                                     double* __restrict__ dT) {
+  constexpr int AX = 16;
+  __shared__ double Ts[kDtWaves][4 * 128];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int pos = blockIdx.x * kDtWaves + w;
+  if (pos >= nb) return;
+  const int i = items[pos];
+  const double* Ti = T + (long)i * 4 * L3;
+  for (int q = lane; q < 4 * L3; q += 64) Ts[w][q] = Ti[q];
+  wave_lds_sync();
+  const double* dDp = dD + (long)pos * L3 * AX;
+  double* out = dT + (long)i * 4 * L3;
+  const double tb0 = Ts[w][c], tb1 = Ts[w][L3 + c], tb2 = Ts[w][2 * L3 + c], tb3 = Ts[w][3 * L3 + c];
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+  for (int a0 = 0; a0 < L3; a0 += 4) {
+    const int a = a0 + g;
+    const double v = dDp[a0 * AX + lane];
+    s0 += v * Ts[w][a];
+    s1 += v * Ts[w][L3 + a];
+    s2 += v * Ts[w][2 * L3 + a];
+    s3 += v * Ts[w][3 * L3 + a];
+    double p0 = v * tb0, p1 = v * tb1, p2 = v * tb2, p3 = v * tb3;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      p0 += shfl_xor_d(p0, off);
+      p1 += shfl_xor_d(p1, off);
+      p2 += shfl_xor_d(p2, off);
+      p3 += shfl_xor_d(p3, off);
+    }
+    // row a: lane c == m writes component m (the second term is added below)
+    const double pm = c == 0 ? p0 : c == 1 ? p1 : c == 2 ? p2 : p3;
+    if (c < 4 && a >= AX) out[c * L3 + a] = pm;
+    if (c < 4 && a < AX) Ts[w][c * L3 + a] = pm;  // stash: T rows a < 16 no longer needed
+  }
+  s0 += shfl_xor_d(s0, 16);
+  s0 += shfl_xor_d(s0, 32);
+  s1 += shfl_xor_d(s1, 16);
+  s1 += shfl_xor_d(s1, 32);
+  s2 += shfl_xor_d(s2, 16);
+  s2 += shfl_xor_d(s2, 32);
+  s3 += shfl_xor_d(s3, 16);
+  s3 += shfl_xor_d(s3, 32);
+  wave_lds_sync();
+  if (g == 0) {
+    out[c] = Ts[w][c] + s0;
+    out[L3 + c] = Ts[w][L3 + c] + s1;
+    out[2 * L3 + c] = Ts[w][2 * L3 + c] + s2;
+    out[3 * L3 + c] = Ts[w][3 * L3 + c] + s3;
   }
 }
 
-template <int BN, bool TRANSB>
-static void gemm_bn(hipStream_t st, const GemmArgs& a) {
-  dim3 grid(a.N / BN, (a.M + 63) / 64);
-  hipLaunchKernelGGL((k_gemm<BN, TRANSB>), grid, dim3(256), 0, st, a);
+template <int NT, bool TRANSB>
+static void gemm_nt(hipStream_t st, const GemmArgs& a) {
+  dim3 grid(a.N / (16 * NT), (a.M + 63) / 64);
+  hipLaunchKernelGGL((k_gemm<NT, TRANSB>), grid, dim3(256), 0, st, a);
   DPAMD_LAUNCH_CHECK();
 }
 
+// Widest column tile (fewest A-fragment reloads) that still gives at least two
+// blocks per CU; N is a multiple of 16 (checked at model load).
 template <bool TRANSB>
 static void gemm(hipStream_t st, const GemmArgs& a) {
   if (a.M <= 0) return;
-  if (a.N % 80 == 0) gemm_bn<80, TRANSB>(st, a);
-  else if (a.N % 64 == 0) gemm_bn<64, TRANSB>(st, a);
-  else gemm_bn<16, TRANSB>(st, a);
+  const long rows = (a.M + 63) / 64;
+  const int tiles = a.N / 16;
+  const int cand[6] = {16, 15, 10, 5, 4, 1};
+  int nt = 1;
+  for (int k = 0; k < 6; ++k) {
+    if (tiles % cand[k]) continue;
+    nt = cand[k];
+    if (rows * (tiles / cand[k]) >= 512) break;
+  }
+  switch (nt) {
+    case 16: gemm_nt<16, TRANSB>(st, a); break;
+    case 15: gemm_nt<15, TRANSB>(st, a); break;
+    case 10: gemm_nt<10, TRANSB>(st, a); break;
+    case 5: gemm_nt<5, TRANSB>(st, a); break;
+    case 4: gemm_nt<4, TRANSB>(st, a); break;
+    default: gemm_nt<1, TRANSB>(st, a); break;
+  }
 }
 
 void launch_fitting(hipStream_t st, const FitNet& net, int rows, const double* D,
@@ -197,8 +288,10 @@ void launch_fitting(hipStream_t st, const FitNet& net, int rows, const double* D
 void launch_dT(hipStream_t st, int nloc, int L3, int axis, const int* items, const double* T,
                const double* dD, double* dT) {
   if (nloc <= 0) return;
-  const size_t bytes = sizeof(double) * (4 * L3 + L3 * axis);
-  hipLaunchKernelGGL(k_dT, dim3(nloc), dim3(256), bytes, st, L3, axis, items, T, dD, dT);
+  if (axis != 16 || L3 > 128 || L3 % 4 != 0)
+    throw HipError{hipErrorInvalidValue, "dE/dT kernel needs axis 16 and L3 <= 128"};
+  hipLaunchKernelGGL(k_dT, dim3((nloc + kDtWaves - 1) / kDtWaves), dim3(kDtWaves * 64), 0, st,
+                     nloc, L3, items, T, dD, dT);
   DPAMD_LAUNCH_CHECK();
 }
 

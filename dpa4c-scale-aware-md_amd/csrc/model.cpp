@@ -68,13 +68,15 @@ std::string parse_model(const unsigned char* buf, size_t len, ModelHost& m) {
   if (!r.ok) return "model file truncated in header";
   if (!(m.rcut > 0) || !(m.rcut_smth >= 0) || !(m.rcut_smth < m.rcut))
     return "need 0 <= rcut_smth < rcut";
+  if (!(m.rcut < 16.0)) return "rcut must be below 16 A";
   for (int t = 0; t < m.ntypes; ++t)
     if (m.sel[t] <= 0) return "sel entries must be positive";
   const int L1 = m.emb[0], L2 = m.emb[1], L3 = m.emb[2];
   if (!emb_supported(L1, L2, L3))
     return "embedding widths " + std::to_string(L1) + "-" + std::to_string(L2) + "-" +
            std::to_string(L3) + " not compiled (supported: 25-50-100, 32-64-128)";
-  if (m.axis < 1 || m.axis > L3) return "axis must be in [1, L3]";
+  if (m.axis < 1 || m.axis > L3 || m.axis > 64 || (m.axis & (m.axis - 1)) != 0)
+    return "axis must be a power of two <= min(64, L3)";
   const int Dn = L3 * m.axis;
   for (int k = 0; k < 3; ++k)
     if (m.fit[k] <= 0 || m.fit[k] % 16 != 0) return "fitting widths must be multiples of 16";

@@ -140,30 +140,47 @@ __global__ void k_cell_scatter(int nall, const int* __restrict__ cell_of,
 // (type, r2, j) and placed in their type section.
 constexpr int kNlWaves = 4;
 
-struct NlLds {
-  double r2[kNlWaves][kMaxCand];
-  int j[kNlWaves][kMaxCand];
-  int t[kNlWaves][kMaxCand];
+// Sort key: (type, r2) packed into one unsigned 64-bit integer whose order is
+// the lexicographic order of the pair: r2 is positive, so its IEEE bits are
+// monotone; offset by bits(2^-64) they fit in 59 bits for r2 < 256 (rcut < 16
+// is enforced at model load) and the type goes above them. Ties (equal type
+// and r2) are broken by the neighbour index j, as in the oracle.
+struct NlKey {
+  unsigned long long key;
+  int j;
+  int t;
 };
 
-__device__ __forceinline__ void nl_push(bool keep, double r2, int j, int t, int& n, double* s_r2,
-                                        int* s_j, int* s_t) {
+struct NlLds {
+  NlKey k[kNlWaves][kMaxCand];
+};
+
+__device__ __forceinline__ unsigned long long nl_pack(int t, double r2) {
+  const unsigned long long lo = 0x3BF0000000000000ull;  // bits of 2^-64
+  unsigned long long b = (unsigned long long)__double_as_longlong(r2);
+  b = b > lo ? b - lo : 0ull;
+  return ((unsigned long long)t << 59) | b;
+}
+
+__device__ __forceinline__ void nl_push(bool keep, double r2, int j, int t, int& n, NlKey* s) {
   const unsigned long long m = __ballot(keep);
   const int lane = threadIdx.x & 63;
   const int before = __popcll(m & ((1ull << lane) - 1ull));
   if (keep) {
     const int q = n + before;
     if (q < kMaxCand) {
-      s_r2[q] = r2;
-      s_j[q] = j;
-      s_t[q] = t;
+      NlKey e;
+      e.key = nl_pack(t, r2);
+      e.j = j;
+      e.t = t;
+      s[q] = e;
     }
   }
   n += __popcll(m);
 }
 
-__device__ void nl_place(const NlParams& np, int i, int n, const double* s_r2, const int* s_j,
-                         const int* s_t, int* __restrict__ nlist, int* __restrict__ nreal,
+__device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s,
+                         int* __restrict__ nlist, int* __restrict__ nreal,
                          int* __restrict__ status) {
   const int lane = threadIdx.x & 63;
   if (n > kMaxCand) {
@@ -177,24 +194,30 @@ __device__ void nl_place(const NlParams& np, int i, int n, const double* s_r2, c
   for (int t = 0; t < kMaxTypes; ++t) cnt[t] = 0;
   for (int base = 0; base < n; base += kWave) {
     const int q = base + lane;
-    const int tq = q < n ? s_t[q] : -1;
+    const int tq = q < n ? s[q].t : -1;
 #pragma unroll
     for (int t = 0; t < kMaxTypes; ++t) cnt[t] += __popcll(__ballot(tq == t));
   }
+  int first[kMaxTypes];  // candidates of lower types
+  int acc = 0;
+#pragma unroll
+  for (int t = 0; t < kMaxTypes; ++t) {
+    first[t] = acc;
+    acc += cnt[t];
+  }
   for (int q = lane; q < n; q += kWave) {
-    const int tq = s_t[q], jq = s_j[q];
-    const double rq = s_r2[q];
+    const NlKey e = s[q];
     int rank = 0;
     for (int p = 0; p < n; ++p) {
-      const double rp = s_r2[p];
-      const bool before = (s_t[p] == tq) && (rp < rq || (rp == rq && s_j[p] < jq));
-      rank += before ? 1 : 0;
+      const NlKey o = s[p];
+      rank += (o.key < e.key || (o.key == e.key && o.j < e.j)) ? 1 : 0;
     }
-    if (rank < np.sel[tq]) row[np.sec[tq] + rank] = jq;
+    rank -= first[e.t];
+    if (rank < np.sel[e.t]) row[np.sec[e.t] + rank] = e.j;
   }
   for (int t = 0; t < np.ntypes; ++t) {
     const int kept = cnt[t] < np.sel[t] ? cnt[t] : np.sel[t];
-    for (int s = np.sec[t] + kept + lane; s < np.sec[t + 1]; s += kWave) row[s] = -1;
+    for (int sl = np.sec[t] + kept + lane; sl < np.sec[t + 1]; sl += kWave) row[sl] = -1;
     if (lane == 0) nreal[(long)i * np.ntypes + t] = kept;
   }
 }
@@ -248,12 +271,12 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells(
             r2 = dx * dx + dy * dy + dz * dz;
             keep = (j != i) && t >= 0 && t < np.ntypes && r2 <= np.rc2;
           }
-          nl_push(keep, r2, j, t, n, lds.r2[w], lds.j[w], lds.t[w]);
+          nl_push(keep, r2, j, t, n, lds.k[w]);
         }
       }
     }
   }
-  nl_place(np, i, n, lds.r2[w], lds.j[w], lds.t[w], nlist, nreal, status);
+  nl_place(np, i, n, lds.k[w], nlist, nreal, status);
 }
 
 // LAMMPS front end: candidates come from the caller's full list (CSR by centre).
@@ -287,9 +310,9 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_csr(
       r2 = dx * dx + dy * dy + dz * dz;
       keep = (j != i) && t >= 0 && t < np.ntypes && r2 <= np.rc2;
     }
-    nl_push(keep, r2, j, t, n, lds.r2[w], lds.j[w], lds.t[w]);
+    nl_push(keep, r2, j, t, n, lds.k[w]);
   }
-  nl_place(np, i, n, lds.r2[w], lds.j[w], lds.t[w], nlist, nreal, status);
+  nl_place(np, i, n, lds.k[w], nlist, nreal, status);
 }
 
 // ---------------------------------------------------------------------------
