@@ -75,7 +75,7 @@ struct dp_model {
   Buf coord_in, atype_in, sfrac, flags, gpos, ext, ext_type, mapping, cell_of, cell_count,
       cell_start, cell_cursor, sorted, nlist, nreal, cand_off, cand, items, Tsec, T, D, dD, dT,
       fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_cursor, rev, force_ws, av_ws,
-      ae_ws, partials, out10, status, scan_tmp;
+      ae_ws, partials, out10, status, scan_tmp, act;
   size_t bytes_now = 0, bytes_peak = 0;
   // type buckets
   std::vector<int> atype_cache;
@@ -100,7 +100,7 @@ struct dp_model {
             &nreal,    &cand_off, &cand,      &items,    &Tsec,       &T,         &D,
             &dD,       &dT,       &fitb,      &e_bucket, &edge_grad,  &cpart,     &rev_count,
             &rev_off,  &rev_cursor, &rev,     &force_ws, &av_ws,      &ae_ws,     &partials,
-            &out10,    &status,   &scan_tmp};
+            &out10,    &status,   &scan_tmp, &act};
   }
 };
 
@@ -299,6 +299,17 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
   ea.dT = dT;
   ea.edge_grad = edge_grad;
   ea.cpart = cpart;
+  {
+    int acc = 0;
+    for (int t = 0; t < nt; ++t) {
+      ea.tile_off[t] = acc;
+      acc += (m.sel[t] + 15) / 16;
+    }
+    ea.tile_off[nt] = acc;
+    ea.tiles_per_atom = acc;
+    const size_t blk = 16 * (size_t)(M->el.L2P + M->el.L3P);
+    ea.act = need<double>(M, M->act, (size_t)std::max(nloc, 1) * acc * blk);
+  }
   auto block_table = [&](int waves) {
     int acc = 0;
     for (int p = 0; p < nt * nt; ++p) {
@@ -366,6 +377,7 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
   nblk = block_table(embed_waves_bwd(M->el));
   launch_embed_bwd(st, M->el, ea, nblk);
   record(M, st, kStEmbBwd + 1);
+  launch_center_sum(st, nloc, nt, nnei, nlist, ext, edge_grad, cpart);
 
   // reverse list + gather
   const long nedge = (long)nloc * nnei;

@@ -3,9 +3,8 @@
 //
 // Work unit: one wave owns one (centre i, neighbour section tj) item and walks
 // its real slots in tiles of 16; a workgroup holds the padded weights of one
-// (ti, tj) net in LDS and serves WAVES items of that pair. G is never written
-// to HBM: the forward kernel contracts each tile into T on the fly and the
-// backward kernel recomputes it.
+// (ti, tj) net in LDS and serves WAVES items of that pair. G itself is never
+// written to HBM: the forward kernel contracts each tile into T on the fly.
 //
 // Forward, per tile (lane = 16g + c, slot column c):
 //   env row R (fp64) -> s = R[0]
@@ -17,12 +16,14 @@
 //      from an LDS copy of X2
 //   T[m][f] += sum_slots R[slot][m] G[slot][f] on VALU, lane-local, reduced
 //      over the 4 lane groups once per item.
-// Backward, per tile: layers 1-3 all transposed for the primal and the
-//   forward-mode tangent dG/ds (same weight fragments, two MFMA chains), then
-//   u = dT.G and v = dT.G' as lane-partial dot products; the layer-3 residual
-//   enters through a folded dT (dT[f'] + dT[f'+L2]) against X2 itself, so no
-//   residual is materialised. dE/dR = u/nnei, dE/ds = R.v/nnei, and the edge
-//   gradient g = sum_m dE/dR_m dR_m/dd is written per slot.
+// The forward also saves tanh of layers 2 and 3 (per tile of 16 slots, in the
+// backward's register order) so the backward does not recompute the primal.
+// Backward, per tile: layer 1 recomputed (elementwise), then the forward-mode
+//   tangent dG/ds through layers 2 and 3 (transposed MFMAs), then u = dT.G and
+//   v = dT.G' as lane-partial dot products; the layer-3 residual enters
+//   through a folded dT (dT[f'] + dT[f'+L2]) against X2 itself, so no residual
+//   is materialised. dE/dR = u/nnei, dE/ds = R.v/nnei, and the edge gradient
+//   g = sum_m dE/dR_m dR_m/dd is written per slot.
 //
 // Reference analogs: the tabulated radial + PairFiLM embedding analog
 // include/dpa_chain/graph_compress.cuh:91-154, the per-row moment accumulation
@@ -143,8 +144,14 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
   double Tacc[S::NU3 * 4];
 #pragma unroll
   for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0;
+  constexpr int BLK = 16 * (S::L2P + S::L3P);
+  double* act = a.act + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
 
-  for (int tile = 0; tile < nr; tile += 16) {
+  // per-lane bases: layer 2 element (t, r) at act2[(4t + r) * 64], layer 3
+  // element (u, r) of slot g + 4r at act3[256u + 16r]
+  double* act2 = act + c * 4 + g;
+  double* act3 = act + 16 * S::L2P + (c >> 2) * 64 + g * 4 + (c & 3);
+  for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
     const int slot = tile + c;
     double Rn[4] = {0.0, 0.0, 0.0, 0.0};
     if (slot < nr) {
@@ -182,6 +189,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int f = 16 * t + 4 * r + g;
         const double th = tanh_fast(acc2[t][r] + P[S::OFF_B2 + f]);
+        act2[(4 * t + r) * 64] = th;
         double res = 0.0;
         if constexpr (S::RES2 != 0) {
           if constexpr (S::X1_ALIGNED) {
@@ -222,7 +230,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int sl = g + 4 * r;
-            double G = tanh_fast(acc3[uu][r] + P[S::OFF_B3 + f]);
+            const double th = tanh_fast(acc3[uu][r] + P[S::OFF_B3 + f]);
+            // backward order: feature 16u + 4(c>>2) + (c&3) of slot sl
+            act3[256 * u + 16 * r] = th;
+            double G = th;
             if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
             if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
 #pragma unroll
@@ -279,6 +290,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   const double* avg = a.envp + p * 8;
   const double* sd = avg + 4;
   const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
+  constexpr int BLK = 16 * (S::L2P + S::L3P);
+  const double* act = a.act + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
 
   {
     const double* dTi = a.dT + (long)i * 4 * S::L3;
@@ -298,24 +311,55 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   }
   wave_lds_sync();
 
-  double fc[3] = {0.0, 0.0, 0.0};
-  double vc[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  const double* act2 = act + c * 4 + g;  // element (t, r) at act2[64 (4t + r)]
+  const double* act3 = act2 + 16 * S::L2P;  // element (u, r) at act3[256u + 64r]
+  // software pipeline: the saved activations and the neighbour coordinates of
+  // tile k+1 are loaded while tile k is computed (one wave per SIMD, so the
+  // registers for a whole tile in flight are available)
+  double nth2[S::NT2][4], nth3[S::NU3][4];
+  double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
+  auto prefetch = [&](int tile, const double* p2, const double* p3) {
+#pragma unroll
+    for (int t = 0; t < S::NT2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) nth2[t][r] = p2[(4 * t + r) * 64];
+#pragma unroll
+    for (int u = 0; u < S::NU3; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) nth3[u][r] = p3[256 * u + 64 * r];
+    if (tile + c < nr) {
+      const long j = row[tile + c];
+      nx0 = a.ext[3 * j];
+      nx1 = a.ext[3 * j + 1];
+      nx2 = a.ext[3 * j + 2];
+    }
+  };
+  if (nr > 0) prefetch(0, act2, act3);
 
-  for (int tile = 0; tile < nr; tile += 16) {
+  for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
     const int slot = tile + c;
     const bool valid = slot < nr;
+    double th2[S::NT2][4], th3[S::NU3][4];
+#pragma unroll
+    for (int t = 0; t < S::NT2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) th2[t][r] = nth2[t][r];
+#pragma unroll
+    for (int u = 0; u < S::NU3; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) th3[u][r] = nth3[u][r];
     double d0 = 0.0, d1 = 0.0, d2 = 0.0;
     double Rn[4] = {0.0, 0.0, 0.0, 0.0};
     if (valid) {
-      const long j = row[slot];
-      d0 = a.ext[3 * j] - xi;
-      d1 = a.ext[3 * j + 1] - yi;
-      d2 = a.ext[3 * j + 2] - zi;
+      d0 = nx0 - xi;
+      d1 = nx1 - yi;
+      d2 = nx2 - zi;
       env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
     }
+    if (tile + 16 < nr) prefetch(tile + 16, act2 + BLK, act3 + BLK);
     const double s = Rn[0];
 
-    // layer 1 and its tangent
+    // layer 1 (recomputed, elementwise) and its tangent
     double x1[S::NQ2], x1t[S::NQ2];
 #pragma unroll
     for (int q = 0; q < S::NQ2; ++q) {
@@ -330,21 +374,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         x1t[q] = 0.0;
       }
     }
-    // layer 2, transposed, primal + tangent sharing the weight fragment
-    d4 acc2[S::NT2], acc2t[S::NT2];
+    // layer 2: tangent product only; tanh of the primal comes from the forward
+    d4 acc2t[S::NT2];
 #pragma unroll
-    for (int t = 0; t < S::NT2; ++t) {
-      acc2[t] = d4{0.0, 0.0, 0.0, 0.0};
-      acc2t[t] = d4{0.0, 0.0, 0.0, 0.0};
-    }
+    for (int t = 0; t < S::NT2; ++t) acc2t[t] = d4{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int q = 0; q < S::NQ2; ++q) {
 #pragma unroll
-      for (int t = 0; t < S::NT2; ++t) {
-        const double wa = P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c];
-        acc2[t] = mfma_f64(wa, x1[q], acc2[t]);
-        acc2t[t] = mfma_f64(wa, x1t[q], acc2t[t]);
-      }
+      for (int t = 0; t < S::NT2; ++t)
+        acc2t[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1t[q], acc2t[t]);
     }
     double x2[S::NT2][4], x2t[S::NT2][4];
 #pragma unroll
@@ -352,7 +390,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int f = 16 * t + 4 * r + g;
-        const double th = tanh_fast(acc2[t][r] + P[S::OFF_B2 + f]);
+        const double th = th2[t][r];
         double res = 0.0, rest = 0.0;
         if constexpr (S::RES2 != 0) {
           if constexpr (S::X1_ALIGNED) {
@@ -374,7 +412,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         x2t[t][r] = live ? rest + (1.0 - th * th) * acc2t[t][r] : 0.0;
       }
     }
-    // u = dT.G, v = dT.G' : residual part through the folded dT against X2
+    // u = dT.G, v = dT.G': residual part through the folded dT against X2
     double up[4] = {0.0, 0.0, 0.0, 0.0}, vp[4] = {0.0, 0.0, 0.0, 0.0};
     if constexpr (S::RES3 != 0) {
 #pragma unroll
@@ -390,20 +428,19 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
           }
         }
     }
-    // layer 3, transposed; tanh part of G and of G'
-#pragma unroll 1
+    // layer 3 tangent, transposed; tanh part of G from the forward
+#pragma unroll
     for (int u0 = 0; u0 < S::NU3; u0 += 2) {
-      d4 acc3[2] = {d4{0.0, 0.0, 0.0, 0.0}, d4{0.0, 0.0, 0.0, 0.0}};
+      // keep the scheduler from hoisting later tile pairs' weight loads
+      __builtin_amdgcn_sched_barrier(0);
       d4 acc3t[2] = {d4{0.0, 0.0, 0.0, 0.0}, d4{0.0, 0.0, 0.0, 0.0}};
 #pragma unroll
       for (int q = 0; q < S::NQ3; ++q) {
 #pragma unroll
         for (int uu = 0; uu < 2; ++uu)
-          if (u0 + uu < S::NU3) {
-            const double wa = P[S::OFF_W3 + (4 * q + g) * S::L3P + 16 * (u0 + uu) + c];
-            acc3[uu] = mfma_f64(wa, x2[q / 4][q % 4], acc3[uu]);
-            acc3t[uu] = mfma_f64(wa, x2t[q / 4][q % 4], acc3t[uu]);
-          }
+          if (u0 + uu < S::NU3)
+            acc3t[uu] = mfma_f64(P[S::OFF_W3 + (4 * q + g) * S::L3P + 16 * (u0 + uu) + c],
+                                 x2t[q / 4][q % 4], acc3t[uu]);
       }
 #pragma unroll
       for (int uu = 0; uu < 2; ++uu) {
@@ -412,7 +449,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int f = 16 * u + 4 * r + g;
-            const double th = tanh_fast(acc3[uu][r] + P[S::OFF_B3 + f]);
+            const double th = th3[u][r];
             const double tt = (1.0 - th * th) * acc3t[uu][r];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
@@ -442,13 +479,6 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       eg[0] = gv[0];
       eg[1] = gv[1];
       eg[2] = gv[2];
-      const double dd[3] = {d0, d1, d2};
-#pragma unroll
-      for (int cc = 0; cc < 3; ++cc) {
-        fc[cc] += gv[cc];
-#pragma unroll
-        for (int e = 0; e < 3; ++e) vc[3 * cc + e] -= gv[cc] * dd[e];
-      }
     }
   }
   // padded slots carry no gradient
@@ -457,20 +487,6 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     eg[0] = 0.0;
     eg[1] = 0.0;
     eg[2] = 0.0;
-  }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-#pragma unroll
-    for (int q = 0; q < 3; ++q) fc[q] += shfl_xor_d(fc[q], off);
-#pragma unroll
-    for (int q = 0; q < 9; ++q) vc[q] += shfl_xor_d(vc[q], off);
-  }
-  if (lane == 0) {
-    double* out = a.cpart + ((long)i * a.ntypes + tj) * 12;
-#pragma unroll
-    for (int q = 0; q < 3; ++q) out[q] = fc[q];
-#pragma unroll
-    for (int q = 0; q < 9; ++q) out[3 + q] = vc[q];
   }
 }
 

@@ -108,6 +108,45 @@ __global__ __launch_bounds__(kGatherWaves * 64) void k_force_gather(
   }
 }
 
+// Centre side of every edge: sum_slots g (force on the centre) and
+// sum_slots -g (x) (x_j - x_i) (frame virial), one wave per centre, written to
+// section 0 of cpart (the other sections stay zero).
+__global__ __launch_bounds__(kGatherWaves * 64) void k_center_sum(
+    int nloc, int ntypes, int nnei, const int* __restrict__ nlist, const double* __restrict__ ext,
+    const double* __restrict__ edge_grad, double* __restrict__ cpart) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = blockIdx.x * kGatherWaves + w;
+  if (i >= nloc) return;
+  const double xi = ext[3 * (long)i], yi = ext[3 * (long)i + 1], zi = ext[3 * (long)i + 2];
+  double f[3] = {0.0, 0.0, 0.0};
+  double v[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  for (int sl = lane; sl < nnei; sl += 64) {
+    const long e = (long)i * nnei + sl;
+    const long j = nlist[e];
+    if (j < 0) continue;
+    const double g[3] = {edge_grad[3 * e], edge_grad[3 * e + 1], edge_grad[3 * e + 2]};
+    const double d[3] = {ext[3 * j] - xi, ext[3 * j + 1] - yi, ext[3 * j + 2] - zi};
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      f[a] += g[a];
+#pragma unroll
+      for (int b = 0; b < 3; ++b) v[3 * a + b] -= g[a] * d[b];
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) f[q] += shfl_xor_d(f[q], off);
+#pragma unroll
+    for (int q = 0; q < 9; ++q) v[q] += shfl_xor_d(v[q], off);
+  }
+  if (lane == 0) {
+    double* out = cpart + (long)i * ntypes * 12;
+    for (int q = 0; q < 3; ++q) out[q] = f[q];
+    for (int q = 0; q < 9; ++q) out[3 + q] = v[q];
+  }
+}
+
 constexpr int kRedBlocks = 256;
 
 // Stage 1: block b sums energies of bucket positions and centre virials of
@@ -179,6 +218,15 @@ void launch_force_gather(hipStream_t st, int ntarget, int nloc, int ntypes, int 
   hipLaunchKernelGGL(k_force_gather, dim3((ntarget + kGatherWaves - 1) / kGatherWaves),
                      dim3(kGatherWaves * 64), 0, st, ntarget, nloc, ntypes, nnei, rev_off, rev,
                      nlist, ext, edge_grad, cpart, force, atom_virial, status);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_center_sum(hipStream_t st, int nloc, int ntypes, int nnei, const int* nlist,
+                       const double* ext, const double* edge_grad, double* cpart) {
+  if (nloc <= 0) return;
+  hipLaunchKernelGGL(k_center_sum, dim3((nloc + kGatherWaves - 1) / kGatherWaves),
+                     dim3(kGatherWaves * 64), 0, st, nloc, ntypes, nnei, nlist, ext, edge_grad,
+                     cpart);
   DPAMD_LAUNCH_CHECK();
 }
 

@@ -54,7 +54,14 @@ struct EmbArgs {
   double* Tsec;        // forward out [nloc][ntypes][4][L3]
   const double* dT;    // backward in [nloc][4][L3]
   double* edge_grad;   // backward out [nloc][nnei][3]
-  double* cpart;       // backward out [nloc][ntypes][12]: centre force 3 + virial 9
+  double* cpart;       // [nloc][ntypes][12]: centre force 3 + virial 9 (section 0 used)
+  // Saved activations: per (centre, tile of 16 slots) a block of
+  // 16*(L2P + L3P) doubles holding tanh of layers 2 and 3 in the backward's
+  // register order; tiles of section tj start at tile_off[tj], tiles_per_atom
+  // in total per centre.
+  double* act;
+  int tile_off[kMaxTypes + 1];
+  int tiles_per_atom;
 };
 
 struct DescArgs {
@@ -128,6 +135,8 @@ void launch_force_gather(hipStream_t, int ntarget, int nloc, int ntypes, int nne
                          const int* rev_off, const int* rev, const int* nlist, const double* ext,
                          const double* edge_grad, const double* cpart, double* force,
                          double* atom_virial, int* status);
+void launch_center_sum(hipStream_t, int nloc, int ntypes, int nnei, const int* nlist,
+                       const double* ext, const double* edge_grad, double* cpart);
 void launch_reduce_ev(hipStream_t, int nbucket, int nloc, int ntypes,
                       const double* atom_energy_bucket, const double* cpart, double* partials,
                       double* out10);
