@@ -104,6 +104,9 @@ __device__ __forceinline__ int find_pair(const EmbArgs& a) {
   return p;
 }
 
+// layer-3 output tiles per group: independent MFMA accumulation chains in flight
+constexpr int kU3 = 4;
+
 template <class S>
 constexpr int fwd_lds_doubles(int waves) {
   return (S::SIZE + 31) / 32 * 32 + waves * 16 * (S::L2P + 2) + waves * 64;
@@ -151,13 +154,23 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
   // element (u, r) of slot g + 4r at act3[256u + 16r]
   double* act2 = act + c * 4 + g;
   double* act3 = act + 16 * S::L2P + (c >> 2) * 64 + g * 4 + (c & 3);
+  // neighbour coordinates of the next tile are fetched during this one
+  double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
+  if (c < nr) {
+    const long j = row[c];
+    nx0 = a.ext[3 * j];
+    nx1 = a.ext[3 * j + 1];
+    nx2 = a.ext[3 * j + 2];
+  }
   for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
     const int slot = tile + c;
     double Rn[4] = {0.0, 0.0, 0.0, 0.0};
-    if (slot < nr) {
-      const long j = row[slot];
-      env_value(a.ext[3 * j] - xi, a.ext[3 * j + 1] - yi, a.ext[3 * j + 2] - zi, a.rcut_smth,
-                a.rcut, avg, sd, Rn);
+    if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, avg, sd, Rn);
+    if (slot + 16 < nr) {
+      const long j = row[slot + 16];
+      nx0 = a.ext[3 * j];
+      nx1 = a.ext[3 * j + 1];
+      nx2 = a.ext[3 * j + 2];
     }
     if (g == 0) {
 #pragma unroll
@@ -211,19 +224,22 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     wave_lds_sync();
     // layer 3, non-transposed, two output tiles at a time
 #pragma unroll
-    for (int u0 = 0; u0 < S::NU3; u0 += 2) {
-      d4 acc3[2] = {d4{0.0, 0.0, 0.0, 0.0}, d4{0.0, 0.0, 0.0, 0.0}};
+    for (int u0 = 0; u0 < S::NU3; u0 += kU3) {
+      __builtin_amdgcn_sched_barrier(0);
+      d4 acc3[kU3];
+#pragma unroll
+      for (int uu = 0; uu < kU3; ++uu) acc3[uu] = d4{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
       for (int q = 0; q < S::NQ3; ++q) {
         const double av = x2[q / 4][q % 4];
 #pragma unroll
-        for (int uu = 0; uu < 2; ++uu)
+        for (int uu = 0; uu < kU3; ++uu)
           if (u0 + uu < S::NU3)
             acc3[uu] = mfma_f64(av, P[S::OFF_W3 + (4 * q + g) * S::L3P + 16 * (u0 + uu) + c],
                                 acc3[uu]);
       }
 #pragma unroll
-      for (int uu = 0; uu < 2; ++uu) {
+      for (int uu = 0; uu < kU3; ++uu) {
         const int u = u0 + uu;
         if (u < S::NU3) {
           const int f = 16 * u + c;
@@ -430,20 +446,22 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     }
     // layer 3 tangent, transposed; tanh part of G from the forward
 #pragma unroll
-    for (int u0 = 0; u0 < S::NU3; u0 += 2) {
-      // keep the scheduler from hoisting later tile pairs' weight loads
+    for (int u0 = 0; u0 < S::NU3; u0 += kU3) {
+      // keep the scheduler from hoisting later tile groups' weight loads
       __builtin_amdgcn_sched_barrier(0);
-      d4 acc3t[2] = {d4{0.0, 0.0, 0.0, 0.0}, d4{0.0, 0.0, 0.0, 0.0}};
+      d4 acc3t[kU3];
+#pragma unroll
+      for (int uu = 0; uu < kU3; ++uu) acc3t[uu] = d4{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
       for (int q = 0; q < S::NQ3; ++q) {
 #pragma unroll
-        for (int uu = 0; uu < 2; ++uu)
+        for (int uu = 0; uu < kU3; ++uu)
           if (u0 + uu < S::NU3)
             acc3t[uu] = mfma_f64(P[S::OFF_W3 + (4 * q + g) * S::L3P + 16 * (u0 + uu) + c],
                                  x2t[q / 4][q % 4], acc3t[uu]);
       }
 #pragma unroll
-      for (int uu = 0; uu < 2; ++uu) {
+      for (int uu = 0; uu < kU3; ++uu) {
         const int u = u0 + uu;
         if (u < S::NU3) {
 #pragma unroll
