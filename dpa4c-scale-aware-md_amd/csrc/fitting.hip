@@ -46,43 +46,47 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   __shared__ double Bs[2][BK * BLD];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+  // element offsets of this thread's share of a K chunk, fixed over chunks
+  int offA[NA], ldsA[NA], offB[NB], ldsB[NB];
+#pragma unroll
+  for (int u = 0; u < NA; ++u) {
+    const int q = tid + 256 * u, r = q / BK, kk = q % BK, gr = row0 + r;
+    offA[u] = gr < a.M ? gr * a.lda + kk : -1;
+    ldsA[u] = r * ALD + kk;
+  }
+#pragma unroll
+  for (int u = 0; u < NB; ++u) {
+    const int q = tid + 256 * u;
+    if (q < BK * BN) {
+      if (!TRANSB) {
+        const int kk = q / BN, n = q % BN;
+        offB[u] = kk * a.ldb + col0 + n;
+        ldsB[u] = kk * BLD + n;
+      } else {
+        const int n = q / BK, kk = q % BK;
+        offB[u] = (col0 + n) * a.ldb + kk;
+        ldsB[u] = kk * BLD + n;
+      }
+    } else {
+      offB[u] = -1;
+      ldsB[u] = 0;
+    }
+  }
   double ra[NA], rb[NB];
   auto fetch = [&](int k0) {
+    const double* Ak = a.A + k0;
+    const double* Bk = TRANSB ? a.B + k0 : a.B + (long)k0 * a.ldb;
 #pragma unroll
-    for (int u = 0; u < NA; ++u) {
-      const int q = tid + 256 * u, r = q / BK, kk = q % BK, gr = row0 + r;
-      ra[u] = gr < a.M ? a.A[(long)gr * a.lda + k0 + kk] : 0.0;
-    }
+    for (int u = 0; u < NA; ++u) ra[u] = offA[u] >= 0 ? Ak[offA[u]] : 0.0;
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int q = tid + 256 * u;
-      double v = 0.0;
-      if (q < BK * BN) {
-        if (!TRANSB) {
-          const int kk = q / BN, n = q % BN;
-          v = a.B[(long)(k0 + kk) * a.ldb + col0 + n];
-        } else {
-          const int n = q / BK, kk = q % BK;
-          v = a.B[(long)(col0 + n) * a.ldb + k0 + kk];
-        }
-      }
-      rb[u] = v;
-    }
+    for (int u = 0; u < NB; ++u) rb[u] = offB[u] >= 0 ? Bk[offB[u]] : 0.0;
   };
   auto stash = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < NA; ++u) {
-      const int q = tid + 256 * u;
-      As[buf][(q / BK) * ALD + q % BK] = ra[u];
-    }
+    for (int u = 0; u < NA; ++u) As[buf][ldsA[u]] = ra[u];
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      const int q = tid + 256 * u;
-      if (q < BK * BN) {
-        if (!TRANSB) Bs[buf][(q / BN) * BLD + q % BN] = rb[u];
-        else Bs[buf][(q % BK) * BLD + q / BK] = rb[u];
-      }
-    }
+    for (int u = 0; u < NB; ++u)
+      if (offB[u] >= 0) Bs[buf][ldsB[u]] = rb[u];
   };
   d4 acc[NT];
 #pragma unroll
@@ -221,28 +225,18 @@ static void gemm_nt(hipStream_t st, const GemmArgs& a) {
   DPAMD_LAUNCH_CHECK();
 }
 
-// Widest column tile (fewest A-fragment reloads) that still gives at least two
-// blocks per CU; N is a multiple of 16 (checked at model load).
+// Column tile: the widest of 8, 5, 4 or 1 MFMA tiles dividing N, which keeps
+// the register footprint low enough for two or more waves per SIMD (the
+// barrier per K chunk is then covered by the other waves); N is a multiple of
+// 16 (checked at model load).
 template <bool TRANSB>
 static void gemm(hipStream_t st, const GemmArgs& a) {
   if (a.M <= 0) return;
-  const long rows = (a.M + 63) / 64;
   const int tiles = a.N / 16;
-  const int cand[6] = {16, 15, 10, 5, 4, 1};
-  int nt = 1;
-  for (int k = 0; k < 6; ++k) {
-    if (tiles % cand[k]) continue;
-    nt = cand[k];
-    if (rows * (tiles / cand[k]) >= 512) break;
-  }
-  switch (nt) {
-    case 16: gemm_nt<16, TRANSB>(st, a); break;
-    case 15: gemm_nt<15, TRANSB>(st, a); break;
-    case 10: gemm_nt<10, TRANSB>(st, a); break;
-    case 5: gemm_nt<5, TRANSB>(st, a); break;
-    case 4: gemm_nt<4, TRANSB>(st, a); break;
-    default: gemm_nt<1, TRANSB>(st, a); break;
-  }
+  if (tiles % 8 == 0) gemm_nt<8, TRANSB>(st, a);
+  else if (tiles % 5 == 0) gemm_nt<5, TRANSB>(st, a);
+  else if (tiles % 4 == 0) gemm_nt<4, TRANSB>(st, a);
+  else gemm_nt<1, TRANSB>(st, a);
 }
 
 void launch_fitting(hipStream_t st, const FitNet& net, int rows, const double* D,
