@@ -143,6 +143,8 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3, 4])
     ap.add_argument("--secondary", type=int, default=1, help="second config reported alongside (-1: none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0,
+                    help="only copy this many bytes device-to-device twice (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build evaluates on one GPU; --gpus above 1 is not "
@@ -155,6 +157,13 @@ def main():
     if hip.device_count() < 1:
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
+    if args.copy_probe:
+        a, b = hip.DeviceArray(nbytes=args.copy_probe), hip.DeviceArray(nbytes=args.copy_probe)
+        for _ in range(2):
+            hip.copy_d2d(b, a, args.copy_probe)
+        hip.synchronize()
+        print(json.dumps({"copy_probe_bytes": args.copy_probe}))
+        return
 
     main_r = run_config(dp, hip, args.config, args.steps, args.warmup)
     n = main_r["n"]
@@ -165,16 +174,25 @@ def main():
     dom = max(kernel_stages, key=lambda k: main_r["stage_ms"].get(k, 0.0))
     kind, amount = main_r["work"][dom]
     t_dom = main_r["stage_ms"][dom] * 1e-3
+    # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # (profiles/cu131k_hbm_traffic.md); only valid for the configuration measured
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "hbm_traffic_cu131k.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tdoc = json.load(f)
+        if tdoc.get("config") == args.config:
+            traffic = tdoc.get("bytes", {}).get(dom)
     if kind == "flop":
         ach = amount / t_dom / 1e12
         roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
                 "peak": PEAK_FP64_MFMA / 1e12, "unit": "TFLOP/s",
-                "frac": round(ach * 1e12 / PEAK_FP64_MFMA, 4), "traffic": None,
+                "frac": round(ach * 1e12 / PEAK_FP64_MFMA, 4), "traffic": traffic,
                 "algorithmic_per_launch": amount, "avg_launch_ms": round(t_dom * 1e3, 4)}
     else:
         ach = amount / t_dom / 1e9
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": 8000.0,
-                "unit": "GB/s", "frac": round(ach * 1e9 / PEAK_HBM, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(ach * 1e9 / PEAK_HBM, 4), "traffic": traffic,
                 "algorithmic_per_launch": amount, "avg_launch_ms": round(t_dom * 1e3, 4)}
     out = {
         "metric": "us/step/atom (1 MI355X, se_e2_a fp64 energy+force+virial)",

@@ -59,6 +59,10 @@ def synchronize():
     check(hip().hipDeviceSynchronize())
 
 
+def copy_d2d(dst: "DeviceArray", src: "DeviceArray", nbytes: int):
+    check(hip().hipMemcpy(dst.ptr, src.ptr, nbytes, D2D))
+
+
 class DeviceArray:
     """A device allocation holding a copy of a numpy array's bytes."""
 
