@@ -104,8 +104,10 @@ __device__ __forceinline__ int find_pair(const EmbArgs& a) {
   return p;
 }
 
-// layer-3 output tiles per group: independent MFMA accumulation chains in flight
+// layer-3 output tiles per group: independent MFMA accumulation chains in
+// flight (the forward runs two waves per SIMD, the backward one)
 constexpr int kU3 = 4;
+constexpr int kU3B = 8;
 
 template <class S>
 constexpr int fwd_lds_doubles(int waves) {
@@ -154,7 +156,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
   // element (u, r) of slot g + 4r at act3[256u + 16r]
   double* act2 = act + c * 4 + g;
   double* act3 = act + 16 * S::L2P + (c >> 2) * 64 + g * 4 + (c & 3);
-  // neighbour coordinates of the next tile are fetched during this one
+  // Neighbour coordinates of tile k+1 are fetched during tile k, from an index
+  // loaded during tile k-1: the memory counter is in order, so no wait on a
+  // load ever has to cover the activation stores issued after it.
   double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
   if (c < nr) {
     const long j = row[c];
@@ -162,16 +166,17 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     nx1 = a.ext[3 * j + 1];
     nx2 = a.ext[3 * j + 2];
   }
+  int jn = 16 + c < nr ? row[16 + c] : 0;
   for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
     const int slot = tile + c;
     double Rn[4] = {0.0, 0.0, 0.0, 0.0};
     if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, avg, sd, Rn);
     if (slot + 16 < nr) {
-      const long j = row[slot + 16];
-      nx0 = a.ext[3 * j];
-      nx1 = a.ext[3 * j + 1];
-      nx2 = a.ext[3 * j + 2];
+      nx0 = a.ext[3 * (long)jn];
+      nx1 = a.ext[3 * (long)jn + 1];
+      nx2 = a.ext[3 * (long)jn + 2];
     }
+    jn = slot + 32 < nr ? row[slot + 32] : 0;
     if (g == 0) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) Rs[c * 4 + m] = Rn[m];
@@ -229,14 +234,23 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       d4 acc3[kU3];
 #pragma unroll
       for (int uu = 0; uu < kU3; ++uu) acc3[uu] = d4{0.0, 0.0, 0.0, 0.0};
+      double wcur[kU3], wnxt[kU3];
+      const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
+#pragma unroll
+      for (int uu = 0; uu < kU3; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
 #pragma unroll
       for (int q = 0; q < S::NQ3; ++q) {
+        if (q + 1 < S::NQ3) {
+#pragma unroll
+          for (int uu = 0; uu < kU3; ++uu)
+            wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
+        }
         const double av = x2[q / 4][q % 4];
 #pragma unroll
         for (int uu = 0; uu < kU3; ++uu)
-          if (u0 + uu < S::NU3)
-            acc3[uu] = mfma_f64(av, P[S::OFF_W3 + (4 * q + g) * S::L3P + 16 * (u0 + uu) + c],
-                                acc3[uu]);
+          if (u0 + uu < S::NU3) acc3[uu] = mfma_f64(av, wcur[uu], acc3[uu]);
+#pragma unroll
+        for (int uu = 0; uu < kU3; ++uu) wcur[uu] = wnxt[uu];
       }
 #pragma unroll
       for (int uu = 0; uu < kU3; ++uu) {
@@ -332,9 +346,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   // software pipeline: the saved activations and the neighbour coordinates of
   // tile k+1 are loaded while tile k is computed (one wave per SIMD, so the
   // registers for a whole tile in flight are available)
+  // Activations and neighbour coordinates of tile k+1 are fetched during tile
+  // k; the neighbour index is loaded one tile earlier still, so the
+  // coordinate loads never wait behind the activation loads (the memory
+  // counter is in order).
   double nth2[S::NT2][4], nth3[S::NU3][4];
   double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
+  int jn = 0;
   auto prefetch = [&](int tile, const double* p2, const double* p3) {
+    if (tile + c < nr) {
+      nx0 = a.ext[3 * (long)jn];
+      nx1 = a.ext[3 * (long)jn + 1];
+      nx2 = a.ext[3 * (long)jn + 2];
+    }
+    jn = tile + 16 + c < nr ? row[tile + 16 + c] : 0;
 #pragma unroll
     for (int t = 0; t < S::NT2; ++t)
 #pragma unroll
@@ -343,13 +368,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     for (int u = 0; u < S::NU3; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) nth3[u][r] = p3[256 * u + 64 * r];
-    if (tile + c < nr) {
-      const long j = row[tile + c];
-      nx0 = a.ext[3 * j];
-      nx1 = a.ext[3 * j + 1];
-      nx2 = a.ext[3 * j + 2];
-    }
   };
+  jn = c < nr ? row[c] : 0;
   if (nr > 0) prefetch(0, act2, act3);
 
   for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
@@ -446,22 +466,32 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     }
     // layer 3 tangent, transposed; tanh part of G from the forward
 #pragma unroll
-    for (int u0 = 0; u0 < S::NU3; u0 += kU3) {
+    for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
       // keep the scheduler from hoisting later tile groups' weight loads
       __builtin_amdgcn_sched_barrier(0);
-      d4 acc3t[kU3];
+      d4 acc3t[kU3B];
 #pragma unroll
-      for (int uu = 0; uu < kU3; ++uu) acc3t[uu] = d4{0.0, 0.0, 0.0, 0.0};
+      for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = d4{0.0, 0.0, 0.0, 0.0};
+      // weight fragments double-buffered one k-step ahead of the MFMAs
+      double wcur[kU3B], wnxt[kU3B];
+      const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
+#pragma unroll
+      for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
 #pragma unroll
       for (int q = 0; q < S::NQ3; ++q) {
+        if (q + 1 < S::NQ3) {
 #pragma unroll
-        for (int uu = 0; uu < kU3; ++uu)
-          if (u0 + uu < S::NU3)
-            acc3t[uu] = mfma_f64(P[S::OFF_W3 + (4 * q + g) * S::L3P + 16 * (u0 + uu) + c],
-                                 x2t[q / 4][q % 4], acc3t[uu]);
+          for (int uu = 0; uu < kU3B; ++uu)
+            wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
+        }
+#pragma unroll
+        for (int uu = 0; uu < kU3B; ++uu)
+          if (u0 + uu < S::NU3) acc3t[uu] = mfma_f64(wcur[uu], x2t[q / 4][q % 4], acc3t[uu]);
+#pragma unroll
+        for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = wnxt[uu];
       }
 #pragma unroll
-      for (int uu = 0; uu < kU3; ++uu) {
+      for (int uu = 0; uu < kU3B; ++uu) {
         const int u = u0 + uu;
         if (u < S::NU3) {
 #pragma unroll
