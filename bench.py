@@ -8,11 +8,13 @@ neighbour list, env matrix + embedding + descriptor, fitting net forward and
 input gradient, embedding backward, force / virial gather and reductions.
 
 Prints ONE JSON line. `value` is microseconds per step per atom on the
-131,072-atom FCC Cu system (config 2) unless --config says otherwise; the
-12,288-atom water system (config 1) is measured in the same run and reported
-under "secondary". The roofline object describes the dominant kernel, timed
-with HIP events on the stream it runs on; the CPU baseline is the repository's
-fp64 CPU restatement (oracle/) timed on a bounded sample of centres.
+131,072-atom FCC Cu system (config 2, fp64) unless --config says otherwise;
+the 12,288-atom water system (config 1, fp64) and the 128,000-atom HEA
+(config 3, mixed precision: fp32 nets on FP32 MFMA, fp64 env matrix, forces
+and virial) are measured in the same run and reported under "secondary". The
+roofline object describes the dominant kernel, timed with HIP events on the
+stream it runs on; the CPU baseline is the repository's fp64 CPU restatement
+(oracle/) timed on a bounded sample of centres.
 """
 from __future__ import annotations
 
@@ -27,8 +29,16 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 PEAK_FP64_MFMA = 78.6e12   # FLOP/s, MI355X dense FP64 matrix
 PEAK_HBM = 8.0e12          # B/s
+PEAK_FP32_MFMA = 157.3e12  # FLOP/s, MI355X dense FP32 matrix
 DT_FS = {0: 0.5, 1: 0.5, 2: 1.0, 3: 1.0, 4: 0.5}
 KIND = {0: "water", 1: "water", 2: "cu", 3: "hea", 4: "water"}
+# config 3 is specified in mixed precision (fp32 nets, fp64 env/force/virial)
+MIXED = {3}
+WORKLOAD = {2: "cu131k FCC Cu 131,072 atoms, rcut 8, sel 138, 32-64-128/240x3",
+            1: "water12k 12,288 atoms, rcut 6, sel [46,92], 25-50-100/240x3",
+            0: "water192", 3: "hea128k BCC 4-type HEA 128,000 atoms, rcut 6, sel 4x40, "
+                              "32-64-128/240x3, mixed precision",
+            4: "water393k 393,216 atoms, rcut 6, sel [46,92], 25-50-100/240x3"}
 
 
 def flops_bytes(pot, n_real, nloc, nb_edges):
@@ -58,7 +68,10 @@ def run_config(dp, hip, config, steps, warmup):
     coord, atype, box = dp.systems.build(config)
     n = len(atype)
     mb = dp.model.to_bytes(dp.model.random_model(KIND[config], seed=1000 + config))
-    pot = dp.DeepPot(file_content=mb, gpu_rank=0)
+    mixed = config in MIXED
+    pot = dp.DeepPot(file_content=mb, gpu_rank=0,
+                     precision=dp.PREC_MIXED if mixed else dp.PREC_FP64)
+    peak_mfma = PEAK_FP32_MFMA if mixed else PEAK_FP64_MFMA
     d_coord = hip.DeviceArray(coord.astype("float64"))
     d_atype = hip.DeviceArray(atype.astype("int32"))
     d_e = hip.DeviceArray(nbytes=8)
@@ -98,12 +111,13 @@ def run_config(dp, hip, config, steps, warmup):
             kind, amount = work[k]
             if kind == "flop":
                 entry.update(tflops=round(amount / (t * 1e-3) / 1e12, 3),
-                             frac=round(amount / (t * 1e-3) / PEAK_FP64_MFMA, 4))
+                             frac=round(amount / (t * 1e-3) / peak_mfma, 4))
             else:
                 entry.update(gbs=round(amount / (t * 1e-3) / 1e9, 1),
                              frac=round(amount / (t * 1e-3) / PEAK_HBM, 4))
         stages[k] = entry
     return dict(n=n, ms=ms, stage_ms=stage_ms, stages=stages, work=work, n_real=n_real,
+                mixed=mixed, peak_mfma=peak_mfma,
                 energy=float(energy), max_abs_fsum=float(abs(force.sum(0)).max()),
                 device_bytes=pot.device_bytes(), mb=mb, coord=coord, atype=atype, box=box)
 
@@ -141,7 +155,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3, 4])
-    ap.add_argument("--secondary", type=int, default=1, help="second config reported alongside (-1: none)")
+    ap.add_argument("--secondary", default="1,3",
+                    help="comma-separated configs reported alongside (-1: none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only copy this many bytes device-to-device twice (HBM counter calibration)")
@@ -185,9 +200,10 @@ def main():
             traffic = tdoc.get("bytes", {}).get(dom)
     if kind == "flop":
         ach = amount / t_dom / 1e12
+        peak = main_r["peak_mfma"]
         roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
-                "peak": PEAK_FP64_MFMA / 1e12, "unit": "TFLOP/s",
-                "frac": round(ach * 1e12 / PEAK_FP64_MFMA, 4), "traffic": traffic,
+                "peak": peak / 1e12, "unit": "TFLOP/s",
+                "frac": round(ach * 1e12 / peak, 4), "traffic": traffic,
                 "algorithmic_per_launch": amount, "avg_launch_ms": round(t_dom * 1e3, 4)}
     else:
         ach = amount / t_dom / 1e9
@@ -205,25 +221,28 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64",
+        "dtype": "f32 nets / f64 env, force, virial" if main_r["mixed"] else "f64",
         "data": "synthetic (seeded lattice + jitter, seeded random-init weights)",
-        "config": {"workload": {2: "cu131k FCC Cu 131,072 atoms, rcut 8, sel 138, 32-64-128/240x3",
-                                1: "water12k 12,288 atoms, rcut 6, sel [46,92], 25-50-100/240x3",
-                                0: "water192", 3: "hea128k", 4: "water393k"}[args.config],
-                   "atoms": n, "dt_fs": DT_FS[args.config]},
+        "config": {"workload": WORKLOAD[args.config], "atoms": n, "dt_fs": DT_FS[args.config]},
         "ns_per_day": round(ns_day, 4),
         "roofline": roof,
         "stages": main_r["stages"],
         "device_bytes_peak": main_r["device_bytes"],
     }
-    if args.secondary >= 0 and args.secondary != args.config:
-        s = run_config(dp, hip, args.secondary, args.steps, args.warmup)
-        out["secondary"] = {"config": args.secondary, "atoms": s["n"],
-                            "us_per_step_atom": round(s["ms"] * 1e3 / s["n"], 5),
-                            "ms_per_step": round(s["ms"], 4),
-                            "ns_per_day": round(DT_FS[args.secondary] * 1e-6 * 86400.0 /
-                                                (s["ms"] * 1e-3), 4),
-                            "stages": s["stages"]}
+    secondary = [int(x) for x in str(args.secondary).split(",") if x.strip()]
+    secondary = [c for c in secondary if c >= 0 and c != args.config]
+    if secondary:
+        out["secondary"] = []
+    for cfg in secondary:
+        s = run_config(dp, hip, cfg, args.steps, args.warmup)
+        out["secondary"].append({
+            "config": cfg, "workload": WORKLOAD[cfg], "atoms": s["n"],
+            "precision": "mixed" if s["mixed"] else "fp64",
+            "us_per_step_atom": round(s["ms"] * 1e3 / s["n"], 5),
+            "ms_per_step": round(s["ms"], 4),
+            "ns_per_day": round(DT_FS[cfg] * 1e-6 * 86400.0 / (s["ms"] * 1e-3), 4),
+            "stages": s["stages"]})
+        del s
     if not args.no_cpu_baseline:
         cb = cpu_baseline(main_r["mb"], main_r["coord"], main_r["atype"], main_r["box"])
         cb["gpu_speedup"] = round(cb["value"] / us_atom, 1)

@@ -25,6 +25,7 @@
 #include <fstream>
 #include <iterator>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/dp_amd.h"
@@ -64,11 +65,12 @@ struct dp_model {
   ModelHost host;
   EmbLayout el{};
   std::string err;
-  // device parameters
-  double* d_emb = nullptr;
+  // device parameters; the nets (d_emb, d_fit) are double in fp64 mode and
+  // float in mixed mode, env statistics and the padded-slot constant are fp64
+  void* d_emb = nullptr;
   double* d_envp = nullptr;
   double* d_tpad = nullptr;
-  double* d_fit = nullptr;
+  void* d_fit = nullptr;
   FitOffsets fo{};
   // workspace
   std::vector<Buf*> bufs;
@@ -253,8 +255,10 @@ struct Outputs {
 };
 
 // Everything after the neighbour list; ext/ext_type/nlist/nreal/mapping ready.
-void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_mapping,
-               int ntarget, const Outputs& out) {
+template <class E>
+void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_mapping,
+                 int ntarget, const Outputs& out) {
+  constexpr bool f32 = sizeof(E) == 4;
   const ModelHost& m = M->host;
   const int nt = m.ntypes, nnei = m.nnei, L3 = m.emb[2], axis = m.axis, Dn = L3 * axis;
   const int nb = M->nbucket;
@@ -264,13 +268,13 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
   const int* items = static_cast<const int*>(M->items.p);
   int* status = static_cast<int*>(M->status.p);
 
-  double* Tsec = need<double>(M, M->Tsec, (size_t)nloc * nt * 4 * L3);
-  double* T = need<double>(M, M->T, (size_t)nloc * 4 * L3);
-  double* D = need<double>(M, M->D, (size_t)std::max(nb, 1) * Dn);
-  double* dD = need<double>(M, M->dD, (size_t)std::max(nb, 1) * Dn);
-  double* dT = need<double>(M, M->dT, (size_t)nloc * 4 * L3);
+  E* Tsec = need<E>(M, M->Tsec, (size_t)nloc * nt * 4 * L3);
+  E* T = need<E>(M, M->T, (size_t)nloc * 4 * L3);
+  E* D = need<E>(M, M->D, (size_t)std::max(nb, 1) * Dn);
+  E* dD = need<E>(M, M->dD, (size_t)std::max(nb, 1) * Dn);
+  E* dT = need<E>(M, M->dT, (size_t)nloc * 4 * L3);
   const int Fmax = std::max(m.fit[0], std::max(m.fit[1], m.fit[2]));
-  double* fitb = need<double>(M, M->fitb, (size_t)8 * std::max(nb, 1) * Fmax);
+  E* fitb = need<E>(M, M->fitb, (size_t)8 * std::max(nb, 1) * Fmax);
   double* e_bucket = need<double>(M, M->e_bucket, (size_t)std::max(nb, 1));
   double* edge_grad = need<double>(M, M->edge_grad, (size_t)nloc * nnei * 3);
   double* cpart = need<double>(M, M->cpart, (size_t)nloc * nt * 12);
@@ -308,7 +312,7 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
     ea.tile_off[nt] = acc;
     ea.tiles_per_atom = acc;
     const size_t blk = 16 * (size_t)(M->el.L2P + M->el.L3P);
-    ea.act = need<double>(M, M->act, (size_t)std::max(nloc, 1) * acc * blk);
+    ea.act = need<E>(M, M->act, (size_t)std::max(nloc, 1) * acc * blk);
   }
   auto block_table = [&](int waves) {
     int acc = 0;
@@ -322,8 +326,8 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
     return acc;
   };
 
-  int nblk = block_table(embed_waves_fwd(M->el));
-  launch_embed_fwd(st, M->el, ea, nblk);
+  int nblk = block_table(embed_waves_fwd(M->el, f32));
+  launch_embed_fwd(st, M->el, ea, nblk, f32);
   record(M, st, kStEmbFwd + 1);
 
   DescArgs da{};
@@ -341,14 +345,14 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
   da.tpad = M->d_tpad;
   da.T = T;
   da.D = D;
-  launch_descriptor(st, da);
+  launch_descriptor(st, da, f32);
   record(M, st, kStDescr + 1);
 
   for (int t = 0; t < nt; ++t) {
     const int rows = M->type_off[t + 1] - M->type_off[t];
     if (rows <= 0) continue;
-    const double* P = M->d_fit + (size_t)t * m.fit_block;
-    FitNet net{};
+    const E* P = static_cast<const E*>(M->d_fit) + (size_t)t * m.fit_block;
+    FitNet<E> net{};
     const int ins[3] = {Dn, m.fit[0], m.fit[1]};
     for (int k = 0; k < 3; ++k) {
       net.L[k].W = P + M->fo.W[k];
@@ -362,9 +366,9 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
     net.bias = m.bias[t];
     const size_t r0 = (size_t)M->type_off[t];
     const size_t slab = (size_t)std::max(nb, 1) * Fmax;
-    FitBufs fb{};
-    double* base = fitb;
-    double** slots[8] = {&fb.H0, &fb.T1, &fb.H1, &fb.T2, &fb.H2, &fb.dZa, &fb.dZb, &fb.dH};
+    FitBufs<E> fb{};
+    E* base = fitb;
+    E** slots[8] = {&fb.H0, &fb.T1, &fb.H1, &fb.T2, &fb.H2, &fb.dZa, &fb.dZb, &fb.dH};
     // slab q holds [rows][F] of every type back to back; F <= Fmax
     for (int q = 0; q < 8; ++q) *slots[q] = base + q * slab + r0 * (size_t)Fmax;
     launch_fitting(st, net, rows, D + r0 * Dn, fb, dD + r0 * Dn, e_bucket + r0);
@@ -374,8 +378,8 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
   launch_dT(st, nb, L3, axis, items, T, dD, dT);
   record(M, st, kStDT + 1);
 
-  nblk = block_table(embed_waves_bwd(M->el));
-  launch_embed_bwd(st, M->el, ea, nblk);
+  nblk = block_table(embed_waves_bwd(M->el, f32));
+  launch_embed_bwd(st, M->el, ea, nblk, f32);
   record(M, st, kStEmbBwd + 1);
   launch_center_sum(st, nloc, nt, nnei, nlist, ext, edge_grad, cpart);
 
@@ -410,6 +414,12 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
   }
   record(M, st, kStReduce + 1);
   (void)nall;
+}
+
+void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_mapping, int ntarget,
+               const Outputs& out) {
+  if (M->precision == DP_PREC_MIXED) run_model_t<float>(M, st, nloc, nall, d_mapping, ntarget, out);
+  else run_model_t<double>(M, st, nloc, nall, d_mapping, ntarget, out);
 }
 
 // Ghosts + cells + nlist for the standalone path. Returns nall.
@@ -535,8 +545,8 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
   *out = nullptr;
   dp_model* M = new dp_model();
   int rc = guarded(M, [&]() {
-    if (precision != DP_PREC_FP64)
-      throw ApiError{DP_ERR_ARG, "only DP_PREC_FP64 is implemented"};
+    if (precision != DP_PREC_FP64 && precision != DP_PREC_MIXED)
+      throw ApiError{DP_ERR_ARG, "precision must be DP_PREC_FP64 or DP_PREC_MIXED"};
     M->precision = precision;
     std::vector<unsigned char> buf;
     if (file_content && content_len) {
@@ -562,18 +572,30 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
       throw ApiError{DP_ERR_NO_GPU, std::string("device is ") + prop.gcnArchName +
                                         ", this library is built for gfx950"};
     const ModelHost& m = M->host;
-    M->el = make_emb_layout(m.emb[0], m.emb[1], m.emb[2]);
+    const bool mixed = precision == DP_PREC_MIXED;
+    M->el = make_emb_layout(m.emb[0], m.emb[1], m.emb[2], mixed);
     std::vector<double> emb, envp, tpad;
     pack_embedding(m, M->el, emb, envp, tpad);
-    auto upload = [&](double*& dst, const std::vector<double>& src) {
-      DPAMD_HIP(hipMalloc(&dst, std::max<size_t>(8, src.size() * 8)));
-      M->bytes_now += src.size() * 8;
-      DPAMD_HIP(hipMemcpy(dst, src.data(), src.size() * 8, hipMemcpyHostToDevice));
+    auto upload = [&](auto*& dst, const auto& src) {
+      const size_t bytes = src.size() * sizeof(src[0]);
+      void* p = nullptr;
+      DPAMD_HIP(hipMalloc(&p, std::max<size_t>(8, bytes)));
+      dst = static_cast<std::remove_reference_t<decltype(dst)>>(p);
+      M->bytes_now += bytes;
+      DPAMD_HIP(hipMemcpy(p, src.data(), bytes, hipMemcpyHostToDevice));
     };
-    upload(M->d_emb, emb);
     upload(M->d_envp, envp);
     upload(M->d_tpad, tpad);
-    upload(M->d_fit, m.fit_params);
+    if (mixed) {
+      // the nets are evaluated in fp32: round the parameters once here
+      const std::vector<float> emb32(emb.begin(), emb.end());
+      const std::vector<float> fit32(m.fit_params.begin(), m.fit_params.end());
+      upload(M->d_emb, emb32);
+      upload(M->d_fit, fit32);
+    } else {
+      upload(M->d_emb, emb);
+      upload(M->d_fit, m.fit_params);
+    }
     M->bytes_peak = M->bytes_now;
     M->fo = fit_offsets(m);
   });
@@ -588,13 +610,14 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
 
 void dp_destroy(dp_model* M) {
   if (!M) return;
-  hipSetDevice(M->device);
+  // teardown is best effort: errors here have nowhere to go
+  (void)hipSetDevice(M->device);
   for (Buf* b : M->bufs)
-    if (b->p) hipFree(b->p);
-  for (double* p : {M->d_emb, M->d_envp, M->d_tpad, M->d_fit})
-    if (p) hipFree(p);
+    if (b->p) (void)hipFree(b->p);
+  for (void* p : {M->d_emb, static_cast<void*>(M->d_envp), static_cast<void*>(M->d_tpad), M->d_fit})
+    if (p) (void)hipFree(p);
   for (auto& e : M->ev)
-    if (e) hipEventDestroy(e);
+    if (e) (void)hipEventDestroy(e);
   delete M;
 }
 
@@ -780,6 +803,7 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
     const ModelHost& m = M->host;
     const int nloc = M->last_nloc, nall = M->last_nall;
     const int Dn = m.emb[2] * m.axis;
+    const size_t net_esize = M->precision == DP_PREC_MIXED ? 4 : 8;
     auto copy = [&](const void* src, size_t bytes) {
       result = (long)bytes;
       if (dst && capacity && src) {
@@ -787,15 +811,21 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
         DPAMD_HIP(hipMemcpy(dst, src, std::min(bytes, capacity), hipMemcpyDeviceToHost));
       }
     };
-    // bucket-ordered arrays are returned in atom order
-    auto copy_bucket = [&](const void* src, size_t per_atom) {
+    // bucket-ordered arrays are returned in atom order, widened to fp64 when
+    // the mode keeps them in fp32 (esize 4)
+    auto copy_bucket = [&](const void* src, size_t per_atom, size_t esize) {
       const size_t bytes = (size_t)nloc * per_atom * sizeof(double);
       result = (long)bytes;
       if (!dst || !capacity || !src) return;
       std::vector<double> tmp((size_t)M->nbucket * per_atom);
       DPAMD_HIP(hipDeviceSynchronize());
-      if (!tmp.empty())
+      if (!tmp.empty() && esize == 8)
         DPAMD_HIP(hipMemcpy(tmp.data(), src, tmp.size() * 8, hipMemcpyDeviceToHost));
+      if (!tmp.empty() && esize == 4) {
+        std::vector<float> t32(tmp.size());
+        DPAMD_HIP(hipMemcpy(t32.data(), src, t32.size() * 4, hipMemcpyDeviceToHost));
+        std::copy(t32.begin(), t32.end(), tmp.begin());
+      }
       std::vector<double> outv((size_t)nloc * per_atom, 0.0);
       for (int p = 0; p < M->nbucket; ++p)
         std::memcpy(&outv[(size_t)M->items_h[p] * per_atom], &tmp[(size_t)p * per_atom],
@@ -810,9 +840,9 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
         if (!M->last_standalone) throw ApiError{DP_ERR_ARG, "no mapping on the LAMMPS path"};
         copy(M->mapping.p, (size_t)nall * 4);
         break;
-      case DP_STAGE_DESCRPT: copy_bucket(M->D.p, Dn); break;
-      case DP_STAGE_DEDD: copy_bucket(M->dD.p, Dn); break;
-      case DP_STAGE_ATOM_ENERGY: copy_bucket(M->e_bucket.p, 1); break;
+      case DP_STAGE_DESCRPT: copy_bucket(M->D.p, Dn, net_esize); break;
+      case DP_STAGE_DEDD: copy_bucket(M->dD.p, Dn, net_esize); break;
+      case DP_STAGE_ATOM_ENERGY: copy_bucket(M->e_bucket.p, 1, 8); break;
       case DP_STAGE_EDGE_GRAD: copy(M->edge_grad.p, (size_t)nloc * m.nnei * 24); break;
       default: throw ApiError{DP_ERR_ARG, "unknown stage"};
     }

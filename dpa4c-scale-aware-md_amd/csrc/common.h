@@ -45,6 +45,24 @@ __device__ __forceinline__ f4 mfma_f32(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ d4 mfma(double a, double b, d4 c) { return mfma_f64(a, b, c); }
+__device__ __forceinline__ f4 mfma(float a, float b, f4 c) { return mfma_f32(a, b, c); }
+
+// Accumulator type and output-row mapping of the 16x16x4 MFMA per element type:
+// register r of lane (g, c) holds D[row(g, r)][c].
+template <class T>
+struct Frag;
+template <>
+struct Frag<double> {
+  using V = d4;
+  static constexpr __host__ __device__ int row(int g, int r) { return g + 4 * r; }
+};
+template <>
+struct Frag<float> {
+  using V = f4;
+  static constexpr __host__ __device__ int row(int g, int r) { return 4 * g + r; }
+};
+
 // Make this wave's LDS writes visible to its own other lanes.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -53,6 +71,10 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 __device__ __forceinline__ double shfl_xor_d(double v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+
+__device__ __forceinline__ float shfl_xor_d(float v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
 

@@ -7,6 +7,10 @@
 // K2P = 4*ceil(L1/4) (k-steps of layer 2), L2P = 16*ceil(L2/16) (16-row
 // output tiles of layer 2), K3P = 4*ceil(L2/4), L3P = 16*ceil(L3/16).
 // Padding entries are zero, so padded features evaluate to tanh(0) = 0.
+// The fp32 kernels (F32) take the k-steps of layer 3 in the order the fp32
+// MFMA leaves layer 2 in registers (features 16t + 4g + r), which reaches
+// past K3P when L2 is not a multiple of 16, so their W3 has L2P rows
+// (K3P = L2P); the element type of the packed array is then float.
 #pragma once
 
 namespace dpamd {
@@ -17,7 +21,7 @@ struct EmbLayout {
   int off_w1, off_b1, off_w2, off_b2, off_w3, off_b3, size, stride;
 };
 
-inline EmbLayout make_emb_layout(int L1, int L2, int L3) {
+inline EmbLayout make_emb_layout(int L1, int L2, int L3, bool f32 = false) {
   EmbLayout e;
   e.L1 = L1;
   e.L2 = L2;
@@ -27,7 +31,7 @@ inline EmbLayout make_emb_layout(int L1, int L2, int L3) {
   e.NT2 = (L2 + 15) / 16;
   e.L2P = 16 * e.NT2;
   e.NQ3 = (L2 + 3) / 4;
-  e.K3P = 4 * e.NQ3;
+  e.K3P = f32 ? 16 * ((L2 + 15) / 16) : 4 * e.NQ3;
   e.NU3 = (L3 + 15) / 16;
   e.L3P = 16 * e.NU3;
   e.off_w1 = 0;
@@ -41,7 +45,7 @@ inline EmbLayout make_emb_layout(int L1, int L2, int L3) {
   return e;
 }
 
-template <int L1_, int L2_, int L3_>
+template <int L1_, int L2_, int L3_, bool F32 = false>
 struct EmbShape {
   static constexpr int L1 = L1_, L2 = L2_, L3 = L3_;
   static constexpr int NQ2 = (L1 + 3) / 4;
@@ -49,7 +53,7 @@ struct EmbShape {
   static constexpr int NT2 = (L2 + 15) / 16;
   static constexpr int L2P = 16 * NT2;
   static constexpr int NQ3 = (L2 + 3) / 4;
-  static constexpr int K3P = 4 * NQ3;
+  static constexpr int K3P = F32 ? L2P : 4 * NQ3;
   static constexpr int NU3 = (L3 + 15) / 16;
   static constexpr int L3P = 16 * NU3;
   static constexpr int OFF_W1 = 0;

@@ -31,78 +31,11 @@
 // amplitude instead of storing it" recompute backward
 // include/dpa_chain/graph_compress.cuh:9-10 and
 // deepmd-op/overlays/op/pt/dpa4c/graph_compress_kernel.cuh:1458-1466.
+#include "env.h"
 #include "fastmath.h"
 #include "kernels.h"
 
 namespace dpamd {
-
-struct EnvOut {
-  double R[4];
-};
-
-// spline5 switch and the normalised env row [sw/r, sw x/r^2, sw y/r^2, sw z/r^2].
-__device__ __forceinline__ void env_value(double d0, double d1, double d2, double rs, double rc,
-                                          const double* avg, const double* sd, double* Rn) {
-  const double r2 = d0 * d0 + d1 * d1 + d2 * d2;
-  const double r = sqrt(r2);
-  double sw;
-  if (r < rs) {
-    sw = 1.0;
-  } else if (r >= rc) {
-    sw = 0.0;
-  } else {
-    const double u = (r - rs) / (rc - rs);
-    const double u2 = u * u, u3 = u2 * u;
-    sw = u3 * (-6.0 * u2 + 15.0 * u - 10.0) + 1.0;
-  }
-  const double inv_r = 1.0 / r;
-  const double inv_r2 = inv_r * inv_r;
-  Rn[0] = (sw * inv_r - avg[0]) / sd[0];
-  Rn[1] = (sw * d0 * inv_r2 - avg[1]) / sd[1];
-  Rn[2] = (sw * d1 * inv_r2 - avg[2]) / sd[2];
-  Rn[3] = (sw * d2 * inv_r2 - avg[3]) / sd[3];
-}
-
-// Edge gradient g = sum_m nd[m] * d(Rn_m)/dd for one slot.
-__device__ __forceinline__ void env_grad(double d0, double d1, double d2, double rs, double rc,
-                                         const double* sd, const double* nd, double* gv) {
-  const double d[3] = {d0, d1, d2};
-  const double r2 = d0 * d0 + d1 * d1 + d2 * d2;
-  const double r = sqrt(r2);
-  double sw, dsw;
-  if (r < rs) {
-    sw = 1.0;
-    dsw = 0.0;
-  } else if (r >= rc) {
-    sw = 0.0;
-    dsw = 0.0;
-  } else {
-    const double u = (r - rs) / (rc - rs);
-    const double u2 = u * u, u3 = u2 * u;
-    sw = u3 * (-6.0 * u2 + 15.0 * u - 10.0) + 1.0;
-    dsw = (3.0 * u2 * (-6.0 * u2 + 15.0 * u - 10.0) + u3 * (-12.0 * u + 15.0)) / (rc - rs);
-  }
-  const double inv_r = 1.0 / r;
-  const double inv_r2 = inv_r * inv_r;
-  const double dR0_dr = dsw * inv_r - sw * inv_r2;
-  const double q = sw * inv_r2;
-  const double dq_dr = dsw * inv_r2 - 2.0 * sw * inv_r2 * inv_r;
-  const double w0 = nd[0] / sd[0];
-  const double w[3] = {nd[1] / sd[1], nd[2] / sd[2], nd[3] / sd[3]};
-  // sum_c w_c d_c, used by the radial part of R_1..3
-  const double wd = w[0] * d[0] + w[1] * d[1] + w[2] * d[2];
-#pragma unroll
-  for (int mm = 0; mm < 3; ++mm) {
-    const double ur = d[mm] * inv_r;
-    gv[mm] = w0 * dR0_dr * ur + w[mm] * q + wd * dq_dr * ur;
-  }
-}
-
-__device__ __forceinline__ int find_pair(const EmbArgs& a) {
-  int p = 0;
-  while (p + 1 < a.npair && (int)blockIdx.x >= a.block_off[p + 1]) ++p;
-  return p;
-}
 
 // layer-3 output tiles per group: independent MFMA accumulation chains in
 // flight (the forward runs two waves per SIMD, the backward one)
@@ -133,7 +66,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
   const int p = find_pair(a);
   const int ti = p / a.ntypes, tj = p % a.ntypes;
   {
-    const double* src = a.emb + (long)p * a.stride;
+    const double* src = static_cast<const double*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
   }
   __syncthreads();
@@ -150,7 +83,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
 #pragma unroll
   for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0;
   constexpr int BLK = 16 * (S::L2P + S::L3P);
-  double* act = a.act + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
+  double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
 
   // per-lane bases: layer 2 element (t, r) at act2[(4t + r) * 64], layer 3
   // element (u, r) of slot g + 4r at act3[256u + 16r]
@@ -282,7 +215,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     Tacc[q] = v;
   }
   if (g == 0) {
-    double* out = a.Tsec + ((long)i * a.ntypes + tj) * 4 * S::L3;
+    double* out = static_cast<double*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
 #pragma unroll
     for (int u = 0; u < S::NU3; ++u) {
       const int f = 16 * u + c;
@@ -307,7 +240,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   const int p = find_pair(a);
   const int ti = p / a.ntypes, tj = p % a.ntypes;
   {
-    const double* src = a.emb + (long)p * a.stride;
+    const double* src = static_cast<const double*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
   }
   __syncthreads();
@@ -321,10 +254,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   const double* sd = avg + 4;
   const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
   constexpr int BLK = 16 * (S::L2P + S::L3P);
-  const double* act = a.act + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
+  const double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
 
   {
-    const double* dTi = a.dT + (long)i * 4 * S::L3;
+    const double* dTi = static_cast<const double*>(a.dT) + (long)i * 4 * S::L3;
     for (int q = lane; q < 4 * S::L3P; q += 64) {
       const int m = q / S::L3P, f = q % S::L3P;
       dTs[q] = f < S::L3 ? dTi[m * S::L3 + f] : 0.0;
@@ -539,9 +472,13 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 }
 
 // T = (sum over sections of Tsec + padded-slot constant) / nnei, and
-// D = T^T T[:, :axis], written in bucket order for the fitting GEMMs.
+// D = T^T T[:, :axis], written in bucket order for the fitting GEMMs. E is the
+// element type of Tsec, T and D (double, or float in mixed mode); the sums are
+// formed in fp64 and rounded once.
+template <class E>
 __global__ __launch_bounds__(256) void k_descriptor(DescArgs a) {
   extern __shared__ double Ts[];
+  const E* Tsec = static_cast<const E*>(a.Tsec);
   const int pos = blockIdx.x;
   const int i = a.items[pos];
   const int ti = a.ext_type[i];
@@ -551,19 +488,19 @@ __global__ __launch_bounds__(256) void k_descriptor(DescArgs a) {
     for (int tj = 0; tj < a.ntypes; ++tj) {
       const long sec = (long)i * a.ntypes + tj;
       const double npad = (double)(a.sel[tj] - a.nreal[sec]);
-      v += a.Tsec[sec * 4 * L3 + q] + npad * a.tpad[((long)(ti * a.ntypes + tj)) * 4 * L3 + q];
+      v += (double)Tsec[sec * 4 * L3 + q] + npad * a.tpad[((long)(ti * a.ntypes + tj)) * 4 * L3 + q];
     }
-    v *= a.inv_nnei;
-    Ts[q] = v;
-    a.T[(long)i * 4 * L3 + q] = v;
+    const E t = (E)(v * a.inv_nnei);
+    Ts[q] = (double)t;
+    static_cast<E*>(a.T)[(long)i * 4 * L3 + q] = t;
   }
   __syncthreads();
   const int nd = L3 * a.axis;
-  double* D = a.D + (long)pos * nd;
+  E* D = static_cast<E*>(a.D) + (long)pos * nd;
   for (int q = threadIdx.x; q < nd; q += blockDim.x) {
     const int ai = q / a.axis, bi = q % a.axis;
-    D[q] = Ts[ai] * Ts[bi] + Ts[L3 + ai] * Ts[L3 + bi] + Ts[2 * L3 + ai] * Ts[2 * L3 + bi] +
-           Ts[3 * L3 + ai] * Ts[3 * L3 + bi];
+    D[q] = (E)(Ts[ai] * Ts[bi] + Ts[L3 + ai] * Ts[L3 + bi] + Ts[2 * L3 + ai] * Ts[2 * L3 + bi] +
+               Ts[3 * L3 + ai] * Ts[3 * L3 + bi]);
   }
 }
 
@@ -577,8 +514,8 @@ bool emb_supported(int L1, int L2, int L3) {
   return (L1 == 25 && L2 == 50 && L3 == 100) || (L1 == 32 && L2 == 64 && L3 == 128);
 }
 
-int embed_waves_fwd(const EmbLayout&) { return kFwdWaves; }
-int embed_waves_bwd(const EmbLayout&) { return kBwdWaves; }
+int embed_waves_fwd(const EmbLayout& e, bool f32) { return f32 ? embed_waves_fwd32(e) : kFwdWaves; }
+int embed_waves_bwd(const EmbLayout& e, bool f32) { return f32 ? embed_waves_bwd32(e) : kBwdWaves; }
 
 template <class S>
 static void fwd_impl(hipStream_t st, const EmbArgs& a, int nblocks) {
@@ -600,21 +537,28 @@ static void bwd_impl(hipStream_t st, const EmbArgs& a, int nblocks) {
   DPAMD_LAUNCH_CHECK();
 }
 
-void launch_embed_fwd(hipStream_t st, const EmbLayout& e, const EmbArgs& a, int nblocks) {
+void launch_embed_fwd(hipStream_t st, const EmbLayout& e, const EmbArgs& a, int nblocks,
+                      bool f32) {
   if (nblocks <= 0) return;
-  if (e.L1 == 25) fwd_impl<ShapeWater>(st, a, nblocks);
+  if (f32) launch_embed_fwd32(st, e, a, nblocks);
+  else if (e.L1 == 25) fwd_impl<ShapeWater>(st, a, nblocks);
   else fwd_impl<ShapeMetal>(st, a, nblocks);
 }
 
-void launch_embed_bwd(hipStream_t st, const EmbLayout& e, const EmbArgs& a, int nblocks) {
+void launch_embed_bwd(hipStream_t st, const EmbLayout& e, const EmbArgs& a, int nblocks,
+                      bool f32) {
   if (nblocks <= 0) return;
-  if (e.L1 == 25) bwd_impl<ShapeWater>(st, a, nblocks);
+  if (f32) launch_embed_bwd32(st, e, a, nblocks);
+  else if (e.L1 == 25) bwd_impl<ShapeWater>(st, a, nblocks);
   else bwd_impl<ShapeMetal>(st, a, nblocks);
 }
 
-void launch_descriptor(hipStream_t st, const DescArgs& a) {
+void launch_descriptor(hipStream_t st, const DescArgs& a, bool f32) {
   if (a.nloc <= 0) return;
-  hipLaunchKernelGGL(k_descriptor, dim3(a.nloc), dim3(256), sizeof(double) * 4 * a.L3, st, a);
+  if (f32)
+    hipLaunchKernelGGL(k_descriptor<float>, dim3(a.nloc), dim3(256), sizeof(double) * 4 * a.L3, st, a);
+  else
+    hipLaunchKernelGGL(k_descriptor<double>, dim3(a.nloc), dim3(256), sizeof(double) * 4 * a.L3, st, a);
   DPAMD_LAUNCH_CHECK();
 }
 

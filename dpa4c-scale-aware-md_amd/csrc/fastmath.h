@@ -1,5 +1,6 @@
-// fp64 hyperbolic tangent for the network kernels.
+// Hyperbolic tangent for the network kernels, fp64 and fp32.
 //
+// fp64:
 // Method (written from the mathematics, not from any vendor library):
 //   tanh(x) = sign(x) * E / (E + 2),  E = expm1(2|x|)
 //   expm1(y) = 2^n (expm1(r) + 1) - 1 with Cody-Waite reduction
@@ -13,6 +14,14 @@
 //     z <- z + z(1 - d z), quadratically convergent.
 // |x| is clamped at 20 (tanh(20) rounds to 1 in fp64). Measured error against
 // libm is a few ulp (tests/test_native.py).
+//
+// fp32 (mixed-precision nets): tanh|x| = 1 - 2 / (e^{2|x|} + 1) with the
+// hardware base-2 exponential and reciprocal (v_exp_f32, v_rcp_f32, each
+// about 1 ulp). The formula cancels near 0, so the error is absolute rather
+// than relative: at most 1.2e-7 against fp64 tanh over [-12, 12] when both
+// hardware operations are correctly rounded (checked on the host), the same
+// order as rounding an O(1) activation to fp32. e^{2|x|} overflows to +inf
+// for |x| > 44, which gives exactly 1.
 #pragma once
 
 #include <cmath>
@@ -60,5 +69,20 @@ DPAMD_HD inline double tanh_fast(double x) {
   z = fma(fma(-d, z, 1.0), z, z);
   return copysign(E * z, x);
 }
+
+DPAMD_HD inline float tanh_f32(float x) {
+  const float t = fabsf(x) * 2.8853900817779268f;  // 2|x| log2(e)
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float e = __builtin_amdgcn_exp2f(t);
+  const float y = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+#else
+  const float e = exp2f(t);
+  const float y = fmaf(-2.0f, 1.0f / (e + 1.0f), 1.0f);
+#endif
+  return copysignf(y, x);
+}
+
+DPAMD_HD inline double tanh_act(double x) { return tanh_fast(x); }
+DPAMD_HD inline float tanh_act(float x) { return tanh_f32(x); }
 
 }  // namespace dpamd

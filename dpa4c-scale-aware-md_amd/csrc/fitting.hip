@@ -1,7 +1,9 @@
 // Fitting net (D -> F0 -> F1 -> F2 -> 1, tanh, y = x + idt*tanh(xW+b) on
-// square layers) forward + input gradient on gfx950 FP64 MFMA, per centre
-// type over the atoms of that type (bucket order), and the descriptor
-// backward dE/dD -> dE/dT.
+// square layers) forward + input gradient on gfx950 MFMA, per centre type
+// over the atoms of that type (bucket order), and the descriptor backward
+// dE/dD -> dE/dT. Element type T: double (FP64 MFMA) in fp64 mode, float
+// (FP32 MFMA) in mixed mode; the per-atom energy is accumulated in fp64 in
+// both.
 //
 // Each layer is one GEMM (rows = atoms) with its elementwise work fused into
 // the epilogue: bias + tanh + residual in the forward, (dH_in + acc) * idt *
@@ -14,22 +16,23 @@
 
 namespace dpamd {
 
+template <class T>
 struct GemmArgs {
   int M, N, K;
-  const double* A;
+  const T* A;
   int lda;
-  const double* B;
+  const T* B;
   int ldb;
   int epi;  // 0 plain store, 1 forward layer, 2 backward layer
-  const double* bias;
-  const double* idt;
-  double* C;
+  const T* bias;
+  const T* idt;
+  T* C;
   int ldc;
-  double* T_out;       // forward: tanh part
-  const double* dHin;  // backward: incoming dH (row stride ld_dhin; 0 = broadcast)
+  T* T_out;       // forward: tanh part
+  const T* dHin;  // backward: incoming dH (row stride ld_dhin; 0 = broadcast)
   int ld_dhin;
-  double* dH_out;      // backward: dH of this layer
-  const double* Tk;    // backward: tanh part of this layer (ld = ldc)
+  T* dH_out;      // backward: dH of this layer
+  const T* Tk;    // backward: tanh part of this layer (ld = ldc)
 };
 
 // C = epi(A[MxK] B[KxN]); B(k,n) = TRANSB ? B[n*ldb + k] : B[k*ldb + n].
@@ -37,13 +40,13 @@ struct GemmArgs {
 // so one A fragment feeds NT MFMAs. K advances 16 at a time through two LDS
 // buffers: the next chunk is fetched into registers while the current one is
 // multiplied, then stored into the other buffer (one barrier per chunk).
-template <int NT, bool TRANSB>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
+template <class T, int NT, bool TRANSB>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
   constexpr int BM = 64, BK = 16, BN = 16 * NT;
   constexpr int ALD = BK + 1, BLD = BN + 1;
   constexpr int NA = BM * BK / 256, NB = (BK * BN + 255) / 256;
-  __shared__ double As[2][BM * ALD];
-  __shared__ double Bs[2][BK * BLD];
+  __shared__ T As[2][BM * ALD];
+  __shared__ T Bs[2][BK * BLD];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
   // element offsets of this thread's share of a K chunk, fixed over chunks
@@ -72,14 +75,14 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
       ldsB[u] = 0;
     }
   }
-  double ra[NA], rb[NB];
+  T ra[NA], rb[NB];
   auto fetch = [&](int k0) {
-    const double* Ak = a.A + k0;
-    const double* Bk = TRANSB ? a.B + k0 : a.B + (long)k0 * a.ldb;
+    const T* Ak = a.A + k0;
+    const T* Bk = TRANSB ? a.B + k0 : a.B + (long)k0 * a.ldb;
 #pragma unroll
-    for (int u = 0; u < NA; ++u) ra[u] = offA[u] >= 0 ? Ak[offA[u]] : 0.0;
+    for (int u = 0; u < NA; ++u) ra[u] = offA[u] >= 0 ? Ak[offA[u]] : T(0);
 #pragma unroll
-    for (int u = 0; u < NB; ++u) rb[u] = offB[u] >= 0 ? Bk[offB[u]] : 0.0;
+    for (int u = 0; u < NB; ++u) rb[u] = offB[u] >= 0 ? Bk[offB[u]] : T(0);
   };
   auto stash = [&](int buf) {
 #pragma unroll
@@ -88,9 +91,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     for (int u = 0; u < NB; ++u)
       if (offB[u] >= 0) Bs[buf][ldsB[u]] = rb[u];
   };
-  d4 acc[NT];
+  typename Frag<T>::V acc[NT];
 #pragma unroll
-  for (int n = 0; n < NT; ++n) acc[n] = d4{0.0, 0.0, 0.0, 0.0};
+  for (int n = 0; n < NT; ++n) acc[n] = typename Frag<T>::V{0, 0, 0, 0};
   fetch(0);
   stash(0);
   __syncthreads();
@@ -98,13 +101,13 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   for (int kc = 0; kc < nk; ++kc) {
     const int buf = kc & 1;
     if (kc + 1 < nk) fetch((kc + 1) * BK);
-    const double* Ab = As[buf] + (16 * w + c) * ALD;
-    const double* Bb = Bs[buf];
+    const T* Ab = As[buf] + (16 * w + c) * ALD;
+    const T* Bb = Bs[buf];
 #pragma unroll
     for (int q = 0; q < BK / 4; ++q) {
-      const double av = Ab[4 * q + g];
+      const T av = Ab[4 * q + g];
 #pragma unroll
-      for (int n = 0; n < NT; ++n) acc[n] = mfma_f64(av, Bb[(4 * q + g) * BLD + 16 * n + c], acc[n]);
+      for (int n = 0; n < NT; ++n) acc[n] = mfma(av, Bb[(4 * q + g) * BLD + 16 * n + c], acc[n]);
     }
     if (kc + 1 < nk) stash(buf ^ 1);
     __syncthreads();
@@ -114,21 +117,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int col = col0 + 16 * n + c;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = row0 + 16 * w + g + 4 * r;
+      const int row = row0 + 16 * w + Frag<T>::row(g, r);
       if (row >= a.M) continue;
       const long o = (long)row * a.ldc + col;
-      const double v = acc[n][r];
+      const T v = acc[n][r];
       if (a.epi == 0) {
         a.C[o] = v;
       } else if (a.epi == 1) {
-        const double t = tanh_fast(v + a.bias[col]);
+        const T t = tanh_act(v + a.bias[col]);
         if (a.T_out) a.T_out[o] = t;
         a.C[o] = a.idt ? a.A[(long)row * a.lda + col] + a.idt[col] * t : t;
       } else {
-        const double dh = v + (a.dHin ? a.dHin[(long)row * a.ld_dhin + col] : 0.0);
+        const T dh = v + (a.dHin ? a.dHin[(long)row * a.ld_dhin + col] : T(0));
         if (a.dH_out) a.dH_out[o] = dh;
-        const double tk = a.Tk[o];
-        a.C[o] = dh * (a.idt ? a.idt[col] : 1.0) * (1.0 - tk * tk);
+        const T tk = a.Tk[o];
+        a.C[o] = dh * (a.idt ? a.idt[col] : T(1)) * (T(1) - tk * tk);
       }
     }
   }
@@ -136,20 +139,20 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 
 // Energy head and the seed of the backward: e = h2.Wo + bo + bias,
 // dZ2 = Wo * idt2 * (1 - t2^2). One wave per atom row.
-__global__ __launch_bounds__(256) void k_head(int rows, int F2, const double* __restrict__ H2,
-                                              const double* __restrict__ T2,
-                                              const double* __restrict__ Wo,
-                                              const double* __restrict__ idt2, double bo,
-                                              double bias, double* __restrict__ e,
-                                              double* __restrict__ dZ2) {
+// The dot product is accumulated in fp64 for both element types.
+template <class T>
+__global__ __launch_bounds__(256) void k_head(int rows, int F2, const T* __restrict__ H2,
+                                              const T* __restrict__ T2, const T* __restrict__ Wo,
+                                              const T* __restrict__ idt2, double bo, double bias,
+                                              double* __restrict__ e, T* __restrict__ dZ2) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= rows) return;
   double acc = 0.0;
   for (int f = lane; f < F2; f += 64) {
     const long o = (long)row * F2 + f;
-    acc += H2[o] * Wo[f];
-    const double t = T2[o];
-    dZ2[o] = Wo[f] * (idt2 ? idt2[f] : 1.0) * (1.0 - t * t);
+    acc += (double)H2[o] * (double)Wo[f];
+    const T t = T2[o];
+    dZ2[o] = Wo[f] * (idt2 ? idt2[f] : T(1)) * (T(1) - t * t);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) acc += shfl_xor_d(acc, off);
@@ -163,32 +166,33 @@ __global__ __launch_bounds__(256) void k_head(int rows, int F2, const double* __
 // lane (g, c) accumulates dD[a][c] T[m][a] over its rows, then the 4 row groups
 // are folded (xor 16, 32); lane c then holds column c.
 constexpr int kDtWaves = 4;
+template <class T>
 __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
                                                      const int* __restrict__ items,
-                                                     const double* __restrict__ T,
-                                                     const double* __restrict__ dD,
-                                                     double* __restrict__ dT) {
+                                                     const T* __restrict__ Tm,
+                                                     const T* __restrict__ dD,
+                                                     T* __restrict__ dT) {
   constexpr int AX = 16;
-  __shared__ double Ts[kDtWaves][4 * 128];
+  __shared__ T Ts[kDtWaves][4 * 128];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int pos = blockIdx.x * kDtWaves + w;
   if (pos >= nb) return;
   const int i = items[pos];
-  const double* Ti = T + (long)i * 4 * L3;
+  const T* Ti = Tm + (long)i * 4 * L3;
   for (int q = lane; q < 4 * L3; q += 64) Ts[w][q] = Ti[q];
   wave_lds_sync();
-  const double* dDp = dD + (long)pos * L3 * AX;
-  double* out = dT + (long)i * 4 * L3;
-  const double tb0 = Ts[w][c], tb1 = Ts[w][L3 + c], tb2 = Ts[w][2 * L3 + c], tb3 = Ts[w][3 * L3 + c];
-  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+  const T* dDp = dD + (long)pos * L3 * AX;
+  T* out = dT + (long)i * 4 * L3;
+  const T tb0 = Ts[w][c], tb1 = Ts[w][L3 + c], tb2 = Ts[w][2 * L3 + c], tb3 = Ts[w][3 * L3 + c];
+  T s0 = 0, s1 = 0, s2 = 0, s3 = 0;
   for (int a0 = 0; a0 < L3; a0 += 4) {
     const int a = a0 + g;
-    const double v = dDp[a0 * AX + lane];
+    const T v = dDp[a0 * AX + lane];
     s0 += v * Ts[w][a];
     s1 += v * Ts[w][L3 + a];
     s2 += v * Ts[w][2 * L3 + a];
     s3 += v * Ts[w][3 * L3 + a];
-    double p0 = v * tb0, p1 = v * tb1, p2 = v * tb2, p3 = v * tb3;
+    T p0 = v * tb0, p1 = v * tb1, p2 = v * tb2, p3 = v * tb3;
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) {
       p0 += shfl_xor_d(p0, off);
@@ -197,7 +201,7 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
       p3 += shfl_xor_d(p3, off);
     }
     // row a: lane c == m writes component m (the second term is added below)
-    const double pm = c == 0 ? p0 : c == 1 ? p1 : c == 2 ? p2 : p3;
+    const T pm = c == 0 ? p0 : c == 1 ? p1 : c == 2 ? p2 : p3;
     if (c < 4 && a >= AX) out[c * L3 + a] = pm;
     if (c < 4 && a < AX) Ts[w][c * L3 + a] = pm;  // stash: T rows a < 16 no longer needed
   }
@@ -218,10 +222,10 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
   }
 }
 
-template <int NT, bool TRANSB>
-static void gemm_nt(hipStream_t st, const GemmArgs& a) {
+template <class T, int NT, bool TRANSB>
+static void gemm_nt(hipStream_t st, const GemmArgs<T>& a) {
   dim3 grid(a.N / (16 * NT), (a.M + 63) / 64);
-  hipLaunchKernelGGL((k_gemm<NT, TRANSB>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((k_gemm<T, NT, TRANSB>), grid, dim3(256), 0, st, a);
   DPAMD_LAUNCH_CHECK();
 }
 
@@ -229,64 +233,76 @@ static void gemm_nt(hipStream_t st, const GemmArgs& a) {
 // the register footprint low enough for two or more waves per SIMD (the
 // barrier per K chunk is then covered by the other waves); N is a multiple of
 // 16 (checked at model load).
-template <bool TRANSB>
-static void gemm(hipStream_t st, const GemmArgs& a) {
+template <bool TRANSB, class T>
+static void gemm(hipStream_t st, const GemmArgs<T>& a) {
   if (a.M <= 0) return;
   const int tiles = a.N / 16;
-  if (tiles % 8 == 0) gemm_nt<8, TRANSB>(st, a);
-  else if (tiles % 5 == 0) gemm_nt<5, TRANSB>(st, a);
-  else if (tiles % 4 == 0) gemm_nt<4, TRANSB>(st, a);
-  else gemm_nt<1, TRANSB>(st, a);
+  if (tiles % 8 == 0) gemm_nt<T, 8, TRANSB>(st, a);
+  else if (tiles % 5 == 0) gemm_nt<T, 5, TRANSB>(st, a);
+  else if (tiles % 4 == 0) gemm_nt<T, 4, TRANSB>(st, a);
+  else gemm_nt<T, 1, TRANSB>(st, a);
 }
 
-void launch_fitting(hipStream_t st, const FitNet& net, int rows, const double* D,
-                    const FitBufs& b, double* dD, double* e_bucket) {
+template <class T>
+void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D,
+                    const FitBufs<T>& b, T* dD, double* e_bucket) {
+  using G = GemmArgs<T>;
   if (rows <= 0) return;
   const int Dn = net.L[0].in, F0 = net.L[0].out, F1 = net.L[1].out, F2 = net.L[2].out;
-  GemmArgs g{};
+  G g{};
   // forward
-  g = GemmArgs{};
+  g = G{};
   g.M = rows; g.N = F0; g.K = Dn; g.A = D; g.lda = Dn; g.B = net.L[0].W; g.ldb = F0;
   g.epi = 1; g.bias = net.L[0].b; g.idt = nullptr; g.C = b.H0; g.ldc = F0;
   gemm<false>(st, g);
-  g = GemmArgs{};
+  g = G{};
   g.M = rows; g.N = F1; g.K = F0; g.A = b.H0; g.lda = F0; g.B = net.L[1].W; g.ldb = F1;
   g.epi = 1; g.bias = net.L[1].b; g.idt = net.L[1].idt; g.C = b.H1; g.ldc = F1; g.T_out = b.T1;
   gemm<false>(st, g);
-  g = GemmArgs{};
+  g = G{};
   g.M = rows; g.N = F2; g.K = F1; g.A = b.H1; g.lda = F1; g.B = net.L[2].W; g.ldb = F2;
   g.epi = 1; g.bias = net.L[2].b; g.idt = net.L[2].idt; g.C = b.H2; g.ldc = F2; g.T_out = b.T2;
   gemm<false>(st, g);
-  hipLaunchKernelGGL(k_head, dim3((rows + 3) / 4), dim3(256), 0, st, rows, F2, b.H2, b.T2, net.Wo,
+  hipLaunchKernelGGL(k_head<T>, dim3((rows + 3) / 4), dim3(256), 0, st, rows, F2, b.H2, b.T2, net.Wo,
                      net.L[2].idt, net.bo, net.bias, e_bucket, b.dZa);
   DPAMD_LAUNCH_CHECK();
   // backward: dH1 = [res2] Wo + dZ2 W2^T, dZ1 = dH1 idt1 (1 - T1^2)
-  g = GemmArgs{};
+  g = G{};
   g.M = rows; g.N = F1; g.K = F2; g.A = b.dZa; g.lda = F2; g.B = net.L[2].W; g.ldb = F2;
   g.epi = 2; g.idt = net.L[1].idt; g.C = b.dZb; g.ldc = F1;
   g.dHin = net.L[2].idt ? net.Wo : nullptr; g.ld_dhin = 0; g.dH_out = b.dH; g.Tk = b.T1;
   gemm<true>(st, g);
   // dH0 = [res1] dH1 + dZ1 W1^T, dZ0 = dH0 (1 - H0^2)
-  g = GemmArgs{};
+  g = G{};
   g.M = rows; g.N = F0; g.K = F1; g.A = b.dZb; g.lda = F1; g.B = net.L[1].W; g.ldb = F1;
   g.epi = 2; g.idt = nullptr; g.C = b.dZa; g.ldc = F0;
   g.dHin = net.L[1].idt ? b.dH : nullptr; g.ld_dhin = F1; g.dH_out = nullptr; g.Tk = b.H0;
   gemm<true>(st, g);
   // dD = dZ0 W0^T
-  g = GemmArgs{};
+  g = G{};
   g.M = rows; g.N = Dn; g.K = F0; g.A = b.dZa; g.lda = F0; g.B = net.L[0].W; g.ldb = F0;
   g.epi = 0; g.C = dD; g.ldc = Dn;
   gemm<true>(st, g);
 }
 
-void launch_dT(hipStream_t st, int nloc, int L3, int axis, const int* items, const double* T,
-               const double* dD, double* dT) {
+template <class T>
+void launch_dT(hipStream_t st, int nloc, int L3, int axis, const int* items, const T* Tm,
+               const T* dD, T* dT) {
   if (nloc <= 0) return;
   if (axis != 16 || L3 > 128 || L3 % 4 != 0)
     throw HipError{hipErrorInvalidValue, "dE/dT kernel needs axis 16 and L3 <= 128"};
-  hipLaunchKernelGGL(k_dT, dim3((nloc + kDtWaves - 1) / kDtWaves), dim3(kDtWaves * 64), 0, st,
-                     nloc, L3, items, T, dD, dT);
+  hipLaunchKernelGGL(k_dT<T>, dim3((nloc + kDtWaves - 1) / kDtWaves), dim3(kDtWaves * 64), 0, st,
+                     nloc, L3, items, Tm, dD, dT);
   DPAMD_LAUNCH_CHECK();
 }
+
+template void launch_fitting<double>(hipStream_t, const FitNet<double>&, int, const double*,
+                                     const FitBufs<double>&, double*, double*);
+template void launch_fitting<float>(hipStream_t, const FitNet<float>&, int, const float*,
+                                    const FitBufs<float>&, float*, double*);
+template void launch_dT<double>(hipStream_t, int, int, int, const int*, const double*,
+                                const double*, double*);
+template void launch_dT<float>(hipStream_t, int, int, int, const int*, const float*, const float*,
+                               float*);
 
 }  // namespace dpamd

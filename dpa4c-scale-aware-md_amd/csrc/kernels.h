@@ -45,21 +45,23 @@ struct EmbArgs {
   int block_off[kMaxPairs + 1];  // first block of each (ti, tj) pair
   int stride;                    // doubles per padded net
   double rcut, rcut_smth, inv_nnei;
-  const double* emb;   // [npair][stride] padded nets
+  // Precision-dependent arrays (double in fp64 mode, float in mixed mode):
+  // emb, Tsec, dT and act; everything else is fp64 in both modes.
+  const void* emb;     // [npair][stride] padded nets
   const double* envp;  // [npair][8] davg[4], dstd[4]
   const double* ext;   // [nall][3]
   const int* nlist;    // [nloc][nnei]
   const int* nreal;    // [nloc][ntypes]
   const int* items;    // centres grouped by type
-  double* Tsec;        // forward out [nloc][ntypes][4][L3]
-  const double* dT;    // backward in [nloc][4][L3]
+  void* Tsec;          // forward out [nloc][ntypes][4][L3]
+  const void* dT;      // backward in [nloc][4][L3]
   double* edge_grad;   // backward out [nloc][nnei][3]
   double* cpart;       // [nloc][ntypes][12]: centre force 3 + virial 9 (section 0 used)
   // Saved activations: per (centre, tile of 16 slots) a block of
   // 16*(L2P + L3P) doubles holding tanh of layers 2 and 3 in the backward's
   // register order; tiles of section tj start at tile_off[tj], tiles_per_atom
   // in total per centre.
-  double* act;
+  void* act;
   int tile_off[kMaxTypes + 1];
   int tiles_per_atom;
 };
@@ -71,10 +73,10 @@ struct DescArgs {
   const int* items;
   const int* ext_type;
   const int* nreal;
-  const double* Tsec;
-  const double* tpad;  // [npair][4][L3]: Rpad[m] * Gpad[f]
-  double* T;           // [nloc][4][L3] atom order
-  double* D;           // [nloc][L3*axis] bucket order
+  const void* Tsec;    // element type of the mode (double / float)
+  const double* tpad;  // [npair][4][L3]: Rpad[m] * Gpad[f], fp64 in both modes
+  void* T;             // [nloc][4][L3] atom order
+  void* D;             // [nloc][L3*axis] bucket order
 };
 
 // Neighbour stage
@@ -97,34 +99,47 @@ void launch_nlist_csr(hipStream_t, int nloc, const NlParams&, const double* ext,
 size_t scan_temp_bytes(int n);
 void exclusive_scan_int(hipStream_t, const int* in, int* out, int n, void* temp, size_t temp_bytes);
 
-// Embedding stage
+// Embedding stage. f32 selects the mixed-precision kernels (fp32 nets and
+// contraction; env rows and edge gradients stay fp64), whose padded-net
+// layout is make_emb_layout(L1, L2, L3, true).
 bool emb_supported(int L1, int L2, int L3);
-void launch_embed_fwd(hipStream_t, const EmbLayout&, const EmbArgs&, int nblocks);
-void launch_embed_bwd(hipStream_t, const EmbLayout&, const EmbArgs&, int nblocks);
-int embed_waves_fwd(const EmbLayout&);
-int embed_waves_bwd(const EmbLayout&);
-void launch_descriptor(hipStream_t, const DescArgs&);
+void launch_embed_fwd(hipStream_t, const EmbLayout&, const EmbArgs&, int nblocks, bool f32);
+void launch_embed_bwd(hipStream_t, const EmbLayout&, const EmbArgs&, int nblocks, bool f32);
+int embed_waves_fwd(const EmbLayout&, bool f32);
+int embed_waves_bwd(const EmbLayout&, bool f32);
+void launch_descriptor(hipStream_t, const DescArgs&, bool f32);
+// fp32 embedding kernels (embed_f32.hip), reached through the two above
+void launch_embed_fwd32(hipStream_t, const EmbLayout&, const EmbArgs&, int nblocks);
+void launch_embed_bwd32(hipStream_t, const EmbLayout&, const EmbArgs&, int nblocks);
+int embed_waves_fwd32(const EmbLayout&);
+int embed_waves_bwd32(const EmbLayout&);
 
-// Fitting stage
+// Fitting stage, element type T = double (fp64 mode) or float (mixed mode);
+// the energy head accumulates in fp64 in both.
+template <class T>
 struct FitLayer {
-  const double* W;    // [in][out]
-  const double* b;    // [out]
-  const double* idt;  // [out] or null
+  const T* W;    // [in][out]
+  const T* b;    // [out]
+  const T* idt;  // [out] or null
   int in, out;
 };
+template <class T>
 struct FitNet {
-  FitLayer L[3];
-  const double* Wo;  // [F2]
+  FitLayer<T> L[3];
+  const T* Wo;   // [F2]
   double bo;
-  double bias;       // bias_atom_e of the type
+  double bias;   // bias_atom_e of the type
 };
+template <class T>
 struct FitBufs {
-  double *H0, *T1, *H1, *T2, *H2, *dZa, *dZb, *dH;  // [rows][F] each
+  T *H0, *T1, *H1, *T2, *H2, *dZa, *dZb, *dH;  // [rows][F] each
 };
-void launch_fitting(hipStream_t, const FitNet&, int rows, const double* D, const FitBufs&,
-                    double* dD, double* e_bucket);
-void launch_dT(hipStream_t, int nloc, int L3, int axis, const int* items, const double* T,
-               const double* dD, double* dT);
+template <class T>
+void launch_fitting(hipStream_t, const FitNet<T>&, int rows, const T* D, const FitBufs<T>&, T* dD,
+                    double* e_bucket);
+template <class T>
+void launch_dT(hipStream_t, int nloc, int L3, int axis, const int* items, const T* Tm, const T* dD,
+               T* dT);
 
 // Force / virial stage
 void launch_rev_count(hipStream_t, long nedge, int nnei, const int* nlist, const int* mapping,

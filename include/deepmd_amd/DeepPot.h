@@ -5,10 +5,16 @@
 // Failures throw deepmd::deepmd_exception, which the pair style turns into
 // error->one (pair_deepmd.cpp:372-374).
 //
-// Link with -ldpamd. Only double precision is evaluated on the GPU; the float
-// overloads convert at the boundary, as the reference's compute<float> does.
+// Link with -ldpamd. The interface is double precision; the float overloads
+// convert at the boundary, as the reference's compute<float> does. The
+// evaluation precision is chosen at init: DP_PREC_FP64 (default) or
+// DP_PREC_MIXED (fp32 nets, fp64 env matrix / forces / virial). Upstream the
+// precision is a property of the trained model, so init() keeps the
+// reference's three arguments and reads the choice from the environment
+// variable DPAMD_PRECISION ("fp64" or "mixed") unless it is passed explicitly.
 #pragma once
 
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -72,15 +78,22 @@ class DeepPot {
   DeepPot& operator=(const DeepPot&) = delete;
 
   void init(const std::string& model, const int& gpu_rank = 0,
-            const std::string& file_content = "") {
+            const std::string& file_content = "", int precision = -1) {
     if (h_) {
       dp_destroy(h_);
       h_ = nullptr;
     }
+    if (precision < 0) {
+      const char* env = std::getenv("DPAMD_PRECISION");
+      precision = DP_PREC_FP64;
+      if (env && std::strcmp(env, "mixed") == 0) precision = DP_PREC_MIXED;
+      else if (env && *env && std::strcmp(env, "fp64") != 0)
+        throw deepmd_exception(std::string("DPAMD_PRECISION must be fp64 or mixed, got ") + env);
+    }
     dp_model* h = nullptr;
     const int rc = dp_create(model.c_str(), gpu_rank,
                              file_content.empty() ? nullptr : file_content.data(),
-                             file_content.size(), DP_PREC_FP64, &h);
+                             file_content.size(), precision, &h);
     if (rc != DP_OK) {
       const std::string msg = h ? dp_last_error(h) : "dp_create failed";
       if (h) dp_destroy(h);

@@ -70,10 +70,10 @@ enum {
   DP_STAGE_NLIST = 0,      /* int32 [nloc][nnei] (extended-atom indices, -1 pad) */
   DP_STAGE_EXT_COORD = 1,  /* f64 [nall][3] extended coordinates */
   DP_STAGE_MAPPING = 2,    /* int32 [nall] owner of each extended atom */
-  DP_STAGE_DESCRPT = 3,    /* f64 [nloc][M1*axis] descriptor D */
+  DP_STAGE_DESCRPT = 3,    /* f64 [nloc][M1*axis] descriptor D (fp32 values in mixed mode) */
   DP_STAGE_ATOM_ENERGY = 4,/* f64 [nloc] */
   DP_STAGE_EDGE_GRAD = 5,  /* f64 [nloc][nnei][3] dE/d(x_j - x_i) */
-  DP_STAGE_DEDD = 6,       /* f64 [nloc][M1*axis] dE/dD */
+  DP_STAGE_DEDD = 6,       /* f64 [nloc][M1*axis] dE/dD (fp32 values in mixed mode) */
   DP_STAGE_EXT_TYPE = 7    /* int32 [nall] */
 };
 
@@ -83,6 +83,12 @@ enum {
  * (deepmd-op/overlays/api_cc/include/DeepPot.h:475-477; called at
  * lammps-deepmd-plugin/src/pair_deepmd.cpp:668). If `file_content` is non-NULL
  * the model is read from those `content_len` bytes instead of `path`.
+ * `precision` DP_PREC_FP64 evaluates everything in fp64; DP_PREC_MIXED
+ * evaluates the embedding nets, the descriptor and the fitting net in fp32
+ * (FP32 MFMA) and the env matrix, edge gradients, forces, virials and energy
+ * sums in fp64 -- the reference's mixed-precision rule (fp32
+ * embedding/fitting, fp64 env matrix, force and virial accumulation), checked
+ * against its acceptance limits (data/numeric-tolerances.json:3-9).
  */
 int dp_create(const char* path, int gpu_rank, const void* file_content, size_t content_len,
               int precision, dp_model** out);
