@@ -42,14 +42,15 @@ namespace dpamd {
 constexpr int kU3 = 4;
 constexpr int kU3B = 8;
 
+// LDS: padded net | env statistics of the pair (8) | per-wave scratch
 template <class S>
 constexpr int fwd_lds_doubles(int waves) {
-  return (S::SIZE + 31) / 32 * 32 + waves * 16 * (S::L2P + 2) + waves * 64;
+  return (S::SIZE + 31) / 32 * 32 + 8 + waves * 16 * (S::L2P + 2) + waves * 64;
 }
 
 template <class S>
 constexpr int bwd_lds_doubles(int waves) {
-  return (S::SIZE + 31) / 32 * 32 + waves * 4 * (S::L3P + S::L2P);
+  return (S::SIZE + 31) / 32 * 32 + 8 + waves * 4 * (S::L3P + S::L2P);
 }
 
 template <class S, int WAVES>
@@ -60,14 +61,16 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
   constexpr int X2LD = S::L2P + 2;
   double* P = lds;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  double* X2s = lds + PS + w * 16 * X2LD;
-  double* Rs = lds + PS + WAVES * 16 * X2LD + w * 64;
+  double* EnvS = lds + PS;
+  double* X2s = lds + PS + 8 + w * 16 * X2LD;
+  double* Rs = lds + PS + 8 + WAVES * 16 * X2LD + w * 64;
 
   const int p = find_pair(a);
   const int ti = p / a.ntypes, tj = p % a.ntypes;
   {
     const double* src = static_cast<const double*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
+    if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
   }
   __syncthreads();
   const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
@@ -75,8 +78,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
   const int i = a.items[a.type_off[ti] + item];
   const int nr = a.nreal[(long)i * a.ntypes + tj];
   const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
-  const double* avg = a.envp + p * 8;
-  const double* sd = avg + 4;
+  // env statistics from LDS: a global load inside the tile loop would be
+  // ordered behind the activation traffic by the in-order vector memory
+  // counter
+  const double* avg = EnvS;
+  const double* sd = EnvS + 4;
   const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
 
   double Tacc[S::NU3 * 4];
@@ -234,7 +240,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   constexpr int PS = (S::SIZE + 31) / 32 * 32;
   double* P = lds;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  double* dTs = lds + PS + w * 4 * (S::L3P + S::L2P);
+  double* EnvS = lds + PS;
+  double* dTs = lds + PS + 8 + w * 4 * (S::L3P + S::L2P);
   double* dTf = dTs + 4 * S::L3P;
 
   const int p = find_pair(a);
@@ -242,6 +249,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   {
     const double* src = static_cast<const double*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
+    if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
   }
   __syncthreads();
   const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
@@ -250,8 +258,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   const int nr = a.nreal[(long)i * a.ntypes + tj];
   const long ebase = (long)i * a.nnei + a.sec[tj];
   const int* row = a.nlist + ebase;
-  const double* avg = a.envp + p * 8;
-  const double* sd = avg + 4;
+  // env statistics from LDS: a global load inside the tile loop would be
+  // ordered behind the activation traffic by the in-order vector memory
+  // counter
+  const double* avg = EnvS;
+  const double* sd = EnvS + 4;
   const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
   constexpr int BLK = 16 * (S::L2P + S::L3P);
   const double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;

@@ -59,13 +59,15 @@ template <class S>
 constexpr int x2_ld() {
   return S::L2P + 4;
 }
+// LDS: padded net | env statistics of the pair (8 doubles = 16 floats) |
+// per-wave scratch
 template <class S>
 constexpr int fwd_lds_floats(int waves) {
-  return lds_params<S>() + waves * 16 * x2_ld<S>() + waves * 64;
+  return lds_params<S>() + 16 + waves * 16 * x2_ld<S>() + waves * 64;
 }
 template <class S>
 constexpr int bwd_lds_floats(int waves) {
-  return lds_params<S>() + waves * 4 * (S::L3P + S::L2P);
+  return lds_params<S>() + 16 + waves * 4 * (S::L3P + S::L2P);
 }
 
 template <class S, int WAVES>
@@ -78,14 +80,16 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
   constexpr int NQ3F = nq3<S>();
   float* P = lds32;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  float* X2s = lds32 + PS + w * 16 * X2LD;
-  float* Rs = lds32 + PS + WAVES * 16 * X2LD + w * 64;
+  double* EnvS = reinterpret_cast<double*>(lds32 + PS);  // PS is a multiple of 64
+  float* X2s = lds32 + PS + 16 + w * 16 * X2LD;
+  float* Rs = lds32 + PS + 16 + WAVES * 16 * X2LD + w * 64;
 
   const int p = find_pair(a);
   const int ti = p / a.ntypes, tj = p % a.ntypes;
   {
     const float* src = static_cast<const float*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
+    if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
   }
   __syncthreads();
   const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
@@ -93,8 +97,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
   const int i = a.items[a.type_off[ti] + item];
   const int nr = a.nreal[(long)i * a.ntypes + tj];
   const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
-  const double* avg = a.envp + p * 8;
-  const double* sd = avg + 4;
+  // env statistics from LDS: a global load inside the tile loop would be
+  // ordered behind the activation traffic by the in-order vector memory
+  // counter
+  const double* avg = EnvS;
+  const double* sd = EnvS + 4;
   const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
 
   float Tacc[S::NU3 * 4];
@@ -243,7 +250,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
   constexpr int NQ3F = nq3<S>();
   float* P = lds32;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  float* dTs = lds32 + PS + w * 4 * (S::L3P + S::L2P);
+  double* EnvS = reinterpret_cast<double*>(lds32 + PS);  // PS is a multiple of 64
+  float* dTs = lds32 + PS + 16 + w * 4 * (S::L3P + S::L2P);
   float* dTf = dTs + 4 * S::L3P;
 
   const int p = find_pair(a);
@@ -251,6 +259,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
   {
     const float* src = static_cast<const float*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
+    if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
   }
   __syncthreads();
   const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
@@ -259,8 +268,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
   const int nr = a.nreal[(long)i * a.ntypes + tj];
   const long ebase = (long)i * a.nnei + a.sec[tj];
   const int* row = a.nlist + ebase;
-  const double* avg = a.envp + p * 8;
-  const double* sd = avg + 4;
+  // env statistics from LDS: a global load inside the tile loop would be
+  // ordered behind the activation traffic by the in-order vector memory
+  // counter
+  const double* avg = EnvS;
+  const double* sd = EnvS + 4;
   const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
   constexpr int BLK = 16 * (S::L2P + S::L3P);
   const float* act =

@@ -1,19 +1,21 @@
 // Hyperbolic tangent for the network kernels, fp64 and fp32.
 //
-// fp64:
-// Method (written from the mathematics, not from any vendor library):
-//   tanh(x) = sign(x) * E / (E + 2),  E = expm1(2|x|)
-//   expm1(y) = 2^n (expm1(r) + 1) - 1 with Cody-Waite reduction
-//     n = rint(y / ln2), r = (y - n*ln2_hi) - n*ln2_lo   (W. J. Cody and
-//     W. Waite, Software Manual for the Elementary Functions, 1980),
-//     ln2_hi = ln 2 rounded to 33 significant bits (n*ln2_hi exact), ln2_lo
-//     the remainder, |r| <= ln2/2;
-//   expm1(r) = r + r^2 (1/2! + r/3! + ... + r^11/13!)  (Taylor series; the
-//     truncation term r^14/14! < 5e-18 for |r| <= ln2/2);
-//   1/(E+2) from the hardware reciprocal seed refined by two Newton steps
-//     z <- z + z(1 - d z), quadratically convergent.
-// |x| is clamped at 20 (tanh(20) rounds to 1 in fp64). Measured error against
-// libm is a few ulp (tests/test_native.py).
+// fp64 (written from the mathematics, not from any vendor library):
+//   tanh|x| = 1 - 2 / (2^t + 1),   t = 2|x| log2(e)
+//   2^t = 2^n 2^f with n = rint(t), f = t - n (exact), |f| <= 1/2;
+//   2^f by a degree-10 polynomial interpolating 2^f at the 11 Chebyshev
+//     nodes of [-1/2, 1/2] (coefficients computed in extended precision and
+//     rounded, the constant term to exactly 1; max relative error below
+//     2e-15 on the interval);
+//   1/(2^t + 1) from the hardware reciprocal seed (about 24 bits) refined by
+//     one Newton step z <- z + z(1 - d z) (about 48 bits).
+// |x| is clamped at 20 (tanh(20) rounds to 1). The error is absolute, not
+// relative: at most about 3e-15 over the real line (tests/test_native.py),
+// which is what the network needs (activations enter sums of O(1) terms) and
+// four orders of magnitude below what the fp64 energy/force tolerances can
+// see; near 0 the relative error is therefore large. Cost: 22 VALU
+// operations, against about 32 for an expm1-based form with full relative
+// accuracy.
 //
 // fp32 (mixed-precision nets): tanh|x| = 1 - 2 / (e^{2|x|} + 1) with the
 // hardware base-2 exponential and reciprocal (v_exp_f32, v_rcp_f32, each
@@ -45,29 +47,24 @@ DPAMD_HD inline double rcp_seed(double d) {
 
 DPAMD_HD inline double tanh_fast(double x) {
   const double ax = fmin(fabs(x), 20.0);
-  const double y = ax + ax;
-  const double n = rint(y * 1.4426950408889634);
-  const double r = fma(-n, 7.440617110012397e-11, fma(-n, 0.6931471804855391, y));
-  double p = 1.6059043836821613e-10;
-  p = fma(p, r, 2.08767569878681e-09);
-  p = fma(p, r, 2.505210838544172e-08);
-  p = fma(p, r, 2.755731922398589e-07);
-  p = fma(p, r, 2.7557319223985893e-06);
-  p = fma(p, r, 2.48015873015873e-05);
-  p = fma(p, r, 0.0001984126984126984);
-  p = fma(p, r, 0.001388888888888889);
-  p = fma(p, r, 0.008333333333333333);
-  p = fma(p, r, 0.041666666666666664);
-  p = fma(p, r, 0.16666666666666666);
-  p = fma(p, r, 0.5);
-  const double em = fma(p, r * r, r);              // expm1(r)
-  const double s = ldexp(1.0, (int)n);             // 2^n, exact
-  const double E = fma(s, em, s - 1.0);            // expm1(y)
-  const double d = E + 2.0;
+  const double t = ax * 2.8853900817779268;  // 2 log2(e)
+  const double n = rint(t);
+  const double f = t - n;
+  double p = 6.881851856054378e-09;
+  p = fma(p, f, 1.020195864756798e-07);
+  p = fma(p, f, 1.3216503079020598e-06);
+  p = fma(p, f, 1.5252692473004133e-05);
+  p = fma(p, f, 0.00015403528490158397);
+  p = fma(p, f, 0.0013333558169839458);
+  p = fma(p, f, 0.009618129108904515);
+  p = fma(p, f, 0.05550410866482973);
+  p = fma(p, f, 0.24022650695907963);
+  p = fma(p, f, 0.6931471805599428);
+  p = fma(p, f, 1.0);  // interpolant value 1 + 2.2e-16, rounded to 1 so tanh(0) = 0
+  const double d = ldexp(p, (int)n) + 1.0;
   double z = rcp_seed(d);
   z = fma(fma(-d, z, 1.0), z, z);
-  z = fma(fma(-d, z, 1.0), z, z);
-  return copysign(E * z, x);
+  return copysign(fma(-2.0, z, 1.0), x);
 }
 
 DPAMD_HD inline float tanh_f32(float x) {
