@@ -160,66 +160,78 @@ __global__ __launch_bounds__(256) void k_head(int rows, int F2, const T* __restr
 }
 
 // dT[m][a] = sum_b dD[a][b] T[m][b] + (a < axis) sum_a' dD[a'][a] T[m][a'].
-// One wave per atom, axis == 16: dD is read coalesced, element e = 64k + lane
-// being (a, b) = (4k + g, c) for lane = 16g + c. First term: lane products
-// dD[a][c] T[m][c] summed over the 16 lanes of a row (xor 1..8). Second term:
-// lane (g, c) accumulates dD[a][c] T[m][a] over its rows, then the 4 row groups
-// are folded (xor 16, 32); lane c then holds column c.
-constexpr int kDtWaves = 4;
+// One wave per atom, axis == 16, L3 <= 128. The atom's dD block (L3 x 16) is
+// read coalesced and stored transposed in LDS (row b, padded stride), so
+// neither term needs a cross-lane reduction: lane a (and a + 64) owns row a
+// of the first term, lane (m, b) = (lane / 16, lane % 16) owns entry (m, b)
+// of the second; the first-term values of rows a < 16 meet their second term
+// through LDS.
+constexpr int kDtWaves = 2;
 template <class T>
 __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
                                                      const int* __restrict__ items,
                                                      const T* __restrict__ Tm,
                                                      const T* __restrict__ dD,
                                                      T* __restrict__ dT) {
-  constexpr int AX = 16;
+  constexpr int AX = 16, LDT = 128 + 1;
+  __shared__ T Dt[kDtWaves][AX * LDT];
   __shared__ T Ts[kDtWaves][4 * 128];
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  __shared__ T F16[kDtWaves][4 * AX];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pos = blockIdx.x * kDtWaves + w;
   if (pos >= nb) return;
   const int i = items[pos];
   const T* Ti = Tm + (long)i * 4 * L3;
   for (int q = lane; q < 4 * L3; q += 64) Ts[w][q] = Ti[q];
-  wave_lds_sync();
   const T* dDp = dD + (long)pos * L3 * AX;
-  T* out = dT + (long)i * 4 * L3;
-  const T tb0 = Ts[w][c], tb1 = Ts[w][L3 + c], tb2 = Ts[w][2 * L3 + c], tb3 = Ts[w][3 * L3 + c];
-  T s0 = 0, s1 = 0, s2 = 0, s3 = 0;
-  for (int a0 = 0; a0 < L3; a0 += 4) {
-    const int a = a0 + g;
-    const T v = dDp[a0 * AX + lane];
-    s0 += v * Ts[w][a];
-    s1 += v * Ts[w][L3 + a];
-    s2 += v * Ts[w][2 * L3 + a];
-    s3 += v * Ts[w][3 * L3 + a];
-    T p0 = v * tb0, p1 = v * tb1, p2 = v * tb2, p3 = v * tb3;
+  const int ne = L3 * AX;  // multiple of 64 (L3 % 4 == 0)
+  for (int e0 = 0; e0 < ne; e0 += 64 * 8) {
+    T v[8];
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-      p0 += shfl_xor_d(p0, off);
-      p1 += shfl_xor_d(p1, off);
-      p2 += shfl_xor_d(p2, off);
-      p3 += shfl_xor_d(p3, off);
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + 64 * u + lane;
+      v[u] = e < ne ? dDp[e] : T(0);
     }
-    // row a: lane c == m writes component m (the second term is added below)
-    const T pm = c == 0 ? p0 : c == 1 ? p1 : c == 2 ? p2 : p3;
-    if (c < 4 && a >= AX) out[c * L3 + a] = pm;
-    if (c < 4 && a < AX) Ts[w][c * L3 + a] = pm;  // stash: T rows a < 16 no longer needed
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + 64 * u + lane;
+      if (e < ne) Dt[w][(e & 15) * LDT + (e >> 4)] = v[u];
+    }
   }
-  s0 += shfl_xor_d(s0, 16);
-  s0 += shfl_xor_d(s0, 32);
-  s1 += shfl_xor_d(s1, 16);
-  s1 += shfl_xor_d(s1, 32);
-  s2 += shfl_xor_d(s2, 16);
-  s2 += shfl_xor_d(s2, 32);
-  s3 += shfl_xor_d(s3, 16);
-  s3 += shfl_xor_d(s3, 32);
   wave_lds_sync();
-  if (g == 0) {
-    out[c] = Ts[w][c] + s0;
-    out[L3 + c] = Ts[w][L3 + c] + s1;
-    out[2 * L3 + c] = Ts[w][2 * L3 + c] + s2;
-    out[3 * L3 + c] = Ts[w][3 * L3 + c] + s3;
+  T* out = dT + (long)i * 4 * L3;
+  // first term
+  for (int a = lane; a < L3; a += 64) {
+    T acc0 = 0, acc1 = 0, acc2 = 0, acc3 = 0;
+#pragma unroll
+    for (int b = 0; b < AX; ++b) {
+      const T d = Dt[w][b * LDT + a];
+      acc0 += d * Ts[w][b];
+      acc1 += d * Ts[w][L3 + b];
+      acc2 += d * Ts[w][2 * L3 + b];
+      acc3 += d * Ts[w][3 * L3 + b];
+    }
+    if (a >= AX) {
+      out[a] = acc0;
+      out[L3 + a] = acc1;
+      out[2 * L3 + a] = acc2;
+      out[3 * L3 + a] = acc3;
+    } else {
+      F16[w][a] = acc0;
+      F16[w][AX + a] = acc1;
+      F16[w][2 * AX + a] = acc2;
+      F16[w][3 * AX + a] = acc3;
+    }
   }
+  // second term
+  const int m = lane >> 4, b = lane & 15;
+  T s = 0;
+  const T* Tr = Ts[w] + m * L3;
+  const T* Dr = Dt[w] + b * LDT;
+#pragma unroll 4
+  for (int a = 0; a < L3; ++a) s += Dr[a] * Tr[a];
+  wave_lds_sync();
+  out[m * L3 + b] = F16[w][m * AX + b] + s;
 }
 
 template <class T, int NT, bool TRANSB>

@@ -179,6 +179,40 @@ __device__ __forceinline__ void nl_push(bool keep, double r2, int j, int t, int&
   n += __popcll(m);
 }
 
+template <int K>
+__device__ __forceinline__ void nl_rank_place(const NlParams& np, int n, const NlKey* s,
+                                              const int* first, int* __restrict__ row) {
+  const int lane = threadIdx.x & 63;
+  unsigned long long ek[K];
+  int ej[K], rank[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int q = lane + kWave * k;
+    ek[k] = ~0ull;
+    ej[k] = 0x7fffffff;
+    rank[k] = 0;
+    if (q < n) {
+      ek[k] = s[q].key;
+      ej[k] = s[q].j;
+    }
+  }
+  for (int p = 0; p < n; ++p) {
+    const unsigned long long ok = s[p].key;
+    const int oj = s[p].j;
+#pragma unroll
+    for (int k = 0; k < K; ++k) rank[k] += (ok < ek[k] || (ok == ek[k] && oj < ej[k])) ? 1 : 0;
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int q = lane + kWave * k;
+    if (q < n) {
+      const int t = s[q].t;
+      const int r = rank[k] - first[t];
+      if (r < np.sel[t]) row[np.sec[t] + r] = ej[k];
+    }
+  }
+}
+
 __device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s,
                          int* __restrict__ nlist, int* __restrict__ nreal,
                          int* __restrict__ status) {
@@ -205,15 +239,15 @@ __device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s,
     first[t] = acc;
     acc += cnt[t];
   }
-  for (int q = lane; q < n; q += kWave) {
-    const NlKey e = s[q];
-    int rank = 0;
-    for (int p = 0; p < n; ++p) {
-      const NlKey o = s[p];
-      rank += (o.key < e.key || (o.key == e.key && o.j < e.j)) ? 1 : 0;
-    }
-    rank -= first[e.t];
-    if (rank < np.sel[e.t]) row[np.sec[e.t] + rank] = e.j;
+  // rank of each candidate in (key, j) order: one pass over the list ranks
+  // every candidate this lane holds (q = lane + 64k, k < K)
+  switch ((n + kWave - 1) / kWave) {
+    case 0: break;
+    case 1: nl_rank_place<1>(np, n, s, first, row); break;
+    case 2: nl_rank_place<2>(np, n, s, first, row); break;
+    case 3: nl_rank_place<3>(np, n, s, first, row); break;
+    case 4: nl_rank_place<4>(np, n, s, first, row); break;
+    default: nl_rank_place<kMaxCand / kWave>(np, n, s, first, row); break;
   }
   for (int t = 0; t < np.ntypes; ++t) {
     const int kept = cnt[t] < np.sel[t] ? cnt[t] : np.sel[t];
