@@ -38,9 +38,9 @@
 namespace dpamd {
 
 // layer-3 output tiles per group: independent MFMA accumulation chains in
-// flight (the forward runs two waves per SIMD, the backward one)
+// flight (both kernels run two waves per SIMD)
 constexpr int kU3 = 4;
-constexpr int kU3B = 8;
+constexpr int kU3B = 4;
 
 // LDS: padded net | env statistics of the pair (8) | per-wave scratch
 template <class S>
@@ -287,34 +287,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 
   const double* act2 = act + c * 4 + g;  // element (t, r) at act2[64 (4t + r)]
   const double* act3 = act2 + 16 * S::L2P;  // element (u, r) at act3[256u + 64r]
-  // software pipeline: the saved activations and the neighbour coordinates of
-  // tile k+1 are loaded while tile k is computed (one wave per SIMD, so the
-  // registers for a whole tile in flight are available)
-  // Activations and neighbour coordinates of tile k+1 are fetched during tile
-  // k; the neighbour index is loaded one tile earlier still, so the
-  // coordinate loads never wait behind the activation loads (the memory
-  // counter is in order).
-  double nth2[S::NT2][4], nth3[S::NU3][4];
+  // Neighbour coordinates of tile k+1 are fetched during tile k (their index
+  // one tile earlier, so the memory counter never orders them behind other
+  // loads). The saved activations of a tile are loaded at its start and
+  // consumed after the layer-2 and layer-3 products: their latency is covered
+  // by those products and by the other wave of the SIMD. Holding them a whole
+  // tile ahead would need the registers of that second wave.
   double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
-  int jn = 0;
-  auto prefetch = [&](int tile, const double* p2, const double* p3) {
-    if (tile + c < nr) {
-      nx0 = a.ext[3 * (long)jn];
-      nx1 = a.ext[3 * (long)jn + 1];
-      nx2 = a.ext[3 * (long)jn + 2];
-    }
-    jn = tile + 16 + c < nr ? row[tile + 16 + c] : 0;
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) nth2[t][r] = p2[(4 * t + r) * 64];
-#pragma unroll
-    for (int u = 0; u < S::NU3; ++u)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) nth3[u][r] = p3[256 * u + 64 * r];
-  };
-  jn = c < nr ? row[c] : 0;
-  if (nr > 0) prefetch(0, act2, act3);
+  int jn = c < nr ? row[c] : 0;
+  if (c < nr) {
+    nx0 = a.ext[3 * (long)jn];
+    nx1 = a.ext[3 * (long)jn + 1];
+    nx2 = a.ext[3 * (long)jn + 2];
+  }
+  jn = 16 + c < nr ? row[16 + c] : 0;
 
   for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
     const int slot = tile + c;
@@ -323,11 +309,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 #pragma unroll
     for (int t = 0; t < S::NT2; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) th2[t][r] = nth2[t][r];
+      for (int r = 0; r < 4; ++r) th2[t][r] = act2[(4 * t + r) * 64];
 #pragma unroll
     for (int u = 0; u < S::NU3; ++u)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) th3[u][r] = nth3[u][r];
+      for (int r = 0; r < 4; ++r) th3[u][r] = act3[256 * u + 64 * r];
     double d0 = 0.0, d1 = 0.0, d2 = 0.0;
     double Rn[4] = {0.0, 0.0, 0.0, 0.0};
     if (valid) {
@@ -336,7 +322,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       d2 = nx2 - zi;
       env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
     }
-    if (tile + 16 < nr) prefetch(tile + 16, act2 + BLK, act3 + BLK);
+    if (slot + 16 < nr) {
+      nx0 = a.ext[3 * (long)jn];
+      nx1 = a.ext[3 * (long)jn + 1];
+      nx2 = a.ext[3 * (long)jn + 2];
+    }
+    jn = slot + 32 < nr ? row[slot + 32] : 0;
     const double s = Rn[0];
 
     // layer 1 (recomputed, elementwise) and its tangent
@@ -519,7 +510,7 @@ __global__ __launch_bounds__(256) void k_descriptor(DescArgs a) {
 using ShapeWater = EmbShape<25, 50, 100>;
 using ShapeMetal = EmbShape<32, 64, 128>;
 constexpr int kFwdWaves = 8;
-constexpr int kBwdWaves = 4;
+constexpr int kBwdWaves = 8;
 
 bool emb_supported(int L1, int L2, int L3) {
   return (L1 == 25 && L2 == 50 && L3 == 100) || (L1 == 32 && L2 == 64 && L3 == 128);
