@@ -75,7 +75,7 @@ struct dp_model {
   // workspace
   std::vector<Buf*> bufs;
   Buf coord_in, atype_in, sfrac, flags, gpos, ext, ext_type, mapping, cell_of, cell_count,
-      cell_start, cell_cursor, sorted, nlist, nreal, cand_off, cand, items, Tsec, T, D, dD, dT,
+      cell_start, cell_cursor, sorted, nlist, nreal, cand_off, cand, items, Tsec, Tt, D, dD, dT,
       fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_cursor, rev, force_ws, av_ws,
       ae_ws, partials, out10, status, scan_tmp, act;
   size_t bytes_now = 0, bytes_peak = 0;
@@ -99,7 +99,7 @@ struct dp_model {
   dp_model() {
     bufs = {&coord_in, &atype_in, &sfrac,     &flags,    &gpos,       &ext,       &ext_type,
             &mapping,  &cell_of,  &cell_count, &cell_start, &cell_cursor, &sorted,  &nlist,
-            &nreal,    &cand_off, &cand,      &items,    &Tsec,       &T,         &D,
+            &nreal,    &cand_off, &cand,      &items,    &Tsec,       &Tt,        &D,
             &dD,       &dT,       &fitb,      &e_bucket, &edge_grad,  &cpart,     &rev_count,
             &rev_off,  &rev_cursor, &rev,     &force_ws, &av_ws,      &ae_ws,     &partials,
             &out10,    &status,   &scan_tmp, &act};
@@ -255,6 +255,28 @@ struct Outputs {
 };
 
 // Everything after the neighbour list; ext/ext_type/nlist/nreal/mapping ready.
+// Arguments of the descriptor kernel for the current buckets: T (and D when
+// non-null) in bucket order from Tsec.
+DescArgs desc_args(dp_model* M, void* Tt, void* D) {
+  const ModelHost& m = M->host;
+  DescArgs da{};
+  da.ntypes = m.ntypes;
+  da.nloc = M->nbucket;
+  da.L3 = m.emb[2];
+  da.axis = m.axis;
+  da.nnei = m.nnei;
+  for (int t = 0; t < m.ntypes; ++t) da.sel[t] = m.sel[t];
+  da.inv_nnei = 1.0 / (double)m.nnei;
+  da.items = static_cast<const int*>(M->items.p);
+  da.ext_type = static_cast<const int*>(M->ext_type.p);
+  da.nreal = static_cast<const int*>(M->nreal.p);
+  da.Tsec = M->Tsec.p;
+  da.tpad = M->d_tpad;
+  da.Tt = Tt;
+  da.D = D;
+  return da;
+}
+
 template <class E>
 void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_mapping,
                  int ntarget, const Outputs& out) {
@@ -269,8 +291,11 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   int* status = static_cast<int*>(M->status.p);
 
   E* Tsec = need<E>(M, M->Tsec, (size_t)nloc * nt * 4 * L3);
-  E* T = need<E>(M, M->T, (size_t)nloc * 4 * L3);
-  E* D = need<E>(M, M->D, (size_t)std::max(nb, 1) * Dn);
+  // T column-major in bucket order; with axis 16 the first fitting GEMM forms
+  // D from it, otherwise D is stored
+  E* Tt = need<E>(M, M->Tt, (size_t)std::max(nb, 1) * 4 * L3);
+  const bool d_from_t = axis == 16;
+  E* D = d_from_t ? nullptr : need<E>(M, M->D, (size_t)std::max(nb, 1) * Dn);
   E* dD = need<E>(M, M->dD, (size_t)std::max(nb, 1) * Dn);
   E* dT = need<E>(M, M->dT, (size_t)nloc * 4 * L3);
   const int Fmax = std::max(m.fit[0], std::max(m.fit[1], m.fit[2]));
@@ -330,22 +355,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   launch_embed_fwd(st, M->el, ea, nblk, f32);
   record(M, st, kStEmbFwd + 1);
 
-  DescArgs da{};
-  da.ntypes = nt;
-  da.nloc = nb;
-  da.L3 = L3;
-  da.axis = axis;
-  da.nnei = nnei;
-  for (int t = 0; t < nt; ++t) da.sel[t] = m.sel[t];
-  da.inv_nnei = 1.0 / (double)nnei;
-  da.items = items;
-  da.ext_type = static_cast<const int*>(M->ext_type.p);
-  da.nreal = nreal;
-  da.Tsec = Tsec;
-  da.tpad = M->d_tpad;
-  da.T = T;
-  da.D = D;
-  launch_descriptor(st, da, f32);
+  launch_descriptor(st, desc_args(M, Tt, D), f32);
   record(M, st, kStDescr + 1);
 
   for (int t = 0; t < nt; ++t) {
@@ -371,11 +381,13 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
     E** slots[8] = {&fb.H0, &fb.T1, &fb.H1, &fb.T2, &fb.H2, &fb.dZa, &fb.dZb, &fb.dH};
     // slab q holds [rows][F] of every type back to back; F <= Fmax
     for (int q = 0; q < 8; ++q) *slots[q] = base + q * slab + r0 * (size_t)Fmax;
-    launch_fitting(st, net, rows, D + r0 * Dn, fb, dD + r0 * Dn, e_bucket + r0);
+    launch_fitting(st, net, rows, d_from_t ? nullptr : D + r0 * Dn,
+                   d_from_t ? Tt + r0 * 4 : nullptr, 4L * nb, L3, fb, dD + r0 * Dn,
+                   e_bucket + r0);
   }
   record(M, st, kStFit + 1);
 
-  launch_dT(st, nb, L3, axis, items, T, dD, dT);
+  launch_dT(st, nb, L3, axis, items, Tt, dD, dT);
   record(M, st, kStDT + 1);
 
   nblk = block_table(embed_waves_bwd(M->el, f32));
@@ -840,7 +852,14 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
         if (!M->last_standalone) throw ApiError{DP_ERR_ARG, "no mapping on the LAMMPS path"};
         copy(M->mapping.p, (size_t)nall * 4);
         break;
-      case DP_STAGE_DESCRPT: copy_bucket(M->D.p, Dn, net_esize); break;
+      case DP_STAGE_DESCRPT:
+        if (M->host.axis == 16 && M->nbucket > 0) {
+          // not stored by the evaluation: form D from the saved Tsec
+          void* Dp = need<char>(M, M->D, (size_t)M->nbucket * Dn * net_esize);
+          launch_descriptor(nullptr, desc_args(M, M->Tt.p, Dp), net_esize == 4);
+        }
+        copy_bucket(M->D.p, Dn, net_esize);
+        break;
       case DP_STAGE_DEDD: copy_bucket(M->dD.p, Dn, net_esize); break;
       case DP_STAGE_ATOM_ENERGY: copy_bucket(M->e_bucket.p, 1, 8); break;
       case DP_STAGE_EDGE_GRAD: copy(M->edge_grad.p, (size_t)nloc * m.nnei * 24); break;

@@ -473,36 +473,59 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   }
 }
 
-// T = (sum over sections of Tsec + padded-slot constant) / nnei, and
-// D = T^T T[:, :axis], written in bucket order for the fitting GEMMs. E is the
-// element type of Tsec, T and D (double, or float in mixed mode); the sums are
-// formed in fp64 and rounded once.
+// T = (sum over sections of Tsec + padded-slot constant) / nnei, written in
+// bucket order as a column-major array Tt [a][pos][4] (element (pos, a, m) at
+// Tt[a * 4 nloc + 4 pos + m]): the first fitting GEMM forms D = T^T T[:, :16]
+// from it one column a at a time with contiguous reads, and dE/dT reads it
+// through L2. When requested, D = T^T T[:, :axis] [pos][L3*axis] as well. E is
+// the element type (double, or float in mixed mode); the sums are formed in
+// fp64 and rounded once. A block handles kDescAtoms consecutive positions so
+// that every layout is written in contiguous runs.
+constexpr int kDescAtoms = 8;
 template <class E>
 __global__ __launch_bounds__(256) void k_descriptor(DescArgs a) {
+  // LDS copy [kDescAtoms][4][L3 + 1]: the padding keeps the column-major
+  // pass (consecutive threads on consecutive (atom, m) rows) off one bank
   extern __shared__ double Ts[];
   const E* Tsec = static_cast<const E*>(a.Tsec);
-  const int pos = blockIdx.x;
-  const int i = a.items[pos];
-  const int ti = a.ext_type[i];
-  const int L3 = a.L3;
-  for (int q = threadIdx.x; q < 4 * L3; q += blockDim.x) {
-    double v = 0.0;
-    for (int tj = 0; tj < a.ntypes; ++tj) {
-      const long sec = (long)i * a.ntypes + tj;
-      const double npad = (double)(a.sel[tj] - a.nreal[sec]);
-      v += (double)Tsec[sec * 4 * L3 + q] + npad * a.tpad[((long)(ti * a.ntypes + tj)) * 4 * L3 + q];
+  const int L3 = a.L3, per = 4 * L3, LR = L3 + 1;
+  const int pos0 = blockIdx.x * kDescAtoms;
+  const int na = min(kDescAtoms, a.nloc - pos0);
+  // thread = (column, one of two atoms of a pass); L3 <= 128
+  const int col = threadIdx.x & 127;
+  for (int k = threadIdx.x >> 7; k < na; k += 2) {
+    if (col >= L3) continue;
+    const int i = a.items[pos0 + k];
+    const int ti = a.ext_type[i];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int e = m * L3 + col;
+      double v = 0.0;
+      for (int tj = 0; tj < a.ntypes; ++tj) {
+        const long sec = (long)i * a.ntypes + tj;
+        const double npad = (double)(a.sel[tj] - a.nreal[sec]);
+        v += (double)Tsec[sec * per + e] + npad * a.tpad[((long)(ti * a.ntypes + tj)) * per + e];
+      }
+      Ts[(k * 4 + m) * LR + col] = (double)(E)(v * a.inv_nnei);
     }
-    const E t = (E)(v * a.inv_nnei);
-    Ts[q] = (double)t;
-    static_cast<E*>(a.T)[(long)i * 4 * L3 + q] = t;
   }
   __syncthreads();
+  {
+    E* Tt = static_cast<E*>(a.Tt);
+    for (int q = threadIdx.x; q < L3 * kDescAtoms * 4; q += blockDim.x) {
+      const int km = q % (4 * kDescAtoms), c2 = q / (4 * kDescAtoms);  // km = 4k + m
+      if ((km >> 2) < na) Tt[((long)c2 * a.nloc + pos0) * 4 + km] = (E)Ts[km * LR + c2];
+    }
+  }
+  if (!a.D) return;
   const int nd = L3 * a.axis;
-  E* D = static_cast<E*>(a.D) + (long)pos * nd;
-  for (int q = threadIdx.x; q < nd; q += blockDim.x) {
-    const int ai = q / a.axis, bi = q % a.axis;
-    D[q] = (E)(Ts[ai] * Ts[bi] + Ts[L3 + ai] * Ts[L3 + bi] + Ts[2 * L3 + ai] * Ts[2 * L3 + bi] +
-               Ts[3 * L3 + ai] * Ts[3 * L3 + bi]);
+  for (int q = threadIdx.x; q < na * nd; q += blockDim.x) {
+    const int k = q / nd, e = q % nd;
+    const int ai = e / a.axis, bi = e % a.axis;
+    const double* T = Ts + k * 4 * LR;
+    static_cast<E*>(a.D)[(long)pos0 * nd + q] =
+        (E)(T[ai] * T[bi] + T[LR + ai] * T[LR + bi] + T[2 * LR + ai] * T[2 * LR + bi] +
+            T[3 * LR + ai] * T[3 * LR + bi]);
   }
 }
 
@@ -557,10 +580,11 @@ void launch_embed_bwd(hipStream_t st, const EmbLayout& e, const EmbArgs& a, int 
 
 void launch_descriptor(hipStream_t st, const DescArgs& a, bool f32) {
   if (a.nloc <= 0) return;
-  if (f32)
-    hipLaunchKernelGGL(k_descriptor<float>, dim3(a.nloc), dim3(256), sizeof(double) * 4 * a.L3, st, a);
-  else
-    hipLaunchKernelGGL(k_descriptor<double>, dim3(a.nloc), dim3(256), sizeof(double) * 4 * a.L3, st, a);
+  if (a.L3 > 128) throw HipError{hipErrorInvalidValue, "descriptor kernel needs L3 <= 128"};
+  const dim3 grid((a.nloc + kDescAtoms - 1) / kDescAtoms);
+  const size_t lds = sizeof(double) * kDescAtoms * 4 * (a.L3 + 1);
+  if (f32) hipLaunchKernelGGL(k_descriptor<float>, grid, dim3(256), lds, st, a);
+  else hipLaunchKernelGGL(k_descriptor<double>, grid, dim3(256), lds, st, a);
   DPAMD_LAUNCH_CHECK();
 }
 

@@ -33,6 +33,10 @@ struct GemmArgs {
   int ld_dhin;
   T* dH_out;      // backward: dH of this layer
   const T* Tk;    // backward: tanh part of this layer (ld = ldc)
+  // A from T (AT kernels): element (row, a, m) of T at Tt[a * ldt + 4 row + m],
+  // A[row][16a + b] = sum_m T[m][a] T[m][b]
+  const T* Tt;
+  long ldt;
 };
 
 // C = epi(A[MxK] B[KxN]); B(k,n) = TRANSB ? B[n*ldb + k] : B[k*ldb + n].
@@ -40,15 +44,33 @@ struct GemmArgs {
 // so one A fragment feeds NT MFMAs. K advances 16 at a time through two LDS
 // buffers: the next chunk is fetched into registers while the current one is
 // multiplied, then stored into the other buffer (one barrier per chunk).
-template <class T, int NT, bool TRANSB>
+// AT: A is the descriptor D = T^T T[:, :16] of each row, formed while staging:
+// K chunk a holds D[row][16a + b] = sum_m T[m][a] T[m][b]; thread (r, part)
+// keeps T[m][4 part .. 4 part + 3] of row r in registers and fetches the 4
+// values T[0..3][a] per chunk (contiguous in the column-major copy of T, so a
+// wave reads 16 rows as one run) instead of 16 values of D.
+template <class T, int NT, bool TRANSB, bool AT = false>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
   constexpr int BM = 64, BK = 16, BN = 16 * NT;
   constexpr int ALD = BK + 1, BLD = BN + 1;
   constexpr int NA = BM * BK / 256, NB = (BK * BN + 255) / 256;
+  static_assert(!AT || NA == 4, "AT staging assumes 4 A elements per thread");
   __shared__ T As[2][BM * ALD];
   __shared__ T Bs[2][BK * BLD];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+  // AT: this thread's row and column quarter, and T[m][4 part + j] of the row
+  const int at_r = tid >> 2, at_part = tid & 3;
+  const T* at_row = nullptr;  // T[.][0][row] of this thread's row
+  T tb[4][4];
+  if constexpr (AT) {
+    if (row0 + at_r < a.M) at_row = a.Tt + 4 * (long)(row0 + at_r);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        tb[m][j] = at_row ? at_row[(4 * at_part + j) * a.ldt + m] : T(0);
+  }
   // element offsets of this thread's share of a K chunk, fixed over chunks
   int offA[NA], ldsA[NA], offB[NB], ldsB[NB];
 #pragma unroll
@@ -77,16 +99,29 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
   }
   T ra[NA], rb[NB];
   auto fetch = [&](int k0) {
-    const T* Ak = a.A + k0;
     const T* Bk = TRANSB ? a.B + k0 : a.B + (long)k0 * a.ldb;
+    if constexpr (AT) {
+      // ra[m] = T[m][a] of this thread's row, a = k0 / 16
 #pragma unroll
-    for (int u = 0; u < NA; ++u) ra[u] = offA[u] >= 0 ? Ak[offA[u]] : T(0);
+      for (int m = 0; m < 4; ++m) ra[m] = at_row ? at_row[(k0 >> 4) * a.ldt + m] : T(0);
+    } else {
+      const T* Ak = a.A + k0;
+#pragma unroll
+      for (int u = 0; u < NA; ++u) ra[u] = offA[u] >= 0 ? Ak[offA[u]] : T(0);
+    }
 #pragma unroll
     for (int u = 0; u < NB; ++u) rb[u] = offB[u] >= 0 ? Bk[offB[u]] : T(0);
   };
   auto stash = [&](int buf) {
+    if constexpr (AT) {
 #pragma unroll
-    for (int u = 0; u < NA; ++u) As[buf][ldsA[u]] = ra[u];
+      for (int j = 0; j < 4; ++j)
+        As[buf][at_r * ALD + 4 * at_part + j] =
+            ra[0] * tb[0][j] + ra[1] * tb[1][j] + ra[2] * tb[2][j] + ra[3] * tb[3][j];
+    } else {
+#pragma unroll
+      for (int u = 0; u < NA; ++u) As[buf][ldsA[u]] = ra[u];
+    }
 #pragma unroll
     for (int u = 0; u < NB; ++u)
       if (offB[u] >= 0) Bs[buf][ldsB[u]] = rb[u];
@@ -170,7 +205,7 @@ constexpr int kDtWaves = 2;
 template <class T>
 __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
                                                      const int* __restrict__ items,
-                                                     const T* __restrict__ Tm,
+                                                     const T* __restrict__ Tt,
                                                      const T* __restrict__ dD,
                                                      T* __restrict__ dT) {
   constexpr int AX = 16, LDT = 128 + 1;
@@ -181,8 +216,10 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
   const int pos = blockIdx.x * kDtWaves + w;
   if (pos >= nb) return;
   const int i = items[pos];
-  const T* Ti = Tm + (long)i * 4 * L3;
-  for (int q = lane; q < 4 * L3; q += 64) Ts[w][q] = Ti[q];
+  // T of this position from the column-major copy: element (a, m) at
+  // Tt[a * 4 nb + 4 pos + m]
+  const T* Ti = Tt + 4 * (long)pos;
+  for (int q = lane; q < 4 * L3; q += 64) Ts[w][(q & 3) * L3 + (q >> 2)] = Ti[(long)(q >> 2) * 4 * nb + (q & 3)];
   const T* dDp = dD + (long)pos * L3 * AX;
   const int ne = L3 * AX;  // multiple of 64 (L3 % 4 == 0)
   for (int e0 = 0; e0 < ne; e0 += 64 * 8) {
@@ -234,10 +271,10 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
   out[m * L3 + b] = F16[w][m * AX + b] + s;
 }
 
-template <class T, int NT, bool TRANSB>
+template <class T, int NT, bool TRANSB, bool AT = false>
 static void gemm_nt(hipStream_t st, const GemmArgs<T>& a) {
   dim3 grid(a.N / (16 * NT), (a.M + 63) / 64);
-  hipLaunchKernelGGL((k_gemm<T, NT, TRANSB>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((k_gemm<T, NT, TRANSB, AT>), grid, dim3(256), 0, st, a);
   DPAMD_LAUNCH_CHECK();
 }
 
@@ -255,9 +292,21 @@ static void gemm(hipStream_t st, const GemmArgs<T>& a) {
   else gemm_nt<T, 1, TRANSB>(st, a);
 }
 
+// First layer with A formed from T: the column tile is the widest of 8, 5, 4
+// or 1 MFMA tiles dividing N, as in gemm().
 template <class T>
-void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D,
-                    const FitBufs<T>& b, T* dD, double* e_bucket) {
+static void gemm_at(hipStream_t st, const GemmArgs<T>& a) {
+  if (a.M <= 0) return;
+  const int tiles = a.N / 16;
+  if (tiles % 8 == 0) gemm_nt<T, 8, false, true>(st, a);
+  else if (tiles % 5 == 0) gemm_nt<T, 5, false, true>(st, a);
+  else if (tiles % 4 == 0) gemm_nt<T, 4, false, true>(st, a);
+  else gemm_nt<T, 1, false, true>(st, a);
+}
+
+template <class T>
+void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, const T* Tt,
+                    long ldt, int L3, const FitBufs<T>& b, T* dD, double* e_bucket) {
   using G = GemmArgs<T>;
   if (rows <= 0) return;
   const int Dn = net.L[0].in, F0 = net.L[0].out, F1 = net.L[1].out, F2 = net.L[2].out;
@@ -266,7 +315,15 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D,
   g = G{};
   g.M = rows; g.N = F0; g.K = Dn; g.A = D; g.lda = Dn; g.B = net.L[0].W; g.ldb = F0;
   g.epi = 1; g.bias = net.L[0].b; g.idt = nullptr; g.C = b.H0; g.ldc = F0;
-  gemm<false>(st, g);
+  if (Tt) {
+    if (Dn != 16 * L3)
+      throw HipError{hipErrorInvalidValue, "descriptor formed from T needs axis 16"};
+    g.Tt = Tt;
+    g.ldt = ldt;
+    gemm_at(st, g);
+  } else {
+    gemm<false>(st, g);
+  }
   g = G{};
   g.M = rows; g.N = F1; g.K = F0; g.A = b.H0; g.lda = F0; g.B = net.L[1].W; g.ldb = F1;
   g.epi = 1; g.bias = net.L[1].b; g.idt = net.L[1].idt; g.C = b.H1; g.ldc = F1; g.T_out = b.T1;
@@ -298,20 +355,22 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D,
 }
 
 template <class T>
-void launch_dT(hipStream_t st, int nloc, int L3, int axis, const int* items, const T* Tm,
+void launch_dT(hipStream_t st, int nloc, int L3, int axis, const int* items, const T* Tt,
                const T* dD, T* dT) {
   if (nloc <= 0) return;
   if (axis != 16 || L3 > 128 || L3 % 4 != 0)
     throw HipError{hipErrorInvalidValue, "dE/dT kernel needs axis 16 and L3 <= 128"};
   hipLaunchKernelGGL(k_dT<T>, dim3((nloc + kDtWaves - 1) / kDtWaves), dim3(kDtWaves * 64), 0, st,
-                     nloc, L3, items, Tm, dD, dT);
+                     nloc, L3, items, Tt, dD, dT);
   DPAMD_LAUNCH_CHECK();
 }
 
 template void launch_fitting<double>(hipStream_t, const FitNet<double>&, int, const double*,
-                                     const FitBufs<double>&, double*, double*);
+                                     const double*, long, int, const FitBufs<double>&, double*,
+                                     double*);
 template void launch_fitting<float>(hipStream_t, const FitNet<float>&, int, const float*,
-                                    const FitBufs<float>&, float*, double*);
+                                    const float*, long, int, const FitBufs<float>&, float*,
+                                    double*);
 template void launch_dT<double>(hipStream_t, int, int, int, const int*, const double*,
                                 const double*, double*);
 template void launch_dT<float>(hipStream_t, int, int, int, const int*, const float*, const float*,

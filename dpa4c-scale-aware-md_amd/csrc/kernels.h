@@ -75,8 +75,8 @@ struct DescArgs {
   const int* nreal;
   const void* Tsec;    // element type of the mode (double / float)
   const double* tpad;  // [npair][4][L3]: Rpad[m] * Gpad[f], fp64 in both modes
-  void* T;             // [nloc][4][L3] atom order
-  void* D;             // [nloc][L3*axis] bucket order
+  void* Tt;            // [L3][nloc][4] bucket order (T column-major)
+  void* D;             // [nloc][L3*axis] bucket order, or null (not formed)
 };
 
 // Neighbour stage
@@ -134,11 +134,17 @@ template <class T>
 struct FitBufs {
   T *H0, *T1, *H1, *T2, *H2, *dZa, *dZb, *dH;  // [rows][F] each
 };
+// The first layer reads its input either from D ([rows][L3*axis]) or, when
+// Tt is given (axis 16), forms D = T^T T[:, :16] on the fly from the
+// column-major copy of T (element (row, a, m) at Tt[a * ldt + 4 row + m]) and
+// D may be null.
 template <class T>
-void launch_fitting(hipStream_t, const FitNet<T>&, int rows, const T* D, const FitBufs<T>&, T* dD,
-                    double* e_bucket);
+void launch_fitting(hipStream_t, const FitNet<T>&, int rows, const T* D, const T* Tt, long ldt,
+                    int L3, const FitBufs<T>&, T* dD, double* e_bucket);
+// Tt column-major in bucket order (element (pos, a, m) at Tt[a * 4 nloc +
+// 4 pos + m]), dT in atom order (items maps bucket position to atom).
 template <class T>
-void launch_dT(hipStream_t, int nloc, int L3, int axis, const int* items, const T* Tm, const T* dD,
+void launch_dT(hipStream_t, int nloc, int L3, int axis, const int* items, const T* Tt, const T* dD,
                T* dT);
 
 // Force / virial stage
