@@ -56,7 +56,8 @@ def flops_bytes(pot, n_real, nloc, nb_edges):
         "embed_fwd": ("flop", emb_fwd * n_real),
         "embed_bwd": ("flop", emb_vjp * n_real),
         "fitting": ("flop", fit * nloc),
-        "descriptor": ("byte", 8.0 * nloc * (nt * 4 * L3 + 4 * L3 + Dn)),
+        # reads the section sums, writes T (the first fitting GEMM forms D from T)
+        "descriptor": ("byte", 8.0 * nloc * (nt * 4 * L3 + 4 * L3)),
         "dE_dT": ("byte", 8.0 * nloc * (Dn + 4 * L3 + 4 * L3)),
         # edge gradient (24 B) + reverse index (4 B) per edge, force 24 B per atom
         "force": ("byte", 28.0 * nb_edges + 24.0 * nloc),
