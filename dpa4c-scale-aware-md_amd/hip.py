@@ -77,6 +77,13 @@ class DeviceArray:
         else:
             check(hip().hipMemset(self.ptr, 0, max(self.nbytes, 8)))
 
+    def upload(self, host: np.ndarray):
+        """Copy a host array of exactly this allocation's size into it."""
+        h = np.ascontiguousarray(host)
+        if h.nbytes != self.nbytes:
+            raise ValueError(f"upload of {h.nbytes} bytes into a {self.nbytes}-byte buffer")
+        check(hip().hipMemcpy(self.ptr, h.ctypes.data, self.nbytes, H2D))
+
     def to_host(self, dtype, shape) -> np.ndarray:
         out = np.empty(shape, dtype=dtype)
         assert out.nbytes == self.nbytes
