@@ -122,12 +122,26 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     }
     const double s = Rn[0];
 
-    // layer 1 -> B operand of layer 2 (feature 4q+g of slot c)
+    // layer 1 -> B operand of layer 2 (feature 4q+g of slot c); four at a
+    // time (shared reciprocal) when every feature is real
     double x1[S::NQ2];
+    if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
 #pragma unroll
-    for (int q = 0; q < S::NQ2; ++q) {
-      const int f = 4 * q + g;
-      x1[q] = (f < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
+      for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
+        double z[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int f = 4 * (q0 + j) + g;
+          z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
+        }
+        tanh_fast4(z, x1 + q0);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < S::NQ2; ++q) {
+        const int f = 4 * q + g;
+        x1[q] = (f < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
+      }
     }
     // layer 2, transposed
     d4 acc2[S::NT2];
@@ -142,10 +156,14 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     double x2[S::NT2][4];
 #pragma unroll
     for (int t = 0; t < S::NT2; ++t) {
+      double z2[4], th2v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z2[r] = acc2[t][r] + P[S::OFF_B2 + 16 * t + 4 * r + g];
+      tanh_fast4(z2, th2v);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int f = 16 * t + 4 * r + g;
-        const double th = tanh_fast(acc2[t][r] + P[S::OFF_B2 + f]);
+        const double th = th2v[r];
         act2[(4 * t + r) * 64] = th;
         double res = 0.0;
         if constexpr (S::RES2 != 0) {
@@ -196,10 +214,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
         const int u = u0 + uu;
         if (u < S::NU3) {
           const int f = 16 * u + c;
+          double z3[4], th3v[4];
+          const double b3 = P[S::OFF_B3 + f];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) z3[r] = acc3[uu][r] + b3;
+          tanh_fast4(z3, th3v);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int sl = g + 4 * r;
-            const double th = tanh_fast(acc3[uu][r] + P[S::OFF_B3 + f]);
+            const double th = th3v[r];
             // backward order: feature 16u + 4(c>>2) + (c&3) of slot sl
             act3[256 * u + 16 * r] = th;
             double G = th;
@@ -332,17 +355,35 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 
     // layer 1 (recomputed, elementwise) and its tangent
     double x1[S::NQ2], x1t[S::NQ2];
+    if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
 #pragma unroll
-    for (int q = 0; q < S::NQ2; ++q) {
-      const int f = 4 * q + g;
-      if (f < S::L1) {
-        const double wv = P[S::OFF_W1 + f];
-        const double th = tanh_fast(s * wv + P[S::OFF_B1 + f]);
-        x1[q] = th;
-        x1t[q] = (1.0 - th * th) * wv;
-      } else {
-        x1[q] = 0.0;
-        x1t[q] = 0.0;
+      for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
+        double z[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int f = 4 * (q0 + j) + g;
+          z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
+        }
+        tanh_fast4(z, x1 + q0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const double th = x1[q0 + j];
+          x1t[q0 + j] = (1.0 - th * th) * P[S::OFF_W1 + 4 * (q0 + j) + g];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < S::NQ2; ++q) {
+        const int f = 4 * q + g;
+        if (f < S::L1) {
+          const double wv = P[S::OFF_W1 + f];
+          const double th = tanh_fast(s * wv + P[S::OFF_B1 + f]);
+          x1[q] = th;
+          x1t[q] = (1.0 - th * th) * wv;
+        } else {
+          x1[q] = 0.0;
+          x1t[q] = 0.0;
+        }
       }
     }
     // layer 2: tangent product only; tanh of the primal comes from the forward

@@ -150,6 +150,20 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int col = col0 + 16 * n + c;
+    // forward epilogue: the four tanh of this column at once (fp64: shared
+    // reciprocal; rows past M hold zeros and are not stored)
+    T th[4];
+    if (a.epi == 1) {
+      T z[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
+      if constexpr (sizeof(T) == 8) {
+        tanh_fast4(z, th);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) th[r] = tanh_act(z[r]);
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = row0 + 16 * w + Frag<T>::row(g, r);
@@ -159,7 +173,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
       if (a.epi == 0) {
         a.C[o] = v;
       } else if (a.epi == 1) {
-        const T t = tanh_act(v + a.bias[col]);
+        const T t = th[r];
         if (a.T_out) a.T_out[o] = t;
         a.C[o] = a.idt ? a.A[(long)row * a.lda + col] + a.idt[col] * t : t;
       } else {

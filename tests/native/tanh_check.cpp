@@ -32,5 +32,20 @@ int main() {
   for (int k = -300; k < 3; ++k) { check(std::ldexp(1.0, k)); check(-std::ldexp(1.3, k)); }
   check(0.0);
   std::printf("max_ulp %.3f at x=%.17g max_abs %.3e\n", max_ulp, worst, max_abs);
-  return max_abs <= 4e-15 ? 0 : 1;
+  // four at a time (shared reciprocal): mixed magnitudes, including the clamp
+  double max_abs4 = 0;
+  std::uniform_real_distribution<double> W(-1.0, 1.0);
+  for (int i = 0; i < 2000000; ++i) {
+    double x[4], y[4];
+    for (int k = 0; k < 4; ++k) x[k] = (i % 3 == 0) ? U(g) : W(g) * std::pow(10.0, (i % 7) - 4);
+    if (i % 11 == 0) x[i % 4] = (i % 2 ? 25.0 : -30.0);
+    if (i % 13 == 0) x[(i + 1) % 4] = 0.0;
+    dpamd::tanh_fast4(x, y);
+    for (int k = 0; k < 4; ++k) max_abs4 = std::fmax(max_abs4, std::fabs(y[k] - std::tanh(x[k])));
+  }
+  double z4[4], zx[4] = {0.0, -0.0, 0.0, 0.0};
+  dpamd::tanh_fast4(zx, z4);
+  const bool zeros = z4[0] == 0.0 && z4[1] == 0.0;
+  std::printf("tanh_fast4 max_abs %.3e, tanh(0) exact %d\n", max_abs4, (int)zeros);
+  return (max_abs <= 4e-15 && max_abs4 <= 4e-15 && zeros) ? 0 : 1;
 }
