@@ -72,6 +72,15 @@ def test_tanh_fast_accuracy(tmp_path):
     assert r.returncode == 0, r.stdout + r.stderr
 
 
+def test_embedding_layouts_agree(tmp_path):
+    """Host packing layout == the kernels' compile-time layout (fp64 and fp32)."""
+    exe = tmp_path / "layout_check"
+    subprocess.run(["g++", "-O1", "-std=c++17", "-o", str(exe),
+                    os.path.join(ROOT, "tests", "native", "layout_check.cpp")], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
 def build_facade(tmp_path):
     exe = tmp_path / "facade_check"
     subprocess.run(["g++", "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"),
