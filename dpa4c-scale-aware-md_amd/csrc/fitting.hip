@@ -209,80 +209,87 @@ __global__ __launch_bounds__(256) void k_head(int rows, int F2, const T* __restr
 }
 
 // dT[m][a] = sum_b dD[a][b] T[m][b] + (a < axis) sum_a' dD[a'][a] T[m][a'].
-// One wave per atom, axis == 16, L3 <= 128. The atom's dD block (L3 x 16) is
-// read coalesced and stored transposed in LDS (row b, padded stride), so
-// neither term needs a cross-lane reduction: lane a (and a + 64) owns row a
-// of the first term, lane (m, b) = (lane / 16, lane % 16) owns entry (m, b)
-// of the second; the first-term values of rows a < 16 meet their second term
-// through LDS.
-constexpr int kDtWaves = 2;
+// One wave per atom, axis == 16, L3 <= 128, L3 % 4 == 0. dD is read as it
+// lies, 4 rows per wave instruction: lane (g, c) = (lane / 16, lane % 16)
+// holds v = dD[a0 + g][c].
+//   First term: the lane's four products v T[m][c] are summed over the 16
+//   lanes of its row by a transposing reduction (xor 8 and 4 exchange halves
+//   of the lanes' value sets, xor 2 and 1 finish), which leaves lane c with
+//   the sum for m = c / 4: five exchanges per row instead of sixteen.
+//   Second term: lane c owns column b = c and accumulates v T[m][a] over its
+//   rows; the four row groups are folded at the end (xor 16, 32).
+// The first-term values of rows a < 16 meet their second term through LDS.
+constexpr int kDtWaves = 4;
 template <class T>
 __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
                                                      const int* __restrict__ items,
                                                      const T* __restrict__ Tt,
                                                      const T* __restrict__ dD,
                                                      T* __restrict__ dT) {
-  constexpr int AX = 16, LDT = 128 + 1;
-  __shared__ T Dt[kDtWaves][AX * LDT];
+  constexpr int AX = 16;
   __shared__ T Ts[kDtWaves][4 * 128];
   __shared__ T F16[kDtWaves][4 * AX];
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int pos = blockIdx.x * kDtWaves + w;
   if (pos >= nb) return;
   const int i = items[pos];
   // T of this position from the column-major copy: element (a, m) at
   // Tt[a * 4 nb + 4 pos + m]
   const T* Ti = Tt + 4 * (long)pos;
-  for (int q = lane; q < 4 * L3; q += 64) Ts[w][(q & 3) * L3 + (q >> 2)] = Ti[(long)(q >> 2) * 4 * nb + (q & 3)];
+  for (int q = lane; q < 4 * L3; q += 64)
+    Ts[w][(q & 3) * L3 + (q >> 2)] = Ti[(long)(q >> 2) * 4 * nb + (q & 3)];
+  wave_lds_sync();
+  const T tb0 = Ts[w][c], tb1 = Ts[w][L3 + c], tb2 = Ts[w][2 * L3 + c], tb3 = Ts[w][3 * L3 + c];
+  const bool hi8 = (c & 8) != 0, hi4 = (c & 4) != 0;
+  const int mine = c >> 2;  // the m whose first-term sum this lane ends with
   const T* dDp = dD + (long)pos * L3 * AX;
-  const int ne = L3 * AX;  // multiple of 64 (L3 % 4 == 0)
-  for (int e0 = 0; e0 < ne; e0 += 64 * 8) {
-    T v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int e = e0 + 64 * u + lane;
-      v[u] = e < ne ? dDp[e] : T(0);
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int e = e0 + 64 * u + lane;
-      if (e < ne) Dt[w][(e & 15) * LDT + (e >> 4)] = v[u];
-    }
-  }
-  wave_lds_sync();
   T* out = dT + (long)i * 4 * L3;
-  // first term
-  for (int a = lane; a < L3; a += 64) {
-    T acc0 = 0, acc1 = 0, acc2 = 0, acc3 = 0;
+  T s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+  for (int a0b = 0; a0b < L3; a0b += 32) {
+    T vb[8];
 #pragma unroll
-    for (int b = 0; b < AX; ++b) {
-      const T d = Dt[w][b * LDT + a];
-      acc0 += d * Ts[w][b];
-      acc1 += d * Ts[w][L3 + b];
-      acc2 += d * Ts[w][2 * L3 + b];
-      acc3 += d * Ts[w][3 * L3 + b];
-    }
-    if (a >= AX) {
-      out[a] = acc0;
-      out[L3 + a] = acc1;
-      out[2 * L3 + a] = acc2;
-      out[3 * L3 + a] = acc3;
-    } else {
-      F16[w][a] = acc0;
-      F16[w][AX + a] = acc1;
-      F16[w][2 * AX + a] = acc2;
-      F16[w][3 * AX + a] = acc3;
+    for (int u = 0; u < 8; ++u) vb[u] = a0b + 4 * u < L3 ? dDp[(a0b + 4 * u) * AX + lane] : T(0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int a0 = a0b + 4 * u;
+      if (a0 >= L3) break;
+      const int a = a0 + g;
+      const T v = vb[u];
+      s0 += v * Ts[w][a];
+      s1 += v * Ts[w][L3 + a];
+      s2 += v * Ts[w][2 * L3 + a];
+      s3 += v * Ts[w][3 * L3 + a];
+      const T p0 = v * tb0, p1 = v * tb1, p2 = v * tb2, p3 = v * tb3;
+      // xor 8: keep the pair {m = 2 hi8, 2 hi8 + 1}, send the other
+      const T k0 = hi8 ? p2 : p0, k1 = hi8 ? p3 : p1;
+      const T q0 = k0 + shfl_xor_d(hi8 ? p0 : p2, 8);
+      const T q1 = k1 + shfl_xor_d(hi8 ? p1 : p3, 8);
+      // xor 4: keep m = 2 hi8 + hi4
+      T r = (hi4 ? q1 : q0) + shfl_xor_d(hi4 ? q0 : q1, 4);
+      r += shfl_xor_d(r, 2);
+      r += shfl_xor_d(r, 1);
+      // lane c (c % 4 == 0) of row group g holds dT1[mine][a]
+      if ((c & 3) == 0) {
+        if (a >= AX) out[mine * L3 + a] = r;
+        else F16[w][mine * AX + a] = r;
+      }
     }
   }
-  // second term
-  const int m = lane >> 4, b = lane & 15;
-  T s = 0;
-  const T* Tr = Ts[w] + m * L3;
-  const T* Dr = Dt[w] + b * LDT;
-#pragma unroll 4
-  for (int a = 0; a < L3; ++a) s += Dr[a] * Tr[a];
+  s0 += shfl_xor_d(s0, 16);
+  s0 += shfl_xor_d(s0, 32);
+  s1 += shfl_xor_d(s1, 16);
+  s1 += shfl_xor_d(s1, 32);
+  s2 += shfl_xor_d(s2, 16);
+  s2 += shfl_xor_d(s2, 32);
+  s3 += shfl_xor_d(s3, 16);
+  s3 += shfl_xor_d(s3, 32);
   wave_lds_sync();
-  out[m * L3 + b] = F16[w][m * AX + b] + s;
+  if (g == 0) {
+    out[c] = F16[w][c] + s0;
+    out[L3 + c] = F16[w][AX + c] + s1;
+    out[2 * L3 + c] = F16[w][2 * AX + c] + s2;
+    out[3 * L3 + c] = F16[w][3 * AX + c] + s3;
+  }
 }
 
 template <class T, int NT, bool TRANSB, bool AT = false>
