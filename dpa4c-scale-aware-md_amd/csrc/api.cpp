@@ -302,8 +302,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   E* fitb = need<E>(M, M->fitb, (size_t)8 * std::max(nb, 1) * Fmax);
   double* e_bucket = need<double>(M, M->e_bucket, (size_t)std::max(nb, 1));
   double* edge_grad = need<double>(M, M->edge_grad, (size_t)nloc * nnei * 3);
-  double* cpart = need<double>(M, M->cpart, (size_t)nloc * nt * 12);
-  DPAMD_HIP(hipMemsetAsync(cpart, 0, sizeof(double) * (size_t)nloc * nt * 12, st));
+  double* cpart = need<double>(M, M->cpart, (size_t)std::max(nloc, 1) * 12);
 
   EmbArgs ea{};
   ea.ntypes = nt;
@@ -327,7 +326,6 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   ea.Tsec = Tsec;
   ea.dT = dT;
   ea.edge_grad = edge_grad;
-  ea.cpart = cpart;
   {
     int acc = 0;
     for (int t = 0; t < nt; ++t) {
@@ -393,7 +391,6 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   nblk = block_table(embed_waves_bwd(M->el, f32));
   launch_embed_bwd(st, M->el, ea, nblk, f32);
   record(M, st, kStEmbBwd + 1);
-  launch_center_sum(st, nloc, nt, nnei, nlist, ext, edge_grad, cpart);
 
   // reverse list + gather
   const long nedge = (long)nloc * nnei;
@@ -410,13 +407,13 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
     exclusive_scan_int(st, rcount, roff, ntarget + 1, tmp, tb);
   }
   launch_rev_fill(st, nedge, nnei, nlist, d_mapping, roff, rcur, rev);
-  launch_force_gather(st, ntarget, nloc, nt, nnei, roff, rev, nlist, ext, edge_grad, cpart,
+  launch_force_gather(st, ntarget, nloc, nnei, roff, rev, nlist, ext, edge_grad, cpart,
                       out.force, out.atom_virial, status);
   record(M, st, kStForce + 1);
 
   double* partials = need<double>(M, M->partials, 256 * 10);
   double* out10 = need<double>(M, M->out10, 10);
-  launch_reduce_ev(st, nb, nloc, nt, e_bucket, cpart, partials, out10);
+  launch_reduce_ev(st, nb, nloc, e_bucket, cpart, partials, out10);
   if (out.energy) DPAMD_HIP(hipMemcpyAsync(out.energy, out10, 8, hipMemcpyDeviceToDevice, st));
   if (out.virial)
     DPAMD_HIP(hipMemcpyAsync(out.virial, out10 + 1, 72, hipMemcpyDeviceToDevice, st));

@@ -2,15 +2,17 @@
 // the deterministic energy / virial reduction.
 //
 // Every edge e = (centre i, slot) with neighbour j contributes +g_e to the
-// centre (summed inside the backward kernel, cpart) and -g_e to the target
-// atom t = mapping[j] (standalone: ghost images folded onto owners) or t = j
-// (LAMMPS path: ghost slots kept for reverse communication). The reverse list
-// is built by count / scan / fill; each target's edges are then ranked by edge
-// id in LDS so the sum order is fixed and the result bit-reproducible, with
-// no floating-point atomics. Atom virial -g (x) (x_j - x_i) is charged to the
-// target, as in deepmd-op/overlays/op/pt/edge_force_virial.cu:1-14, :138-146
-// (dual-CSR gather, one warp per node there, one 64-lane wave here). The frame
-// sums follow the fixed two-stage fp64 reduction of edge_force_virial.cu:187-256.
+// centre and -g_e to the target atom t = mapping[j] (standalone: ghost images
+// folded onto owners) or t = j (LAMMPS path: ghost slots kept for reverse
+// communication). One wave per atom t sums both sides: its own row of edges
+// (t < nloc, coalesced) and the edges pointing at it, found through a reverse
+// list built by count / scan / fill. The incoming edges are ranked by edge id
+// in LDS first, so the sum order is fixed and the result bit-reproducible,
+// with no floating-point atomics. Atom virial -g (x) (x_j - x_i) is charged to
+// the target, as in deepmd-op/overlays/op/pt/edge_force_virial.cu:1-14,
+// :138-146 (dual-CSR gather, one warp per node there, one 64-lane wave here);
+// the frame virial is summed per centre from its own row. The frame sums
+// follow the fixed two-stage fp64 reduction of edge_force_virial.cu:187-256.
 #include "kernels.h"
 
 namespace dpamd {
@@ -37,10 +39,36 @@ __global__ void k_rev_fill(long nedge, const int* __restrict__ nlist,
 
 constexpr int kGatherWaves = 4;
 
+// Sort this wave's incoming edge ids (s_in[0..n)) into s_out by rank: one
+// pass over the list ranks all K ids a lane holds (q = lane + 64k). Edge ids
+// are distinct.
+template <int K>
+__device__ __forceinline__ void rank_edges(int n, const int* s_in, int* s_out) {
+  const int lane = threadIdx.x & 63;
+  int ek[K], rank[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int q = lane + 64 * k;
+    ek[k] = q < n ? s_in[q] : 0x7fffffff;
+    rank[k] = 0;
+  }
+  for (int p = 0; p < n; ++p) {
+    const int o = s_in[p];
+#pragma unroll
+    for (int k = 0; k < K; ++k) rank[k] += o < ek[k] ? 1 : 0;
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (lane + 64 * k < n) s_out[rank[k]] = ek[k];
+}
+
+// force[t] = sum over t's own row of g (t < nloc) - sum over edges into t of g;
+// atom_virial[t] = -sum over edges into t of g (x) d; cpart[t] (t < nloc) =
+// the row's force and frame-virial sums (3 + 9).
 __global__ __launch_bounds__(kGatherWaves * 64) void k_force_gather(
-    int ntarget, int nloc, int ntypes, int nnei, const int* __restrict__ rev_off,
+    int ntarget, int nloc, int nnei, const int* __restrict__ rev_off,
     const int* __restrict__ rev, const int* __restrict__ nlist, const double* __restrict__ ext,
-    const double* __restrict__ edge_grad, const double* __restrict__ cpart,
+    const double* __restrict__ edge_grad, double* __restrict__ cpart,
     double* __restrict__ force, double* __restrict__ atom_virial, int* __restrict__ status) {
   __shared__ int s_in[kGatherWaves][kMaxRev];
   __shared__ int s_sorted[kGatherWaves][kMaxRev];
@@ -54,12 +82,33 @@ __global__ __launch_bounds__(kGatherWaves * 64) void k_force_gather(
     n = kMaxRev;
   }
   for (int q = lane; q < n; q += 64) s_in[w][q] = rev[beg + q];
+  // own row (centre side) while the reverse ids land in LDS
+  double fo[3] = {0.0, 0.0, 0.0};
+  double vo[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  if (t < nloc) {
+    const double xi = ext[3 * (long)t], yi = ext[3 * (long)t + 1], zi = ext[3 * (long)t + 2];
+    for (int sl = lane; sl < nnei; sl += 64) {
+      const long e = (long)t * nnei + sl;
+      const long j = nlist[e];
+      if (j < 0) continue;
+      const double g[3] = {edge_grad[3 * e], edge_grad[3 * e + 1], edge_grad[3 * e + 2]};
+      const double d[3] = {ext[3 * j] - xi, ext[3 * j + 1] - yi, ext[3 * j + 2] - zi};
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        fo[a] += g[a];
+#pragma unroll
+        for (int b = 0; b < 3; ++b) vo[3 * a + b] -= g[a] * d[b];
+      }
+    }
+  }
   wave_lds_sync();
-  for (int q = lane; q < n; q += 64) {
-    const int eq = s_in[w][q];
-    int rank = 0;
-    for (int p = 0; p < n; ++p) rank += (s_in[w][p] < eq) ? 1 : 0;
-    s_sorted[w][rank] = eq;
+  switch ((n + 63) / 64) {
+    case 0: break;
+    case 1: rank_edges<1>(n, s_in[w], s_sorted[w]); break;
+    case 2: rank_edges<2>(n, s_in[w], s_sorted[w]); break;
+    case 3: rank_edges<3>(n, s_in[w], s_sorted[w]); break;
+    case 4: rank_edges<4>(n, s_in[w], s_sorted[w]); break;
+    default: rank_edges<kMaxRev / 64>(n, s_in[w], s_sorted[w]); break;
   }
   wave_lds_sync();
   double f[3] = {0.0, 0.0, 0.0};
@@ -85,73 +134,38 @@ __global__ __launch_bounds__(kGatherWaves * 64) void k_force_gather(
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
 #pragma unroll
-    for (int q = 0; q < 3; ++q) f[q] += shfl_xor_d(f[q], off);
+    for (int q = 0; q < 3; ++q) {
+      f[q] += shfl_xor_d(f[q], off);
+      fo[q] += shfl_xor_d(fo[q], off);
+    }
     if (atom_virial) {
 #pragma unroll
       for (int q = 0; q < 9; ++q) v[q] += shfl_xor_d(v[q], off);
     }
+    if (t < nloc) {
+#pragma unroll
+      for (int q = 0; q < 9; ++q) vo[q] += shfl_xor_d(vo[q], off);
+    }
   }
   if (lane == 0) {
     if (t < nloc) {
-      for (int tj = 0; tj < ntypes; ++tj) {
-        const double* cp = cpart + ((long)t * ntypes + tj) * 12;
-        f[0] += cp[0];
-        f[1] += cp[1];
-        f[2] += cp[2];
-      }
+      double* cp = cpart + (long)t * 12;
+      for (int q = 0; q < 3; ++q) cp[q] = fo[q];
+      for (int q = 0; q < 9; ++q) cp[3 + q] = vo[q];
     }
-    force[3 * (long)t] = f[0];
-    force[3 * (long)t + 1] = f[1];
-    force[3 * (long)t + 2] = f[2];
+    force[3 * (long)t] = f[0] + fo[0];
+    force[3 * (long)t + 1] = f[1] + fo[1];
+    force[3 * (long)t + 2] = f[2] + fo[2];
     if (atom_virial)
       for (int q = 0; q < 9; ++q) atom_virial[9 * (long)t + q] = v[q];
-  }
-}
-
-// Centre side of every edge: sum_slots g (force on the centre) and
-// sum_slots -g (x) (x_j - x_i) (frame virial), one wave per centre, written to
-// section 0 of cpart (the other sections stay zero).
-__global__ __launch_bounds__(kGatherWaves * 64) void k_center_sum(
-    int nloc, int ntypes, int nnei, const int* __restrict__ nlist, const double* __restrict__ ext,
-    const double* __restrict__ edge_grad, double* __restrict__ cpart) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i = blockIdx.x * kGatherWaves + w;
-  if (i >= nloc) return;
-  const double xi = ext[3 * (long)i], yi = ext[3 * (long)i + 1], zi = ext[3 * (long)i + 2];
-  double f[3] = {0.0, 0.0, 0.0};
-  double v[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
-  for (int sl = lane; sl < nnei; sl += 64) {
-    const long e = (long)i * nnei + sl;
-    const long j = nlist[e];
-    if (j < 0) continue;
-    const double g[3] = {edge_grad[3 * e], edge_grad[3 * e + 1], edge_grad[3 * e + 2]};
-    const double d[3] = {ext[3 * j] - xi, ext[3 * j + 1] - yi, ext[3 * j + 2] - zi};
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-      f[a] += g[a];
-#pragma unroll
-      for (int b = 0; b < 3; ++b) v[3 * a + b] -= g[a] * d[b];
-    }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-#pragma unroll
-    for (int q = 0; q < 3; ++q) f[q] += shfl_xor_d(f[q], off);
-#pragma unroll
-    for (int q = 0; q < 9; ++q) v[q] += shfl_xor_d(v[q], off);
-  }
-  if (lane == 0) {
-    double* out = cpart + (long)i * ntypes * 12;
-    for (int q = 0; q < 3; ++q) out[q] = f[q];
-    for (int q = 0; q < 9; ++q) out[3 + q] = v[q];
   }
 }
 
 constexpr int kRedBlocks = 256;
 
 // Stage 1: block b sums energies of bucket positions and centre virials of
-// sections b, b + 256, ...; stage 2 (one block) adds the 256 partials in order.
-__global__ __launch_bounds__(256) void k_reduce_ev1(int nbucket, int nloc, int ntypes,
+// centres b, b + 256, ...; stage 2 (one block) adds the 256 partials in order.
+__global__ __launch_bounds__(256) void k_reduce_ev1(int nbucket, int nloc,
                                                     const double* __restrict__ e_bucket,
                                                     const double* __restrict__ cpart,
                                                     double* __restrict__ partials) {
@@ -161,8 +175,7 @@ __global__ __launch_bounds__(256) void k_reduce_ev1(int nbucket, int nloc, int n
   for (int q = 0; q < 10; ++q) acc[q] = 0.0;
   const long stride = (long)kRedBlocks * 256;
   for (long p = (long)blockIdx.x * 256 + threadIdx.x; p < nbucket; p += stride) acc[0] += e_bucket[p];
-  const long nsec = (long)nloc * ntypes;
-  for (long s = (long)blockIdx.x * 256 + threadIdx.x; s < nsec; s += stride)
+  for (long s = (long)blockIdx.x * 256 + threadIdx.x; s < nloc; s += stride)
     for (int q = 0; q < 9; ++q) acc[1 + q] += cpart[s * 12 + 3 + q];
   for (int q = 0; q < 10; ++q) sm[q][threadIdx.x] = acc[q];
   __syncthreads();
@@ -210,30 +223,21 @@ void launch_rev_fill(hipStream_t st, long nedge, int, const int* nlist, const in
   DPAMD_LAUNCH_CHECK();
 }
 
-void launch_force_gather(hipStream_t st, int ntarget, int nloc, int ntypes, int nnei,
-                         const int* rev_off, const int* rev, const int* nlist, const double* ext,
-                         const double* edge_grad, const double* cpart, double* force,
+void launch_force_gather(hipStream_t st, int ntarget, int nloc, int nnei, const int* rev_off,
+                         const int* rev, const int* nlist, const double* ext,
+                         const double* edge_grad, double* cpart, double* force,
                          double* atom_virial, int* status) {
   if (ntarget <= 0) return;
   hipLaunchKernelGGL(k_force_gather, dim3((ntarget + kGatherWaves - 1) / kGatherWaves),
-                     dim3(kGatherWaves * 64), 0, st, ntarget, nloc, ntypes, nnei, rev_off, rev,
-                     nlist, ext, edge_grad, cpart, force, atom_virial, status);
+                     dim3(kGatherWaves * 64), 0, st, ntarget, nloc, nnei, rev_off, rev, nlist,
+                     ext, edge_grad, cpart, force, atom_virial, status);
   DPAMD_LAUNCH_CHECK();
 }
 
-void launch_center_sum(hipStream_t st, int nloc, int ntypes, int nnei, const int* nlist,
-                       const double* ext, const double* edge_grad, double* cpart) {
-  if (nloc <= 0) return;
-  hipLaunchKernelGGL(k_center_sum, dim3((nloc + kGatherWaves - 1) / kGatherWaves),
-                     dim3(kGatherWaves * 64), 0, st, nloc, ntypes, nnei, nlist, ext, edge_grad,
-                     cpart);
-  DPAMD_LAUNCH_CHECK();
-}
-
-void launch_reduce_ev(hipStream_t st, int nbucket, int nloc, int ntypes, const double* e_bucket,
+void launch_reduce_ev(hipStream_t st, int nbucket, int nloc, const double* e_bucket,
                       const double* cpart, double* partials, double* out10) {
-  hipLaunchKernelGGL(k_reduce_ev1, dim3(kRedBlocks), dim3(256), 0, st, nbucket, nloc, ntypes,
-                     e_bucket, cpart, partials);
+  hipLaunchKernelGGL(k_reduce_ev1, dim3(kRedBlocks), dim3(256), 0, st, nbucket, nloc, e_bucket,
+                     cpart, partials);
   DPAMD_LAUNCH_CHECK();
   hipLaunchKernelGGL(k_reduce_ev2, dim3(1), dim3(256), 0, st, partials, out10);
   DPAMD_LAUNCH_CHECK();

@@ -56,7 +56,6 @@ struct EmbArgs {
   void* Tsec;          // forward out [nloc][ntypes][4][L3]
   const void* dT;      // backward in [nloc][4][L3]
   double* edge_grad;   // backward out [nloc][nnei][3]
-  double* cpart;       // [nloc][ntypes][12]: centre force 3 + virial 9 (section 0 used)
   // Saved activations: per (centre, tile of 16 slots) a block of
   // 16*(L2P + L3P) doubles holding tanh of layers 2 and 3 in the backward's
   // register order; tiles of section tj start at tile_off[tj], tiles_per_atom
@@ -152,15 +151,14 @@ void launch_rev_count(hipStream_t, long nedge, int nnei, const int* nlist, const
                       int* count);
 void launch_rev_fill(hipStream_t, long nedge, int nnei, const int* nlist, const int* mapping,
                      const int* off, int* cursor, int* rev);
-void launch_force_gather(hipStream_t, int ntarget, int nloc, int ntypes, int nnei,
-                         const int* rev_off, const int* rev, const int* nlist, const double* ext,
-                         const double* edge_grad, const double* cpart, double* force,
+// cpart [nloc][12]: each centre's own-row force (3) and frame virial (9),
+// written by the gather and summed by the reduction.
+void launch_force_gather(hipStream_t, int ntarget, int nloc, int nnei, const int* rev_off,
+                         const int* rev, const int* nlist, const double* ext,
+                         const double* edge_grad, double* cpart, double* force,
                          double* atom_virial, int* status);
-void launch_center_sum(hipStream_t, int nloc, int ntypes, int nnei, const int* nlist,
-                       const double* ext, const double* edge_grad, double* cpart);
-void launch_reduce_ev(hipStream_t, int nbucket, int nloc, int ntypes,
-                      const double* atom_energy_bucket, const double* cpart, double* partials,
-                      double* out10);
+void launch_reduce_ev(hipStream_t, int nbucket, int nloc, const double* atom_energy_bucket,
+                      const double* cpart, double* partials, double* out10);
 void launch_scatter_energy(hipStream_t, int nloc, const int* items, const double* e_bucket,
                            double* atom_energy);
 
