@@ -263,6 +263,12 @@ __device__ __forceinline__ void nl_empty_row(const NlParams& np, int i, int* __r
   if (lane < np.ntypes) nreal[(long)i * np.ntypes + lane] = 0;
 }
 
+// The 27-cell stencil as 9 contiguous runs of the cell-sorted atoms (cells
+// x-1..x+1 of one (y, z) row are adjacent in cell order). Lanes 0..8 read the
+// run bounds at once; candidate q of the concatenated runs is then found by
+// counting run offsets <= q, so the candidates of a wave-wide batch are loaded
+// independently (four rounds of 64 in flight) instead of cell after cell.
+// Candidate order does not matter: the rank pass orders by (type, r^2, j).
 __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells(
     int nloc, BoxParams bp, NlParams np, const double* __restrict__ ext,
     const int* __restrict__ ext_type, const int* __restrict__ cell_of,
@@ -281,33 +287,56 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells(
   const int ci = cell_of[i];
   const int c0 = ci % bp.ncell[0], c1 = (ci / bp.ncell[0]) % bp.ncell[1];
   const int c2 = ci / (bp.ncell[0] * bp.ncell[1]);
+  int rbeg = 0, rcnt = 0;
+  if (lane < 9) {
+    const int y = c1 + lane % 3 - 1, z = c2 + lane / 3 - 1;
+    if (y >= 0 && y < bp.ncell[1] && z >= 0 && z < bp.ncell[2]) {
+      const int x0 = c0 > 0 ? c0 - 1 : 0, x1 = c0 + 1 < bp.ncell[0] ? c0 + 1 : bp.ncell[0] - 1;
+      const int rowc = (z * bp.ncell[1] + y) * bp.ncell[0];
+      rbeg = cell_start[rowc + x0];
+      rcnt = cell_start[rowc + x1 + 1] - rbeg;
+    }
+  }
+  int incl = rcnt;
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) {
+    const int v = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += v;
+  }
+  const int total = __shfl(incl, 8, kWave);
+  int roff[9], rdel[9];  // run start in the concatenation, and sorted index - q
+#pragma unroll
+  for (int k = 0; k < 9; ++k) {
+    roff[k] = __shfl(incl - rcnt, k, kWave);
+    rdel[k] = __shfl(rbeg, k, kWave) - roff[k];
+  }
   int n = 0;
-  for (int z = c2 - 1; z <= c2 + 1; ++z) {
-    if (z < 0 || z >= bp.ncell[2]) continue;
-    for (int y = c1 - 1; y <= c1 + 1; ++y) {
-      if (y < 0 || y >= bp.ncell[1]) continue;
-      for (int x = c0 - 1; x <= c0 + 1; ++x) {
-        if (x < 0 || x >= bp.ncell[0]) continue;
-        const int cc = (z * bp.ncell[1] + y) * bp.ncell[0] + x;
-        const int beg = cell_start[cc], end = cell_start[cc + 1];
-        for (int base = beg; base < end; base += kWave) {
-          const int p = base + lane;
-          bool keep = false;
-          double r2 = 0.0;
-          int j = -1, t = -1;
-          if (p < end) {
-            const CellAtom a = sorted[p];
-            j = a.idx;
-            t = a.type;
-            const double dx = a.x - xi;
-            const double dy = a.y - yi;
-            const double dz = a.z - zi;
-            r2 = dx * dx + dy * dy + dz * dz;
-            keep = (j != i) && t >= 0 && t < np.ntypes && r2 <= np.rc2;
-          }
-          nl_push(keep, r2, j, t, n, lds.k[w]);
-        }
+  for (int base = 0; base < total; base += 4 * kWave) {
+    CellAtom ca[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int q = base + kWave * u + lane;
+      ca[u].idx = -1;
+      if (q < total) {
+        int del = rdel[0];
+#pragma unroll
+        for (int k = 1; k < 9; ++k) del = roff[k] <= q ? rdel[k] : del;
+        ca[u] = sorted[q + del];
       }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      bool keep = false;
+      double r2 = 0.0;
+      const int j = ca[u].idx, t = ca[u].type;
+      if (j >= 0) {
+        const double dx = ca[u].x - xi;
+        const double dy = ca[u].y - yi;
+        const double dz = ca[u].z - zi;
+        r2 = dx * dx + dy * dy + dz * dz;
+        keep = (j != i) && t >= 0 && t < np.ntypes && r2 <= np.rc2;
+      }
+      nl_push(keep, r2, j, t, n, lds.k[w]);
     }
   }
   nl_place(np, i, n, lds.k[w], nlist, nreal, status);
