@@ -274,6 +274,7 @@ DescArgs desc_args(dp_model* M, void* Tt, void* D) {
   da.tpad = M->d_tpad;
   da.Tt = Tt;
   da.D = D;
+  da.from_tt = m.ntypes == 1;  // the forward wrote T itself
   return da;
 }
 
@@ -326,6 +327,9 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   ea.Tsec = Tsec;
   ea.dT = dT;
   ea.edge_grad = edge_grad;
+  ea.Tt = nt == 1 ? static_cast<void*>(Tt) : nullptr;
+  ea.ldt = 4L * nb;
+  ea.tpad = M->d_tpad;
   {
     int acc = 0;
     for (int t = 0; t < nt; ++t) {
@@ -353,7 +357,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   launch_embed_fwd(st, M->el, ea, nblk, f32);
   record(M, st, kStEmbFwd + 1);
 
-  launch_descriptor(st, desc_args(M, Tt, D), f32);
+  if (nt > 1 || D) launch_descriptor(st, desc_args(M, Tt, D), f32);
   record(M, st, kStDescr + 1);
 
   for (int t = 0; t < nt; ++t) {

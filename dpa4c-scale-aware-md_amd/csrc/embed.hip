@@ -243,7 +243,22 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     v += shfl_xor_d(v, 32);
     Tacc[q] = v;
   }
-  if (g == 0) {
+  if (g == 0 && a.Tt) {
+    // single neighbour type: this section is all of T
+    const double npad = (double)(a.sel[tj] - nr);
+    const double* tp = a.tpad + (long)p * 4 * S::L3;
+    double* Tt = static_cast<double*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
+#pragma unroll
+    for (int u = 0; u < S::NU3; ++u) {
+      const int f = 16 * u + c;
+      if (f < S::L3) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          Tt[f * a.ldt + m] =
+              (double)(((double)Tacc[u * 4 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
+      }
+    }
+  } else if (g == 0) {
     double* out = static_cast<double*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
 #pragma unroll
     for (int u = 0; u < S::NU3; ++u) {
@@ -536,6 +551,13 @@ __global__ __launch_bounds__(256) void k_descriptor(DescArgs a) {
   const int col = threadIdx.x & 127;
   for (int k = threadIdx.x >> 7; k < na; k += 2) {
     if (col >= L3) continue;
+    if (a.from_tt) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        Ts[(k * 4 + m) * LR + col] =
+            (double)static_cast<const E*>(a.Tt)[((long)col * a.nloc + pos0 + k) * 4 + m];
+      continue;
+    }
     const int i = a.items[pos0 + k];
     const int ti = a.ext_type[i];
 #pragma unroll
@@ -551,7 +573,7 @@ __global__ __launch_bounds__(256) void k_descriptor(DescArgs a) {
     }
   }
   __syncthreads();
-  {
+  if (!a.from_tt) {
     E* Tt = static_cast<E*>(a.Tt);
     for (int q = threadIdx.x; q < L3 * kDescAtoms * 4; q += blockDim.x) {
       const int km = q % (4 * kDescAtoms), c2 = q / (4 * kDescAtoms);  // km = 4k + m

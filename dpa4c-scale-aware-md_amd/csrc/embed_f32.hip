@@ -228,7 +228,22 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
     v += shfl_xor_d(v, 32);
     Tacc[q] = v;
   }
-  if (g == 0) {
+  if (g == 0 && a.Tt) {
+    // single neighbour type: this section is all of T
+    const double npad = (double)(a.sel[tj] - nr);
+    const double* tp = a.tpad + (long)p * 4 * S::L3;
+    float* Tt = static_cast<float*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
+#pragma unroll
+    for (int u = 0; u < S::NU3; ++u) {
+      const int f = 16 * u + c;
+      if (f < S::L3) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          Tt[f * a.ldt + m] =
+              (float)(((double)Tacc[u * 4 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
+      }
+    }
+  } else if (g == 0) {
     float* out = static_cast<float*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
 #pragma unroll
     for (int u = 0; u < S::NU3; ++u) {

@@ -63,6 +63,12 @@ struct EmbArgs {
   void* act;
   int tile_off[kMaxTypes + 1];
   int tiles_per_atom;
+  // With a single neighbour type the forward writes T itself, (Tsec + npad
+  // tpad) / nnei, into the column-major bucket layout Tt (element (pos, a, m)
+  // at Tt[a * ldt + 4 pos + m]) instead of Tsec; null otherwise.
+  void* Tt;
+  long ldt;
+  const double* tpad;  // [npair][4][L3]
 };
 
 struct DescArgs {
@@ -76,6 +82,7 @@ struct DescArgs {
   const double* tpad;  // [npair][4][L3]: Rpad[m] * Gpad[f], fp64 in both modes
   void* Tt;            // [L3][nloc][4] bucket order (T column-major)
   void* D;             // [nloc][L3*axis] bucket order, or null (not formed)
+  int from_tt;         // T is already in Tt (written by the forward): only form D
 };
 
 // Neighbour stage
