@@ -72,6 +72,7 @@ struct dp_model {
   double* d_tpad = nullptr;
   void* d_fit = nullptr;
   FitOffsets fo{};
+  void* blas = nullptr;  // rocBLAS handle for the plain input-gradient GEMM
   // workspace
   std::vector<Buf*> bufs;
   Buf coord_in, atype_in, sfrac, flags, gpos, ext, ext_type, mapping, cell_of, cell_count,
@@ -385,7 +386,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
     for (int q = 0; q < 8; ++q) *slots[q] = base + q * slab + r0 * (size_t)Fmax;
     launch_fitting(st, net, rows, d_from_t ? nullptr : D + r0 * Dn,
                    d_from_t ? Tt + r0 * 4 : nullptr, 4L * nb, L3, fb, dD + r0 * Dn,
-                   e_bucket + r0);
+                   e_bucket + r0, M->blas);
   }
   record(M, st, kStFit + 1);
 
@@ -611,6 +612,8 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
     }
     M->bytes_peak = M->bytes_now;
     M->fo = fit_offsets(m);
+    M->blas = blas_create();
+    if (!M->blas) throw ApiError{DP_ERR_NO_GPU, "rocblas_create_handle failed"};
   });
   if (rc != DP_OK) {
     // keep the handle so the caller can read dp_last_error, unless nothing usable
@@ -631,6 +634,7 @@ void dp_destroy(dp_model* M) {
     if (p) (void)hipFree(p);
   for (auto& e : M->ev)
     if (e) (void)hipEventDestroy(e);
+  blas_destroy(M->blas);
   delete M;
 }
 

@@ -11,6 +11,8 @@
 // e = h.w_head + b_head + bias_atom_e[type]
 // (deepmd-op/overlays/op/pt/graph_fitting.cu:1-25, :614-719); the reference's
 // fused tile analog is deepmd-op/overlays/op/pt/tiled_fitting.cuh:4-60.
+#include <rocblas/rocblas.h>
+
 #include "fastmath.h"
 #include "kernels.h"
 
@@ -325,9 +327,43 @@ static void gemm_at(hipStream_t st, const GemmArgs<T>& a) {
   else gemm_nt<T, 1, false, true>(st, a);
 }
 
+// dD = dZ0 W0^T (row-major [rows][Dn]; W0 row-major [Dn][F0]) through the
+// vendor BLAS: it is a plain GEMM with no epilogue, where rocBLAS' tuned
+// kernels beat this file's (measured on MI355X for rows 131072, Dn 2048, F0
+// 240: 2.03 vs 2.49 ms in fp64). In column-major terms C' = W0'^T A' with
+// C' = dD^T [Dn x rows], W0' [F0 x Dn], A' = dZ0^T [F0 x rows].
+static void blas_gemm_nt(void* handle, hipStream_t st, int rows, int Dn, int F0, const double* dZ,
+                         const double* W, double* dD) {
+  auto h = static_cast<rocblas_handle>(handle);
+  const double one = 1.0, zero = 0.0;
+  if (rocblas_set_stream(h, st) != rocblas_status_success ||
+      rocblas_dgemm(h, rocblas_operation_transpose, rocblas_operation_none, Dn, rows, F0, &one, W, F0,
+                    dZ, F0, &zero, dD, Dn) != rocblas_status_success)
+    throw HipError{hipErrorLaunchFailure, "rocblas_dgemm (dE/dD)"};
+}
+static void blas_gemm_nt(void* handle, hipStream_t st, int rows, int Dn, int F0, const float* dZ,
+                         const float* W, float* dD) {
+  auto h = static_cast<rocblas_handle>(handle);
+  const float one = 1.0f, zero = 0.0f;
+  if (rocblas_set_stream(h, st) != rocblas_status_success ||
+      rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, Dn, rows, F0, &one, W, F0,
+                    dZ, F0, &zero, dD, Dn) != rocblas_status_success)
+    throw HipError{hipErrorLaunchFailure, "rocblas_sgemm (dE/dD)"};
+}
+
+void* blas_create() {
+  rocblas_handle h = nullptr;
+  if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
+  return h;
+}
+
+void blas_destroy(void* h) {
+  if (h) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(h));
+}
+
 template <class T>
 void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, const T* Tt,
-                    long ldt, int L3, const FitBufs<T>& b, T* dD, double* e_bucket) {
+                    long ldt, int L3, const FitBufs<T>& b, T* dD, double* e_bucket, void* blas) {
   using G = GemmArgs<T>;
   if (rows <= 0) return;
   const int Dn = net.L[0].in, F0 = net.L[0].out, F1 = net.L[1].out, F2 = net.L[2].out;
@@ -369,6 +405,10 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   g.dHin = net.L[1].idt ? b.dH : nullptr; g.ld_dhin = F1; g.dH_out = nullptr; g.Tk = b.H0;
   gemm<true>(st, g);
   // dD = dZ0 W0^T
+  if (blas) {
+    blas_gemm_nt(blas, st, rows, Dn, F0, b.dZa, net.L[0].W, dD);
+    return;
+  }
   g = G{};
   g.M = rows; g.N = Dn; g.K = F0; g.A = b.dZa; g.lda = F0; g.B = net.L[0].W; g.ldb = F0;
   g.epi = 0; g.C = dD; g.ldc = Dn;
@@ -388,10 +428,10 @@ void launch_dT(hipStream_t st, int nloc, int L3, int axis, const int* items, con
 
 template void launch_fitting<double>(hipStream_t, const FitNet<double>&, int, const double*,
                                      const double*, long, int, const FitBufs<double>&, double*,
-                                     double*);
+                                     double*, void*);
 template void launch_fitting<float>(hipStream_t, const FitNet<float>&, int, const float*,
                                     const float*, long, int, const FitBufs<float>&, float*,
-                                    double*);
+                                    double*, void*);
 template void launch_dT<double>(hipStream_t, int, int, int, const int*, const double*,
                                 const double*, double*);
 template void launch_dT<float>(hipStream_t, int, int, int, const int*, const float*, const float*,

@@ -144,9 +144,13 @@ struct FitBufs {
 // Tt is given (axis 16), forms D = T^T T[:, :16] on the fly from the
 // column-major copy of T (element (row, a, m) at Tt[a * ldt + 4 row + m]) and
 // D may be null.
+// blas: a rocBLAS handle (blas_create) for the plain input-gradient GEMM, or
+// null for this library's own GEMM kernel.
 template <class T>
 void launch_fitting(hipStream_t, const FitNet<T>&, int rows, const T* D, const T* Tt, long ldt,
-                    int L3, const FitBufs<T>&, T* dD, double* e_bucket);
+                    int L3, const FitBufs<T>&, T* dD, double* e_bucket, void* blas);
+void* blas_create();
+void blas_destroy(void* handle);
 // Tt column-major in bucket order (element (pos, a, m) at Tt[a * 4 nloc +
 // 4 pos + m]), dT in atom order (items maps bucket position to atom).
 template <class T>
