@@ -153,6 +153,7 @@ struct NlKey {
 
 struct NlLds {
   NlKey k[kNlWaves][kMaxCand];
+  int claim[kNlWaves][kMaxCand];  // rank -> candidate, to detect equal keys
 };
 
 __device__ __forceinline__ unsigned long long nl_pack(int t, double r2) {
@@ -179,9 +180,15 @@ __device__ __forceinline__ void nl_push(bool keep, double r2, int j, int t, int&
   n += __popcll(m);
 }
 
+// Rank = #{keys below} + #{equal keys with a smaller index}. The first pass
+// counts keys below only; equal keys are rare (exact r^2 ties), so each
+// candidate then claims the LDS slot of its rank, and only if two candidates
+// of the wave claimed the same slot does a second pass add the index
+// tie-break.
 template <int K>
 __device__ __forceinline__ void nl_rank_place(const NlParams& np, int n, const NlKey* s,
-                                              const int* first, int* __restrict__ row) {
+                                              int* claim, const int* first,
+                                              int* __restrict__ row) {
   const int lane = threadIdx.x & 63;
   unsigned long long ek[K];
   int ej[K], rank[K];
@@ -198,9 +205,24 @@ __device__ __forceinline__ void nl_rank_place(const NlParams& np, int n, const N
   }
   for (int p = 0; p < n; ++p) {
     const unsigned long long ok = s[p].key;
-    const int oj = s[p].j;
 #pragma unroll
-    for (int k = 0; k < K; ++k) rank[k] += (ok < ek[k] || (ok == ek[k] && oj < ej[k])) ? 1 : 0;
+    for (int k = 0; k < K; ++k) rank[k] += ok < ek[k] ? 1 : 0;
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (lane + kWave * k < n) claim[rank[k]] = lane + kWave * k;
+  wave_lds_sync();
+  bool clash = false;
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (lane + kWave * k < n && claim[rank[k]] != lane + kWave * k) clash = true;
+  if (__ballot(clash)) {
+    for (int p = 0; p < n; ++p) {
+      const unsigned long long ok = s[p].key;
+      const int oj = s[p].j;
+#pragma unroll
+      for (int k = 0; k < K; ++k) rank[k] += (ok == ek[k] && oj < ej[k]) ? 1 : 0;
+    }
   }
 #pragma unroll
   for (int k = 0; k < K; ++k) {
@@ -213,7 +235,7 @@ __device__ __forceinline__ void nl_rank_place(const NlParams& np, int n, const N
   }
 }
 
-__device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s,
+__device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s, int* claim,
                          int* __restrict__ nlist, int* __restrict__ nreal,
                          int* __restrict__ status) {
   const int lane = threadIdx.x & 63;
@@ -243,11 +265,11 @@ __device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s,
   // every candidate this lane holds (q = lane + 64k, k < K)
   switch ((n + kWave - 1) / kWave) {
     case 0: break;
-    case 1: nl_rank_place<1>(np, n, s, first, row); break;
-    case 2: nl_rank_place<2>(np, n, s, first, row); break;
-    case 3: nl_rank_place<3>(np, n, s, first, row); break;
-    case 4: nl_rank_place<4>(np, n, s, first, row); break;
-    default: nl_rank_place<kMaxCand / kWave>(np, n, s, first, row); break;
+    case 1: nl_rank_place<1>(np, n, s, claim, first, row); break;
+    case 2: nl_rank_place<2>(np, n, s, claim, first, row); break;
+    case 3: nl_rank_place<3>(np, n, s, claim, first, row); break;
+    case 4: nl_rank_place<4>(np, n, s, claim, first, row); break;
+    default: nl_rank_place<kMaxCand / kWave>(np, n, s, claim, first, row); break;
   }
   for (int t = 0; t < np.ntypes; ++t) {
     const int kept = cnt[t] < np.sel[t] ? cnt[t] : np.sel[t];
@@ -339,7 +361,7 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells(
       nl_push(keep, r2, j, t, n, lds.k[w]);
     }
   }
-  nl_place(np, i, n, lds.k[w], nlist, nreal, status);
+  nl_place(np, i, n, lds.k[w], lds.claim[w], nlist, nreal, status);
 }
 
 // LAMMPS front end: candidates come from the caller's full list (CSR by centre).
@@ -375,7 +397,7 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_csr(
     }
     nl_push(keep, r2, j, t, n, lds.k[w]);
   }
-  nl_place(np, i, n, lds.k[w], nlist, nreal, status);
+  nl_place(np, i, n, lds.k[w], lds.claim[w], nlist, nreal, status);
 }
 
 // ---------------------------------------------------------------------------

@@ -96,6 +96,29 @@ def test_lammps_path(dp, orc, case):
     assert np.abs(f2 - ref2["force"]).max() <= F_TOL
 
 
+@pytest.mark.parametrize("kind", ["fcc", "bcc"])
+def test_nlist_exact_ties(dp, orc, kind):
+    """Perfect lattices (no displacement): every neighbour shell is a set of
+    exactly equal distances, so the sel order inside a shell is decided by the
+    index tie-break alone, and sel truncation (Cu: 176 in range, 138 kept) cuts
+    through a tied shell. The GPU list must still equal the oracle's."""
+    if kind == "fcc":
+        coord, atype, box = dp.systems.fcc(6, 3.615, seed=5, sigma=0.0)
+        m = dp.model.random_model("cu", seed=1002)
+    else:
+        coord, atype, box = dp.systems.bcc_hea(8, 3.2, seed=6, sigma=0.0)
+        m = dp.model.random_model("hea", seed=1003)
+    mb = model_bytes(m)
+    O = orc.Oracle(mb)
+    ext, et, mp, nl = O.neighbor_list(coord, atype, box)
+    pot = dp.DeepPot(file_content=mb)
+    e, f, v = pot.compute(coord, atype, box)
+    assert np.array_equal(pot.stage(dp.STAGE_NLIST, np.int32, nl.shape), nl)
+    ref = O.compute(coord, atype, box)
+    assert abs(e - ref["energy"]) / len(atype) <= E_TOL
+    assert np.abs(f - ref["force"]).max() <= F_TOL
+
+
 def test_virtual_atoms(dp, orc):
     (coord, atype, box), m = CASES["water192"]()
     atype = atype.copy()
