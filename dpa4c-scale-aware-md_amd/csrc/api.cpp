@@ -61,6 +61,7 @@ const char* kStageNames[kNumStages] = {"ghost+cells", "nlist",  "embed_fwd",
 
 struct dp_model {
   int device = 0;
+  int ncu = 256;  // compute units of the device
   int precision = DP_PREC_FP64;
   ModelHost host;
   EmbLayout el{};
@@ -342,13 +343,25 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
     const size_t blk = 16 * (size_t)(M->el.L2P + M->el.L3P);
     ea.act = need<E>(M, M->act, (size_t)std::max(nloc, 1) * acc * blk);
   }
+  // Blocks of WAVES * ipw items: each block stages its pair's net in LDS once
+  // and its waves then walk ipw items each, which amortises the staging and
+  // the start-up latency of a block. ipw aims at about 32 tiles of 16 slots
+  // per wave, as long as the grid still gives every compute unit three blocks
+  // or more (fewer leave a tail where some units idle).
   auto block_table = [&](int waves) {
+    long items = 0;
+    for (int p = 0; p < nt * nt; ++p) items += M->type_off[p / nt + 1] - M->type_off[p / nt];
+    const long tiles = std::max(1, (ea.tiles_per_atom + nt - 1) / nt);  // per item
+    const long by_tiles = (32 + tiles - 1) / tiles;
+    const long by_grid = items / ((long)waves * 3 * M->ncu);
+    ea.ipw = (int)std::clamp(std::min(by_tiles, by_grid), 1L, 16L);
+    const int per = waves * ea.ipw;
     int acc = 0;
     for (int p = 0; p < nt * nt; ++p) {
       ea.block_off[p] = acc;
       const int ti = p / nt;
       const int cnt = M->type_off[ti + 1] - M->type_off[ti];
-      acc += (cnt + waves - 1) / waves;
+      acc += (cnt + per - 1) / per;
     }
     ea.block_off[nt * nt] = acc;
     return acc;
@@ -582,6 +595,7 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
     DPAMD_HIP(hipSetDevice(M->device));
     hipDeviceProp_t prop;
     DPAMD_HIP(hipGetDeviceProperties(&prop, M->device));
+    M->ncu = std::max(1, prop.multiProcessorCount);
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
       throw ApiError{DP_ERR_NO_GPU, std::string("device is ") + prop.gcnArchName +
                                         ", this library is built for gfx950"};

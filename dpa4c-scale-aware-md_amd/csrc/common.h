@@ -63,6 +63,13 @@ struct Frag<float> {
   static constexpr __host__ __device__ int row(int g, int r) { return 4 * g + r; }
 };
 
+// Four consecutive elements read with 16-byte vector loads (one for float,
+// two for double); the address must be 16-byte aligned.
+template <class T>
+struct alignas(16) Vec4 {
+  T x, y, z, w;
+};
+
 // Make this wave's LDS writes visible to its own other lanes.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -73,199 +73,202 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
   }
   __syncthreads();
-  const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
-  if (item >= a.type_off[ti + 1] - a.type_off[ti]) return;
-  const int i = a.items[a.type_off[ti] + item];
-  const int nr = a.nreal[(long)i * a.ntypes + tj];
-  const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
-  // env statistics from LDS: a global load inside the tile loop would be
-  // ordered behind the activation traffic by the in-order vector memory
-  // counter
-  const double* avg = EnvS;
-  const double* sd = EnvS + 4;
-  const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
+  const int nitems = a.type_off[ti + 1] - a.type_off[ti];
+  for (int it = 0; it < a.ipw; ++it) {
+    const int item = (((int)blockIdx.x - a.block_off[p]) * a.ipw + it) * WAVES + w;
+    if (item >= nitems) break;
+    const int i = a.items[a.type_off[ti] + item];
+    const int nr = a.nreal[(long)i * a.ntypes + tj];
+    const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
+    // env statistics from LDS: a global load inside the tile loop would be
+    // ordered behind the activation traffic by the in-order vector memory
+    // counter
+    const double* avg = EnvS;
+    const double* sd = EnvS + 4;
+    const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
 
-  double Tacc[S::NU3 * 4];
-#pragma unroll
-  for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0;
-  constexpr int BLK = 16 * (S::L2P + S::L3P);
-  double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
+    double Tacc[S::NU3 * 4];
+  #pragma unroll
+    for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0;
+    constexpr int BLK = 16 * (S::L2P + S::L3P);
+    double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
 
-  // per-lane bases: layer 2 element (t, r) at act2[(4t + r) * 64], layer 3
-  // element (u, r) of slot g + 4r at act3[256u + 16r]
-  double* act2 = act + c * 4 + g;
-  double* act3 = act + 16 * S::L2P + (c >> 2) * 64 + g * 4 + (c & 3);
-  // Neighbour coordinates of tile k+1 are fetched during tile k, from an index
-  // loaded during tile k-1: the memory counter is in order, so no wait on a
-  // load ever has to cover the activation stores issued after it.
-  double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
-  if (c < nr) {
-    const long j = row[c];
-    nx0 = a.ext[3 * j];
-    nx1 = a.ext[3 * j + 1];
-    nx2 = a.ext[3 * j + 2];
-  }
-  int jn = 16 + c < nr ? row[16 + c] : 0;
-  for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
-    const int slot = tile + c;
-    double Rn[4] = {0.0, 0.0, 0.0, 0.0};
-    if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, avg, sd, Rn);
-    if (slot + 16 < nr) {
-      nx0 = a.ext[3 * (long)jn];
-      nx1 = a.ext[3 * (long)jn + 1];
-      nx2 = a.ext[3 * (long)jn + 2];
+    // per-lane bases: layer 2 element (t, r) at act2[(4t + r) * 64], layer 3
+    // element (u, r) of slot g + 4r at act3[256u + 16r]
+    double* act2 = act + c * 4 + g;
+    double* act3 = act + 16 * S::L2P + (c >> 2) * 64 + g * 4 + (c & 3);
+    // Neighbour coordinates of tile k+1 are fetched during tile k, from an index
+    // loaded during tile k-1: the memory counter is in order, so no wait on a
+    // load ever has to cover the activation stores issued after it.
+    double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
+    if (c < nr) {
+      const long j = row[c];
+      nx0 = a.ext[3 * j];
+      nx1 = a.ext[3 * j + 1];
+      nx2 = a.ext[3 * j + 2];
     }
-    jn = slot + 32 < nr ? row[slot + 32] : 0;
-    if (g == 0) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) Rs[c * 4 + m] = Rn[m];
-    }
-    const double s = Rn[0];
-
-    // layer 1 -> B operand of layer 2 (feature 4q+g of slot c); four at a
-    // time (shared reciprocal) when every feature is real
-    double x1[S::NQ2];
-    if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
-#pragma unroll
-      for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
-        double z[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int f = 4 * (q0 + j) + g;
-          z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
-        }
-        tanh_fast4(z, x1 + q0);
+    int jn = 16 + c < nr ? row[16 + c] : 0;
+    for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
+      const int slot = tile + c;
+      double Rn[4] = {0.0, 0.0, 0.0, 0.0};
+      if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, avg, sd, Rn);
+      if (slot + 16 < nr) {
+        nx0 = a.ext[3 * (long)jn];
+        nx1 = a.ext[3 * (long)jn + 1];
+        nx2 = a.ext[3 * (long)jn + 2];
       }
-    } else {
-#pragma unroll
+      jn = slot + 32 < nr ? row[slot + 32] : 0;
+      if (g == 0) {
+  #pragma unroll
+        for (int m = 0; m < 4; ++m) Rs[c * 4 + m] = Rn[m];
+      }
+      const double s = Rn[0];
+
+      // layer 1 -> B operand of layer 2 (feature 4q+g of slot c); four at a
+      // time (shared reciprocal) when every feature is real
+      double x1[S::NQ2];
+      if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
+  #pragma unroll
+        for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
+          double z[4];
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int f = 4 * (q0 + j) + g;
+            z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
+          }
+          tanh_fast4(z, x1 + q0);
+        }
+      } else {
+  #pragma unroll
+        for (int q = 0; q < S::NQ2; ++q) {
+          const int f = 4 * q + g;
+          x1[q] = (f < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
+        }
+      }
+      // layer 2, transposed
+      d4 acc2[S::NT2];
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) acc2[t] = d4{0.0, 0.0, 0.0, 0.0};
+  #pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
-        const int f = 4 * q + g;
-        x1[q] = (f < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
+  #pragma unroll
+        for (int t = 0; t < S::NT2; ++t)
+          acc2[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1[q], acc2[t]);
       }
-    }
-    // layer 2, transposed
-    d4 acc2[S::NT2];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) acc2[t] = d4{0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-    for (int q = 0; q < S::NQ2; ++q) {
-#pragma unroll
-      for (int t = 0; t < S::NT2; ++t)
-        acc2[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1[q], acc2[t]);
-    }
-    double x2[S::NT2][4];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) {
-      double z2[4], th2v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) z2[r] = acc2[t][r] + P[S::OFF_B2 + 16 * t + 4 * r + g];
-      tanh_fast4(z2, th2v);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int f = 16 * t + 4 * r + g;
-        const double th = th2v[r];
-        act2[(4 * t + r) * 64] = th;
-        double res = 0.0;
-        if constexpr (S::RES2 != 0) {
-          if constexpr (S::X1_ALIGNED) {
-            res = x1[(S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r];
-          } else {
-            const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
-            res = (f1 < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f1] + P[S::OFF_B1 + f1]) : 0.0;
+      double x2[S::NT2][4];
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) {
+        double z2[4], th2v[4];
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) z2[r] = acc2[t][r] + P[S::OFF_B2 + 16 * t + 4 * r + g];
+        tanh_fast4(z2, th2v);
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int f = 16 * t + 4 * r + g;
+          const double th = th2v[r];
+          act2[(4 * t + r) * 64] = th;
+          double res = 0.0;
+          if constexpr (S::RES2 != 0) {
+            if constexpr (S::X1_ALIGNED) {
+              res = x1[(S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r];
+            } else {
+              const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
+              res = (f1 < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f1] + P[S::OFF_B1 + f1]) : 0.0;
+            }
           }
+          x2[t][r] = (f < S::L2) ? res + th : 0.0;
         }
-        x2[t][r] = (f < S::L2) ? res + th : 0.0;
       }
-    }
-    if constexpr (S::RES3 != 0) {
-#pragma unroll
-      for (int t = 0; t < S::NT2; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) X2s[c * X2LD + 16 * t + 4 * r + g] = x2[t][r];
-    }
-    wave_lds_sync();
-    // layer 3, non-transposed, two output tiles at a time
-#pragma unroll
-    for (int u0 = 0; u0 < S::NU3; u0 += kU3) {
-      __builtin_amdgcn_sched_barrier(0);
-      d4 acc3[kU3];
-#pragma unroll
-      for (int uu = 0; uu < kU3; ++uu) acc3[uu] = d4{0.0, 0.0, 0.0, 0.0};
-      double wcur[kU3], wnxt[kU3];
-      const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
-#pragma unroll
-      for (int uu = 0; uu < kU3; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
-#pragma unroll
-      for (int q = 0; q < S::NQ3; ++q) {
-        if (q + 1 < S::NQ3) {
-#pragma unroll
+      if constexpr (S::RES3 != 0) {
+  #pragma unroll
+        for (int t = 0; t < S::NT2; ++t)
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) X2s[c * X2LD + 16 * t + 4 * r + g] = x2[t][r];
+      }
+      wave_lds_sync();
+      // layer 3, non-transposed, two output tiles at a time
+  #pragma unroll
+      for (int u0 = 0; u0 < S::NU3; u0 += kU3) {
+        __builtin_amdgcn_sched_barrier(0);
+        d4 acc3[kU3];
+  #pragma unroll
+        for (int uu = 0; uu < kU3; ++uu) acc3[uu] = d4{0.0, 0.0, 0.0, 0.0};
+        double wcur[kU3], wnxt[kU3];
+        const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
+  #pragma unroll
+        for (int uu = 0; uu < kU3; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
+  #pragma unroll
+        for (int q = 0; q < S::NQ3; ++q) {
+          if (q + 1 < S::NQ3) {
+  #pragma unroll
+            for (int uu = 0; uu < kU3; ++uu)
+              wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
+          }
+          const double av = x2[q / 4][q % 4];
+  #pragma unroll
           for (int uu = 0; uu < kU3; ++uu)
-            wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
+            if (u0 + uu < S::NU3) acc3[uu] = mfma_f64(av, wcur[uu], acc3[uu]);
+  #pragma unroll
+          for (int uu = 0; uu < kU3; ++uu) wcur[uu] = wnxt[uu];
         }
-        const double av = x2[q / 4][q % 4];
-#pragma unroll
-        for (int uu = 0; uu < kU3; ++uu)
-          if (u0 + uu < S::NU3) acc3[uu] = mfma_f64(av, wcur[uu], acc3[uu]);
-#pragma unroll
-        for (int uu = 0; uu < kU3; ++uu) wcur[uu] = wnxt[uu];
-      }
-#pragma unroll
-      for (int uu = 0; uu < kU3; ++uu) {
-        const int u = u0 + uu;
-        if (u < S::NU3) {
-          const int f = 16 * u + c;
-          double z3[4], th3v[4];
-          const double b3 = P[S::OFF_B3 + f];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) z3[r] = acc3[uu][r] + b3;
-          tanh_fast4(z3, th3v);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int sl = g + 4 * r;
-            const double th = th3v[r];
-            // backward order: feature 16u + 4(c>>2) + (c&3) of slot sl
-            act3[256 * u + 16 * r] = th;
-            double G = th;
-            if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
-            if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
+  #pragma unroll
+        for (int uu = 0; uu < kU3; ++uu) {
+          const int u = u0 + uu;
+          if (u < S::NU3) {
+            const int f = 16 * u + c;
+            double z3[4], th3v[4];
+            const double b3 = P[S::OFF_B3 + f];
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) z3[r] = acc3[uu][r] + b3;
+            tanh_fast4(z3, th3v);
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int sl = g + 4 * r;
+              const double th = th3v[r];
+              // backward order: feature 16u + 4(c>>2) + (c&3) of slot sl
+              act3[256 * u + 16 * r] = th;
+              double G = th;
+              if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
+              if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
+  #pragma unroll
+              for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
+            }
           }
         }
       }
+      wave_lds_sync();
     }
-    wave_lds_sync();
-  }
-#pragma unroll
-  for (int q = 0; q < S::NU3 * 4; ++q) {
-    double v = Tacc[q];
-    v += shfl_xor_d(v, 16);
-    v += shfl_xor_d(v, 32);
-    Tacc[q] = v;
-  }
-  if (g == 0 && a.Tt) {
-    // single neighbour type: this section is all of T
-    const double npad = (double)(a.sel[tj] - nr);
-    const double* tp = a.tpad + (long)p * 4 * S::L3;
-    double* Tt = static_cast<double*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
-#pragma unroll
-    for (int u = 0; u < S::NU3; ++u) {
-      const int f = 16 * u + c;
-      if (f < S::L3) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          Tt[f * a.ldt + m] =
-              (double)(((double)Tacc[u * 4 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
+  #pragma unroll
+    for (int q = 0; q < S::NU3 * 4; ++q) {
+      double v = Tacc[q];
+      v += shfl_xor_d(v, 16);
+      v += shfl_xor_d(v, 32);
+      Tacc[q] = v;
+    }
+    if (g == 0 && a.Tt) {
+      // single neighbour type: this section is all of T
+      const double npad = (double)(a.sel[tj] - nr);
+      const double* tp = a.tpad + (long)p * 4 * S::L3;
+      double* Tt = static_cast<double*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
+  #pragma unroll
+      for (int u = 0; u < S::NU3; ++u) {
+        const int f = 16 * u + c;
+        if (f < S::L3) {
+  #pragma unroll
+          for (int m = 0; m < 4; ++m)
+            Tt[f * a.ldt + m] =
+                (double)(((double)Tacc[u * 4 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
+        }
       }
-    }
-  } else if (g == 0) {
-    double* out = static_cast<double*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
-#pragma unroll
-    for (int u = 0; u < S::NU3; ++u) {
-      const int f = 16 * u + c;
-      if (f < S::L3) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) out[m * S::L3 + f] = Tacc[u * 4 + m];
+    } else if (g == 0) {
+      double* out = static_cast<double*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
+  #pragma unroll
+      for (int u = 0; u < S::NU3; ++u) {
+        const int f = 16 * u + c;
+        if (f < S::L3) {
+  #pragma unroll
+          for (int m = 0; m < 4; ++m) out[m * S::L3 + f] = Tacc[u * 4 + m];
+        }
       }
     }
   }
@@ -290,242 +293,245 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
   }
   __syncthreads();
-  const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
-  if (item >= a.type_off[ti + 1] - a.type_off[ti]) return;
-  const int i = a.items[a.type_off[ti] + item];
-  const int nr = a.nreal[(long)i * a.ntypes + tj];
-  const long ebase = (long)i * a.nnei + a.sec[tj];
-  const int* row = a.nlist + ebase;
-  // env statistics from LDS: a global load inside the tile loop would be
-  // ordered behind the activation traffic by the in-order vector memory
-  // counter
-  const double* avg = EnvS;
-  const double* sd = EnvS + 4;
-  const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
-  constexpr int BLK = 16 * (S::L2P + S::L3P);
-  const double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
+  const int nitems = a.type_off[ti + 1] - a.type_off[ti];
+  for (int it = 0; it < a.ipw; ++it) {
+    const int item = (((int)blockIdx.x - a.block_off[p]) * a.ipw + it) * WAVES + w;
+    if (item >= nitems) break;
+    const int i = a.items[a.type_off[ti] + item];
+    const int nr = a.nreal[(long)i * a.ntypes + tj];
+    const long ebase = (long)i * a.nnei + a.sec[tj];
+    const int* row = a.nlist + ebase;
+    // env statistics from LDS: a global load inside the tile loop would be
+    // ordered behind the activation traffic by the in-order vector memory
+    // counter
+    const double* avg = EnvS;
+    const double* sd = EnvS + 4;
+    const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
+    constexpr int BLK = 16 * (S::L2P + S::L3P);
+    const double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
 
-  {
-    const double* dTi = static_cast<const double*>(a.dT) + (long)i * 4 * S::L3;
-    for (int q = lane; q < 4 * S::L3P; q += 64) {
-      const int m = q / S::L3P, f = q % S::L3P;
-      dTs[q] = f < S::L3 ? dTi[m * S::L3 + f] : 0.0;
-    }
-    for (int q = lane; q < 4 * S::L2P; q += 64) {
-      const int m = q / S::L2P, f = q % S::L2P;
-      double v = 0.0;
-      if (f < S::L2) {
-        if constexpr (S::RES3 == 2) v = dTi[m * S::L3 + f] + dTi[m * S::L3 + f + S::L2];
-        if constexpr (S::RES3 == 1) v = dTi[m * S::L3 + f];
+    {
+      const double* dTi = static_cast<const double*>(a.dT) + (long)i * 4 * S::L3;
+      for (int q = lane; q < 4 * S::L3P; q += 64) {
+        const int m = q / S::L3P, f = q % S::L3P;
+        dTs[q] = f < S::L3 ? dTi[m * S::L3 + f] : 0.0;
       }
-      dTf[q] = v;
+      for (int q = lane; q < 4 * S::L2P; q += 64) {
+        const int m = q / S::L2P, f = q % S::L2P;
+        double v = 0.0;
+        if (f < S::L2) {
+          if constexpr (S::RES3 == 2) v = dTi[m * S::L3 + f] + dTi[m * S::L3 + f + S::L2];
+          if constexpr (S::RES3 == 1) v = dTi[m * S::L3 + f];
+        }
+        dTf[q] = v;
+      }
     }
-  }
-  wave_lds_sync();
+    wave_lds_sync();
 
-  const double* act2 = act + c * 4 + g;  // element (t, r) at act2[64 (4t + r)]
-  const double* act3 = act2 + 16 * S::L2P;  // element (u, r) at act3[256u + 64r]
-  // Neighbour coordinates of tile k+1 are fetched during tile k (their index
-  // one tile earlier, so the memory counter never orders them behind other
-  // loads). The saved activations of a tile are loaded at its start and
-  // consumed after the layer-2 and layer-3 products: their latency is covered
-  // by those products and by the other wave of the SIMD. Holding them a whole
-  // tile ahead would need the registers of that second wave.
-  double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
-  int jn = c < nr ? row[c] : 0;
-  if (c < nr) {
-    nx0 = a.ext[3 * (long)jn];
-    nx1 = a.ext[3 * (long)jn + 1];
-    nx2 = a.ext[3 * (long)jn + 2];
-  }
-  jn = 16 + c < nr ? row[16 + c] : 0;
-
-  for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
-    const int slot = tile + c;
-    const bool valid = slot < nr;
-    double th2[S::NT2][4], th3[S::NU3][4];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) th2[t][r] = act2[(4 * t + r) * 64];
-#pragma unroll
-    for (int u = 0; u < S::NU3; ++u)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) th3[u][r] = act3[256 * u + 64 * r];
-    double d0 = 0.0, d1 = 0.0, d2 = 0.0;
-    double Rn[4] = {0.0, 0.0, 0.0, 0.0};
-    if (valid) {
-      d0 = nx0 - xi;
-      d1 = nx1 - yi;
-      d2 = nx2 - zi;
-      env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
-    }
-    if (slot + 16 < nr) {
+    const double* act2 = act + c * 4 + g;  // element (t, r) at act2[64 (4t + r)]
+    const double* act3 = act2 + 16 * S::L2P;  // element (u, r) at act3[256u + 64r]
+    // Neighbour coordinates of tile k+1 are fetched during tile k (their index
+    // one tile earlier, so the memory counter never orders them behind other
+    // loads). The saved activations of a tile are loaded at its start and
+    // consumed after the layer-2 and layer-3 products: their latency is covered
+    // by those products and by the other wave of the SIMD. Holding them a whole
+    // tile ahead would need the registers of that second wave.
+    double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
+    int jn = c < nr ? row[c] : 0;
+    if (c < nr) {
       nx0 = a.ext[3 * (long)jn];
       nx1 = a.ext[3 * (long)jn + 1];
       nx2 = a.ext[3 * (long)jn + 2];
     }
-    jn = slot + 32 < nr ? row[slot + 32] : 0;
-    const double s = Rn[0];
+    jn = 16 + c < nr ? row[16 + c] : 0;
 
-    // layer 1 (recomputed, elementwise) and its tangent
-    double x1[S::NQ2], x1t[S::NQ2];
-    if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
-#pragma unroll
-      for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
-        double z[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int f = 4 * (q0 + j) + g;
-          z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
-        }
-        tanh_fast4(z, x1 + q0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const double th = x1[q0 + j];
-          x1t[q0 + j] = (1.0 - th * th) * P[S::OFF_W1 + 4 * (q0 + j) + g];
-        }
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < S::NQ2; ++q) {
-        const int f = 4 * q + g;
-        if (f < S::L1) {
-          const double wv = P[S::OFF_W1 + f];
-          const double th = tanh_fast(s * wv + P[S::OFF_B1 + f]);
-          x1[q] = th;
-          x1t[q] = (1.0 - th * th) * wv;
-        } else {
-          x1[q] = 0.0;
-          x1t[q] = 0.0;
-        }
-      }
-    }
-    // layer 2: tangent product only; tanh of the primal comes from the forward
-    d4 acc2t[S::NT2];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) acc2t[t] = d4{0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-    for (int q = 0; q < S::NQ2; ++q) {
-#pragma unroll
+    for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
+      const int slot = tile + c;
+      const bool valid = slot < nr;
+      double th2[S::NT2][4], th3[S::NU3][4];
+  #pragma unroll
       for (int t = 0; t < S::NT2; ++t)
-        acc2t[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1t[q], acc2t[t]);
-    }
-    double x2[S::NT2][4], x2t[S::NT2][4];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int f = 16 * t + 4 * r + g;
-        const double th = th2[t][r];
-        double res = 0.0, rest = 0.0;
-        if constexpr (S::RES2 != 0) {
-          if constexpr (S::X1_ALIGNED) {
-            const int q1 = (S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r;
-            res = x1[q1];
-            rest = x1t[q1];
-          } else {
-            const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
-            if (f1 < S::L1) {
-              const double wv = P[S::OFF_W1 + f1];
-              const double y = tanh_fast(s * wv + P[S::OFF_B1 + f1]);
-              res = y;
-              rest = (1.0 - y * y) * wv;
-            }
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) th2[t][r] = act2[(4 * t + r) * 64];
+  #pragma unroll
+      for (int u = 0; u < S::NU3; ++u)
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) th3[u][r] = act3[256 * u + 64 * r];
+      double d0 = 0.0, d1 = 0.0, d2 = 0.0;
+      double Rn[4] = {0.0, 0.0, 0.0, 0.0};
+      if (valid) {
+        d0 = nx0 - xi;
+        d1 = nx1 - yi;
+        d2 = nx2 - zi;
+        env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
+      }
+      if (slot + 16 < nr) {
+        nx0 = a.ext[3 * (long)jn];
+        nx1 = a.ext[3 * (long)jn + 1];
+        nx2 = a.ext[3 * (long)jn + 2];
+      }
+      jn = slot + 32 < nr ? row[slot + 32] : 0;
+      const double s = Rn[0];
+
+      // layer 1 (recomputed, elementwise) and its tangent
+      double x1[S::NQ2], x1t[S::NQ2];
+      if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
+  #pragma unroll
+        for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
+          double z[4];
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int f = 4 * (q0 + j) + g;
+            z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
+          }
+          tanh_fast4(z, x1 + q0);
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const double th = x1[q0 + j];
+            x1t[q0 + j] = (1.0 - th * th) * P[S::OFF_W1 + 4 * (q0 + j) + g];
           }
         }
-        const bool live = f < S::L2;
-        x2[t][r] = live ? res + th : 0.0;
-        x2t[t][r] = live ? rest + (1.0 - th * th) * acc2t[t][r] : 0.0;
+      } else {
+  #pragma unroll
+        for (int q = 0; q < S::NQ2; ++q) {
+          const int f = 4 * q + g;
+          if (f < S::L1) {
+            const double wv = P[S::OFF_W1 + f];
+            const double th = tanh_fast(s * wv + P[S::OFF_B1 + f]);
+            x1[q] = th;
+            x1t[q] = (1.0 - th * th) * wv;
+          } else {
+            x1[q] = 0.0;
+            x1t[q] = 0.0;
+          }
+        }
       }
-    }
-    // u = dT.G, v = dT.G': residual part through the folded dT against X2
-    double up[4] = {0.0, 0.0, 0.0, 0.0}, vp[4] = {0.0, 0.0, 0.0, 0.0};
-    if constexpr (S::RES3 != 0) {
-#pragma unroll
-      for (int t = 0; t < S::NT2; ++t)
-#pragma unroll
+      // layer 2: tangent product only; tanh of the primal comes from the forward
+      d4 acc2t[S::NT2];
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) acc2t[t] = d4{0.0, 0.0, 0.0, 0.0};
+  #pragma unroll
+      for (int q = 0; q < S::NQ2; ++q) {
+  #pragma unroll
+        for (int t = 0; t < S::NT2; ++t)
+          acc2t[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1t[q], acc2t[t]);
+      }
+      double x2[S::NT2][4], x2t[S::NT2][4];
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) {
+  #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int f = 16 * t + 4 * r + g;
-#pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            const double wv = dTf[m * S::L2P + f];
-            up[m] += wv * x2[t][r];
-            vp[m] += wv * x2t[t][r];
+          const double th = th2[t][r];
+          double res = 0.0, rest = 0.0;
+          if constexpr (S::RES2 != 0) {
+            if constexpr (S::X1_ALIGNED) {
+              const int q1 = (S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r;
+              res = x1[q1];
+              rest = x1t[q1];
+            } else {
+              const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
+              if (f1 < S::L1) {
+                const double wv = P[S::OFF_W1 + f1];
+                const double y = tanh_fast(s * wv + P[S::OFF_B1 + f1]);
+                res = y;
+                rest = (1.0 - y * y) * wv;
+              }
+            }
           }
+          const bool live = f < S::L2;
+          x2[t][r] = live ? res + th : 0.0;
+          x2t[t][r] = live ? rest + (1.0 - th * th) * acc2t[t][r] : 0.0;
         }
-    }
-    // layer 3 tangent, transposed; tanh part of G from the forward
-#pragma unroll
-    for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
-      // keep the scheduler from hoisting later tile groups' weight loads
-      __builtin_amdgcn_sched_barrier(0);
-      d4 acc3t[kU3B];
-#pragma unroll
-      for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = d4{0.0, 0.0, 0.0, 0.0};
-      // weight fragments double-buffered one k-step ahead of the MFMAs
-      double wcur[kU3B], wnxt[kU3B];
-      const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
-#pragma unroll
-      for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
-#pragma unroll
-      for (int q = 0; q < S::NQ3; ++q) {
-        if (q + 1 < S::NQ3) {
-#pragma unroll
-          for (int uu = 0; uu < kU3B; ++uu)
-            wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
-        }
-#pragma unroll
-        for (int uu = 0; uu < kU3B; ++uu)
-          if (u0 + uu < S::NU3) acc3t[uu] = mfma_f64(wcur[uu], x2t[q / 4][q % 4], acc3t[uu]);
-#pragma unroll
-        for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = wnxt[uu];
       }
-#pragma unroll
-      for (int uu = 0; uu < kU3B; ++uu) {
-        const int u = u0 + uu;
-        if (u < S::NU3) {
-#pragma unroll
+      // u = dT.G, v = dT.G': residual part through the folded dT against X2
+      double up[4] = {0.0, 0.0, 0.0, 0.0}, vp[4] = {0.0, 0.0, 0.0, 0.0};
+      if constexpr (S::RES3 != 0) {
+  #pragma unroll
+        for (int t = 0; t < S::NT2; ++t)
+  #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int f = 16 * u + 4 * r + g;
-            const double th = th3[u][r];
-            const double tt = (1.0 - th * th) * acc3t[uu][r];
-#pragma unroll
+            const int f = 16 * t + 4 * r + g;
+  #pragma unroll
             for (int m = 0; m < 4; ++m) {
-              const double wv = dTs[m * S::L3P + f];
-              up[m] += wv * th;
-              vp[m] += wv * tt;
+              const double wv = dTf[m * S::L2P + f];
+              up[m] += wv * x2[t][r];
+              vp[m] += wv * x2t[t][r];
+            }
+          }
+      }
+      // layer 3 tangent, transposed; tanh part of G from the forward
+  #pragma unroll
+      for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
+        // keep the scheduler from hoisting later tile groups' weight loads
+        __builtin_amdgcn_sched_barrier(0);
+        d4 acc3t[kU3B];
+  #pragma unroll
+        for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = d4{0.0, 0.0, 0.0, 0.0};
+        // weight fragments double-buffered one k-step ahead of the MFMAs
+        double wcur[kU3B], wnxt[kU3B];
+        const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
+  #pragma unroll
+        for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
+  #pragma unroll
+        for (int q = 0; q < S::NQ3; ++q) {
+          if (q + 1 < S::NQ3) {
+  #pragma unroll
+            for (int uu = 0; uu < kU3B; ++uu)
+              wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
+          }
+  #pragma unroll
+          for (int uu = 0; uu < kU3B; ++uu)
+            if (u0 + uu < S::NU3) acc3t[uu] = mfma_f64(wcur[uu], x2t[q / 4][q % 4], acc3t[uu]);
+  #pragma unroll
+          for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = wnxt[uu];
+        }
+  #pragma unroll
+        for (int uu = 0; uu < kU3B; ++uu) {
+          const int u = u0 + uu;
+          if (u < S::NU3) {
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int f = 16 * u + 4 * r + g;
+              const double th = th3[u][r];
+              const double tt = (1.0 - th * th) * acc3t[uu][r];
+  #pragma unroll
+              for (int m = 0; m < 4; ++m) {
+                const double wv = dTs[m * S::L3P + f];
+                up[m] += wv * th;
+                vp[m] += wv * tt;
+              }
             }
           }
         }
       }
+  #pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        up[m] += shfl_xor_d(up[m], 16);
+        up[m] += shfl_xor_d(up[m], 32);
+        vp[m] += shfl_xor_d(vp[m], 16);
+        vp[m] += shfl_xor_d(vp[m], 32);
+      }
+      if (valid && g == 0) {
+        double nd[4];
+  #pragma unroll
+        for (int m = 0; m < 4; ++m) nd[m] = up[m] * a.inv_nnei;
+        nd[0] += (Rn[0] * vp[0] + Rn[1] * vp[1] + Rn[2] * vp[2] + Rn[3] * vp[3]) * a.inv_nnei;
+        double gv[3];
+        env_grad(d0, d1, d2, a.rcut_smth, a.rcut, sd, nd, gv);
+        double* eg = a.edge_grad + (ebase + slot) * 3;
+        eg[0] = gv[0];
+        eg[1] = gv[1];
+        eg[2] = gv[2];
+      }
     }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      up[m] += shfl_xor_d(up[m], 16);
-      up[m] += shfl_xor_d(up[m], 32);
-      vp[m] += shfl_xor_d(vp[m], 16);
-      vp[m] += shfl_xor_d(vp[m], 32);
+    // padded slots carry no gradient
+    for (int sl = nr + lane; sl < a.sel[tj]; sl += 64) {
+      double* eg = a.edge_grad + (ebase + sl) * 3;
+      eg[0] = 0.0;
+      eg[1] = 0.0;
+      eg[2] = 0.0;
     }
-    if (valid && g == 0) {
-      double nd[4];
-#pragma unroll
-      for (int m = 0; m < 4; ++m) nd[m] = up[m] * a.inv_nnei;
-      nd[0] += (Rn[0] * vp[0] + Rn[1] * vp[1] + Rn[2] * vp[2] + Rn[3] * vp[3]) * a.inv_nnei;
-      double gv[3];
-      env_grad(d0, d1, d2, a.rcut_smth, a.rcut, sd, nd, gv);
-      double* eg = a.edge_grad + (ebase + slot) * 3;
-      eg[0] = gv[0];
-      eg[1] = gv[1];
-      eg[2] = gv[2];
-    }
-  }
-  // padded slots carry no gradient
-  for (int sl = nr + lane; sl < a.sel[tj]; sl += 64) {
-    double* eg = a.edge_grad + (ebase + sl) * 3;
-    eg[0] = 0.0;
-    eg[1] = 0.0;
-    eg[2] = 0.0;
   }
 }
 
@@ -538,39 +544,79 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 // fp64 and rounded once. A block handles kDescAtoms consecutive positions so
 // that every layout is written in contiguous runs.
 constexpr int kDescAtoms = 8;
-template <class E>
+
+// Sum of the sections of items q and q + blockDim.x (item = atom k of the
+// block and 4 consecutive elements e = 4g..4g+3 of its [4][L3] row) into the
+// LDS copy. Every section value and padded-slot constant of both items is
+// loaded before any is summed, so a thread has 4 NT vector loads in flight.
+template <class E, int NT>
+__device__ __forceinline__ void desc_sum(const DescArgs& a, double* Ts, int pos0, int na, int q) {
+  const E* Tsec = static_cast<const E*>(a.Tsec);
+  const int L3 = a.L3, per = 4 * L3, LR = L3 + 1, G = per / 4;
+  constexpr int R = 2;
+  Vec4<E> ts[R][NT];
+  Vec4<double> tp[R][NT];
+  int nrl[R][NT];
+  int kk[R], e0[R];
+  bool ok[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int qq = q + r * (int)blockDim.x;
+    ok[r] = qq < na * G;
+    kk[r] = ok[r] ? qq / G : 0;
+    e0[r] = 4 * (qq - kk[r] * G);
+    if (ok[r]) {
+      const int i = a.items[pos0 + kk[r]];
+      const int ti = a.ext_type[i];
+#pragma unroll
+      for (int tj = 0; tj < NT; ++tj) {
+        const long sec = (long)i * NT + tj;
+        ts[r][tj] = *reinterpret_cast<const Vec4<E>*>(Tsec + sec * per + e0[r]);
+        tp[r][tj] = *reinterpret_cast<const Vec4<double>*>(a.tpad + (long)(ti * NT + tj) * per + e0[r]);
+        nrl[r][tj] = a.nreal[sec];
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (!ok[r]) continue;
+    double v[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int tj = 0; tj < NT; ++tj) {
+      const double np = (double)(a.sel[tj] - nrl[r][tj]);
+      v[0] += (double)ts[r][tj].x + np * tp[r][tj].x;
+      v[1] += (double)ts[r][tj].y + np * tp[r][tj].y;
+      v[2] += (double)ts[r][tj].z + np * tp[r][tj].z;
+      v[3] += (double)ts[r][tj].w + np * tp[r][tj].w;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int m = (e0[r] + c) / L3, col = e0[r] + c - m * L3;
+      Ts[(kk[r] * 4 + m) * LR + col] = (double)(E)(v[c] * a.inv_nnei);
+    }
+  }
+}
+
+template <class E, int NT>
 __global__ __launch_bounds__(256) void k_descriptor(DescArgs a) {
   // LDS copy [kDescAtoms][4][L3 + 1]: the padding keeps the column-major
   // pass (consecutive threads on consecutive (atom, m) rows) off one bank
   extern __shared__ double Ts[];
-  const E* Tsec = static_cast<const E*>(a.Tsec);
-  const int L3 = a.L3, per = 4 * L3, LR = L3 + 1;
+  const int L3 = a.L3, LR = L3 + 1;
   const int pos0 = blockIdx.x * kDescAtoms;
   const int na = min(kDescAtoms, a.nloc - pos0);
-  // thread = (column, one of two atoms of a pass); L3 <= 128
-  const int col = threadIdx.x & 127;
-  for (int k = threadIdx.x >> 7; k < na; k += 2) {
-    if (col >= L3) continue;
-    if (a.from_tt) {
+  if (a.from_tt) {
+    // thread = (column, one of two atoms of a pass); L3 <= 128
+    const int col = threadIdx.x & 127;
+    for (int k = threadIdx.x >> 7; k < na; k += 2) {
+      if (col >= L3) continue;
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         Ts[(k * 4 + m) * LR + col] =
             (double)static_cast<const E*>(a.Tt)[((long)col * a.nloc + pos0 + k) * 4 + m];
-      continue;
     }
-    const int i = a.items[pos0 + k];
-    const int ti = a.ext_type[i];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = m * L3 + col;
-      double v = 0.0;
-      for (int tj = 0; tj < a.ntypes; ++tj) {
-        const long sec = (long)i * a.ntypes + tj;
-        const double npad = (double)(a.sel[tj] - a.nreal[sec]);
-        v += (double)Tsec[sec * per + e] + npad * a.tpad[((long)(ti * a.ntypes + tj)) * per + e];
-      }
-      Ts[(k * 4 + m) * LR + col] = (double)(E)(v * a.inv_nnei);
-    }
+  } else {
+    for (int q = threadIdx.x; q < na * L3; q += 2 * blockDim.x) desc_sum<E, NT>(a, Ts, pos0, na, q);
   }
   __syncthreads();
   if (!a.from_tt) {
@@ -641,13 +687,21 @@ void launch_embed_bwd(hipStream_t st, const EmbLayout& e, const EmbArgs& a, int 
   else bwd_impl<ShapeMetal>(st, a, nblocks);
 }
 
+template <int NT>
+static void desc_dispatch(hipStream_t st, const DescArgs& a, bool f32, dim3 grid, size_t lds) {
+  if constexpr (NT < kMaxTypes) {
+    if (a.ntypes != NT) return desc_dispatch<NT + 1>(st, a, f32, grid, lds);
+  }
+  if (f32) hipLaunchKernelGGL((k_descriptor<float, NT>), grid, dim3(256), lds, st, a);
+  else hipLaunchKernelGGL((k_descriptor<double, NT>), grid, dim3(256), lds, st, a);
+}
+
 void launch_descriptor(hipStream_t st, const DescArgs& a, bool f32) {
   if (a.nloc <= 0) return;
   if (a.L3 > 128) throw HipError{hipErrorInvalidValue, "descriptor kernel needs L3 <= 128"};
   const dim3 grid((a.nloc + kDescAtoms - 1) / kDescAtoms);
   const size_t lds = sizeof(double) * kDescAtoms * 4 * (a.L3 + 1);
-  if (f32) hipLaunchKernelGGL(k_descriptor<float>, grid, dim3(256), lds, st, a);
-  else hipLaunchKernelGGL(k_descriptor<double>, grid, dim3(256), lds, st, a);
+  desc_dispatch<1>(st, a, f32, grid, lds);
   DPAMD_LAUNCH_CHECK();
 }
 

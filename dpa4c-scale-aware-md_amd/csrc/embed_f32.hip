@@ -92,165 +92,168 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
     if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
   }
   __syncthreads();
-  const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
-  if (item >= a.type_off[ti + 1] - a.type_off[ti]) return;
-  const int i = a.items[a.type_off[ti] + item];
-  const int nr = a.nreal[(long)i * a.ntypes + tj];
-  const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
-  // env statistics from LDS: a global load inside the tile loop would be
-  // ordered behind the activation traffic by the in-order vector memory
-  // counter
-  const double* avg = EnvS;
-  const double* sd = EnvS + 4;
-  const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
+  const int nitems = a.type_off[ti + 1] - a.type_off[ti];
+  for (int it = 0; it < a.ipw; ++it) {
+    const int item = (((int)blockIdx.x - a.block_off[p]) * a.ipw + it) * WAVES + w;
+    if (item >= nitems) break;
+    const int i = a.items[a.type_off[ti] + item];
+    const int nr = a.nreal[(long)i * a.ntypes + tj];
+    const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
+    // env statistics from LDS: a global load inside the tile loop would be
+    // ordered behind the activation traffic by the in-order vector memory
+    // counter
+    const double* avg = EnvS;
+    const double* sd = EnvS + 4;
+    const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
 
-  float Tacc[S::NU3 * 4];
-#pragma unroll
-  for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0f;
-  constexpr int BLK = 16 * (S::L2P + S::L3P);
-  float* act = static_cast<float*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
-  f4* act2 = reinterpret_cast<f4*>(act) + lane;                // (t) at act2[64t]
-  f4* act3 = reinterpret_cast<f4*>(act + 16 * S::L2P) + lane;  // (u) at act3[64u]
+    float Tacc[S::NU3 * 4];
+  #pragma unroll
+    for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0f;
+    constexpr int BLK = 16 * (S::L2P + S::L3P);
+    float* act = static_cast<float*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
+    f4* act2 = reinterpret_cast<f4*>(act) + lane;                // (t) at act2[64t]
+    f4* act3 = reinterpret_cast<f4*>(act + 16 * S::L2P) + lane;  // (u) at act3[64u]
 
-  // neighbour coordinates one tile ahead, their index two tiles ahead
-  double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
-  if (c < nr) {
-    const long j = row[c];
-    nx0 = a.ext[3 * j];
-    nx1 = a.ext[3 * j + 1];
-    nx2 = a.ext[3 * j + 2];
-  }
-  int jn = 16 + c < nr ? row[16 + c] : 0;
-  for (int tile = 0; tile < nr; tile += 16, act2 += BLK / 4, act3 += BLK / 4) {
-    const int slot = tile + c;
-    double Rn[4] = {0.0, 0.0, 0.0, 0.0};
-    if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, avg, sd, Rn);
-    if (slot + 16 < nr) {
-      nx0 = a.ext[3 * (long)jn];
-      nx1 = a.ext[3 * (long)jn + 1];
-      nx2 = a.ext[3 * (long)jn + 2];
+    // neighbour coordinates one tile ahead, their index two tiles ahead
+    double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
+    if (c < nr) {
+      const long j = row[c];
+      nx0 = a.ext[3 * j];
+      nx1 = a.ext[3 * j + 1];
+      nx2 = a.ext[3 * j + 2];
     }
-    jn = slot + 32 < nr ? row[slot + 32] : 0;
-    if (g == 0) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) Rs[c * 4 + m] = (float)Rn[m];
-    }
-    const float s = (float)Rn[0];
+    int jn = 16 + c < nr ? row[16 + c] : 0;
+    for (int tile = 0; tile < nr; tile += 16, act2 += BLK / 4, act3 += BLK / 4) {
+      const int slot = tile + c;
+      double Rn[4] = {0.0, 0.0, 0.0, 0.0};
+      if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, avg, sd, Rn);
+      if (slot + 16 < nr) {
+        nx0 = a.ext[3 * (long)jn];
+        nx1 = a.ext[3 * (long)jn + 1];
+        nx2 = a.ext[3 * (long)jn + 2];
+      }
+      jn = slot + 32 < nr ? row[slot + 32] : 0;
+      if (g == 0) {
+  #pragma unroll
+        for (int m = 0; m < 4; ++m) Rs[c * 4 + m] = (float)Rn[m];
+      }
+      const float s = (float)Rn[0];
 
-    // layer 1 -> B operand of layer 2 (feature kf1(q, g) of slot c)
-    float x1[S::NQ2];
-#pragma unroll
-    for (int q = 0; q < S::NQ2; ++q) {
-      const int f = kf1<S>(q, g);
-      x1[q] = (f < S::L1) ? tanh_f32(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0f;
-    }
-    // layer 2, transposed: register r of tile t is feature 16t + 4g + r
-    f4 acc2[S::NT2];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) acc2[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int q = 0; q < S::NQ2; ++q) {
-      const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::L2P + c;
-#pragma unroll
-      for (int t = 0; t < S::NT2; ++t) acc2[t] = mfma_f32(W2[16 * t], x1[q], acc2[t]);
-    }
-    float x2[S::NT2][4];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) {
-      f4 th4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int f = 16 * t + 4 * g + r;
-        const float th = tanh_f32(acc2[t][r] + P[S::OFF_B2 + f]);
-        th4[r] = th;
-        float res = 0.0f;
-        if constexpr (S::RES2 != 0) {
-          if constexpr (S::X1_ALIGNED) {
-            res = x1[(S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r];
-          } else {
-            const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
-            res = (f1 < S::L1) ? tanh_f32(s * P[S::OFF_W1 + f1] + P[S::OFF_B1 + f1]) : 0.0f;
+      // layer 1 -> B operand of layer 2 (feature kf1(q, g) of slot c)
+      float x1[S::NQ2];
+  #pragma unroll
+      for (int q = 0; q < S::NQ2; ++q) {
+        const int f = kf1<S>(q, g);
+        x1[q] = (f < S::L1) ? tanh_f32(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0f;
+      }
+      // layer 2, transposed: register r of tile t is feature 16t + 4g + r
+      f4 acc2[S::NT2];
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) acc2[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+      for (int q = 0; q < S::NQ2; ++q) {
+        const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::L2P + c;
+  #pragma unroll
+        for (int t = 0; t < S::NT2; ++t) acc2[t] = mfma_f32(W2[16 * t], x1[q], acc2[t]);
+      }
+      float x2[S::NT2][4];
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) {
+        f4 th4;
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int f = 16 * t + 4 * g + r;
+          const float th = tanh_f32(acc2[t][r] + P[S::OFF_B2 + f]);
+          th4[r] = th;
+          float res = 0.0f;
+          if constexpr (S::RES2 != 0) {
+            if constexpr (S::X1_ALIGNED) {
+              res = x1[(S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r];
+            } else {
+              const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
+              res = (f1 < S::L1) ? tanh_f32(s * P[S::OFF_W1 + f1] + P[S::OFF_B1 + f1]) : 0.0f;
+            }
+          }
+          x2[t][r] = (f < S::L2) ? res + th : 0.0f;
+        }
+        act2[64 * t] = th4;
+      }
+      if constexpr (S::RES3 != 0) {
+  #pragma unroll
+        for (int t = 0; t < S::NT2; ++t)
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) X2s[c * X2LD + 16 * t + 4 * g + r] = x2[t][r];
+      }
+      wave_lds_sync();
+      // layer 3, non-transposed: register r of tile u is slot 4g + r, feature 16u + c
+  #pragma unroll
+      for (int u0 = 0; u0 < S::NU3; u0 += kU3F) {
+        __builtin_amdgcn_sched_barrier(0);
+        f4 acc3[kU3F];
+  #pragma unroll
+        for (int uu = 0; uu < kU3F; ++uu) acc3[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+        for (int q = 0; q < NQ3F; ++q) {
+          const float av = x2[q >> 2][q & 3];
+          const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::L3P + 16 * u0 + c;
+  #pragma unroll
+          for (int uu = 0; uu < kU3F; ++uu)
+            if (u0 + uu < S::NU3) acc3[uu] = mfma_f32(av, W3[16 * uu], acc3[uu]);
+        }
+  #pragma unroll
+        for (int uu = 0; uu < kU3F; ++uu) {
+          const int u = u0 + uu;
+          if (u < S::NU3) {
+            const int f = 16 * u + c;
+            f4 th4;
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int sl = 4 * g + r;
+              const float th = tanh_f32(acc3[uu][r] + P[S::OFF_B3 + f]);
+              th4[r] = th;
+              float G = th;
+              if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
+              if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
+  #pragma unroll
+              for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
+            }
+            act3[64 * u] = th4;
           }
         }
-        x2[t][r] = (f < S::L2) ? res + th : 0.0f;
       }
-      act2[64 * t] = th4;
+      wave_lds_sync();
     }
-    if constexpr (S::RES3 != 0) {
-#pragma unroll
-      for (int t = 0; t < S::NT2; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) X2s[c * X2LD + 16 * t + 4 * g + r] = x2[t][r];
+  #pragma unroll
+    for (int q = 0; q < S::NU3 * 4; ++q) {
+      float v = Tacc[q];
+      v += shfl_xor_d(v, 16);
+      v += shfl_xor_d(v, 32);
+      Tacc[q] = v;
     }
-    wave_lds_sync();
-    // layer 3, non-transposed: register r of tile u is slot 4g + r, feature 16u + c
-#pragma unroll
-    for (int u0 = 0; u0 < S::NU3; u0 += kU3F) {
-      __builtin_amdgcn_sched_barrier(0);
-      f4 acc3[kU3F];
-#pragma unroll
-      for (int uu = 0; uu < kU3F; ++uu) acc3[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int q = 0; q < NQ3F; ++q) {
-        const float av = x2[q >> 2][q & 3];
-        const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::L3P + 16 * u0 + c;
-#pragma unroll
-        for (int uu = 0; uu < kU3F; ++uu)
-          if (u0 + uu < S::NU3) acc3[uu] = mfma_f32(av, W3[16 * uu], acc3[uu]);
-      }
-#pragma unroll
-      for (int uu = 0; uu < kU3F; ++uu) {
-        const int u = u0 + uu;
-        if (u < S::NU3) {
-          const int f = 16 * u + c;
-          f4 th4;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int sl = 4 * g + r;
-            const float th = tanh_f32(acc3[uu][r] + P[S::OFF_B3 + f]);
-            th4[r] = th;
-            float G = th;
-            if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
-            if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
-          }
-          act3[64 * u] = th4;
+    if (g == 0 && a.Tt) {
+      // single neighbour type: this section is all of T
+      const double npad = (double)(a.sel[tj] - nr);
+      const double* tp = a.tpad + (long)p * 4 * S::L3;
+      float* Tt = static_cast<float*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
+  #pragma unroll
+      for (int u = 0; u < S::NU3; ++u) {
+        const int f = 16 * u + c;
+        if (f < S::L3) {
+  #pragma unroll
+          for (int m = 0; m < 4; ++m)
+            Tt[f * a.ldt + m] =
+                (float)(((double)Tacc[u * 4 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
         }
       }
-    }
-    wave_lds_sync();
-  }
-#pragma unroll
-  for (int q = 0; q < S::NU3 * 4; ++q) {
-    float v = Tacc[q];
-    v += shfl_xor_d(v, 16);
-    v += shfl_xor_d(v, 32);
-    Tacc[q] = v;
-  }
-  if (g == 0 && a.Tt) {
-    // single neighbour type: this section is all of T
-    const double npad = (double)(a.sel[tj] - nr);
-    const double* tp = a.tpad + (long)p * 4 * S::L3;
-    float* Tt = static_cast<float*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
-#pragma unroll
-    for (int u = 0; u < S::NU3; ++u) {
-      const int f = 16 * u + c;
-      if (f < S::L3) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          Tt[f * a.ldt + m] =
-              (float)(((double)Tacc[u * 4 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
-      }
-    }
-  } else if (g == 0) {
-    float* out = static_cast<float*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
-#pragma unroll
-    for (int u = 0; u < S::NU3; ++u) {
-      const int f = 16 * u + c;
-      if (f < S::L3) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) out[m * S::L3 + f] = Tacc[u * 4 + m];
+    } else if (g == 0) {
+      float* out = static_cast<float*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
+  #pragma unroll
+      for (int u = 0; u < S::NU3; ++u) {
+        const int f = 16 * u + c;
+        if (f < S::L3) {
+  #pragma unroll
+          for (int m = 0; m < 4; ++m) out[m * S::L3 + f] = Tacc[u * 4 + m];
+        }
       }
     }
   }
@@ -277,219 +280,222 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
     if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
   }
   __syncthreads();
-  const int item = ((int)blockIdx.x - a.block_off[p]) * WAVES + w;
-  if (item >= a.type_off[ti + 1] - a.type_off[ti]) return;
-  const int i = a.items[a.type_off[ti] + item];
-  const int nr = a.nreal[(long)i * a.ntypes + tj];
-  const long ebase = (long)i * a.nnei + a.sec[tj];
-  const int* row = a.nlist + ebase;
-  // env statistics from LDS: a global load inside the tile loop would be
-  // ordered behind the activation traffic by the in-order vector memory
-  // counter
-  const double* avg = EnvS;
-  const double* sd = EnvS + 4;
-  const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
-  constexpr int BLK = 16 * (S::L2P + S::L3P);
-  const float* act =
-      static_cast<const float*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
+  const int nitems = a.type_off[ti + 1] - a.type_off[ti];
+  for (int it = 0; it < a.ipw; ++it) {
+    const int item = (((int)blockIdx.x - a.block_off[p]) * a.ipw + it) * WAVES + w;
+    if (item >= nitems) break;
+    const int i = a.items[a.type_off[ti] + item];
+    const int nr = a.nreal[(long)i * a.ntypes + tj];
+    const long ebase = (long)i * a.nnei + a.sec[tj];
+    const int* row = a.nlist + ebase;
+    // env statistics from LDS: a global load inside the tile loop would be
+    // ordered behind the activation traffic by the in-order vector memory
+    // counter
+    const double* avg = EnvS;
+    const double* sd = EnvS + 4;
+    const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
+    constexpr int BLK = 16 * (S::L2P + S::L3P);
+    const float* act =
+        static_cast<const float*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
 
-  {
-    const float* dTi = static_cast<const float*>(a.dT) + (long)i * 4 * S::L3;
-    for (int q = lane; q < 4 * S::L3P; q += 64) {
-      const int m = q / S::L3P, f = q % S::L3P;
-      dTs[q] = f < S::L3 ? dTi[m * S::L3 + f] : 0.0f;
-    }
-    for (int q = lane; q < 4 * S::L2P; q += 64) {
-      const int m = q / S::L2P, f = q % S::L2P;
-      float v = 0.0f;
-      if (f < S::L2) {
-        if constexpr (S::RES3 == 2) v = dTi[m * S::L3 + f] + dTi[m * S::L3 + f + S::L2];
-        if constexpr (S::RES3 == 1) v = dTi[m * S::L3 + f];
+    {
+      const float* dTi = static_cast<const float*>(a.dT) + (long)i * 4 * S::L3;
+      for (int q = lane; q < 4 * S::L3P; q += 64) {
+        const int m = q / S::L3P, f = q % S::L3P;
+        dTs[q] = f < S::L3 ? dTi[m * S::L3 + f] : 0.0f;
       }
-      dTf[q] = v;
-    }
-  }
-  wave_lds_sync();
-
-  const f4* act2 = reinterpret_cast<const f4*>(act) + lane;  // (t) at act2[64t]
-  // (u, r) at act3[256u + 4r]
-  const float* act3 = act + 16 * S::L2P + 64 * (c >> 2) + 16 * g + (c & 3);
-  // activations and neighbour coordinates of tile k+1 fetched during tile k,
-  // the neighbour index one tile earlier
-  f4 nth2[S::NT2];
-  float nth3[S::NU3][4];
-  double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
-  int jn = 0;
-  auto prefetch = [&](int tile, const f4* p2, const float* p3) {
-    if (tile + c < nr) {
-      nx0 = a.ext[3 * (long)jn];
-      nx1 = a.ext[3 * (long)jn + 1];
-      nx2 = a.ext[3 * (long)jn + 2];
-    }
-    jn = tile + 16 + c < nr ? row[tile + 16 + c] : 0;
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) nth2[t] = p2[64 * t];
-#pragma unroll
-    for (int u = 0; u < S::NU3; ++u)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) nth3[u][r] = p3[256 * u + 4 * r];
-  };
-  jn = c < nr ? row[c] : 0;
-  if (nr > 0) prefetch(0, act2, act3);
-
-  for (int tile = 0; tile < nr; tile += 16, act2 += BLK / 4, act3 += BLK) {
-    const int slot = tile + c;
-    const bool valid = slot < nr;
-    f4 th2[S::NT2];
-    float th3[S::NU3][4];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) th2[t] = nth2[t];
-#pragma unroll
-    for (int u = 0; u < S::NU3; ++u)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) th3[u][r] = nth3[u][r];
-    double d0 = 0.0, d1 = 0.0, d2 = 0.0;
-    double Rn[4] = {0.0, 0.0, 0.0, 0.0};
-    if (valid) {
-      d0 = nx0 - xi;
-      d1 = nx1 - yi;
-      d2 = nx2 - zi;
-      env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
-    }
-    if (tile + 16 < nr) prefetch(tile + 16, act2 + BLK / 4, act3 + BLK);
-    const float s = (float)Rn[0];
-
-    // layer 1 (recomputed) and its tangent
-    float x1[S::NQ2], x1t[S::NQ2];
-#pragma unroll
-    for (int q = 0; q < S::NQ2; ++q) {
-      const int f = kf1<S>(q, g);
-      if (f < S::L1) {
-        const float wv = P[S::OFF_W1 + f];
-        const float th = tanh_f32(s * wv + P[S::OFF_B1 + f]);
-        x1[q] = th;
-        x1t[q] = (1.0f - th * th) * wv;
-      } else {
-        x1[q] = 0.0f;
-        x1t[q] = 0.0f;
-      }
-    }
-    // layer 2 tangent (transposed); tanh of the primal from the forward
-    f4 acc2t[S::NT2];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) acc2t[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int q = 0; q < S::NQ2; ++q) {
-      const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::L2P + c;
-#pragma unroll
-      for (int t = 0; t < S::NT2; ++t) acc2t[t] = mfma_f32(W2[16 * t], x1t[q], acc2t[t]);
-    }
-    float x2[S::NT2][4], x2t[S::NT2][4];
-#pragma unroll
-    for (int t = 0; t < S::NT2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int f = 16 * t + 4 * g + r;
-        const float th = th2[t][r];
-        float res = 0.0f, rest = 0.0f;
-        if constexpr (S::RES2 != 0) {
-          if constexpr (S::X1_ALIGNED) {
-            const int q1 = (S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r;
-            res = x1[q1];
-            rest = x1t[q1];
-          } else {
-            const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
-            if (f1 < S::L1) {
-              const float wv = P[S::OFF_W1 + f1];
-              const float y = tanh_f32(s * wv + P[S::OFF_B1 + f1]);
-              res = y;
-              rest = (1.0f - y * y) * wv;
-            }
-          }
+      for (int q = lane; q < 4 * S::L2P; q += 64) {
+        const int m = q / S::L2P, f = q % S::L2P;
+        float v = 0.0f;
+        if (f < S::L2) {
+          if constexpr (S::RES3 == 2) v = dTi[m * S::L3 + f] + dTi[m * S::L3 + f + S::L2];
+          if constexpr (S::RES3 == 1) v = dTi[m * S::L3 + f];
         }
-        const bool live = f < S::L2;
-        x2[t][r] = live ? res + th : 0.0f;
-        x2t[t][r] = live ? rest + (1.0f - th * th) * acc2t[t][r] : 0.0f;
+        dTf[q] = v;
       }
     }
-    // u = dT.G, v = dT.G': the layer-3 residual through the folded dT
-    float up[4] = {0.0f, 0.0f, 0.0f, 0.0f}, vp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (S::RES3 != 0) {
-#pragma unroll
-      for (int t = 0; t < S::NT2; ++t)
-#pragma unroll
+    wave_lds_sync();
+
+    const f4* act2 = reinterpret_cast<const f4*>(act) + lane;  // (t) at act2[64t]
+    // (u, r) at act3[256u + 4r]
+    const float* act3 = act + 16 * S::L2P + 64 * (c >> 2) + 16 * g + (c & 3);
+    // activations and neighbour coordinates of tile k+1 fetched during tile k,
+    // the neighbour index one tile earlier
+    f4 nth2[S::NT2];
+    float nth3[S::NU3][4];
+    double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
+    int jn = 0;
+    auto prefetch = [&](int tile, const f4* p2, const float* p3) {
+      if (tile + c < nr) {
+        nx0 = a.ext[3 * (long)jn];
+        nx1 = a.ext[3 * (long)jn + 1];
+        nx2 = a.ext[3 * (long)jn + 2];
+      }
+      jn = tile + 16 + c < nr ? row[tile + 16 + c] : 0;
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) nth2[t] = p2[64 * t];
+  #pragma unroll
+      for (int u = 0; u < S::NU3; ++u)
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) nth3[u][r] = p3[256 * u + 4 * r];
+    };
+    jn = c < nr ? row[c] : 0;
+    if (nr > 0) prefetch(0, act2, act3);
+
+    for (int tile = 0; tile < nr; tile += 16, act2 += BLK / 4, act3 += BLK) {
+      const int slot = tile + c;
+      const bool valid = slot < nr;
+      f4 th2[S::NT2];
+      float th3[S::NU3][4];
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) th2[t] = nth2[t];
+  #pragma unroll
+      for (int u = 0; u < S::NU3; ++u)
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) th3[u][r] = nth3[u][r];
+      double d0 = 0.0, d1 = 0.0, d2 = 0.0;
+      double Rn[4] = {0.0, 0.0, 0.0, 0.0};
+      if (valid) {
+        d0 = nx0 - xi;
+        d1 = nx1 - yi;
+        d2 = nx2 - zi;
+        env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
+      }
+      if (tile + 16 < nr) prefetch(tile + 16, act2 + BLK / 4, act3 + BLK);
+      const float s = (float)Rn[0];
+
+      // layer 1 (recomputed) and its tangent
+      float x1[S::NQ2], x1t[S::NQ2];
+  #pragma unroll
+      for (int q = 0; q < S::NQ2; ++q) {
+        const int f = kf1<S>(q, g);
+        if (f < S::L1) {
+          const float wv = P[S::OFF_W1 + f];
+          const float th = tanh_f32(s * wv + P[S::OFF_B1 + f]);
+          x1[q] = th;
+          x1t[q] = (1.0f - th * th) * wv;
+        } else {
+          x1[q] = 0.0f;
+          x1t[q] = 0.0f;
+        }
+      }
+      // layer 2 tangent (transposed); tanh of the primal from the forward
+      f4 acc2t[S::NT2];
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) acc2t[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+      for (int q = 0; q < S::NQ2; ++q) {
+        const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::L2P + c;
+  #pragma unroll
+        for (int t = 0; t < S::NT2; ++t) acc2t[t] = mfma_f32(W2[16 * t], x1t[q], acc2t[t]);
+      }
+      float x2[S::NT2][4], x2t[S::NT2][4];
+  #pragma unroll
+      for (int t = 0; t < S::NT2; ++t) {
+  #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int f = 16 * t + 4 * g + r;
-#pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            const float wv = dTf[m * S::L2P + f];
-            up[m] += wv * x2[t][r];
-            vp[m] += wv * x2t[t][r];
+          const float th = th2[t][r];
+          float res = 0.0f, rest = 0.0f;
+          if constexpr (S::RES2 != 0) {
+            if constexpr (S::X1_ALIGNED) {
+              const int q1 = (S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r;
+              res = x1[q1];
+              rest = x1t[q1];
+            } else {
+              const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
+              if (f1 < S::L1) {
+                const float wv = P[S::OFF_W1 + f1];
+                const float y = tanh_f32(s * wv + P[S::OFF_B1 + f1]);
+                res = y;
+                rest = (1.0f - y * y) * wv;
+              }
+            }
           }
+          const bool live = f < S::L2;
+          x2[t][r] = live ? res + th : 0.0f;
+          x2t[t][r] = live ? rest + (1.0f - th * th) * acc2t[t][r] : 0.0f;
         }
-    }
-    // layer 3 tangent, transposed: register r of tile u is feature 16u + 4g + r
-#pragma unroll
-    for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
-      __builtin_amdgcn_sched_barrier(0);
-      f4 acc3t[kU3B];
-#pragma unroll
-      for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int q = 0; q < NQ3F; ++q) {
-        const float bv = x2t[q >> 2][q & 3];
-        const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::L3P + 16 * u0 + c;
-#pragma unroll
-        for (int uu = 0; uu < kU3B; ++uu)
-          if (u0 + uu < S::NU3) acc3t[uu] = mfma_f32(W3[16 * uu], bv, acc3t[uu]);
       }
-#pragma unroll
-      for (int uu = 0; uu < kU3B; ++uu) {
-        const int u = u0 + uu;
-        if (u < S::NU3) {
-#pragma unroll
+      // u = dT.G, v = dT.G': the layer-3 residual through the folded dT
+      float up[4] = {0.0f, 0.0f, 0.0f, 0.0f}, vp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (S::RES3 != 0) {
+  #pragma unroll
+        for (int t = 0; t < S::NT2; ++t)
+  #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int f = 16 * u + 4 * g + r;
-            const float th = th3[u][r];
-            const float tt = (1.0f - th * th) * acc3t[uu][r];
-#pragma unroll
+            const int f = 16 * t + 4 * g + r;
+  #pragma unroll
             for (int m = 0; m < 4; ++m) {
-              const float wv = dTs[m * S::L3P + f];
-              up[m] += wv * th;
-              vp[m] += wv * tt;
+              const float wv = dTf[m * S::L2P + f];
+              up[m] += wv * x2[t][r];
+              vp[m] += wv * x2t[t][r];
+            }
+          }
+      }
+      // layer 3 tangent, transposed: register r of tile u is feature 16u + 4g + r
+  #pragma unroll
+      for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
+        __builtin_amdgcn_sched_barrier(0);
+        f4 acc3t[kU3B];
+  #pragma unroll
+        for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+        for (int q = 0; q < NQ3F; ++q) {
+          const float bv = x2t[q >> 2][q & 3];
+          const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::L3P + 16 * u0 + c;
+  #pragma unroll
+          for (int uu = 0; uu < kU3B; ++uu)
+            if (u0 + uu < S::NU3) acc3t[uu] = mfma_f32(W3[16 * uu], bv, acc3t[uu]);
+        }
+  #pragma unroll
+        for (int uu = 0; uu < kU3B; ++uu) {
+          const int u = u0 + uu;
+          if (u < S::NU3) {
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int f = 16 * u + 4 * g + r;
+              const float th = th3[u][r];
+              const float tt = (1.0f - th * th) * acc3t[uu][r];
+  #pragma unroll
+              for (int m = 0; m < 4; ++m) {
+                const float wv = dTs[m * S::L3P + f];
+                up[m] += wv * th;
+                vp[m] += wv * tt;
+              }
             }
           }
         }
       }
+  #pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        up[m] += shfl_xor_d(up[m], 16);
+        up[m] += shfl_xor_d(up[m], 32);
+        vp[m] += shfl_xor_d(vp[m], 16);
+        vp[m] += shfl_xor_d(vp[m], 32);
+      }
+      if (valid && g == 0) {
+        double nd[4];
+  #pragma unroll
+        for (int m = 0; m < 4; ++m) nd[m] = (double)up[m] * a.inv_nnei;
+        nd[0] += (Rn[0] * (double)vp[0] + Rn[1] * (double)vp[1] + Rn[2] * (double)vp[2] +
+                  Rn[3] * (double)vp[3]) *
+                 a.inv_nnei;
+        double gv[3];
+        env_grad(d0, d1, d2, a.rcut_smth, a.rcut, sd, nd, gv);
+        double* eg = a.edge_grad + (ebase + slot) * 3;
+        eg[0] = gv[0];
+        eg[1] = gv[1];
+        eg[2] = gv[2];
+      }
     }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      up[m] += shfl_xor_d(up[m], 16);
-      up[m] += shfl_xor_d(up[m], 32);
-      vp[m] += shfl_xor_d(vp[m], 16);
-      vp[m] += shfl_xor_d(vp[m], 32);
+    // padded slots carry no gradient
+    for (int sl = nr + lane; sl < a.sel[tj]; sl += 64) {
+      double* eg = a.edge_grad + (ebase + sl) * 3;
+      eg[0] = 0.0;
+      eg[1] = 0.0;
+      eg[2] = 0.0;
     }
-    if (valid && g == 0) {
-      double nd[4];
-#pragma unroll
-      for (int m = 0; m < 4; ++m) nd[m] = (double)up[m] * a.inv_nnei;
-      nd[0] += (Rn[0] * (double)vp[0] + Rn[1] * (double)vp[1] + Rn[2] * (double)vp[2] +
-                Rn[3] * (double)vp[3]) *
-               a.inv_nnei;
-      double gv[3];
-      env_grad(d0, d1, d2, a.rcut_smth, a.rcut, sd, nd, gv);
-      double* eg = a.edge_grad + (ebase + slot) * 3;
-      eg[0] = gv[0];
-      eg[1] = gv[1];
-      eg[2] = gv[2];
-    }
-  }
-  // padded slots carry no gradient
-  for (int sl = nr + lane; sl < a.sel[tj]; sl += 64) {
-    double* eg = a.edge_grad + (ebase + sl) * 3;
-    eg[0] = 0.0;
-    eg[1] = 0.0;
-    eg[2] = 0.0;
   }
 }
 

@@ -69,6 +69,9 @@ struct EmbArgs {
   void* Tt;
   long ldt;
   const double* tpad;  // [npair][4][L3]
+  // items per wave: block b of a pair serves items (b ipw + k) WAVES + w,
+  // k < ipw, so its weights are staged in LDS once for WAVES * ipw items
+  int ipw;
 };
 
 struct DescArgs {
