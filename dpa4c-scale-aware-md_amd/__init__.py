@@ -29,8 +29,8 @@ STAGE_ATOM_ENERGY, STAGE_EDGE_GRAD, STAGE_DEDD, STAGE_EXT_TYPE = 4, 5, 6, 7
 PREC_FP64, PREC_MIXED = 0, 1
 
 EXPORTED = ("dp_create", "dp_destroy", "dp_get_info", "dp_last_error", "dp_compute",
-            "dp_compute_nlist", "dp_compute_device", "dp_debug_copy", "dp_stage_times",
-            "dp_device_bytes")
+            "dp_compute_nlist", "dp_compute_device", "dp_compute_device_async", "dp_sync",
+            "dp_debug_copy", "dp_stage_times", "dp_device_bytes")
 
 
 class DeepmdException(RuntimeError):
@@ -62,6 +62,8 @@ def lib():
         L.dp_compute.argtypes = [P, I, P, P, P, P, P, P, P, P]
         L.dp_compute_nlist.argtypes = [P, I, I, P, P, P, I, P, P, P, I, I, P, P, P, P, P]
         L.dp_compute_device.argtypes = [P, I, P, P, P, I, P, P, P, P, P, P]
+        L.dp_compute_device_async.argtypes = [P, I, P, P, P, I, P, P, P, P, P, P]
+        L.dp_sync.argtypes = [P]
         L.dp_debug_copy.argtypes = [P, I, P, C.c_size_t]
         L.dp_debug_copy.restype = C.c_long
         L.dp_stage_times.argtypes = [P, I, P, I, P, C.c_size_t]
@@ -187,6 +189,21 @@ class DeepPot:
         self._check(lib().dp_compute_device(self._h, natoms, d_coord, d_atype, _ptr(boxa), ago,
                                             d_energy, d_force, d_virial, d_atom_energy or None,
                                             d_atom_virial or None, stream or None))
+
+    def compute_device_async(self, d_coord: int, d_atype: int, natoms: int, box, d_energy: int,
+                             d_force: int, d_virial: int, d_atom_energy: int = 0,
+                             d_atom_virial: int = 0, ago: int = 1, stream: int = 0):
+        """Enqueue a device-resident evaluation and return without waiting
+        (dp_compute_device_async); sync() waits and reports deferred errors."""
+        boxa = np.ascontiguousarray(box, np.float64).reshape(9)
+        self._check(lib().dp_compute_device_async(self._h, natoms, d_coord, d_atype, _ptr(boxa),
+                                                  ago, d_energy, d_force, d_virial,
+                                                  d_atom_energy or None, d_atom_virial or None,
+                                                  stream or None))
+
+    def sync(self):
+        """Wait for the queued asynchronous evaluations (dp_sync)."""
+        self._check(lib().dp_sync(self._h))
 
     # ---- introspection -----------------------------------------------------
     def stage(self, which: int, dtype, shape):

@@ -74,12 +74,19 @@ struct dp_model {
   void* d_fit = nullptr;
   FitOffsets fo{};
   void* blas = nullptr;  // rocBLAS handle for the plain input-gradient GEMM
+  // With several centre types the per-type fitting chains run concurrently,
+  // each on a stream of its own (default priority) with its own rocBLAS
+  // handle, forked from and joined back into the evaluation stream.
+  hipStream_t fit_st[kMaxTypes] = {};
+  void* fit_blas[kMaxTypes] = {};
+  hipEvent_t fork_ev = nullptr;
+  hipEvent_t join_ev[kMaxTypes] = {};
   // workspace
   std::vector<Buf*> bufs;
   Buf coord_in, atype_in, sfrac, flags, gpos, ext, ext_type, mapping, cell_of, cell_count,
       cell_start, cell_cursor, sorted, nlist, nreal, cand_off, cand, items, Tsec, Tt, D, dD, dT,
       fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_cursor, rev, force_ws, av_ws,
-      ae_ws, partials, out10, status, scan_tmp, act;
+      ae_ws, partials, out10, status, scan_tmp, act, nall_d;
   size_t bytes_now = 0, bytes_peak = 0;
   // type buckets
   std::vector<int> atype_cache;
@@ -90,12 +97,25 @@ struct dp_model {
   // LAMMPS candidate cache
   bool cand_valid = false;
   int cand_nloc = -1;
-  // last evaluation sizes (debug copies)
+  // last evaluation sizes (debug copies); on the standalone path last_nall is
+  // the capacity of the extended arrays and the count itself is in nall_d
   int last_nloc = 0, last_nall = 0;
   bool last_standalone = true;
+  // asynchronous evaluations (dp_compute_device_async): the status word is
+  // sticky across them and copied to pinned host memory after each one
+  int* status_host = nullptr;
+  hipStream_t async_stream = nullptr;
+  bool async_pending = false;
   // stage timers
   bool timing = false;
-  hipEvent_t ev[kNumStages + 1] = {};
+  // one event set per evaluation in a ring, so that evaluations queued by
+  // dp_compute_device_async are timed too; stage_ms is the mean over the
+  // evaluations harvested since the previous synchronisation point
+  static constexpr int kRing = 32;
+  hipEvent_t ev[kRing][kNumStages + 1] = {};
+  int ev_cur = 0, ev_head = 0, ev_pending = 0;
+  double st_sum[kNumStages] = {0};
+  int st_count = 0;
   float stage_ms[kNumStages] = {0};
 
   dp_model() {
@@ -104,7 +124,7 @@ struct dp_model {
             &nreal,    &cand_off, &cand,      &items,    &Tsec,       &Tt,        &D,
             &dD,       &dT,       &fitb,      &e_bucket, &edge_grad,  &cpart,     &rev_count,
             &rev_off,  &rev_cursor, &rev,     &force_ws, &av_ws,      &ae_ws,     &partials,
-            &out10,    &status,   &scan_tmp, &act};
+            &out10,    &status,   &scan_tmp, &act,       &nall_d};
   }
 };
 
@@ -115,6 +135,8 @@ T* need(dp_model* M, Buf& b, size_t count) {
   const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
   if (bytes > b.cap) {
     if (b.p) {
+      // queued asynchronous evaluations may still use the old buffer
+      if (M->async_pending) DPAMD_HIP(hipStreamSynchronize(M->async_stream));
       DPAMD_HIP(hipFree(b.p));
       M->bytes_now -= b.cap;
     }
@@ -127,30 +149,6 @@ T* need(dp_model* M, Buf& b, size_t count) {
     M->bytes_peak = std::max(M->bytes_peak, M->bytes_now);
   }
   return static_cast<T*>(b.p);
-}
-
-// Grow while keeping the first `keep` bytes.
-template <class T>
-T* need_keep(dp_model* M, Buf& b, size_t count, size_t keep_count, hipStream_t st) {
-  const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
-  if (bytes <= b.cap) return static_cast<T*>(b.p);
-  void* old = b.p;
-  const size_t old_cap = b.cap;
-  const size_t nb = bytes + bytes / 8;
-  void* np = nullptr;
-  DPAMD_HIP(hipMalloc(&np, nb));
-  M->bytes_now += nb;
-  M->bytes_peak = std::max(M->bytes_peak, M->bytes_now);
-  if (old && keep_count)
-    DPAMD_HIP(hipMemcpyAsync(np, old, keep_count * sizeof(T), hipMemcpyDeviceToDevice, st));
-  if (old) {
-    DPAMD_HIP(hipStreamSynchronize(st));
-    DPAMD_HIP(hipFree(old));
-    M->bytes_now -= old_cap;
-  }
-  b.p = np;
-  b.cap = nb;
-  return static_cast<T*>(np);
 }
 
 struct ApiError {
@@ -221,7 +219,7 @@ BoxParams make_open_frame(int n, const double* coord, double rcut) {
 }
 
 void record(dp_model* M, hipStream_t st, int stage) {
-  if (M->timing) DPAMD_HIP(hipEventRecord(M->ev[stage], st));
+  if (M->timing) DPAMD_HIP(hipEventRecord(M->ev[M->ev_cur][stage], st));
 }
 
 // Group centres by type (stable) when the types change.
@@ -374,9 +372,29 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   if (nt > 1 || D) launch_descriptor(st, desc_args(M, Tt, D), f32);
   record(M, st, kStDescr + 1);
 
+  int active = 0;
+  for (int t = 0; t < nt; ++t) active += M->type_off[t + 1] > M->type_off[t];
+  const bool fork = active > 1;
+  if (fork) {
+    if (!M->fork_ev) DPAMD_HIP(hipEventCreateWithFlags(&M->fork_ev, hipEventDisableTiming));
+    DPAMD_HIP(hipEventRecord(M->fork_ev, st));
+  }
   for (int t = 0; t < nt; ++t) {
     const int rows = M->type_off[t + 1] - M->type_off[t];
     if (rows <= 0) continue;
+    hipStream_t fst = st;
+    void* blas = M->blas;
+    if (fork) {
+      if (!M->fit_st[t]) {
+        DPAMD_HIP(hipStreamCreateWithFlags(&M->fit_st[t], hipStreamNonBlocking));
+        DPAMD_HIP(hipEventCreateWithFlags(&M->join_ev[t], hipEventDisableTiming));
+        M->fit_blas[t] = blas_create();
+        if (!M->fit_blas[t]) throw ApiError{DP_ERR_NO_GPU, "rocblas_create_handle failed"};
+      }
+      fst = M->fit_st[t];
+      blas = M->fit_blas[t];
+      DPAMD_HIP(hipStreamWaitEvent(fst, M->fork_ev, 0));
+    }
     const E* P = static_cast<const E*>(M->d_fit) + (size_t)t * m.fit_block;
     FitNet<E> net{};
     const int ins[3] = {Dn, m.fit[0], m.fit[1]};
@@ -397,9 +415,13 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
     E** slots[8] = {&fb.H0, &fb.T1, &fb.H1, &fb.T2, &fb.H2, &fb.dZa, &fb.dZb, &fb.dH};
     // slab q holds [rows][F] of every type back to back; F <= Fmax
     for (int q = 0; q < 8; ++q) *slots[q] = base + q * slab + r0 * (size_t)Fmax;
-    launch_fitting(st, net, rows, d_from_t ? nullptr : D + r0 * Dn,
+    launch_fitting(fst, net, rows, d_from_t ? nullptr : D + r0 * Dn,
                    d_from_t ? Tt + r0 * 4 : nullptr, 4L * nb, L3, fb, dD + r0 * Dn,
-                   e_bucket + r0, M->blas);
+                   e_bucket + r0, blas);
+    if (fork) {
+      DPAMD_HIP(hipEventRecord(M->join_ev[t], fst));
+      DPAMD_HIP(hipStreamWaitEvent(st, M->join_ev[t], 0));
+    }
   }
   record(M, st, kStFit + 1);
 
@@ -416,8 +438,8 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   int* roff = need<int>(M, M->rev_off, (size_t)ntarget + 1);
   int* rcur = need<int>(M, M->rev_cursor, (size_t)ntarget + 1);
   int* rev = need<int>(M, M->rev, (size_t)std::max<long>(nedge, 1));
-  DPAMD_HIP(hipMemsetAsync(rcount, 0, sizeof(int) * ((size_t)ntarget + 1), st));
-  DPAMD_HIP(hipMemsetAsync(rcur, 0, sizeof(int) * ((size_t)ntarget + 1), st));
+  launch_fill_int(st, (long)ntarget + 1, 0, rcount);
+  launch_fill_int(st, (long)ntarget + 1, 0, rcur);
   launch_rev_count(st, nedge, nnei, nlist, d_mapping, rcount);
   {
     const size_t tb = scan_temp_bytes(ntarget + 1);
@@ -436,7 +458,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   if (out.virial)
     DPAMD_HIP(hipMemcpyAsync(out.virial, out10 + 1, 72, hipMemcpyDeviceToDevice, st));
   if (out.atom_energy) {
-    DPAMD_HIP(hipMemsetAsync(out.atom_energy, 0, sizeof(double) * (size_t)ntarget, st));
+    launch_fill_int(st, 2L * ntarget, 0, reinterpret_cast<int*>(out.atom_energy));
     launch_scatter_energy(st, nb, items, e_bucket, out.atom_energy);
   }
   record(M, st, kStReduce + 1);
@@ -449,35 +471,36 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
   else run_model_t<double>(M, st, nloc, nall, d_mapping, ntarget, out);
 }
 
-// Ghosts + cells + nlist for the standalone path. Returns nall.
+// Ghosts + cells + nlist for the standalone path, with no host round trip:
+// the extended arrays are sized for every ghost candidate (nshift images of
+// each local atom, the most the box can produce), the number of ghosts is
+// counted on the device into nall_d, and the kernels over the extended atoms
+// read it from there. Returns the capacity nall_cap (>= nall).
 int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* d_coord,
                            const int* d_atype, const BoxParams& bp) {
   const ModelHost& m = M->host;
+  const long nf = bp.nshift > 0 ? (long)bp.nshift * nloc : 0;
+  if (nloc + nf >= (1L << 31) - 1) throw ApiError{DP_ERR_CAPACITY, "too many ghost candidates"};
+  const int nall_cap = nloc + (int)nf;
   double* sfrac = need<double>(M, M->sfrac, (size_t)nloc * 3);
-  double* ext = need<double>(M, M->ext, (size_t)nloc * 3 * 2);
-  int* ext_type = need<int>(M, M->ext_type, (size_t)nloc * 2);
-  int* mapping = need<int>(M, M->mapping, (size_t)nloc * 2);
+  double* ext = need<double>(M, M->ext, (size_t)nall_cap * 3);
+  int* ext_type = need<int>(M, M->ext_type, (size_t)nall_cap);
+  int* mapping = need<int>(M, M->mapping, (size_t)nall_cap);
+  int* nall_d = need<int>(M, M->nall_d, 1);
   launch_wrap(st, nloc, d_coord, d_atype, bp, ext, ext_type, mapping, sfrac);
-  int nall = nloc;
-  if (bp.nshift > 0 && nloc > 0) {
-    const long nf = (long)bp.nshift * nloc;
-    if (nf >= (1L << 31) - 1) throw ApiError{DP_ERR_CAPACITY, "too many ghost candidates"};
+  if (nf > 0) {
     int* flags = need<int>(M, M->flags, (size_t)nf);
     int* pos = need<int>(M, M->gpos, (size_t)nf);
     launch_ghost_flags(st, nloc, bp, sfrac, flags);
     const size_t tb = scan_temp_bytes((int)nf);
     void* tmp = need<char>(M, M->scan_tmp, tb);
     exclusive_scan_int(st, flags, pos, (int)nf, tmp, tb);
-    int last[2] = {0, 0};
-    DPAMD_HIP(hipMemcpyAsync(&last[0], pos + nf - 1, 4, hipMemcpyDeviceToHost, st));
-    DPAMD_HIP(hipMemcpyAsync(&last[1], flags + nf - 1, 4, hipMemcpyDeviceToHost, st));
-    DPAMD_HIP(hipStreamSynchronize(st));
-    nall = nloc + last[0] + last[1];
-    ext = need_keep<double>(M, M->ext, (size_t)nall * 3, (size_t)nloc * 3, st);
-    ext_type = need_keep<int>(M, M->ext_type, (size_t)nall, (size_t)nloc, st);
-    mapping = need_keep<int>(M, M->mapping, (size_t)nall, (size_t)nloc, st);
+    launch_ghost_total(st, nloc, nf, flags, pos, nall_d);
     launch_ghost_fill(st, nloc, bp, flags, pos, ext, ext_type, mapping);
+  } else {
+    launch_fill_int(st, 1, nloc, nall_d);
   }
+  const int nall = nall_cap;
   // cells
   const int ncell = bp.ncell[0] * bp.ncell[1] * bp.ncell[2];
   int* cell_of = need<int>(M, M->cell_of, (size_t)nall);
@@ -485,15 +508,15 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
   int* cstart = need<int>(M, M->cell_start, (size_t)ncell + 1);
   int* ccur = need<int>(M, M->cell_cursor, (size_t)ncell + 1);
   CellAtom* sorted = need<CellAtom>(M, M->sorted, (size_t)nall);
-  DPAMD_HIP(hipMemsetAsync(ccount, 0, sizeof(int) * ((size_t)ncell + 1), st));
-  DPAMD_HIP(hipMemsetAsync(ccur, 0, sizeof(int) * ((size_t)ncell + 1), st));
-  launch_cell_assign(st, nall, bp, ext, cell_of, ccount);
+  launch_fill_int(st, (long)ncell + 1, 0, ccount);
+  launch_fill_int(st, (long)ncell + 1, 0, ccur);
+  launch_cell_assign(st, nall, nall_d, bp, ext, cell_of, ccount);
   {
     const size_t tb = scan_temp_bytes(ncell + 1);
     void* tmp = need<char>(M, M->scan_tmp, tb);
     exclusive_scan_int(st, ccount, cstart, ncell + 1, tmp, tb);
   }
-  launch_cell_scatter(st, nall, cell_of, cstart, ccur, ext, ext_type, sorted);
+  launch_cell_scatter(st, nall, nall_d, cell_of, cstart, ccur, ext, ext_type, sorted);
   record(M, st, kStGeom + 1);
   NlParams np{};
   np.ntypes = m.ntypes;
@@ -509,10 +532,7 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
   return nall;
 }
 
-void check_status(dp_model* M, hipStream_t st) {
-  int s = 0;
-  DPAMD_HIP(hipMemcpyAsync(&s, M->status.p, 4, hipMemcpyDeviceToHost, st));
-  DPAMD_HIP(hipStreamSynchronize(st));
+void throw_status(int s) {
   if (s & kStatusNeighbourOverflow)
     throw ApiError{DP_ERR_CAPACITY, "more than " + std::to_string(kMaxCand) +
                                         " neighbours within rcut of one atom"};
@@ -521,26 +541,74 @@ void check_status(dp_model* M, hipStream_t st) {
                    "more than " + std::to_string(kMaxRev) + " edges point at one atom"};
 }
 
-void begin(dp_model* M, hipStream_t st) {
+void check_status(dp_model* M, hipStream_t st) {
+  int s = 0;
+  DPAMD_HIP(hipMemcpyAsync(&s, M->status.p, 4, hipMemcpyDeviceToHost, st));
+  DPAMD_HIP(hipStreamSynchronize(st));
+  throw_status(s);
+}
+
+// Adds the stage times of the oldest pending event set (waiting for it).
+void harvest_oldest(dp_model* M) {
+  const int k = (M->ev_head - M->ev_pending + dp_model::kRing) % dp_model::kRing;
+  DPAMD_HIP(hipEventSynchronize(M->ev[k][kNumStages]));
+  for (int q = 0; q < kNumStages; ++q) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, M->ev[k][q], M->ev[k][q + 1]) != hipSuccess) ms = 0.f;
+    M->st_sum[q] += ms;
+  }
+  ++M->st_count;
+  --M->ev_pending;
+}
+
+// Stage times = mean over the evaluations since the previous call.
+void stage_times_of_last(dp_model* M) {
+  if (!M->timing) return;
+  while (M->ev_pending > 0) harvest_oldest(M);
+  if (M->st_count == 0) return;
+  for (int q = 0; q < kNumStages; ++q) {
+    M->stage_ms[q] = (float)(M->st_sum[q] / M->st_count);
+    M->st_sum[q] = 0.0;
+  }
+  M->st_count = 0;
+}
+
+// Waits for the evaluations queued by dp_compute_device_async and reports a
+// capacity error any of them raised (clearing it).
+void settle_async(dp_model* M) {
+  if (!M->async_pending) return;
+  M->async_pending = false;
+  DPAMD_HIP(hipStreamSynchronize(M->async_stream));
+  int s = 0;
+  DPAMD_HIP(hipMemcpy(&s, M->status.p, 4, hipMemcpyDeviceToHost));
+  stage_times_of_last(M);
+  if (s) {
+    *M->status_host = 0;
+    throw_status(s);
+  }
+}
+
+// async: the status word is cleared only by the first evaluation after a
+// settle, so a flag raised by any queued evaluation survives until read
+void begin(dp_model* M, hipStream_t st, bool async = false) {
   DPAMD_HIP(hipSetDevice(M->device));
-  need<int>(M, M->status, 1);
-  DPAMD_HIP(hipMemsetAsync(M->status.p, 0, 4, st));
+  if (!async) settle_async(M);
+  int* status = need<int>(M, M->status, 1);
+  if (!async || !M->async_pending) launch_fill_int(st, 1, 0, status);
   if (M->timing) {
+    if (M->ev_pending == dp_model::kRing) harvest_oldest(M);
+    M->ev_cur = M->ev_head;
+    M->ev_head = (M->ev_head + 1) % dp_model::kRing;
+    ++M->ev_pending;
     for (int q = 0; q <= kNumStages; ++q)
-      if (!M->ev[q]) DPAMD_HIP(hipEventCreate(&M->ev[q]));
-    DPAMD_HIP(hipEventRecord(M->ev[0], st));
+      if (!M->ev[M->ev_cur][q]) DPAMD_HIP(hipEventCreate(&M->ev[M->ev_cur][q]));
+    DPAMD_HIP(hipEventRecord(M->ev[M->ev_cur][0], st));
   }
 }
 
 void finish(dp_model* M, hipStream_t st) {
   check_status(M, st);
-  if (M->timing) {
-    for (int q = 0; q < kNumStages; ++q) {
-      float ms = 0.f;
-      if (hipEventElapsedTime(&ms, M->ev[q], M->ev[q + 1]) != hipSuccess) ms = 0.f;
-      M->stage_ms[q] = ms;
-    }
-  }
+  stage_times_of_last(M);
 }
 
 template <class F>
@@ -559,6 +627,51 @@ int guarded(dp_model* M, F&& f) {
   } catch (const std::exception& e) {
     M->err = e.what();
     return DP_ERR_ARG;
+  }
+}
+
+// One standalone evaluation on device buffers (dp_compute_device and its
+// asynchronous form). async: no host synchronisation unless the type buckets
+// must be rebuilt, and the status word is copied to pinned memory instead of
+// being checked.
+void device_step(dp_model* M, int natoms, const double* d_coord, const int* d_atype,
+                 const double* box, int ago, double* d_energy, double* d_force, double* d_virial,
+                 double* d_atom_energy, double* d_atom_virial, hipStream_t st, bool async) {
+  if (natoms < 0 || (natoms > 0 && (!d_coord || !d_atype || !d_force)))
+    throw ApiError{DP_ERR_ARG, "null device pointer"};
+  if (!box) throw ApiError{DP_ERR_ARG, "dp_compute_device needs a periodic box"};
+  if (async) {
+    DPAMD_HIP(hipSetDevice(M->device));
+    if (!M->status_host) {
+      DPAMD_HIP(hipHostMalloc(reinterpret_cast<void**>(&M->status_host), 64, hipHostMallocDefault));
+      *M->status_host = 0;
+    }
+    // a flag raised by an earlier queued evaluation that has landed already
+    if (M->async_pending && *static_cast<volatile int*>(M->status_host)) settle_async(M);
+    if (M->async_pending && M->async_stream != st) settle_async(M);
+  }
+  begin(M, st, async);
+  if (ago == 0 || !M->buckets_valid || (int)M->atype_cache.size() != natoms) {
+    std::vector<int> at(natoms);
+    if (natoms)
+      DPAMD_HIP(hipMemcpyAsync(at.data(), d_atype, sizeof(int) * natoms, hipMemcpyDeviceToHost, st));
+    DPAMD_HIP(hipStreamSynchronize(st));
+    M->buckets_valid = false;
+    update_buckets(M, natoms, at.data(), st);
+  }
+  const BoxParams bp = make_box(box, M->host.rcut);
+  const int nall = build_standalone_nlist(M, st, natoms, d_coord, d_atype, bp);
+  Outputs o{d_energy, d_force, d_virial, d_atom_energy, d_atom_virial};
+  run_model(M, st, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o);
+  M->last_nloc = natoms;
+  M->last_nall = nall;
+  M->last_standalone = true;
+  if (async) {
+    DPAMD_HIP(hipMemcpyAsync(M->status_host, M->status.p, 4, hipMemcpyDeviceToHost, st));
+    M->async_stream = st;
+    M->async_pending = true;
+  } else {
+    finish(M, st);
   }
 }
 
@@ -646,9 +759,18 @@ void dp_destroy(dp_model* M) {
     if (b->p) (void)hipFree(b->p);
   for (void* p : {M->d_emb, static_cast<void*>(M->d_envp), static_cast<void*>(M->d_tpad), M->d_fit})
     if (p) (void)hipFree(p);
-  for (auto& e : M->ev)
-    if (e) (void)hipEventDestroy(e);
+  if (M->async_pending) (void)hipStreamSynchronize(M->async_stream);
+  for (auto& set : M->ev)
+    for (hipEvent_t e : set)
+      if (e) (void)hipEventDestroy(e);
+  if (M->status_host) (void)hipHostFree(M->status_host);
   blas_destroy(M->blas);
+  for (int t = 0; t < kMaxTypes; ++t) {
+    blas_destroy(M->fit_blas[t]);
+    if (M->fit_st[t]) (void)hipStreamDestroy(M->fit_st[t]);
+    if (M->join_ev[t]) (void)hipEventDestroy(M->join_ev[t]);
+  }
+  if (M->fork_ev) (void)hipEventDestroy(M->fork_ev);
   delete M;
 }
 
@@ -680,27 +802,25 @@ int dp_compute_device(dp_model* M, int natoms, const double* d_coord, const int*
                       double* d_virial, double* d_atom_energy, double* d_atom_virial,
                       void* stream) {
   return guarded(M, [&]() {
-    if (natoms < 0 || (natoms > 0 && (!d_coord || !d_atype || !d_force)))
-      throw ApiError{DP_ERR_ARG, "null device pointer"};
-    if (!box) throw ApiError{DP_ERR_ARG, "dp_compute_device needs a periodic box"};
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    begin(M, st);
-    if (ago == 0 || !M->buckets_valid || (int)M->atype_cache.size() != natoms) {
-      std::vector<int> at(natoms);
-      if (natoms)
-        DPAMD_HIP(hipMemcpyAsync(at.data(), d_atype, sizeof(int) * natoms, hipMemcpyDeviceToHost, st));
-      DPAMD_HIP(hipStreamSynchronize(st));
-      M->buckets_valid = false;
-      update_buckets(M, natoms, at.data(), st);
-    }
-    const BoxParams bp = make_box(box, M->host.rcut);
-    const int nall = build_standalone_nlist(M, st, natoms, d_coord, d_atype, bp);
-    Outputs o{d_energy, d_force, d_virial, d_atom_energy, d_atom_virial};
-    run_model(M, st, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o);
-    M->last_nloc = natoms;
-    M->last_nall = nall;
-    M->last_standalone = true;
-    finish(M, st);
+    device_step(M, natoms, d_coord, d_atype, box, ago, d_energy, d_force, d_virial, d_atom_energy,
+                d_atom_virial, static_cast<hipStream_t>(stream), false);
+  });
+}
+
+int dp_compute_device_async(dp_model* M, int natoms, const double* d_coord, const int* d_atype,
+                            const double* box, int ago, double* d_energy, double* d_force,
+                            double* d_virial, double* d_atom_energy, double* d_atom_virial,
+                            void* stream) {
+  return guarded(M, [&]() {
+    device_step(M, natoms, d_coord, d_atype, box, ago, d_energy, d_force, d_virial, d_atom_energy,
+                d_atom_virial, static_cast<hipStream_t>(stream), true);
+  });
+}
+
+int dp_sync(dp_model* M) {
+  return guarded(M, [&]() {
+    DPAMD_HIP(hipSetDevice(M->device));
+    settle_async(M);
   });
 }
 
@@ -832,7 +952,13 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
   long result = 0;
   const int rc = guarded(M, [&]() {
     const ModelHost& m = M->host;
-    const int nloc = M->last_nloc, nall = M->last_nall;
+    const int nloc = M->last_nloc;
+    int nall = M->last_nall;
+    if (M->last_standalone && M->nall_d.p) {
+      // the standalone path counts its ghosts on the device
+      DPAMD_HIP(hipDeviceSynchronize());
+      DPAMD_HIP(hipMemcpy(&nall, M->nall_d.p, sizeof(int), hipMemcpyDeviceToHost));
+    }
     const int Dn = m.emb[2] * m.axis;
     const size_t net_esize = M->precision == DP_PREC_MIXED ? 4 : 8;
     auto copy = [&](const void* src, size_t bytes) {
@@ -890,6 +1016,12 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
 
 int dp_stage_times(dp_model* M, int enable, double* times, int n, char* names, size_t names_len) {
   if (!M) return DP_ERR_ARG;
+  if (M->timing != (enable != 0)) {
+    // start (or stop) timing afresh: sets recorded before are not read
+    M->ev_pending = 0;
+    M->st_count = 0;
+    for (double& v : M->st_sum) v = 0.0;
+  }
   M->timing = enable != 0;
   for (int q = 0; q < std::min(n, (int)kNumStages); ++q) times[q] = M->stage_ms[q];
   if (names && names_len) {

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
 
     double Tacc[S::NU3 * 4];
-  #pragma unroll
+#pragma unroll
     for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0;
     constexpr int BLK = 16 * (S::L2P + S::L3P);
     double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       }
       jn = slot + 32 < nr ? row[slot + 32] : 0;
       if (g == 0) {
-  #pragma unroll
+#pragma unroll
         for (int m = 0; m < 4; ++m) Rs[c * 4 + m] = Rn[m];
       }
       const double s = Rn[0];
@@ -128,10 +128,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       // time (shared reciprocal) when every feature is real
       double x1[S::NQ2];
       if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
-  #pragma unroll
+#pragma unroll
         for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
           double z[4];
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int f = 4 * (q0 + j) + g;
             z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
           tanh_fast4(z, x1 + q0);
         }
       } else {
-  #pragma unroll
+#pragma unroll
         for (int q = 0; q < S::NQ2; ++q) {
           const int f = 4 * q + g;
           x1[q] = (f < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
@@ -147,22 +147,22 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       }
       // layer 2, transposed
       d4 acc2[S::NT2];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) acc2[t] = d4{0.0, 0.0, 0.0, 0.0};
-  #pragma unroll
+#pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < S::NT2; ++t)
           acc2[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1[q], acc2[t]);
       }
       double x2[S::NT2][4];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) {
         double z2[4], th2v[4];
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) z2[r] = acc2[t][r] + P[S::OFF_B2 + 16 * t + 4 * r + g];
         tanh_fast4(z2, th2v);
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int f = 16 * t + 4 * r + g;
           const double th = th2v[r];
@@ -180,48 +180,48 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
         }
       }
       if constexpr (S::RES3 != 0) {
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < S::NT2; ++t)
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 4; ++r) X2s[c * X2LD + 16 * t + 4 * r + g] = x2[t][r];
       }
       wave_lds_sync();
       // layer 3, non-transposed, two output tiles at a time
-  #pragma unroll
+#pragma unroll
       for (int u0 = 0; u0 < S::NU3; u0 += kU3) {
         __builtin_amdgcn_sched_barrier(0);
         d4 acc3[kU3];
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3; ++uu) acc3[uu] = d4{0.0, 0.0, 0.0, 0.0};
         double wcur[kU3], wnxt[kU3];
         const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
-  #pragma unroll
+#pragma unroll
         for (int q = 0; q < S::NQ3; ++q) {
           if (q + 1 < S::NQ3) {
-  #pragma unroll
+#pragma unroll
             for (int uu = 0; uu < kU3; ++uu)
               wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
           }
           const double av = x2[q / 4][q % 4];
-  #pragma unroll
+#pragma unroll
           for (int uu = 0; uu < kU3; ++uu)
             if (u0 + uu < S::NU3) acc3[uu] = mfma_f64(av, wcur[uu], acc3[uu]);
-  #pragma unroll
+#pragma unroll
           for (int uu = 0; uu < kU3; ++uu) wcur[uu] = wnxt[uu];
         }
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3; ++uu) {
           const int u = u0 + uu;
           if (u < S::NU3) {
             const int f = 16 * u + c;
             double z3[4], th3v[4];
             const double b3 = P[S::OFF_B3 + f];
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 4; ++r) z3[r] = acc3[uu][r] + b3;
             tanh_fast4(z3, th3v);
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int sl = g + 4 * r;
               const double th = th3v[r];
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
               double G = th;
               if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
               if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
-  #pragma unroll
+#pragma unroll
               for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
             }
           }
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       }
       wave_lds_sync();
     }
-  #pragma unroll
+#pragma unroll
     for (int q = 0; q < S::NU3 * 4; ++q) {
       double v = Tacc[q];
       v += shfl_xor_d(v, 16);
@@ -250,11 +250,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       const double npad = (double)(a.sel[tj] - nr);
       const double* tp = a.tpad + (long)p * 4 * S::L3;
       double* Tt = static_cast<double*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
-  #pragma unroll
+#pragma unroll
       for (int u = 0; u < S::NU3; ++u) {
         const int f = 16 * u + c;
         if (f < S::L3) {
-  #pragma unroll
+#pragma unroll
           for (int m = 0; m < 4; ++m)
             Tt[f * a.ldt + m] =
                 (double)(((double)Tacc[u * 4 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
@@ -262,11 +262,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       }
     } else if (g == 0) {
       double* out = static_cast<double*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
-  #pragma unroll
+#pragma unroll
       for (int u = 0; u < S::NU3; ++u) {
         const int f = 16 * u + c;
         if (f < S::L3) {
-  #pragma unroll
+#pragma unroll
           for (int m = 0; m < 4; ++m) out[m * S::L3 + f] = Tacc[u * 4 + m];
         }
       }
@@ -349,13 +349,13 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       const int slot = tile + c;
       const bool valid = slot < nr;
       double th2[S::NT2][4], th3[S::NU3][4];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t)
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) th2[t][r] = act2[(4 * t + r) * 64];
-  #pragma unroll
+#pragma unroll
       for (int u = 0; u < S::NU3; ++u)
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) th3[u][r] = act3[256 * u + 64 * r];
       double d0 = 0.0, d1 = 0.0, d2 = 0.0;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
@@ -376,23 +376,23 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       // layer 1 (recomputed, elementwise) and its tangent
       double x1[S::NQ2], x1t[S::NQ2];
       if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
-  #pragma unroll
+#pragma unroll
         for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
           double z[4];
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int f = 4 * (q0 + j) + g;
             z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
           }
           tanh_fast4(z, x1 + q0);
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 4; ++j) {
             const double th = x1[q0 + j];
             x1t[q0 + j] = (1.0 - th * th) * P[S::OFF_W1 + 4 * (q0 + j) + g];
           }
         }
       } else {
-  #pragma unroll
+#pragma unroll
         for (int q = 0; q < S::NQ2; ++q) {
           const int f = 4 * q + g;
           if (f < S::L1) {
@@ -408,18 +408,18 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       }
       // layer 2: tangent product only; tanh of the primal comes from the forward
       d4 acc2t[S::NT2];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) acc2t[t] = d4{0.0, 0.0, 0.0, 0.0};
-  #pragma unroll
+#pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < S::NT2; ++t)
           acc2t[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1t[q], acc2t[t]);
       }
       double x2[S::NT2][4], x2t[S::NT2][4];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) {
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int f = 16 * t + 4 * r + g;
           const double th = th2[t][r];
@@ -447,12 +447,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       // u = dT.G, v = dT.G': residual part through the folded dT against X2
       double up[4] = {0.0, 0.0, 0.0, 0.0}, vp[4] = {0.0, 0.0, 0.0, 0.0};
       if constexpr (S::RES3 != 0) {
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < S::NT2; ++t)
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int f = 16 * t + 4 * r + g;
-  #pragma unroll
+#pragma unroll
             for (int m = 0; m < 4; ++m) {
               const double wv = dTf[m * S::L2P + f];
               up[m] += wv * x2[t][r];
@@ -461,41 +461,41 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
           }
       }
       // layer 3 tangent, transposed; tanh part of G from the forward
-  #pragma unroll
+#pragma unroll
       for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
         // keep the scheduler from hoisting later tile groups' weight loads
         __builtin_amdgcn_sched_barrier(0);
         d4 acc3t[kU3B];
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = d4{0.0, 0.0, 0.0, 0.0};
         // weight fragments double-buffered one k-step ahead of the MFMAs
         double wcur[kU3B], wnxt[kU3B];
         const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
-  #pragma unroll
+#pragma unroll
         for (int q = 0; q < S::NQ3; ++q) {
           if (q + 1 < S::NQ3) {
-  #pragma unroll
+#pragma unroll
             for (int uu = 0; uu < kU3B; ++uu)
               wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
           }
-  #pragma unroll
+#pragma unroll
           for (int uu = 0; uu < kU3B; ++uu)
             if (u0 + uu < S::NU3) acc3t[uu] = mfma_f64(wcur[uu], x2t[q / 4][q % 4], acc3t[uu]);
-  #pragma unroll
+#pragma unroll
           for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = wnxt[uu];
         }
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) {
           const int u = u0 + uu;
           if (u < S::NU3) {
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int f = 16 * u + 4 * r + g;
               const double th = th3[u][r];
               const double tt = (1.0 - th * th) * acc3t[uu][r];
-  #pragma unroll
+#pragma unroll
               for (int m = 0; m < 4; ++m) {
                 const double wv = dTs[m * S::L3P + f];
                 up[m] += wv * th;
@@ -505,7 +505,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
           }
         }
       }
-  #pragma unroll
+#pragma unroll
       for (int m = 0; m < 4; ++m) {
         up[m] += shfl_xor_d(up[m], 16);
         up[m] += shfl_xor_d(up[m], 32);
@@ -514,7 +514,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       }
       if (valid && g == 0) {
         double nd[4];
-  #pragma unroll
+#pragma unroll
         for (int m = 0; m < 4; ++m) nd[m] = up[m] * a.inv_nnei;
         nd[0] += (Rn[0] * vp[0] + Rn[1] * vp[1] + Rn[2] * vp[2] + Rn[3] * vp[3]) * a.inv_nnei;
         double gv[3];

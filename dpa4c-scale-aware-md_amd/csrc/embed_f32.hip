@@ -107,7 +107,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
     const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
 
     float Tacc[S::NU3 * 4];
-  #pragma unroll
+#pragma unroll
     for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0f;
     constexpr int BLK = 16 * (S::L2P + S::L3P);
     float* act = static_cast<float*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
@@ -134,33 +134,33 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
       }
       jn = slot + 32 < nr ? row[slot + 32] : 0;
       if (g == 0) {
-  #pragma unroll
+#pragma unroll
         for (int m = 0; m < 4; ++m) Rs[c * 4 + m] = (float)Rn[m];
       }
       const float s = (float)Rn[0];
 
       // layer 1 -> B operand of layer 2 (feature kf1(q, g) of slot c)
       float x1[S::NQ2];
-  #pragma unroll
+#pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
         const int f = kf1<S>(q, g);
         x1[q] = (f < S::L1) ? tanh_f32(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0f;
       }
       // layer 2, transposed: register r of tile t is feature 16t + 4g + r
       f4 acc2[S::NT2];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) acc2[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  #pragma unroll
+#pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
         const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::L2P + c;
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < S::NT2; ++t) acc2[t] = mfma_f32(W2[16 * t], x1[q], acc2[t]);
       }
       float x2[S::NT2][4];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) {
         f4 th4;
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int f = 16 * t + 4 * g + r;
           const float th = tanh_f32(acc2[t][r] + P[S::OFF_B2 + f]);
@@ -179,34 +179,34 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
         act2[64 * t] = th4;
       }
       if constexpr (S::RES3 != 0) {
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < S::NT2; ++t)
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 4; ++r) X2s[c * X2LD + 16 * t + 4 * g + r] = x2[t][r];
       }
       wave_lds_sync();
       // layer 3, non-transposed: register r of tile u is slot 4g + r, feature 16u + c
-  #pragma unroll
+#pragma unroll
       for (int u0 = 0; u0 < S::NU3; u0 += kU3F) {
         __builtin_amdgcn_sched_barrier(0);
         f4 acc3[kU3F];
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3F; ++uu) acc3[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  #pragma unroll
+#pragma unroll
         for (int q = 0; q < NQ3F; ++q) {
           const float av = x2[q >> 2][q & 3];
           const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::L3P + 16 * u0 + c;
-  #pragma unroll
+#pragma unroll
           for (int uu = 0; uu < kU3F; ++uu)
             if (u0 + uu < S::NU3) acc3[uu] = mfma_f32(av, W3[16 * uu], acc3[uu]);
         }
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3F; ++uu) {
           const int u = u0 + uu;
           if (u < S::NU3) {
             const int f = 16 * u + c;
             f4 th4;
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int sl = 4 * g + r;
               const float th = tanh_f32(acc3[uu][r] + P[S::OFF_B3 + f]);
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
               float G = th;
               if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
               if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
-  #pragma unroll
+#pragma unroll
               for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
             }
             act3[64 * u] = th4;
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
       }
       wave_lds_sync();
     }
-  #pragma unroll
+#pragma unroll
     for (int q = 0; q < S::NU3 * 4; ++q) {
       float v = Tacc[q];
       v += shfl_xor_d(v, 16);
@@ -235,11 +235,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
       const double npad = (double)(a.sel[tj] - nr);
       const double* tp = a.tpad + (long)p * 4 * S::L3;
       float* Tt = static_cast<float*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
-  #pragma unroll
+#pragma unroll
       for (int u = 0; u < S::NU3; ++u) {
         const int f = 16 * u + c;
         if (f < S::L3) {
-  #pragma unroll
+#pragma unroll
           for (int m = 0; m < 4; ++m)
             Tt[f * a.ldt + m] =
                 (float)(((double)Tacc[u * 4 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
@@ -247,11 +247,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
       }
     } else if (g == 0) {
       float* out = static_cast<float*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
-  #pragma unroll
+#pragma unroll
       for (int u = 0; u < S::NU3; ++u) {
         const int f = 16 * u + c;
         if (f < S::L3) {
-  #pragma unroll
+#pragma unroll
           for (int m = 0; m < 4; ++m) out[m * S::L3 + f] = Tacc[u * 4 + m];
         }
       }
@@ -332,11 +332,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
         nx2 = a.ext[3 * (long)jn + 2];
       }
       jn = tile + 16 + c < nr ? row[tile + 16 + c] : 0;
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) nth2[t] = p2[64 * t];
-  #pragma unroll
+#pragma unroll
       for (int u = 0; u < S::NU3; ++u)
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) nth3[u][r] = p3[256 * u + 4 * r];
     };
     jn = c < nr ? row[c] : 0;
@@ -347,11 +347,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       const bool valid = slot < nr;
       f4 th2[S::NT2];
       float th3[S::NU3][4];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) th2[t] = nth2[t];
-  #pragma unroll
+#pragma unroll
       for (int u = 0; u < S::NU3; ++u)
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) th3[u][r] = nth3[u][r];
       double d0 = 0.0, d1 = 0.0, d2 = 0.0;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 
       // layer 1 (recomputed) and its tangent
       float x1[S::NQ2], x1t[S::NQ2];
-  #pragma unroll
+#pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
         const int f = kf1<S>(q, g);
         if (f < S::L1) {
@@ -381,18 +381,18 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       }
       // layer 2 tangent (transposed); tanh of the primal from the forward
       f4 acc2t[S::NT2];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) acc2t[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  #pragma unroll
+#pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
         const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::L2P + c;
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < S::NT2; ++t) acc2t[t] = mfma_f32(W2[16 * t], x1t[q], acc2t[t]);
       }
       float x2[S::NT2][4], x2t[S::NT2][4];
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < S::NT2; ++t) {
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int f = 16 * t + 4 * g + r;
           const float th = th2[t][r];
@@ -420,12 +420,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       // u = dT.G, v = dT.G': the layer-3 residual through the folded dT
       float up[4] = {0.0f, 0.0f, 0.0f, 0.0f}, vp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if constexpr (S::RES3 != 0) {
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < S::NT2; ++t)
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int f = 16 * t + 4 * g + r;
-  #pragma unroll
+#pragma unroll
             for (int m = 0; m < 4; ++m) {
               const float wv = dTf[m * S::L2P + f];
               up[m] += wv * x2[t][r];
@@ -434,30 +434,30 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
           }
       }
       // layer 3 tangent, transposed: register r of tile u is feature 16u + 4g + r
-  #pragma unroll
+#pragma unroll
       for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
         __builtin_amdgcn_sched_barrier(0);
         f4 acc3t[kU3B];
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  #pragma unroll
+#pragma unroll
         for (int q = 0; q < NQ3F; ++q) {
           const float bv = x2t[q >> 2][q & 3];
           const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::L3P + 16 * u0 + c;
-  #pragma unroll
+#pragma unroll
           for (int uu = 0; uu < kU3B; ++uu)
             if (u0 + uu < S::NU3) acc3t[uu] = mfma_f32(W3[16 * uu], bv, acc3t[uu]);
         }
-  #pragma unroll
+#pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) {
           const int u = u0 + uu;
           if (u < S::NU3) {
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int f = 16 * u + 4 * g + r;
               const float th = th3[u][r];
               const float tt = (1.0f - th * th) * acc3t[uu][r];
-  #pragma unroll
+#pragma unroll
               for (int m = 0; m < 4; ++m) {
                 const float wv = dTs[m * S::L3P + f];
                 up[m] += wv * th;
@@ -467,7 +467,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
           }
         }
       }
-  #pragma unroll
+#pragma unroll
       for (int m = 0; m < 4; ++m) {
         up[m] += shfl_xor_d(up[m], 16);
         up[m] += shfl_xor_d(up[m], 32);
@@ -476,7 +476,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       }
       if (valid && g == 0) {
         double nd[4];
-  #pragma unroll
+#pragma unroll
         for (int m = 0; m < 4; ++m) nd[m] = (double)up[m] * a.inv_nnei;
         nd[0] += (Rn[0] * (double)vp[0] + Rn[1] * (double)vp[1] + Rn[2] * (double)vp[2] +
                   Rn[3] * (double)vp[3]) *

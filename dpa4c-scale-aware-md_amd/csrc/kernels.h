@@ -94,10 +94,19 @@ void launch_wrap(hipStream_t, int nloc, const double* coord, const int* atype, c
 void launch_ghost_flags(hipStream_t, int nloc, const BoxParams&, const double* sfrac, int* flags);
 void launch_ghost_fill(hipStream_t, int nloc, const BoxParams&, const int* flags, const int* pos,
                        double* ext, int* ext_type, int* mapping);
-void launch_cell_assign(hipStream_t, int nall, const BoxParams&, const double* ext, int* cell_of,
-                        int* cell_count);
-void launch_cell_scatter(hipStream_t, int nall, const int* cell_of, const int* cell_start,
-                         int* cursor, const double* ext, const int* ext_type, CellAtom* sorted);
+// Cell kernels over cap atoms, or over *d_count of them when d_count is given
+// (a count produced on the device, at most cap).
+void launch_cell_assign(hipStream_t, int cap, const int* d_count, const BoxParams&,
+                        const double* ext, int* cell_of, int* cell_count);
+void launch_cell_scatter(hipStream_t, int cap, const int* d_count, const int* cell_of,
+                         const int* cell_start, int* cursor, const double* ext,
+                         const int* ext_type, CellAtom* sorted);
+// nall = nloc + number of flagged ghost candidates, from the flags and their
+// exclusive scan, into device memory
+void launch_ghost_total(hipStream_t, int nloc, long nf, const int* flags, const int* pos,
+                        int* nall);
+// p[0 .. n) = v (a kernel rather than a memset node, so it can be captured)
+void launch_fill_int(hipStream_t, long n, int v, int* p);
 void launch_nlist_cells(hipStream_t, int nloc, const BoxParams&, const NlParams&, const double* ext,
                         const int* ext_type, const int* cell_of, const int* cell_start,
                         const CellAtom* sorted, int* nlist, int* nreal, int* status);

@@ -108,21 +108,25 @@ __device__ __forceinline__ int cell_of_point(const BoxParams& bp, double x0, dou
   return (c[2] * bp.ncell[1] + c[1]) * bp.ncell[0] + c[0];
 }
 
-__global__ void k_cell_assign(int nall, BoxParams bp, const double* __restrict__ ext,
-                              int* __restrict__ cell_of, int* __restrict__ cell_count) {
+// The atom count is cap, or *d_count when given (ghost count known on the
+// device only; the grid then covers the capacity cap).
+__global__ void k_cell_assign(int cap, const int* __restrict__ d_count, BoxParams bp,
+                              const double* __restrict__ ext, int* __restrict__ cell_of,
+                              int* __restrict__ cell_count) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= nall) return;
+  if (n >= (d_count ? *d_count : cap)) return;
   const int c = cell_of_point(bp, ext[3 * n], ext[3 * n + 1], ext[3 * n + 2]);
   cell_of[n] = c;
   atomicAdd(&cell_count[c], 1);
 }
 
-__global__ void k_cell_scatter(int nall, const int* __restrict__ cell_of,
+__global__ void k_cell_scatter(int cap, const int* __restrict__ d_count,
+                               const int* __restrict__ cell_of,
                                const int* __restrict__ cell_start, int* __restrict__ cursor,
                                const double* __restrict__ ext, const int* __restrict__ ext_type,
                                CellAtom* __restrict__ sorted) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= nall) return;
+  if (n >= (d_count ? *d_count : cap)) return;
   const int c = cell_of[n];
   const int p = cell_start[c] + atomicAdd(&cursor[c], 1);
   CellAtom a;
@@ -428,19 +432,45 @@ void launch_ghost_fill(hipStream_t st, int nloc, const BoxParams& bp, const int*
   DPAMD_LAUNCH_CHECK();
 }
 
-void launch_cell_assign(hipStream_t st, int nall, const BoxParams& bp, const double* ext,
-                        int* cell_of, int* cell_count) {
-  if (nall <= 0) return;
-  hipLaunchKernelGGL(k_cell_assign, dim3((nall + 255) / 256), dim3(256), 0, st, nall, bp, ext,
-                     cell_of, cell_count);
+void launch_cell_assign(hipStream_t st, int cap, const int* d_count, const BoxParams& bp,
+                        const double* ext, int* cell_of, int* cell_count) {
+  if (cap <= 0) return;
+  hipLaunchKernelGGL(k_cell_assign, dim3((cap + 255) / 256), dim3(256), 0, st, cap, d_count, bp,
+                     ext, cell_of, cell_count);
   DPAMD_LAUNCH_CHECK();
 }
 
-void launch_cell_scatter(hipStream_t st, int nall, const int* cell_of, const int* cell_start,
-                         int* cursor, const double* ext, const int* ext_type, CellAtom* sorted) {
-  if (nall <= 0) return;
-  hipLaunchKernelGGL(k_cell_scatter, dim3((nall + 255) / 256), dim3(256), 0, st, nall, cell_of,
-                     cell_start, cursor, ext, ext_type, sorted);
+void launch_cell_scatter(hipStream_t st, int cap, const int* d_count, const int* cell_of,
+                         const int* cell_start, int* cursor, const double* ext,
+                         const int* ext_type, CellAtom* sorted) {
+  if (cap <= 0) return;
+  hipLaunchKernelGGL(k_cell_scatter, dim3((cap + 255) / 256), dim3(256), 0, st, cap, d_count,
+                     cell_of, cell_start, cursor, ext, ext_type, sorted);
+  DPAMD_LAUNCH_CHECK();
+}
+
+// nall = nloc + (exclusive scan of the ghost flags at the last candidate) +
+// (that candidate's own flag)
+__global__ void k_ghost_total(int nloc, long nf, const int* __restrict__ flags,
+                              const int* __restrict__ pos, int* __restrict__ nall) {
+  if (threadIdx.x == 0) *nall = nloc + pos[nf - 1] + flags[nf - 1];
+}
+
+void launch_ghost_total(hipStream_t st, int nloc, long nf, const int* flags, const int* pos,
+                        int* nall) {
+  if (nf <= 0) return;
+  hipLaunchKernelGGL(k_ghost_total, dim3(1), dim3(64), 0, st, nloc, nf, flags, pos, nall);
+  DPAMD_LAUNCH_CHECK();
+}
+
+__global__ void k_fill_int(long n, int v, int* __restrict__ p) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+void launch_fill_int(hipStream_t st, long n, int v, int* p) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_fill_int, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, n, v, p);
   DPAMD_LAUNCH_CHECK();
 }
 

@@ -166,6 +166,26 @@ class DeepPot {
                        nghost, lmp_list, ago, fparam, aparam, charge_spin);
   }
 
+  // Device-resident step on device pointers (dp_compute_device, or with
+  // async = true dp_compute_device_async: queued on `stream` with no host
+  // synchronisation; sync() waits and reports a deferred capacity error). The
+  // step the reference hands between the MD engine's and the model's streams
+  // (DeepPot.h:14-18 and :395-445 of deepmd-op/overlays/api_cc/include).
+  void compute_device(double* d_energy, double* d_force, double* d_virial, double* d_atom_energy,
+                      double* d_atom_virial, const double* d_coord, const int* d_atype,
+                      const int natoms, const std::vector<double>& box, const int ago = 1,
+                      void* stream = nullptr, const bool async = false) {
+    require_init();
+    if (box.size() != 9) throw deepmd_exception("DeePMD-kit (MI355X): box must hold 9 values");
+    check((async ? dp_compute_device_async : dp_compute_device)(
+        h_, natoms, d_coord, d_atype, box.data(), ago, d_energy, d_force, d_virial, d_atom_energy,
+        d_atom_virial, stream));
+  }
+  void sync() {
+    require_init();
+    check(dp_sync(h_));
+  }
+
   dp_model* handle() const { return h_; }
 
  private:

@@ -153,6 +153,37 @@ int dp_compute_device(dp_model* model, int natoms, const double* d_coord, const 
                       double* d_virial, double* d_atom_energy, double* d_atom_virial,
                       void* stream);
 
+/*
+ * Asynchronous form of dp_compute_device for an MD loop that keeps its data on
+ * the GPU: the evaluation is enqueued on `stream` and the call returns without
+ * waiting for it, so consecutive steps (and the caller's own kernels between
+ * them) queue back to back with no host round trip. With ago != 0 and the
+ * same natoms as the previous call nothing is read back, and nothing is
+ * allocated once the buffers have grown to the system's size; ago == 0 reads
+ * the types back once, as dp_compute_device does. The outputs are complete
+ * when `stream` reaches the point of the call. A capacity error raised by the
+ * kernels (more than 512 neighbours within rcut of one atom, more than 1024
+ * edges pointing at one atom) is returned by the first later call of this
+ * function that sees it, or by dp_sync; the outputs of that evaluation and of
+ * those queued after it are then invalid. Any other entry point first waits
+ * for the queued evaluations (and returns such an error). Analog of the
+ * reference's GPU-resident step, which hands the model outputs to the MD
+ * engine's stream through events with no host synchronisation
+ * (deepmd-op/overlays/api_cc/include/DeepPot.h:14-18,
+ * deepmd-op/overlays/api_cc/src/DeepPotPTExpt.cc:194-222, used at
+ * deepmd-op/overlays/lmp/pair_deepmd_kokkos.cpp:555-606).
+ */
+int dp_compute_device_async(dp_model* model, int natoms, const double* d_coord,
+                            const int* d_atype, const double* box, int ago, double* d_energy,
+                            double* d_force, double* d_virial, double* d_atom_energy,
+                            double* d_atom_virial, void* stream);
+
+/* Waits for every evaluation queued by dp_compute_device_async; returns
+ * DP_ERR_CAPACITY (and clears the flag) if any of them overflowed, DP_OK
+ * otherwise. Stage times then refer to the last of them. No counterpart in the
+ * reference, whose errors surface at the next synchronous call. */
+int dp_sync(dp_model* model);
+
 /* Copy a stage buffer of the last evaluation (DP_STAGE_*) to host memory.
  * Returns the buffer's size in bytes (copies min(size, capacity) bytes);
  * negative on error. No counterpart in the reference: parity tests use it to
@@ -160,10 +191,13 @@ int dp_compute_device(dp_model* model, int natoms, const double* d_coord, const 
  * analogue is its DPA_DUMP_FRAME hook, graph_compress.cu:1354-1378). */
 long dp_debug_copy(dp_model* model, int stage, void* dst, size_t capacity);
 
-/* Per-stage GPU time of the last evaluation in milliseconds (hipEvent pairs),
- * filled into times[0..n-1] in pipeline order; returns the number of stages
- * and writes their names into names (NUL separated) when non-NULL. The
- * reference's analogue is its DPA_KTIME stage timer (graph_compress.cu:1394-1427). */
+/* Per-stage GPU time in milliseconds (hipEvent pairs) of the last synchronous
+ * evaluation, or the mean over the evaluations queued by
+ * dp_compute_device_async up to the last dp_sync, filled into times[0..n-1] in
+ * pipeline order; returns the number of stages and writes their names into
+ * names (NUL separated) when non-NULL. `enable` switches the timers on or off
+ * for the evaluations that follow. The reference's analogue is its DPA_KTIME
+ * stage timer (graph_compress.cu:1394-1427). */
 int dp_stage_times(dp_model* model, int enable, double* times, int n, char* names, size_t names_len);
 
 /* Peak device bytes allocated by this handle so far (memory high-water mark). */
