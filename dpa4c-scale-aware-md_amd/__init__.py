@@ -30,6 +30,7 @@ PREC_FP64, PREC_MIXED = 0, 1
 
 EXPORTED = ("dp_create", "dp_destroy", "dp_get_info", "dp_last_error", "dp_compute",
             "dp_compute_nlist", "dp_compute_device", "dp_compute_device_async", "dp_sync",
+            "dp_graph_stats",
             "dp_debug_copy", "dp_stage_times", "dp_device_bytes")
 
 
@@ -64,6 +65,7 @@ def lib():
         L.dp_compute_device.argtypes = [P, I, P, P, P, I, P, P, P, P, P, P]
         L.dp_compute_device_async.argtypes = [P, I, P, P, P, I, P, P, P, P, P, P]
         L.dp_sync.argtypes = [P]
+        L.dp_graph_stats.argtypes = [P, C.POINTER(C.c_long), C.POINTER(C.c_long)]
         L.dp_debug_copy.argtypes = [P, I, P, C.c_size_t]
         L.dp_debug_copy.restype = C.c_long
         L.dp_stage_times.argtypes = [P, I, P, I, P, C.c_size_t]
@@ -204,6 +206,12 @@ class DeepPot:
     def sync(self):
         """Wait for the queued asynchronous evaluations (dp_sync)."""
         self._check(lib().dp_sync(self._h))
+
+    def graph_stats(self):
+        """(graphs in use, captures, replays) of the DPAMD_GRAPH replay."""
+        cap, rep = C.c_long(0), C.c_long(0)
+        on = lib().dp_graph_stats(self._h, C.byref(cap), C.byref(rep))
+        return bool(on == 1), cap.value, rep.value
 
     # ---- introspection -----------------------------------------------------
     def stage(self, which: int, dtype, shape):

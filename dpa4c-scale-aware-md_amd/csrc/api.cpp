@@ -106,6 +106,18 @@ struct dp_model {
   int* status_host = nullptr;
   hipStream_t async_stream = nullptr;
   bool async_pending = false;
+  // Graph replay of queued evaluations (DPAMD_GRAPH=1): the step is captured
+  // once per key (sizes, pointers, box, stream, buffer and bucket
+  // generations) on a stream of its own and replayed while the key holds.
+  bool graph_on = false, graph_broken = false;
+  hipStream_t graph_st = nullptr;
+  hipEvent_t graph_in = nullptr, graph_out = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  std::vector<unsigned char> graph_key;
+  int graph_warm = 0;
+  long graph_captures = 0, graph_replays = 0;
+  unsigned long buf_gen = 0, bucket_gen = 0;  // bumped by any reallocation / rebucketing
   // stage timers
   bool timing = false;
   // one event set per evaluation in a ring, so that evaluations queued by
@@ -145,6 +157,7 @@ T* need(dp_model* M, Buf& b, size_t count) {
     b.cap = 0;
     DPAMD_HIP(hipMalloc(&b.p, nb));
     b.cap = nb;
+    ++M->buf_gen;
     M->bytes_now += nb;
     M->bytes_peak = std::max(M->bytes_peak, M->bytes_now);
   }
@@ -238,6 +251,7 @@ void update_buckets(dp_model* M, int nloc, const int* atype_host, hipStream_t st
   }
   M->type_off[nt] = (int)M->items_h.size();
   M->nbucket = M->type_off[nt];
+  ++M->bucket_gen;
   int* d_items = need<int>(M, M->items, std::max(1, M->nbucket));
   if (M->nbucket)
     DPAMD_HIP(hipMemcpyAsync(d_items, M->items_h.data(), sizeof(int) * M->nbucket,
@@ -583,6 +597,9 @@ void settle_async(dp_model* M) {
   DPAMD_HIP(hipMemcpy(&s, M->status.p, 4, hipMemcpyDeviceToHost));
   stage_times_of_last(M);
   if (s) {
+    // replayed graphs never clear the word themselves
+    launch_fill_int(M->async_stream, 1, 0, static_cast<int*>(M->status.p));
+    DPAMD_HIP(hipStreamSynchronize(M->async_stream));
     *M->status_host = 0;
     throw_status(s);
   }
@@ -630,6 +647,87 @@ int guarded(dp_model* M, F&& f) {
   }
 }
 
+void graph_reset(dp_model* M) {
+  if (M->graph_exec) (void)hipGraphExecDestroy(M->graph_exec);
+  if (M->graph) (void)hipGraphDestroy(M->graph);
+  M->graph_exec = nullptr;
+  M->graph = nullptr;
+}
+
+// Runs the queued evaluation `body` as a graph replay (capturing it first
+// when the key is new and one eager evaluation with that key has sized every
+// buffer). Returns false when the caller must run it eagerly: the first call
+// with a key, or after a failed capture (graphs are then off for the handle).
+// The graph lives on a stream of its own: it waits for `st` on entry and
+// `st` waits for it on exit, as the reference's replay does
+// (DeepPotPTExpt.cc:122-191).
+template <class Body>
+bool graph_step(dp_model* M, hipStream_t st, int natoms, const double* d_coord,
+                const int* d_atype, const double* box, const Outputs& o, Body&& body) {
+  std::vector<unsigned char> key;
+  auto put = [&](const void* p, size_t n) {
+    const auto* b = static_cast<const unsigned char*>(p);
+    key.insert(key.end(), b, b + n);
+  };
+  const void* ptrs[8] = {d_coord, d_atype, o.energy, o.force, o.virial, o.atom_energy,
+                         o.atom_virial, st};
+  put(&natoms, sizeof natoms);
+  put(ptrs, sizeof ptrs);
+  put(box, 9 * sizeof(double));
+  put(&M->buf_gen, sizeof M->buf_gen);
+  put(&M->bucket_gen, sizeof M->bucket_gen);
+  if (key != M->graph_key) {
+    graph_reset(M);
+    M->graph_key = key;
+    M->graph_warm = 0;
+  }
+  if (!M->graph_exec && M->graph_warm < 1) {
+    ++M->graph_warm;  // eager run with this key first
+    return false;
+  }
+  DPAMD_HIP(hipSetDevice(M->device));
+  if (!M->graph_st) {
+    DPAMD_HIP(hipStreamCreateWithFlags(&M->graph_st, hipStreamNonBlocking));
+    DPAMD_HIP(hipEventCreateWithFlags(&M->graph_in, hipEventDisableTiming));
+    DPAMD_HIP(hipEventCreateWithFlags(&M->graph_out, hipEventDisableTiming));
+  }
+  DPAMD_HIP(hipEventRecord(M->graph_in, st));
+  DPAMD_HIP(hipStreamWaitEvent(M->graph_st, M->graph_in, 0));
+  if (!M->graph_exec) {
+    const unsigned long gen = M->buf_gen;
+    bool ok = hipStreamBeginCapture(M->graph_st, hipStreamCaptureModeRelaxed) == hipSuccess;
+    if (ok) {
+      try {
+        body(M->graph_st);
+      } catch (...) {
+        ok = false;
+      }
+      hipGraph_t g = nullptr;
+      ok = hipStreamEndCapture(M->graph_st, &g) == hipSuccess && ok && g;
+      // a buffer reallocated while capturing would leave stale pointers
+      ok = ok && M->buf_gen == gen;
+      if (ok) ok = hipGraphInstantiate(&M->graph_exec, g, nullptr, nullptr, 0) == hipSuccess;
+      if (ok) M->graph = g;
+      else if (g) (void)hipGraphDestroy(g);
+    }
+    if (!ok) {
+      (void)hipGetLastError();
+      graph_reset(M);
+      M->graph_broken = true;
+      // nothing was enqueued by the failed capture: run eagerly after all
+      DPAMD_HIP(hipEventRecord(M->graph_out, M->graph_st));
+      DPAMD_HIP(hipStreamWaitEvent(st, M->graph_out, 0));
+      return false;
+    }
+    ++M->graph_captures;
+  }
+  DPAMD_HIP(hipGraphLaunch(M->graph_exec, M->graph_st));
+  ++M->graph_replays;
+  DPAMD_HIP(hipEventRecord(M->graph_out, M->graph_st));
+  DPAMD_HIP(hipStreamWaitEvent(st, M->graph_out, 0));
+  return true;
+}
+
 // One standalone evaluation on device buffers (dp_compute_device and its
 // asynchronous form). async: no host synchronisation unless the type buckets
 // must be rebuilt, and the status word is copied to pinned memory instead of
@@ -650,8 +748,8 @@ void device_step(dp_model* M, int natoms, const double* d_coord, const int* d_at
     if (M->async_pending && *static_cast<volatile int*>(M->status_host)) settle_async(M);
     if (M->async_pending && M->async_stream != st) settle_async(M);
   }
-  begin(M, st, async);
   if (ago == 0 || !M->buckets_valid || (int)M->atype_cache.size() != natoms) {
+    DPAMD_HIP(hipSetDevice(M->device));
     std::vector<int> at(natoms);
     if (natoms)
       DPAMD_HIP(hipMemcpyAsync(at.data(), d_atype, sizeof(int) * natoms, hipMemcpyDeviceToHost, st));
@@ -660,14 +758,30 @@ void device_step(dp_model* M, int natoms, const double* d_coord, const int* d_at
     update_buckets(M, natoms, at.data(), st);
   }
   const BoxParams bp = make_box(box, M->host.rcut);
-  const int nall = build_standalone_nlist(M, st, natoms, d_coord, d_atype, bp);
   Outputs o{d_energy, d_force, d_virial, d_atom_energy, d_atom_virial};
-  run_model(M, st, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o);
+  // the evaluation proper: no host synchronisation, no allocation once sized
+  auto body = [&](hipStream_t s) {
+    const int nall = build_standalone_nlist(M, s, natoms, d_coord, d_atype, bp);
+    run_model(M, s, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o);
+    if (async) DPAMD_HIP(hipMemcpyAsync(M->status_host, M->status.p, 4, hipMemcpyDeviceToHost, s));
+    M->last_nall = nall;
+  };
   M->last_nloc = natoms;
-  M->last_nall = nall;
   M->last_standalone = true;
+  const bool try_graph = async && M->graph_on && !M->graph_broken && !M->timing && natoms > 0;
+  if (try_graph && !M->async_pending) {
+    // a graph does not clear the status word: start the queue from zero
+    DPAMD_HIP(hipSetDevice(M->device));
+    launch_fill_int(st, 1, 0, need<int>(M, M->status, 1));
+  }
+  if (try_graph && graph_step(M, st, natoms, d_coord, d_atype, box, o, body)) {
+    M->async_stream = st;
+    M->async_pending = true;
+    return;
+  }
+  begin(M, st, async);
+  body(st);
   if (async) {
-    DPAMD_HIP(hipMemcpyAsync(M->status_host, M->status.p, 4, hipMemcpyDeviceToHost, st));
     M->async_stream = st;
     M->async_pending = true;
   } else {
@@ -739,6 +853,7 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
     }
     M->bytes_peak = M->bytes_now;
     M->fo = fit_offsets(m);
+    if (const char* g = std::getenv("DPAMD_GRAPH")) M->graph_on = std::atoi(g) != 0;
     M->blas = blas_create();
     if (!M->blas) throw ApiError{DP_ERR_NO_GPU, "rocblas_create_handle failed"};
   });
@@ -771,6 +886,10 @@ void dp_destroy(dp_model* M) {
     if (M->join_ev[t]) (void)hipEventDestroy(M->join_ev[t]);
   }
   if (M->fork_ev) (void)hipEventDestroy(M->fork_ev);
+  graph_reset(M);
+  if (M->graph_st) (void)hipStreamDestroy(M->graph_st);
+  if (M->graph_in) (void)hipEventDestroy(M->graph_in);
+  if (M->graph_out) (void)hipEventDestroy(M->graph_out);
   delete M;
 }
 
@@ -815,6 +934,13 @@ int dp_compute_device_async(dp_model* M, int natoms, const double* d_coord, cons
     device_step(M, natoms, d_coord, d_atype, box, ago, d_energy, d_force, d_virial, d_atom_energy,
                 d_atom_virial, static_cast<hipStream_t>(stream), true);
   });
+}
+
+int dp_graph_stats(const dp_model* M, long* captures, long* replays) {
+  if (!M) return DP_ERR_ARG;
+  if (captures) *captures = M->graph_captures;
+  if (replays) *replays = M->graph_replays;
+  return M->graph_on && !M->graph_broken ? 1 : 0;
 }
 
 int dp_sync(dp_model* M) {

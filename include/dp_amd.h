@@ -178,6 +178,18 @@ int dp_compute_device_async(dp_model* model, int natoms, const double* d_coord,
                             double* d_force, double* d_virial, double* d_atom_energy,
                             double* d_atom_virial, void* stream);
 
+/* With the environment variable DPAMD_GRAPH=1 set when the handle is
+ * created, dp_compute_device_async replays the evaluation as a HIP graph: the
+ * first call with a given key (natoms, every pointer, the box, the stream)
+ * runs eagerly and sizes the buffers, the second captures the evaluation on a
+ * stream of the handle's own, and later calls with the same key replay it
+ * (a new key captures again; a failed capture turns graphs off for the
+ * handle). Stage timing (dp_stage_times) runs eagerly. As the reference's
+ * DPA_MODEL_GRAPH replay (deepmd-op/overlays/api_cc/src/DeepPotPTExpt.cc:
+ * 122-191), keyed on pointers and sizes. dp_graph_stats reports the captures
+ * and replays so far and returns 1 while graphs are in use, 0 otherwise. */
+int dp_graph_stats(const dp_model* model, long* captures, long* replays);
+
 /* Waits for every evaluation queued by dp_compute_device_async; returns
  * DP_ERR_CAPACITY (and clears the flag) if any of them overflowed, DP_OK
  * otherwise. Stage times then refer to the last of them. No counterpart in the

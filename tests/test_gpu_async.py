@@ -80,3 +80,35 @@ def test_async_capacity_error_reported_by_sync(dp):
     pot.compute_device(dc2.ptr, da2.ptr, n2, box2, *[b.ptr for b in ref2], ago=0)
     for got, want in zip(_host(out2, n2), _host(ref2, n2)):
         assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("case", ["hea1024", "cu864"])
+def test_graph_replay_matches_eager(dp, monkeypatch, case):
+    """DPAMD_GRAPH=1: the third queued call with one key is captured and
+    replayed, later ones replay; between replays the coordinates change in
+    place and a second handle evaluates them eagerly, and every replay must
+    equal that eager result bit for bit (hea1024 forks the per-type fitting
+    chains onto their own streams inside the graph, cu864 has one type)."""
+    hip = importlib.import_module("dpamd.hip")
+    (coord, atype, box), m = CASES[case]()
+    n = len(atype)
+    mb = model_bytes(m)
+    monkeypatch.setenv("DPAMD_GRAPH", "1")
+    pot_g = dp.DeepPot(file_content=mb)
+    monkeypatch.delenv("DPAMD_GRAPH")
+    pot_e = dp.DeepPot(file_content=mb)
+    rng = np.random.default_rng(23)
+    dc = hip.DeviceArray(np.ascontiguousarray(coord, np.float64))
+    da = hip.DeviceArray(atype.astype(np.int32))
+    out, ref = _outputs(hip, n), _outputs(hip, n)
+    steps = 6
+    for k in range(steps):
+        dc.upload(np.ascontiguousarray(coord + rng.normal(0.0, 0.02, coord.shape), np.float64))
+        pot_g.compute_device_async(dc.ptr, da.ptr, n, box, *[b.ptr for b in out],
+                                   ago=0 if k == 0 else 1)
+        pot_g.sync()
+        pot_e.compute_device(dc.ptr, da.ptr, n, box, *[b.ptr for b in ref], ago=0)
+        for got, want in zip(_host(out, n), _host(ref, n)):
+            assert np.array_equal(got, want), f"step {k}"
+    on, captures, replays = pot_g.graph_stats()
+    assert on and captures == 1 and replays == steps - 2, (on, captures, replays)
