@@ -86,7 +86,7 @@ struct dp_model {
   Buf coord_in, atype_in, sfrac, flags, gpos, ext, ext_type, mapping, cell_of, cell_count,
       cell_start, cell_cursor, sorted, nlist, nreal, cand_off, cand, items, Tsec, Tt, D, dD, dT,
       fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_cursor, rev, force_ws, av_ws,
-      ae_ws, partials, out10, status, scan_tmp, act, nall_d;
+      ae_ws, partials, out10, status, scan_tmp, act, nall_d, split_ws;
   size_t bytes_now = 0, bytes_peak = 0;
   // type buckets
   std::vector<int> atype_cache;
@@ -136,7 +136,7 @@ struct dp_model {
             &nreal,    &cand_off, &cand,      &items,    &Tsec,       &Tt,        &D,
             &dD,       &dT,       &fitb,      &e_bucket, &edge_grad,  &cpart,     &rev_count,
             &rev_off,  &rev_cursor, &rev,     &force_ws, &av_ws,      &ae_ws,     &partials,
-            &out10,    &status,   &scan_tmp, &act,       &nall_d};
+            &out10,    &status,   &scan_tmp, &act,       &nall_d,    &split_ws};
   }
 };
 
@@ -387,7 +387,16 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   record(M, st, kStDescr + 1);
 
   int active = 0;
-  for (int t = 0; t < nt; ++t) active += M->type_off[t + 1] > M->type_off[t];
+  size_t ws_need = 0, ws_off = 0;
+  for (int t = 0; t < nt; ++t) {
+    const int rows = M->type_off[t + 1] - M->type_off[t];
+    active += rows > 0;
+    const int sp = rows > 0 ? fit_splits(rows, m.fit[0], Dn, M->ncu) : 1;
+    if (sp > 1) ws_need += (size_t)sp * rows * m.fit[0];
+  }
+  // split-K slices of the first layer, one region per type (the chains run
+  // concurrently)
+  E* split_ws = ws_need ? need<E>(M, M->split_ws, ws_need) : nullptr;
   const bool fork = active > 1;
   if (fork) {
     if (!M->fork_ev) DPAMD_HIP(hipEventCreateWithFlags(&M->fork_ev, hipEventDisableTiming));
@@ -425,6 +434,9 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
     const size_t r0 = (size_t)M->type_off[t];
     const size_t slab = (size_t)std::max(nb, 1) * Fmax;
     FitBufs<E> fb{};
+    fb.split = fit_splits(rows, m.fit[0], Dn, M->ncu);
+    if (fb.split > 1) fb.ws = split_ws + ws_off;
+    ws_off += (size_t)fb.split * rows * m.fit[0];
     E* base = fitb;
     E** slots[8] = {&fb.H0, &fb.T1, &fb.H1, &fb.T2, &fb.H2, &fb.dZa, &fb.dZb, &fb.dH};
     // slab q holds [rows][F] of every type back to back; F <= Fmax

@@ -176,7 +176,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
           }
           x2[t][r] = (f < S::L2) ? res + th : 0.0f;
         }
-        act2[64 * t] = th4;
+        __builtin_nontemporal_store(th4, &act2[64 * t]);
       }
       if constexpr (S::RES3 != 0) {
 #pragma unroll
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
 #pragma unroll
               for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
             }
-            act3[64 * u] = th4;
+            __builtin_nontemporal_store(th4, &act3[64 * u]);
           }
         }
       }

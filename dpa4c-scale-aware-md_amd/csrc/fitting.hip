@@ -39,6 +39,11 @@ struct GemmArgs {
   // A[row][16a + b] = sum_m T[m][a] T[m][b]
   const T* Tt;
   long ldt;
+  // split K: blockIdx.z takes chunks [z per, (z+1) per) of the K loop and
+  // stores its partial product to ws + z M ldc (plain store); a separate
+  // epilogue kernel sums the slices in order
+  int split;
+  T* ws;
 };
 
 // C = epi(A[MxK] B[KxN]); B(k,n) = TRANSB ? B[n*ldb + k] : B[k*ldb + n].
@@ -131,11 +136,19 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
   typename Frag<T>::V acc[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) acc[n] = typename Frag<T>::V{0, 0, 0, 0};
-  fetch(0);
-  stash(0);
+  int kc0 = 0, nk = a.K / BK;
+  if (a.split > 1) {
+    const int per = (nk + a.split - 1) / a.split;
+    kc0 = blockIdx.z * per;
+    nk = min(nk, kc0 + per);
+  }
+  // (a slice past the end of K keeps zeros: it is still stored, and summed)
+  if (kc0 < nk) {
+    fetch(kc0 * BK);
+    stash(kc0 & 1);
+  }
   __syncthreads();
-  const int nk = a.K / BK;
-  for (int kc = 0; kc < nk; ++kc) {
+  for (int kc = kc0; kc < nk; ++kc) {
     const int buf = kc & 1;
     if (kc + 1 < nk) fetch((kc + 1) * BK);
     const T* Ab = As[buf] + (16 * w + c) * ALD;
@@ -148,6 +161,17 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
     }
     if (kc + 1 < nk) stash(buf ^ 1);
     __syncthreads();
+  }
+  if (a.split > 1) {
+    T* out = a.ws + (long)blockIdx.z * a.M * a.ldc;
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = row0 + 16 * w + Frag<T>::row(g, r);
+        if (row < a.M) out[(long)row * a.ldc + col0 + 16 * n + c] = acc[n][r];
+      }
+    return;
   }
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
@@ -186,6 +210,51 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
       }
     }
   }
+}
+
+// Split-K forward epilogue of a layer without residual: C = tanh(sum over
+// the split slices in order + bias), four consecutive columns per thread.
+template <class T>
+__global__ __launch_bounds__(256) void k_splitk_tanh(int M, int N, int split,
+                                                    const T* __restrict__ ws,
+                                                    const T* __restrict__ bias,
+                                                    T* __restrict__ C) {
+  const long q = (long)blockIdx.x * blockDim.x + threadIdx.x;  // 4-column group
+  const int g4 = N / 4;
+  if (q >= (long)M * g4) return;
+  const long row = q / g4;
+  const int col = 4 * (int)(q - row * g4);
+  const long o = row * N + col;
+  T z[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) z[j] = ws[o + j];
+  for (int k = 1; k < split; ++k) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) z[j] += ws[(long)k * M * N + o + j];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) z[j] += bias[col + j];
+  T th[4];
+  if constexpr (sizeof(T) == 8) {
+    tanh_fast4(z, th);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) th[j] = tanh_act(z[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) C[o + j] = th[j];
+}
+
+// K slices for the first fitting layer: split only when the row blocks alone
+// leave the device short of work (fewer than two blocks per compute unit),
+// and keep at least 8 K chunks of 16 per slice.
+int fit_splits(int rows, int N, int K, int ncu) {
+  const int cols = N % 128 == 0 ? N / 128 : N % 80 == 0 ? N / 80 : N % 64 == 0 ? N / 64 : N / 16;
+  const long blocks = (long)cols * ((rows + 63) / 64);
+  const int nk = K / 16;
+  int split = 1;
+  while (blocks * split < 2L * ncu && nk / (2 * split) >= 8) split *= 2;
+  return split;
 }
 
 // Energy head and the seed of the backward: e = h2.Wo + bo + bias,
@@ -296,7 +365,7 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
 
 template <class T, int NT, bool TRANSB, bool AT = false>
 static void gemm_nt(hipStream_t st, const GemmArgs<T>& a) {
-  dim3 grid(a.N / (16 * NT), (a.M + 63) / 64);
+  dim3 grid(a.N / (16 * NT), (a.M + 63) / 64, a.split > 1 ? a.split : 1);
   hipLaunchKernelGGL((k_gemm<T, NT, TRANSB, AT>), grid, dim3(256), 0, st, a);
   DPAMD_LAUNCH_CHECK();
 }
@@ -372,6 +441,10 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   g = G{};
   g.M = rows; g.N = F0; g.K = Dn; g.A = D; g.lda = Dn; g.B = net.L[0].W; g.ldb = F0;
   g.epi = 1; g.bias = net.L[0].b; g.idt = nullptr; g.C = b.H0; g.ldc = F0;
+  if (b.split > 1) {
+    g.split = b.split;
+    g.ws = b.ws;
+  }
   if (Tt) {
     if (Dn != 16 * L3)
       throw HipError{hipErrorInvalidValue, "descriptor formed from T needs axis 16"};
@@ -380,6 +453,12 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
     gemm_at(st, g);
   } else {
     gemm<false>(st, g);
+  }
+  if (b.split > 1) {
+    const long groups = (long)rows * (F0 / 4);
+    hipLaunchKernelGGL(k_splitk_tanh<T>, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st,
+                       rows, F0, b.split, b.ws, net.L[0].b, b.H0);
+    DPAMD_LAUNCH_CHECK();
   }
   g = G{};
   g.M = rows; g.N = F1; g.K = F0; g.A = b.H0; g.lda = F0; g.B = net.L[1].W; g.ldb = F1;

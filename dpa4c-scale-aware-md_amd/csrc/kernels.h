@@ -151,7 +151,13 @@ struct FitNet {
 template <class T>
 struct FitBufs {
   T *H0, *T1, *H1, *T2, *H2, *dZa, *dZb, *dH;  // [rows][F] each
+  // first layer split over K into `split` slices (fit_splits) summed through
+  // ws [split][rows][F0] when split > 1
+  int split;
+  T* ws;
 };
+// K slices fit_splits(rows, F0, Dn, compute units) for the first fitting layer
+int fit_splits(int rows, int N, int K, int ncu);
 // The first layer reads its input either from D ([rows][L3*axis]) or, when
 // Tt is given (axis 16), forms D = T^T T[:, :16] on the fly from the
 // column-major copy of T (element (row, a, m) at Tt[a * ldt + 4 row + m]) and
