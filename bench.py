@@ -47,9 +47,12 @@ WORKLOAD = {2: "cu131k FCC Cu 131,072 atoms, rcut 8, sel 138, 32-64-128/240x3",
             4: "water393k 393,216 atoms, rcut 6, sel [46,92], 25-50-100/240x3"}
 
 
-def flops_bytes(pot, n_real, nloc, nb_edges):
+def flops_bytes(pot, n_real, nloc, nb_edges, mixed=False):
     """Algorithmic FLOPs / bytes of each stage for one step (real slots only;
-    padded slots are a per-(type, type) constant and not evaluated)."""
+    padded slots are a per-(type, type) constant and not evaluated). The
+    descriptor arrays (section sums, T, dE/dD, dE/dT) are fp32 in mixed mode.
+    With one neighbour type the forward writes T itself and the descriptor
+    pass does not run, so it has no work of its own."""
     L1, L2, L3 = (pot.info.emb[k] for k in range(3))
     M2 = pot.info.axis
     F0, F1, F2 = (pot.info.fit[k] for k in range(3))
@@ -58,17 +61,21 @@ def flops_bytes(pot, n_real, nloc, nb_edges):
     emb_fwd = 2.0 * (L1 + L1 * L2 + L2 * L3) + 2.0 * 4 * L3
     emb_vjp = 2.0 * (L1 * L2 + L2 * L3) + 2.0 * L1 + 2.0 * (2 * 4 * L3)
     fit = 2.0 * (Dn * F0 + F0 * F1 + F1 * F2 + F2) + 2.0 * (F2 * F1 + F1 * F0 + F0 * Dn)
-    return {
+    es = 4.0 if mixed else 8.0
+    work = {
         "embed_fwd": ("flop", emb_fwd * n_real),
         "embed_bwd": ("flop", emb_vjp * n_real),
         "fitting": ("flop", fit * nloc),
-        # reads the section sums, writes T (the first fitting GEMM forms D from T)
-        "descriptor": ("byte", 8.0 * nloc * (nt * 4 * L3 + 4 * L3)),
-        "dE_dT": ("byte", 8.0 * nloc * (Dn + 4 * L3 + 4 * L3)),
+        # reads dE/dD and T, writes dE/dT
+        "dE_dT": ("byte", es * nloc * (Dn + 4 * L3 + 4 * L3)),
         # edge gradient (24 B) + reverse index (4 B) per edge, force 24 B per atom
         "force": ("byte", 28.0 * nb_edges + 24.0 * nloc),
         "nlist": ("byte", 4.0 * nloc * pot.nnei + 24.0 * nloc),
     }
+    if nt > 1:
+        # reads the section sums, writes T (the first fitting GEMM forms D from T)
+        work["descriptor"] = ("byte", es * nloc * (nt * 4 * L3 + 4 * L3))
+    return work
 
 
 def run_config(dp, hip, config, steps, warmup):
@@ -124,7 +131,7 @@ def run_config(dp, hip, config, steps, warmup):
     ms_sync = (time.perf_counter() - t2) * 1e3 / steps
     energy = d_e.to_host(np.float64, (1,))[0]
     force = d_f.to_host(np.float64, (n, 3))
-    work = flops_bytes(pot, n_real, n, n_real)
+    work = flops_bytes(pot, n_real, n, n_real, mixed)
     stages = {}
     for k, t in stage_ms.items():
         entry = {"ms": round(t, 4)}
@@ -207,7 +214,8 @@ def main():
     us_atom = main_r["ms"] * 1e3 / n
     ns_day = DT_FS[args.config] * 1e-6 * 86400.0 / (main_r["ms"] * 1e-3)
     # dominant single-launch kernel
-    kernel_stages = ["embed_bwd", "embed_fwd", "descriptor", "dE_dT", "nlist"]
+    kernel_stages = [k for k in ("embed_bwd", "embed_fwd", "descriptor", "dE_dT", "nlist")
+                     if k in main_r["work"]]
     dom = max(kernel_stages, key=lambda k: main_r["stage_ms"].get(k, 0.0))
     kind, amount = main_r["work"][dom]
     t_dom = main_r["stage_ms"][dom] * 1e-3
