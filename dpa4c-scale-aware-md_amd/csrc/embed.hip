@@ -48,9 +48,17 @@ constexpr int fwd_lds_doubles(int waves) {
   return (S::SIZE + 31) / 32 * 32 + 8 + waves * 16 * (S::L2P + 2) + waves * 64;
 }
 
+// layer-1 stash [16 slots][K2P + 1] per wave, for a layer-2 [x, x] residual
+// whose features do not fall in the lane that computed them (L1 % 16 != 0)
+template <class S>
+constexpr int x1_stash_doubles() {
+  return (S::RES2 != 0 && !S::X1_ALIGNED) ? 16 * (S::K2P + 1) : 0;
+}
+
 template <class S>
 constexpr int bwd_lds_doubles(int waves) {
-  return (S::SIZE + 31) / 32 * 32 + 8 + waves * 4 * (S::L3P + S::L2P);
+  return (S::SIZE + 31) / 32 * 32 + 8 + waves * 4 * (S::L3P + S::L2P) +
+         waves * x1_stash_doubles<S>();
 }
 
 template <class S, int WAVES>
@@ -148,6 +156,14 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
           x1[q] = (f < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
         }
       }
+      // a residual feature f % L1 lives in another lane group: stash layer 1
+      // in this wave's X2 buffer (overwritten by X2 only after every read)
+      constexpr int X1LD = S::K2P + 1;
+      if constexpr (S::RES2 != 0 && !S::X1_ALIGNED) {
+#pragma unroll
+        for (int q = 0; q < S::NQ2; ++q) X2s[c * X1LD + 4 * q + g] = x1[q];
+        wave_lds_sync();
+      }
       // layer 2, transposed
       d4 acc2[S::NT2];
 #pragma unroll
@@ -176,7 +192,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
               res = x1[(S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r];
             } else {
               const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
-              res = (f1 < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f1] + P[S::OFF_B1 + f1]) : 0.0;
+              res = (f1 < S::L1) ? X2s[c * X1LD + f1] : 0.0;
             }
           }
           x2[t][r] = (f < S::L2) ? res + th : 0.0;
@@ -287,6 +303,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   double* EnvS = lds + PS;
   double* dTs = lds + PS + 8 + w * 4 * (S::L3P + S::L2P);
   double* dTf = dTs + 4 * S::L3P;
+  // layer-1 stash (see x1_stash_doubles)
+  double* X1s = lds + PS + 8 + WAVES * 4 * (S::L3P + S::L2P) + w * x1_stash_doubles<S>();
+  constexpr int X1LD = S::K2P + 1;
 
   const int p = find_pair(a);
   const int ti = p / a.ntypes, tj = p % a.ntypes;
@@ -409,6 +428,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
           }
         }
       }
+      if constexpr (S::RES2 != 0 && !S::X1_ALIGNED) {
+#pragma unroll
+        for (int q = 0; q < S::NQ2; ++q) X1s[c * X1LD + 4 * q + g] = x1[q];
+        wave_lds_sync();
+      }
       // layer 2: tangent product only; tanh of the primal comes from the forward
       d4 acc2t[S::NT2];
 #pragma unroll
@@ -435,10 +459,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
             } else {
               const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
               if (f1 < S::L1) {
-                const double wv = P[S::OFF_W1 + f1];
-                const double y = tanh_fast(s * wv + P[S::OFF_B1 + f1]);
+                const double y = X1s[c * X1LD + f1];
                 res = y;
-                rest = (1.0 - y * y) * wv;
+                rest = (1.0 - y * y) * P[S::OFF_W1 + f1];
               }
             }
           }
