@@ -119,6 +119,41 @@ def test_nlist_exact_ties(dp, orc, kind):
     assert np.abs(f - ref["force"]).max() <= F_TOL
 
 
+@pytest.mark.parametrize("kind", ["water", "cu"])
+def test_open_system(dp, orc, kind):
+    """An isolated cluster (box = NULL: no periodic images): a water droplet
+    cut from the 12k box and an FCC Cu particle whose inner atoms overflow sel.
+    The GPU list must equal the oracle's brute-force one bit for bit, E / F /
+    V / atom virials must agree, and, the energy being invariant under
+    rotations and translations of the whole cluster, the total force and the
+    total torque sum(r x F) must vanish."""
+    if kind == "water":
+        coord, atype, _ = dp.systems.build(1)
+        m = dp.model.random_model("water", seed=1001)
+    else:
+        coord, atype, _ = dp.systems.fcc(8, 3.615, seed=7)
+        m = dp.model.random_model("cu", seed=1002)
+    centre = coord.mean(0)
+    keep = np.linalg.norm(coord - centre, axis=1) < 11.0
+    coord = np.ascontiguousarray(coord[keep] - centre)
+    atype = np.ascontiguousarray(atype[keep])
+    n = len(atype)
+    mb = model_bytes(m)
+    O = orc.Oracle(mb)
+    off, cand = O.candidates(n, coord, atype, O.m["rcut"], "brute")
+    nl = O.format_nlist(n, coord, atype, off, cand)
+    ref = O.eval_ext(n, coord, atype, nl)
+    pot = dp.DeepPot(file_content=mb)
+    e, f, v, ae, av = pot.compute(coord, atype, None, atomic=True)
+    assert np.array_equal(pot.stage(dp.STAGE_NLIST, np.int32, nl.shape), nl)
+    assert abs(e - ref["energy"]) / n <= E_TOL
+    assert np.abs(f - ref["force"]).max() <= F_TOL
+    assert np.abs(v - ref["virial"]).max() <= V_TOL
+    assert np.abs(av - ref["atom_virial"]).max() <= V_TOL
+    assert np.abs(f.sum(0)).max() <= 1e-9
+    assert np.abs(np.cross(coord, f).sum(0)).max() <= 1e-8
+
+
 def test_virtual_atoms(dp, orc):
     (coord, atype, box), m = CASES["water192"]()
     atype = atype.copy()

@@ -223,6 +223,9 @@ def test_invariances(dp, orc, water):
     b = O.eval_ext(24, ext2, ts, O.format_nlist(24, ext2, ts, off2, cand2))
     assert b["energy"] == pytest.approx(a["energy"], abs=1e-10)
     np.testing.assert_allclose(b["force"], a["force"] @ R.T, atol=1e-10)
+    # rotation invariance of an isolated cluster: no net force, no net torque
+    assert np.abs(a["force"].sum(0)).max() < 1e-10
+    assert np.abs(np.cross(sub, a["force"]).sum(0)).max() < 1e-9
 
 
 def test_padded_slots_use_net_at_s_pad(dp, orc):
