@@ -12,7 +12,10 @@
 //   reverse list + force / atom-virial gather        force.hip
 //   energy / virial reduction                        force.hip
 // The LAMMPS path replaces the first three stages with sel formatting of the
-// caller's candidate list and keeps ghost forces in ghost slots.
+// caller's candidate list and keeps ghost forces in ghost slots. On the
+// standalone device path no stage waits for the host: the ghost count stays
+// on the device, and dp_compute_device_async only queues the evaluation
+// (optionally as a replayed HIP graph), leaving capacity errors for dp_sync.
 //
 // This file is compiled with -ffp-contract=off: the box geometry (cutoff in
 // fractional units) must match the oracle's bit for bit because it decides
