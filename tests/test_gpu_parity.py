@@ -154,6 +154,45 @@ def test_open_system(dp, orc, kind):
     assert np.abs(np.cross(coord, f).sum(0)).max() <= 1e-8
 
 
+def _check_against_oracle(dp, orc, m, coord, atype, box):
+    mb = model_bytes(m)
+    O = orc.Oracle(mb)
+    ref = O.compute(coord, atype, box)
+    pot = dp.DeepPot(file_content=mb)
+    e, f, v, ae, av = pot.compute(coord, atype, box, atomic=True)
+    assert np.array_equal(pot.stage(dp.STAGE_NLIST, np.int32, ref["nlist"].shape), ref["nlist"])
+    n = len(atype)
+    assert abs(e - ref["energy"]) / n <= E_TOL
+    assert np.abs(ae - ref["atom_energy"]).max() <= E_TOL
+    assert np.abs(f - ref["force"]).max() <= F_TOL
+    assert np.abs(v - ref["virial"]).max() <= V_TOL
+    return ref
+
+
+def test_edge_cases(dp, orc):
+    """Edge inputs: an empty system, a single atom whose slots are all padding,
+    a water model evaluated on oxygen only (one type has no atoms, so its
+    fitting net and its pairs are skipped), and a dimer at exactly rcut
+    (r^2 == rcut^2 is kept, as the oracle's inclusive test)."""
+    cu = dp.model.random_model("cu", seed=1002)
+    water = dp.model.random_model("water", seed=1000)
+    box = np.diag([30.0, 30.0, 30.0]).reshape(9)
+    pot = dp.DeepPot(file_content=model_bytes(cu))
+    e, f, v = pot.compute(np.zeros((0, 3)), np.zeros(0, np.int32), box)
+    assert e == 0.0 and f.shape == (0, 3) and not np.any(v)
+    ref = _check_against_oracle(dp, orc, cu, np.array([[1.0, 2.0, 3.0]]), np.array([0], np.int32),
+                                box)
+    assert np.all(ref["nlist"] == -1)
+    (coord, atype, wbox), _ = CASES["water192"]()
+    oxy = atype == 0
+    ref = _check_against_oracle(dp, orc, water, np.ascontiguousarray(coord[oxy]),
+                                np.ascontiguousarray(atype[oxy]), wbox)
+    assert np.all(ref["nlist"][:, 46:] == -1)
+    dimer = np.array([[5.0, 5.0, 5.0], [13.0, 5.0, 5.0]])
+    ref = _check_against_oracle(dp, orc, cu, dimer, np.array([0, 0], np.int32), box)
+    assert ref["nlist"][0, 0] == 1 and ref["nlist"][1, 0] == 0
+
+
 def test_virtual_atoms(dp, orc):
     (coord, atype, box), m = CASES["water192"]()
     atype = atype.copy()
