@@ -87,8 +87,8 @@ struct dp_model {
   // workspace
   std::vector<Buf*> bufs;
   Buf coord_in, atype_in, sfrac, flags, gpos, ext, ext_type, mapping, cell_of, cell_count,
-      cell_start, cell_cursor, sorted, nlist, nreal, cand_off, cand, items, Tsec, Tt, D, dD, dT,
-      fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_cursor, rev, force_ws, av_ws,
+      cell_start, cell_rank, sorted, nlist, nreal, cand_off, cand, items, Tsec, Tt, D, dD, dT,
+      fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_rank, rev, force_ws, av_ws,
       ae_ws, partials, out10, status, scan_tmp, act, nall_d, split_ws;
   size_t bytes_now = 0, bytes_peak = 0;
   // type buckets
@@ -135,10 +135,10 @@ struct dp_model {
 
   dp_model() {
     bufs = {&coord_in, &atype_in, &sfrac,     &flags,    &gpos,       &ext,       &ext_type,
-            &mapping,  &cell_of,  &cell_count, &cell_start, &cell_cursor, &sorted,  &nlist,
+            &mapping,  &cell_of,  &cell_count, &cell_start, &cell_rank, &sorted,   &nlist,
             &nreal,    &cand_off, &cand,      &items,    &Tsec,       &Tt,        &D,
             &dD,       &dT,       &fitb,      &e_bucket, &edge_grad,  &cpart,     &rev_count,
-            &rev_off,  &rev_cursor, &rev,     &force_ws, &av_ws,      &ae_ws,     &partials,
+            &rev_off,  &rev_rank, &rev,       &force_ws, &av_ws,      &ae_ws,     &partials,
             &out10,    &status,   &scan_tmp, &act,       &nall_d,    &split_ws};
   }
 };
@@ -465,17 +465,16 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   const long nedge = (long)nloc * nnei;
   int* rcount = need<int>(M, M->rev_count, (size_t)ntarget + 1);
   int* roff = need<int>(M, M->rev_off, (size_t)ntarget + 1);
-  int* rcur = need<int>(M, M->rev_cursor, (size_t)ntarget + 1);
+  int* rrank = need<int>(M, M->rev_rank, (size_t)std::max<long>(nedge, 1));
   int* rev = need<int>(M, M->rev, (size_t)std::max<long>(nedge, 1));
   launch_fill_int(st, (long)ntarget + 1, 0, rcount);
-  launch_fill_int(st, (long)ntarget + 1, 0, rcur);
-  launch_rev_count(st, nedge, nnei, nlist, d_mapping, rcount);
+  launch_rev_count(st, nedge, nnei, nlist, d_mapping, rcount, rrank);
   {
     const size_t tb = scan_temp_bytes(ntarget + 1);
     void* tmp = need<char>(M, M->scan_tmp, tb);
     exclusive_scan_int(st, rcount, roff, ntarget + 1, tmp, tb);
   }
-  launch_rev_fill(st, nedge, nnei, nlist, d_mapping, roff, rcur, rev);
+  launch_rev_fill(st, nedge, nnei, nlist, d_mapping, roff, rrank, rev);
   launch_force_gather(st, ntarget, nloc, nnei, roff, rev, nlist, ext, edge_grad, cpart,
                       out.force, out.atom_virial, status);
   record(M, st, kStForce + 1);
@@ -535,17 +534,16 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
   int* cell_of = need<int>(M, M->cell_of, (size_t)nall);
   int* ccount = need<int>(M, M->cell_count, (size_t)ncell + 1);
   int* cstart = need<int>(M, M->cell_start, (size_t)ncell + 1);
-  int* ccur = need<int>(M, M->cell_cursor, (size_t)ncell + 1);
+  int* crank = need<int>(M, M->cell_rank, (size_t)nall);
   CellAtom* sorted = need<CellAtom>(M, M->sorted, (size_t)nall);
   launch_fill_int(st, (long)ncell + 1, 0, ccount);
-  launch_fill_int(st, (long)ncell + 1, 0, ccur);
-  launch_cell_assign(st, nall, nall_d, bp, ext, cell_of, ccount);
+  launch_cell_assign(st, nall, nall_d, bp, ext, cell_of, crank, ccount);
   {
     const size_t tb = scan_temp_bytes(ncell + 1);
     void* tmp = need<char>(M, M->scan_tmp, tb);
     exclusive_scan_int(st, ccount, cstart, ncell + 1, tmp, tb);
   }
-  launch_cell_scatter(st, nall, nall_d, cell_of, cstart, ccur, ext, ext_type, sorted);
+  launch_cell_scatter(st, nall, nall_d, cell_of, crank, cstart, ext, ext_type, sorted);
   record(M, st, kStGeom + 1);
   NlParams np{};
   np.ntypes = m.ntypes;

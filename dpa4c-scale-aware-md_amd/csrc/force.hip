@@ -17,24 +17,28 @@
 
 namespace dpamd {
 
+// The count keeps each edge's rank among the edges into its target (the value
+// its increment returned), so the fill is a plain scatter; that order is
+// arbitrary and the gather ranks the ids again.
 __global__ void k_rev_count(long nedge, const int* __restrict__ nlist,
-                            const int* __restrict__ mapping, int* __restrict__ count) {
+                            const int* __restrict__ mapping, int* __restrict__ count,
+                            int* __restrict__ rank) {
   const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= nedge) return;
   const int j = nlist[e];
   if (j < 0) return;
-  atomicAdd(&count[mapping ? mapping[j] : j], 1);
+  rank[e] = atomicAdd(&count[mapping ? mapping[j] : j], 1);
 }
 
 __global__ void k_rev_fill(long nedge, const int* __restrict__ nlist,
                            const int* __restrict__ mapping, const int* __restrict__ off,
-                           int* __restrict__ cursor, int* __restrict__ rev) {
+                           const int* __restrict__ rank, int* __restrict__ rev) {
   const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= nedge) return;
   const int j = nlist[e];
   if (j < 0) return;
   const int t = mapping ? mapping[j] : j;
-  rev[off[t] + atomicAdd(&cursor[t], 1)] = (int)e;
+  rev[off[t] + rank[e]] = (int)e;
 }
 
 constexpr int kGatherWaves = 4;
@@ -208,18 +212,18 @@ __global__ void k_scatter_energy(int n, const int* __restrict__ items,
 }
 
 void launch_rev_count(hipStream_t st, long nedge, int, const int* nlist, const int* mapping,
-                      int* count) {
+                      int* count, int* rank) {
   if (nedge <= 0) return;
   hipLaunchKernelGGL(k_rev_count, dim3((unsigned)((nedge + 255) / 256)), dim3(256), 0, st, nedge,
-                     nlist, mapping, count);
+                     nlist, mapping, count, rank);
   DPAMD_LAUNCH_CHECK();
 }
 
 void launch_rev_fill(hipStream_t st, long nedge, int, const int* nlist, const int* mapping,
-                     const int* off, int* cursor, int* rev) {
+                     const int* off, const int* rank, int* rev) {
   if (nedge <= 0) return;
   hipLaunchKernelGGL(k_rev_fill, dim3((unsigned)((nedge + 255) / 256)), dim3(256), 0, st, nedge,
-                     nlist, mapping, off, cursor, rev);
+                     nlist, mapping, off, rank, rev);
   DPAMD_LAUNCH_CHECK();
 }
 

@@ -96,10 +96,11 @@ void launch_ghost_fill(hipStream_t, int nloc, const BoxParams&, const int* flags
                        double* ext, int* ext_type, int* mapping);
 // Cell kernels over cap atoms, or over *d_count of them when d_count is given
 // (a count produced on the device, at most cap).
+// (cell_rank: an atom's rank within its cell, from the count)
 void launch_cell_assign(hipStream_t, int cap, const int* d_count, const BoxParams&,
-                        const double* ext, int* cell_of, int* cell_count);
+                        const double* ext, int* cell_of, int* cell_rank, int* cell_count);
 void launch_cell_scatter(hipStream_t, int cap, const int* d_count, const int* cell_of,
-                         const int* cell_start, int* cursor, const double* ext,
+                         const int* cell_rank, const int* cell_start, const double* ext,
                          const int* ext_type, CellAtom* sorted);
 // nall = nloc + number of flagged ghost candidates, from the flags and their
 // exclusive scan, into device memory
@@ -176,10 +177,11 @@ void launch_dT(hipStream_t, int nloc, int L3, int axis, const int* items, const 
                T* dT);
 
 // Force / virial stage
+// (rank: each edge's rank among the edges into its target, from the count)
 void launch_rev_count(hipStream_t, long nedge, int nnei, const int* nlist, const int* mapping,
-                      int* count);
+                      int* count, int* rank);
 void launch_rev_fill(hipStream_t, long nedge, int nnei, const int* nlist, const int* mapping,
-                     const int* off, int* cursor, int* rev);
+                     const int* off, const int* rank, int* rev);
 // cpart [nloc][12]: each centre's own-row force (3) and frame virial (9),
 // written by the gather and summed by the reduction.
 void launch_force_gather(hipStream_t, int ntarget, int nloc, int nnei, const int* rev_off,

@@ -110,25 +110,28 @@ __device__ __forceinline__ int cell_of_point(const BoxParams& bp, double x0, dou
 
 // The atom count is cap, or *d_count when given (ghost count known on the
 // device only; the grid then covers the capacity cap).
+// Each atom's rank among the atoms of its cell is the value its count
+// increment returned, so the scatter needs no second round of atomics (the
+// order within a cell is arbitrary; the neighbour list sorts its candidates).
 __global__ void k_cell_assign(int cap, const int* __restrict__ d_count, BoxParams bp,
                               const double* __restrict__ ext, int* __restrict__ cell_of,
-                              int* __restrict__ cell_count) {
+                              int* __restrict__ cell_rank, int* __restrict__ cell_count) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= (d_count ? *d_count : cap)) return;
   const int c = cell_of_point(bp, ext[3 * n], ext[3 * n + 1], ext[3 * n + 2]);
   cell_of[n] = c;
-  atomicAdd(&cell_count[c], 1);
+  cell_rank[n] = atomicAdd(&cell_count[c], 1);
 }
 
 __global__ void k_cell_scatter(int cap, const int* __restrict__ d_count,
-                               const int* __restrict__ cell_of,
-                               const int* __restrict__ cell_start, int* __restrict__ cursor,
+                               const int* __restrict__ cell_of, const int* __restrict__ cell_rank,
+                               const int* __restrict__ cell_start,
                                const double* __restrict__ ext, const int* __restrict__ ext_type,
                                CellAtom* __restrict__ sorted) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= (d_count ? *d_count : cap)) return;
   const int c = cell_of[n];
-  const int p = cell_start[c] + atomicAdd(&cursor[c], 1);
+  const int p = cell_start[c] + cell_rank[n];
   CellAtom a;
   a.x = ext[3 * n];
   a.y = ext[3 * n + 1];
@@ -433,19 +436,19 @@ void launch_ghost_fill(hipStream_t st, int nloc, const BoxParams& bp, const int*
 }
 
 void launch_cell_assign(hipStream_t st, int cap, const int* d_count, const BoxParams& bp,
-                        const double* ext, int* cell_of, int* cell_count) {
+                        const double* ext, int* cell_of, int* cell_rank, int* cell_count) {
   if (cap <= 0) return;
   hipLaunchKernelGGL(k_cell_assign, dim3((cap + 255) / 256), dim3(256), 0, st, cap, d_count, bp,
-                     ext, cell_of, cell_count);
+                     ext, cell_of, cell_rank, cell_count);
   DPAMD_LAUNCH_CHECK();
 }
 
 void launch_cell_scatter(hipStream_t st, int cap, const int* d_count, const int* cell_of,
-                         const int* cell_start, int* cursor, const double* ext,
+                         const int* cell_rank, const int* cell_start, const double* ext,
                          const int* ext_type, CellAtom* sorted) {
   if (cap <= 0) return;
   hipLaunchKernelGGL(k_cell_scatter, dim3((cap + 255) / 256), dim3(256), 0, st, cap, d_count,
-                     cell_of, cell_start, cursor, ext, ext_type, sorted);
+                     cell_of, cell_rank, cell_start, ext, ext_type, sorted);
   DPAMD_LAUNCH_CHECK();
 }
 
