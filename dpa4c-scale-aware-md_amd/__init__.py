@@ -17,7 +17,7 @@ import os
 
 import numpy as np
 
-from . import model, systems  # noqa: F401
+from . import dpa4c, model, systems  # noqa: F401
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libdpamd.so")

@@ -24,3 +24,10 @@ def load_oracle():
         sys.path.insert(0, ROOT)
     from oracle import oracle as orc  # noqa: E402
     return orc
+
+
+def load_dpa4c_oracle():
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    from oracle import dpa4c_oracle  # noqa: E402
+    return dpa4c_oracle
