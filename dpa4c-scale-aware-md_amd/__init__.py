@@ -26,11 +26,13 @@ _LIB = None
 MAX_TYPES = 8
 STAGE_NLIST, STAGE_EXT_COORD, STAGE_MAPPING, STAGE_DESCRPT = 0, 1, 2, 3
 STAGE_ATOM_ENERGY, STAGE_EDGE_GRAD, STAGE_DEDD, STAGE_EXT_TYPE = 4, 5, 6, 7
+STAGE_C4_MOMENTS, STAGE_C4_COTANGENTS = 8, 9
 PREC_FP64, PREC_MIXED = 0, 1
+MODEL_SE_E2_A, MODEL_DPA4C = 0, 1
 
 EXPORTED = ("dp_create", "dp_destroy", "dp_get_info", "dp_last_error", "dp_compute",
             "dp_compute_nlist", "dp_compute_device", "dp_compute_device_async", "dp_sync",
-            "dp_graph_stats",
+            "dp_graph_stats", "dp_compute_canonical_graph_device",
             "dp_debug_copy", "dp_stage_times", "dp_device_bytes")
 
 
@@ -43,7 +45,7 @@ class ModelInfo(C.Structure):
                 ("rcut", C.c_double), ("rcut_smth", C.c_double), ("emb", C.c_int * 3),
                 ("axis", C.c_int), ("fit", C.c_int * 3), ("dim_fparam", C.c_int),
                 ("dim_aparam", C.c_int), ("precision", C.c_int),
-                ("type_map", (C.c_char * 16) * MAX_TYPES)]
+                ("type_map", (C.c_char * 16) * MAX_TYPES), ("model_kind", C.c_int)]
 
 
 def lib():
@@ -66,6 +68,8 @@ def lib():
         L.dp_compute_device_async.argtypes = [P, I, P, P, P, I, P, P, P, P, P, P]
         L.dp_sync.argtypes = [P]
         L.dp_graph_stats.argtypes = [P, C.POINTER(C.c_long), C.POINTER(C.c_long)]
+        L.dp_compute_canonical_graph_device.argtypes = [P, P, P, P, P, P, P, P, P, P, I, I,
+                                                        C.c_int64, P]
         L.dp_debug_copy.argtypes = [P, I, P, C.c_size_t]
         L.dp_debug_copy.restype = C.c_long
         L.dp_stage_times.argtypes = [P, I, P, I, P, C.c_size_t]
@@ -81,7 +85,8 @@ def _ptr(a):
 
 
 class DeepPot:
-    """se_e2_a model evaluated on one gfx950 GPU."""
+    """A DeePMD model (se_e2_a, or DPA4C-Nano) evaluated on one gfx950 GPU;
+    the family is read from the model file."""
 
     def __init__(self, model_path: str | None = None, gpu_rank: int = 0,
                  file_content: bytes | None = None, precision: int = PREC_FP64):
@@ -107,7 +112,8 @@ class DeepPot:
         self._ntypes = info.ntypes
         self.nnei = info.nnei
         self.sel = [info.sel[t] for t in range(info.ntypes)]
-        self.ndescrpt = info.emb[2] * info.axis
+        self.model_kind = info.model_kind
+        self.ndescrpt = 70 if info.model_kind == MODEL_DPA4C else info.emb[2] * info.axis
 
     def __del__(self):
         if getattr(self, "_h", None):
@@ -202,6 +208,19 @@ class DeepPot:
                                                   ago, d_energy, d_force, d_virial,
                                                   d_atom_energy or None, d_atom_virial or None,
                                                   stream or None))
+
+    def compute_canonical_graph_device(self, d_atom_energy: int, d_force: int,
+                                       d_atom_virial: int, d_atype: int, d_source: int,
+                                       d_edge_vec: int, d_destination_row_ptr: int,
+                                       d_source_row_ptr: int, d_source_order: int, nloc: int,
+                                       nall_nodes: int, edge_storage: int, stream: int = 0):
+        """DPA4C evaluation of a compact canonical graph on raw device pointers
+        (dp_compute_canonical_graph_device, mirroring
+        DeepPot::compute_canonical_graph_gpu)."""
+        self._check(lib().dp_compute_canonical_graph_device(
+            self._h, d_atom_energy or None, d_force, d_atom_virial, d_atype, d_source, d_edge_vec,
+            d_destination_row_ptr, d_source_row_ptr, d_source_order, nloc, nall_nodes,
+            edge_storage, stream or None))
 
     def sync(self):
         """Wait for the queued asynchronous evaluations (dp_sync)."""

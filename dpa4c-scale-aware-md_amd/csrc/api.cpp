@@ -67,6 +67,12 @@ struct dp_model {
   int ncu = 256;  // compute units of the device
   int precision = DP_PREC_FP64;
   ModelHost host;
+  // model kind: se_e2_a (DPAMDSEA files) or DPA4C-Nano (DPAMDC4N files)
+  enum Kind { kSeA = 0, kDpa4c = 1 };
+  int kind = kSeA;
+  C4Host c4;
+  C4Params c4p{};
+  void* d_c4 = nullptr;  // every DPA4C parameter array, packed
   EmbLayout el{};
   std::string err;
   // device parameters; the nets (d_emb, d_fit) are double in fp64 mode and
@@ -89,7 +95,7 @@ struct dp_model {
   Buf coord_in, atype_in, sfrac, flags, gpos, ext, ext_type, mapping, cell_of, cell_count,
       cell_start, cell_rank, sorted, nlist, nreal, cand_off, cand, items, Tsec, Tt, D, dD, dT,
       fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_rank, rev, force_ws, av_ws,
-      ae_ws, partials, out10, status, scan_tmp, act, nall_d, split_ws;
+      ae_ws, partials, out10, status, scan_tmp, act, nall_d, split_ws, c4_mom, c4_cot;
   size_t bytes_now = 0, bytes_peak = 0;
   // type buckets
   std::vector<int> atype_cache;
@@ -139,7 +145,8 @@ struct dp_model {
             &nreal,    &cand_off, &cand,      &items,    &Tsec,       &Tt,        &D,
             &dD,       &dT,       &fitb,      &e_bucket, &edge_grad,  &cpart,     &rev_count,
             &rev_off,  &rev_rank, &rev,       &force_ws, &av_ws,      &ae_ws,     &partials,
-            &out10,    &status,   &scan_tmp, &act,       &nall_d,    &split_ws};
+            &out10,    &status,   &scan_tmp, &act,       &nall_d,    &split_ws,  &c4_mom,
+            &c4_cot};
   }
 };
 
@@ -295,6 +302,9 @@ DescArgs desc_args(dp_model* M, void* Tt, void* D) {
   return da;
 }
 
+void gather_and_reduce(dp_model* M, hipStream_t st, int nloc, int ntarget, const int* d_mapping,
+                       const double* e_vals, int ne, const int* items, const Outputs& out);
+
 template <class E>
 void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_mapping,
                  int ntarget, const Outputs& out) {
@@ -306,7 +316,6 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   const int* nlist = static_cast<const int*>(M->nlist.p);
   const int* nreal = static_cast<const int*>(M->nreal.p);
   const int* items = static_cast<const int*>(M->items.p);
-  int* status = static_cast<int*>(M->status.p);
 
   E* Tsec = need<E>(M, M->Tsec, (size_t)nloc * nt * 4 * L3);
   // T column-major in bucket order; with axis 16 the first fitting GEMM forms
@@ -320,7 +329,6 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   E* fitb = need<E>(M, M->fitb, (size_t)8 * std::max(nb, 1) * Fmax);
   double* e_bucket = need<double>(M, M->e_bucket, (size_t)std::max(nb, 1));
   double* edge_grad = need<double>(M, M->edge_grad, (size_t)nloc * nnei * 3);
-  double* cpart = need<double>(M, M->cpart, (size_t)std::max(nloc, 1) * 12);
 
   EmbArgs ea{};
   ea.ntypes = nt;
@@ -460,8 +468,21 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   nblk = block_table(embed_waves_bwd(M->el, f32));
   launch_embed_bwd(st, M->el, ea, nblk, f32);
   record(M, st, kStEmbBwd + 1);
+  gather_and_reduce(M, st, nloc, ntarget, d_mapping, e_bucket, nb, items, out);
+  (void)nall;
+}
 
-  // reverse list + gather
+// Reverse list + force / atom-virial gather from the edge gradients, then the
+// energy / virial reduction. Atom energies e_vals[0..ne) are in bucket order
+// (items maps a position to its atom) or, with items null, in atom order.
+void gather_and_reduce(dp_model* M, hipStream_t st, int nloc, int ntarget, const int* d_mapping,
+                       const double* e_vals, int ne, const int* items, const Outputs& out) {
+  const int nnei = M->host.nnei;
+  const int* nlist = static_cast<const int*>(M->nlist.p);
+  const double* ext = static_cast<const double*>(M->ext.p);
+  const double* edge_grad = static_cast<const double*>(M->edge_grad.p);
+  int* status = static_cast<int*>(M->status.p);
+  double* cpart = need<double>(M, M->cpart, (size_t)std::max(nloc, 1) * 12);
   const long nedge = (long)nloc * nnei;
   int* rcount = need<int>(M, M->rev_count, (size_t)ntarget + 1);
   int* roff = need<int>(M, M->rev_off, (size_t)ntarget + 1);
@@ -481,22 +502,75 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
 
   double* partials = need<double>(M, M->partials, 256 * 10);
   double* out10 = need<double>(M, M->out10, 10);
-  launch_reduce_ev(st, nb, nloc, e_bucket, cpart, partials, out10);
+  launch_reduce_ev(st, ne, nloc, e_vals, cpart, partials, out10);
   if (out.energy) DPAMD_HIP(hipMemcpyAsync(out.energy, out10, 8, hipMemcpyDeviceToDevice, st));
   if (out.virial)
     DPAMD_HIP(hipMemcpyAsync(out.virial, out10 + 1, 72, hipMemcpyDeviceToDevice, st));
   if (out.atom_energy) {
     launch_fill_int(st, 2L * ntarget, 0, reinterpret_cast<int*>(out.atom_energy));
-    launch_scatter_energy(st, nb, items, e_bucket, out.atom_energy);
+    if (items) {
+      launch_scatter_energy(st, ne, items, e_vals, out.atom_energy);
+    } else if (ne > 0) {
+      DPAMD_HIP(hipMemcpyAsync(out.atom_energy, e_vals, sizeof(double) * ne,
+                               hipMemcpyDeviceToDevice, st));
+    }
   }
   record(M, st, kStReduce + 1);
-  (void)nall;
+}
+
+// DPA4C-Nano on the sel-sorted list: moments, node pass (readout, fitting,
+// readout VJP), edge gradients, then the shared gather and reduction. Stage
+// timers: moments under embed_fwd, the node pass under fitting, the edge
+// gradients under embed_bwd.
+void run_c4(dp_model* M, hipStream_t st, int nloc, const int* d_mapping, int ntarget,
+            const Outputs& out) {
+  const ModelHost& m = M->host;
+  C4Nlist src{};
+  src.nlist = static_cast<const int*>(M->nlist.p);
+  src.nreal = static_cast<const int*>(M->nreal.p);
+  src.ext = static_cast<const double*>(M->ext.p);
+  src.ext_type = static_cast<const int*>(M->ext_type.p);
+  src.nnei = m.nnei;
+  for (int t = 0; t <= m.ntypes; ++t) src.sec[t] = m.sec[t];
+  int* status = static_cast<int*>(M->status.p);
+  float* mom = need<float>(M, M->c4_mom, (size_t)std::max(nloc, 1) * kC4Mom);
+  float* cot = need<float>(M, M->c4_cot, (size_t)std::max(nloc, 1) * kC4Mom);
+  double* e = need<double>(M, M->e_bucket, (size_t)std::max(nloc, 1));
+  double* eg = need<double>(M, M->edge_grad, (size_t)std::max(nloc, 1) * m.nnei * 3);
+  launch_c4_moments(st, M->c4p, src, nloc, mom, status);
+  record(M, st, kStEmbFwd + 1);
+  record(M, st, kStDescr + 1);
+  launch_c4_node(st, M->c4p, nloc, src.ext_type, mom, e, cot);
+  record(M, st, kStFit + 1);
+  record(M, st, kStDT + 1);
+  launch_c4_edge_grad(st, M->c4p, src, nloc, cot, eg);
+  record(M, st, kStEmbBwd + 1);
+  gather_and_reduce(M, st, nloc, ntarget, d_mapping, e, nloc, nullptr, out);
 }
 
 void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_mapping, int ntarget,
                const Outputs& out) {
+  if (M->kind == dp_model::kDpa4c) return run_c4(M, st, nloc, d_mapping, ntarget, out);
   if (M->precision == DP_PREC_MIXED) run_model_t<float>(M, st, nloc, nall, d_mapping, ntarget, out);
   else run_model_t<double>(M, st, nloc, nall, d_mapping, ntarget, out);
+}
+
+// Neighbour-list parameters of the model. DPA4C keeps r^2 < rcut^2 (strict,
+// deepmd-op/overlays/op/pt/dpa4c/exact_cut.cuh:10-20) and never drops a
+// neighbour: a section that overflows its capacity is an error.
+NlParams nl_params(const dp_model* M) {
+  const ModelHost& m = M->host;
+  NlParams np{};
+  np.ntypes = m.ntypes;
+  np.nnei = m.nnei;
+  for (int t = 0; t < m.ntypes; ++t) np.sel[t] = m.sel[t];
+  for (int t = 0; t <= m.ntypes; ++t) np.sec[t] = m.sec[t];
+  np.rc2 = m.rcut * m.rcut;
+  if (M->kind == dp_model::kDpa4c) {
+    np.rc2 = std::nextafter(np.rc2, 0.0);
+    np.sel_strict = 1;
+  }
+  return np;
 }
 
 // Ghosts + cells + nlist for the standalone path, with no host round trip:
@@ -545,12 +619,7 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
   }
   launch_cell_scatter(st, nall, nall_d, cell_of, crank, cstart, ext, ext_type, sorted);
   record(M, st, kStGeom + 1);
-  NlParams np{};
-  np.ntypes = m.ntypes;
-  np.nnei = m.nnei;
-  for (int t = 0; t < m.ntypes; ++t) np.sel[t] = m.sel[t];
-  for (int t = 0; t <= m.ntypes; ++t) np.sec[t] = m.sec[t];
-  np.rc2 = m.rcut * m.rcut;
+  const NlParams np = nl_params(M);
   int* nlist = need<int>(M, M->nlist, (size_t)std::max(nloc, 1) * m.nnei);
   int* nreal = need<int>(M, M->nreal, (size_t)std::max(nloc, 1) * m.ntypes);
   launch_nlist_cells(st, nloc, bp, np, ext, ext_type, cell_of, cstart, sorted, nlist, nreal,
@@ -566,6 +635,11 @@ void throw_status(int s) {
   if (s & kStatusReverseOverflow)
     throw ApiError{DP_ERR_CAPACITY,
                    "more than " + std::to_string(kMaxRev) + " edges point at one atom"};
+  if (s & kStatusSelOverflow)
+    throw ApiError{DP_ERR_CAPACITY,
+                   "more neighbours of one type within rcut than the model's sel holds"};
+  if (s & kStatusBadInput)
+    throw ApiError{DP_ERR_ARG, "atom type or edge source outside the model / graph"};
 }
 
 void check_status(dp_model* M, hipStream_t st) {
@@ -802,6 +876,58 @@ void device_step(dp_model* M, int natoms, const double* d_coord, const int* d_at
   }
 }
 
+// Packs every DPA4C parameter array into one device allocation (each array
+// 256-byte aligned) and points the kernel parameters at it.
+void upload_c4(dp_model* M) {
+  const C4Host& c = M->c4;
+  const ModelHost& m = M->host;
+  std::vector<unsigned char> blob;
+  auto put = [&](const void* src, size_t bytes) {
+    const size_t off = (blob.size() + 255) & ~size_t(255);
+    blob.resize(off + bytes);
+    std::memcpy(blob.data() + off, src, bytes);
+    return off;
+  };
+  const size_t o_table = put(c.table.data(), c.table.size() * 4);
+  const size_t o_film = put(c.film.data(), c.film.size() * 4);
+  const size_t o_ro = put(c.ro.data(), c.ro.size() * 4);
+  const size_t o_temb = put(c.temb.data(), c.temb.size() * 4);
+  const size_t o_mean = put(c.mean.data(), c.mean.size() * 4);
+  const size_t o_istd = put(c.istd.data(), c.istd.size() * 4);
+  const size_t o_w0t = put(c.w0t.data(), c.w0t.size() * 4);
+  const size_t o_b0 = put(c.b0.data(), c.b0.size() * 4);
+  const size_t o_wh = put(c.wh.data(), c.wh.size() * 4);
+  const size_t o_bias = put(c.bias.data(), c.bias.size() * 8);
+  DPAMD_HIP(hipMalloc(&M->d_c4, blob.size()));
+  M->bytes_now += blob.size();
+  M->bytes_peak = std::max(M->bytes_peak, M->bytes_now);
+  DPAMD_HIP(hipMemcpy(M->d_c4, blob.data(), blob.size(), hipMemcpyHostToDevice));
+  const auto* base = static_cast<const unsigned char*>(M->d_c4);
+  C4Params& p = M->c4p;
+  p.table = reinterpret_cast<const float*>(base + o_table);
+  p.film = reinterpret_cast<const float*>(base + o_film);
+  p.ro = reinterpret_cast<const float*>(base + o_ro);
+  p.temb = reinterpret_cast<const float*>(base + o_temb);
+  p.mean = reinterpret_cast<const float*>(base + o_mean);
+  p.istd = reinterpret_cast<const float*>(base + o_istd);
+  p.w0t = reinterpret_cast<const float*>(base + o_w0t);
+  p.b0 = reinterpret_cast<const float*>(base + o_b0);
+  p.wh = reinterpret_cast<const float*>(base + o_wh);
+  p.bias = reinterpret_cast<const double*>(base + o_bias);
+  p.bh = c.bh;
+  p.nt = m.ntypes;
+  p.n_int = c.n_int;
+  p.H = c.H;
+  p.act = c.act;
+  p.resnet = c.resnet;
+  p.rcut = (float)m.rcut;
+  p.inv_rcut = (float)(1.0 / m.rcut);
+  p.eps2 = (float)(c.eps * c.eps);
+  p.floor = (float)c.floor;
+  p.stride = (float)c.stride;
+  p.inv_stride = (float)(1.0 / c.stride);
+}
+
 }  // namespace
 
 extern "C" {
@@ -825,7 +951,10 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
       if (!f) throw ApiError{DP_ERR_MODEL, std::string("cannot open model file ") + path};
       buf.assign(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
     }
-    const std::string perr = parse_model(buf.data(), buf.size(), M->host);
+    const bool c4 = buf.size() >= 8 && std::memcmp(buf.data(), "DPAMDC4N", 8) == 0;
+    M->kind = c4 ? dp_model::kDpa4c : dp_model::kSeA;
+    const std::string perr = c4 ? parse_c4_model(buf.data(), buf.size(), M->host, M->c4)
+                                : parse_model(buf.data(), buf.size(), M->host);
     if (!perr.empty()) throw ApiError{DP_ERR_MODEL, perr};
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
@@ -839,6 +968,12 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
       throw ApiError{DP_ERR_NO_GPU, std::string("device is ") + prop.gcnArchName +
                                         ", this library is built for gfx950"};
+    if (c4) {
+      // DPA4C nets are fp32 by definition (fp64 energies, forces and virials)
+      M->precision = DP_PREC_MIXED;
+      upload_c4(M);
+      return;
+    }
     const ModelHost& m = M->host;
     const bool mixed = precision == DP_PREC_MIXED;
     M->el = make_emb_layout(m.emb[0], m.emb[1], m.emb[2], mixed);
@@ -885,7 +1020,8 @@ void dp_destroy(dp_model* M) {
   (void)hipSetDevice(M->device);
   for (Buf* b : M->bufs)
     if (b->p) (void)hipFree(b->p);
-  for (void* p : {M->d_emb, static_cast<void*>(M->d_envp), static_cast<void*>(M->d_tpad), M->d_fit})
+  for (void* p : {M->d_emb, static_cast<void*>(M->d_envp), static_cast<void*>(M->d_tpad), M->d_fit,
+                  M->d_c4})
     if (p) (void)hipFree(p);
   if (M->async_pending) (void)hipStreamSynchronize(M->async_stream);
   for (auto& set : M->ev)
@@ -924,6 +1060,14 @@ int dp_get_info(const dp_model* M, dp_model_info* info) {
   }
   info->axis = m.axis;
   info->precision = M->precision;
+  info->model_kind = M->kind == dp_model::kDpa4c ? DP_MODEL_DPA4C : DP_MODEL_SE_E2_A;
+  if (M->kind == dp_model::kDpa4c) {
+    // channel widths C0, C1, C2 and the hidden width of the fitting net
+    info->emb[0] = 8;
+    info->emb[1] = 4;
+    info->emb[2] = 4;
+    info->fit[0] = M->c4.H;
+  }
   return DP_OK;
 }
 
@@ -1052,12 +1196,7 @@ int dp_compute_nlist(dp_model* M, int nall, int nghost, const double* coord, con
       M->cand_nloc = nloc;
     }
     record(M, st, kStGeom + 1);
-    NlParams np{};
-    np.ntypes = m.ntypes;
-    np.nnei = m.nnei;
-    for (int t = 0; t < m.ntypes; ++t) np.sel[t] = m.sel[t];
-    for (int t = 0; t <= m.ntypes; ++t) np.sec[t] = m.sec[t];
-    np.rc2 = m.rcut * m.rcut;
+    const NlParams np = nl_params(M);
     int* nlist = need<int>(M, M->nlist, (size_t)std::max(nloc, 1) * m.nnei);
     int* nreal = need<int>(M, M->nreal, (size_t)std::max(nloc, 1) * m.ntypes);
     launch_nlist_csr(st, nloc, np, ext, ext_type, static_cast<const long*>(M->cand_off.p),
@@ -1083,6 +1222,58 @@ int dp_compute_nlist(dp_model* M, int nall, int nghost, const double* coord, con
       DPAMD_HIP(hipMemcpy(atom_energy, ae, sizeof(double) * nall, hipMemcpyDeviceToHost));
     if (atom_virial && nall)
       DPAMD_HIP(hipMemcpy(atom_virial, av, sizeof(double) * 9 * nall, hipMemcpyDeviceToHost));
+  });
+}
+
+int dp_compute_canonical_graph_device(dp_model* M, double* d_atom_energy, double* d_force,
+                                      double* d_atom_virial, const int64_t* d_atype,
+                                      const uint32_t* d_source, const float* d_edge_vec,
+                                      const int64_t* d_destination_row_ptr,
+                                      const int64_t* d_source_row_ptr,
+                                      const uint32_t* d_source_order, int nloc, int nall_nodes,
+                                      int64_t edge_storage, void* stream) {
+  return guarded(M, [&]() {
+    if (M->kind != dp_model::kDpa4c)
+      throw ApiError{DP_ERR_MODEL, "compute_canonical_graph_gpu requires a DPA4C model"};
+    if (nloc < 0 || nall_nodes <= 0 || nloc > nall_nodes || edge_storage < 2 ||
+        (uint64_t)edge_storage > 0xffffffffull)
+      throw ApiError{DP_ERR_ARG, "invalid compact canonical graph dimensions."};
+    if (!d_atype || !d_source || !d_edge_vec || !d_destination_row_ptr || !d_source_row_ptr ||
+        !d_source_order || !d_force || !d_atom_virial || (nloc > 0 && !d_atom_energy))
+      throw ApiError{DP_ERR_ARG, "null device pointer"};
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    begin(M, st);
+    int* status = static_cast<int*>(M->status.p);
+    C4Graph g{};
+    g.row_ptr = reinterpret_cast<const long*>(d_destination_row_ptr);
+    g.source = d_source;
+    g.edge_vec = d_edge_vec;
+    g.atype = reinterpret_cast<const long*>(d_atype);
+    g.nall = nall_nodes;
+    g.storage = edge_storage;
+    g.status = status;
+    float* mom = need<float>(M, M->c4_mom, (size_t)std::max(nloc, 1) * kC4Mom);
+    float* cot = need<float>(M, M->c4_cot, (size_t)std::max(nloc, 1) * kC4Mom);
+    double* eg = need<double>(M, M->edge_grad, (size_t)edge_storage * 3);
+    record(M, st, kStNlist + 1);
+    launch_c4_moments(st, M->c4p, g, nloc, mom, status);
+    record(M, st, kStEmbFwd + 1);
+    record(M, st, kStDescr + 1);
+    launch_c4_node(st, M->c4p, nloc, g.atype, mom, d_atom_energy, cot);
+    record(M, st, kStFit + 1);
+    record(M, st, kStDT + 1);
+    launch_c4_edge_grad(st, M->c4p, g, nloc, cot, eg);
+    launch_c4_zero_tail(st, g.row_ptr, nloc, edge_storage, eg);
+    record(M, st, kStEmbBwd + 1);
+    launch_c4_graph_force(st, nall_nodes, g.row_ptr, reinterpret_cast<const long*>(d_source_row_ptr),
+                          d_source_order, d_edge_vec, eg, edge_storage, d_force, d_atom_virial,
+                          status);
+    record(M, st, kStForce + 1);
+    record(M, st, kStReduce + 1);
+    M->last_nloc = nloc;
+    M->last_nall = nall_nodes;
+    M->last_standalone = false;
+    finish(M, st);
   });
 }
 
@@ -1137,6 +1328,8 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
         copy(M->mapping.p, (size_t)nall * 4);
         break;
       case DP_STAGE_DESCRPT:
+        if (M->kind == dp_model::kDpa4c)
+          throw ApiError{DP_ERR_ARG, "the DPA4C path keeps its descriptor in registers"};
         if (M->host.axis == 16 && M->nbucket > 0) {
           // not stored by the evaluation: form D from the saved Tsec
           void* Dp = need<char>(M, M->D, (size_t)M->nbucket * Dn * net_esize);
@@ -1144,8 +1337,17 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
         }
         copy_bucket(M->D.p, Dn, net_esize);
         break;
-      case DP_STAGE_DEDD: copy_bucket(M->dD.p, Dn, net_esize); break;
-      case DP_STAGE_ATOM_ENERGY: copy_bucket(M->e_bucket.p, 1, 8); break;
+      case DP_STAGE_DEDD:
+        if (M->kind == dp_model::kDpa4c)
+          throw ApiError{DP_ERR_ARG, "the DPA4C path keeps dE/dD in registers"};
+        copy_bucket(M->dD.p, Dn, net_esize);
+        break;
+      case DP_STAGE_ATOM_ENERGY:
+        if (M->kind == dp_model::kDpa4c) copy(M->e_bucket.p, (size_t)nloc * 8);
+        else copy_bucket(M->e_bucket.p, 1, 8);
+        break;
+      case DP_STAGE_C4_MOMENTS: copy(M->c4_mom.p, (size_t)nloc * kC4Mom * 4); break;
+      case DP_STAGE_C4_COTANGENTS: copy(M->c4_cot.p, (size_t)nloc * kC4Mom * 4); break;
       case DP_STAGE_EDGE_GRAD: copy(M->edge_grad.p, (size_t)nloc * m.nnei * 24); break;
       default: throw ApiError{DP_ERR_ARG, "unknown stage"};
     }

@@ -89,6 +89,8 @@ __device__ __forceinline__ float shfl_xor_d(float v, int mask) {
 enum StatusBit : int {
   kStatusNeighbourOverflow = 1,  // > kMaxCand candidates within rcut of a centre
   kStatusReverseOverflow = 2,    // > kMaxRev edges pointing at one atom
+  kStatusBadInput = 4,           // atom type or source index outside the model / graph
+  kStatusSelOverflow = 8,        // more neighbours of one type than a strict sel holds
 };
 
 }  // namespace dpamd

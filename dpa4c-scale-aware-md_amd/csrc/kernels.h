@@ -29,6 +29,7 @@ struct NlParams {
   int sel[kMaxTypes];
   int sec[kMaxTypes + 1];
   double rc2;
+  int sel_strict;  // a section holding more than sel[t] atoms raises kStatusSelOverflow
 };
 
 struct CellAtom {
@@ -192,5 +193,62 @@ void launch_reduce_ev(hipStream_t, int nbucket, int nloc, const double* atom_ene
                       const double* cpart, double* partials, double* out10);
 void launch_scatter_energy(hipStream_t, int nloc, const int* items, const double* e_bucket,
                            double* atom_energy);
+
+// DPA4C-Nano (dpa4c.hip). Per node the moments / cotangents are 44 floats:
+// scalar [8], vector [3][4], tensor [5][4], the two envelope masses, 2 pad.
+constexpr int kC4Mom = 44;
+constexpr int kC4Out = 70;   // descriptor width
+constexpr int kC4W0Ld = 72;  // row stride of the transposed first fitting layer
+struct C4Params {
+  const float* table;  // [n_int][6][8]: coefficient k of channel c at [i][k][c]
+  const float* film;   // [nt*nt][8][2] PairFiLM (scale, shift)
+  const float* ro;     // readout: Ma[4][4], Mt[4][4], Pv[4][4], Pt[4][2]
+  const float* temb;   // [nt][8] type embedding
+  const float* mean;   // [70]
+  const float* istd;   // [70]
+  const float* w0t;    // [H][kC4W0Ld] first fitting layer, transposed
+  const float* b0;     // [H]
+  const float* wh;     // [H] head
+  const double* bias;  // [nt] bias_atom_e
+  float bh;            // head bias
+  int nt, n_int, H, act, resnet;
+  float rcut, inv_rcut, eps2, floor, stride, inv_stride;
+};
+// edges of a node from the sel-sorted list (standalone and LAMMPS paths)
+struct C4Nlist {
+  const int* nlist;  // [nloc][nnei]
+  const int* nreal;  // [nloc][nt]
+  const double* ext;
+  const int* ext_type;
+  int nnei;
+  int sec[kMaxTypes + 1];
+};
+// edges of a node from a destination CSR of fp32 vectors (canonical graph)
+struct C4Graph {
+  const long* row_ptr;     // [nall + 1]
+  const unsigned* source;  // [edges]
+  const float* edge_vec;   // [edges][3] = x_src - x_dst
+  const long* atype;       // [nall]
+  long nall;
+  long storage;            // edge slots; positions at or beyond are rejected
+  int* status;
+};
+void launch_c4_moments(hipStream_t, const C4Params&, const C4Nlist&, int nnodes, float* mom,
+                       int* status);
+void launch_c4_moments(hipStream_t, const C4Params&, const C4Graph&, int nnodes, float* mom,
+                       int* status);
+void launch_c4_node(hipStream_t, const C4Params&, int nnodes, const int* type, const float* mom,
+                    double* energy, float* cot);
+void launch_c4_node(hipStream_t, const C4Params&, int nnodes, const long* type, const float* mom,
+                    double* energy, float* cot);
+// edge gradients dE/dd: [nloc][nnei][3] at the list's slots, or [edges][3]
+void launch_c4_edge_grad(hipStream_t, const C4Params&, const C4Nlist&, int nnodes,
+                         const float* cot, double* eg);
+void launch_c4_edge_grad(hipStream_t, const C4Params&, const C4Graph&, int nnodes,
+                         const float* cot, double* eg);
+void launch_c4_zero_tail(hipStream_t, const long* drow, int nloc, long storage, double* eg);
+void launch_c4_graph_force(hipStream_t, int nall, const long* drow, const long* srow,
+                           const unsigned* sorder, const float* edge_vec, const double* eg,
+                           long storage, double* force, double* atom_virial, int* status);
 
 }  // namespace dpamd

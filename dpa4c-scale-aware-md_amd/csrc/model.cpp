@@ -25,6 +25,15 @@ struct Reader {
     off += sizeof(T);
     return v;
   }
+  void floats(std::vector<float>& out, size_t count) {
+    out.resize(count);
+    if (off + count * 4 > n) {
+      ok = false;
+      return;
+    }
+    std::memcpy(out.data(), p + off, count * 4);
+    off += count * 4;
+  }
   void doubles(std::vector<double>& out, size_t count) {
     out.resize(count);
     if (off + count * 8 > n) {
@@ -192,6 +201,75 @@ void pack_embedding(const ModelHost& m, const EmbLayout& e, std::vector<double>&
     for (int q = 0; q < 4; ++q)
       for (int f = 0; f < L3; ++f) tpad[((size_t)p * 4 + q) * L3 + f] = Rpad[q] * G[f];
   }
+}
+
+std::string parse_c4_model(const unsigned char* buf, size_t len, ModelHost& m, C4Host& c) {
+  if (len < 8 || std::memcmp(buf, "DPAMDC4N", 8) != 0) return "not a DPAMDC4N DPA4C model file";
+  Reader r{buf, len, 8};
+  const uint32_t ver = r.get<uint32_t>();
+  if (ver != 1) return "unsupported model file version " + std::to_string(ver);
+  const uint32_t nt = r.get<uint32_t>();
+  if (nt < 1 || nt > (uint32_t)kMaxTypes) return "ntypes must be in [1, 8]";
+  m = ModelHost{};
+  m.ntypes = (int)nt;
+  for (int t = 0; t < m.ntypes; ++t) {
+    m.sel[t] = (int)r.get<uint32_t>();
+    m.sec[t] = m.nnei;
+    m.nnei += m.sel[t];
+  }
+  m.sec[m.ntypes] = m.nnei;
+  m.rcut = r.get<double>();
+  c.eps = r.get<double>();
+  c.floor = r.get<double>();
+  c.stride = r.get<double>();
+  c.n_int = (int)r.get<uint32_t>();
+  const uint32_t channels = r.get<uint32_t>(), lmax = r.get<uint32_t>();
+  const uint32_t nl = r.get<uint32_t>();
+  if (!r.ok) return "model file truncated in header";
+  if (channels != 8 || lmax != 2)
+    return "only the DPA4C Nano profile (8 channels, lmax 2) is compiled";
+  if (nl != 1) return "only a fitting net with one hidden layer (DPA4C Nano) is compiled";
+  c.H = (int)r.get<uint32_t>();
+  c.act = (int)r.get<uint32_t>();
+  c.resnet = (int)r.get<uint32_t>();
+  m.type_map.clear();
+  for (int t = 0; t < m.ntypes; ++t) {
+    char name[17] = {0};
+    for (int q = 0; q < 16; ++q) name[q] = (char)r.get<uint8_t>();
+    m.type_map.emplace_back(name);
+  }
+  if (!r.ok) return "model file truncated in header";
+  if (!(m.rcut > 0) || !(m.rcut < 16.0)) return "rcut must be in (0, 16) A";
+  if (!(c.eps >= 0) || !(c.floor >= 0) || !(c.stride > 0)) return "need eps, floor >= 0, stride > 0";
+  if (c.n_int < 1 || c.n_int > (1 << 20)) return "bad table interval count";
+  if ((c.n_int - 1) * c.stride < m.rcut - 1e-9) return "radial table does not cover rcut";
+  if (c.H < 1 || c.H > 1024) return "hidden width must be in [1, 1024]";
+  if (c.act != 0 && c.act != 1) return "activation must be 0 (tanh) or 1 (silu)";
+  for (int t = 0; t < m.ntypes; ++t)
+    if (m.sel[t] <= 0) return "sel entries must be positive";
+  if (m.nnei > 4096) return "sum(sel) must be at most 4096";
+  const int ntt = m.ntypes * m.ntypes;
+  r.floats(c.table, (size_t)c.n_int * 48);
+  r.floats(c.film, (size_t)ntt * 16);
+  r.floats(c.ro, 16 + 16 + 16 + 8);
+  r.floats(c.temb, (size_t)m.ntypes * 8);
+  r.floats(c.mean, kC4Out);
+  r.floats(c.istd, kC4Out);
+  std::vector<float> w0;
+  r.floats(w0, (size_t)kC4Out * c.H);
+  r.floats(c.b0, (size_t)c.H);
+  r.floats(c.wh, (size_t)c.H);
+  std::vector<float> bh;
+  r.floats(bh, 1);
+  r.doubles(c.bias, (size_t)m.ntypes);
+  if (!r.ok) return "model file truncated in parameters";
+  if (r.off != len) return "trailing bytes in model file";
+  c.bh = bh[0];
+  // first layer transposed: row h holds W0[:, h], padded to kC4W0Ld
+  c.w0t.assign((size_t)c.H * kC4W0Ld, 0.f);
+  for (int q = 0; q < kC4Out; ++q)
+    for (int h = 0; h < c.H; ++h) c.w0t[(size_t)h * kC4W0Ld + q] = w0[(size_t)q * c.H + h];
+  return "";
 }
 
 }  // namespace dpamd

@@ -39,4 +39,17 @@ struct FitOffsets {
 };
 FitOffsets fit_offsets(const ModelHost& m);
 
+// Host representation of a DPA4C-Nano model file (layout documented in the
+// package's dpa4c.py). Parsing also fills the neighbour-list fields of a
+// ModelHost (ntypes, sel / sec / nnei, rcut, type_map) so the standalone
+// pipeline builds the edge list the same way for both model kinds.
+struct C4Host {
+  double eps = 0, floor = 0, stride = 0;
+  int n_int = 0, H = 0, act = 0, resnet = 0;
+  std::vector<float> table, film, ro, temb, mean, istd, w0t, b0, wh;
+  float bh = 0.f;
+  std::vector<double> bias;
+};
+std::string parse_c4_model(const unsigned char* buf, size_t len, ModelHost& m, C4Host& c);
+
 }  // namespace dpamd

@@ -279,6 +279,7 @@ __device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s, int* 
     default: nl_rank_place<kMaxCand / kWave>(np, n, s, claim, first, row); break;
   }
   for (int t = 0; t < np.ntypes; ++t) {
+    if (np.sel_strict && cnt[t] > np.sel[t] && lane == 0) atomicOr(status, kStatusSelOverflow);
     const int kept = cnt[t] < np.sel[t] ? cnt[t] : np.sel[t];
     for (int sl = np.sec[t] + kept + lane; sl < np.sec[t + 1]; sl += kWave) row[sl] = -1;
     if (lane == 0) nreal[(long)i * np.ntypes + t] = kept;

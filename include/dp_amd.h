@@ -1,5 +1,6 @@
 /*
- * dp_amd.h — C ABI of the MI355X-native DeePMD se_e2_a evaluator (libdpamd.so).
+ * dp_amd.h — C ABI of the MI355X-native DeePMD evaluator (libdpamd.so): se_e2_a
+ * models and the DPA4C compressed descriptor (Nano profile).
  *
  * This is the drop-in boundary for the per-step energy / force / virial call
  * that `pair_style deepmd` makes through the DeePMD C++ model API. Every entry
@@ -48,6 +49,10 @@ enum {
 
 enum { DP_PREC_FP64 = 0, DP_PREC_MIXED = 1 };
 
+/* Model families: se_e2_a (DPAMDSEA files) and the DPA4C compressed
+ * degree-wise descriptor in its Nano profile (DPAMDC4N files). */
+enum { DP_MODEL_SE_E2_A = 0, DP_MODEL_DPA4C = 1 };
+
 typedef struct dp_model dp_model;
 
 typedef struct {
@@ -61,8 +66,10 @@ typedef struct {
   int fit[3];
   int dim_fparam;   /* always 0 for se_e2_a energy models here */
   int dim_aparam;   /* always 0 */
-  int precision;    /* DP_PREC_* in use */
+  int precision;    /* DP_PREC_* in use (DP_PREC_MIXED for DPA4C: fp32 nets) */
   char type_map[DP_MAX_TYPES][16];
+  int model_kind;   /* DP_MODEL_*; for DPA4C emb = {C0, C1, C2} channel widths,
+                       fit[0] = hidden width, axis = rcut_smth = 0 */
 } dp_model_info;
 
 /* Stage buffers of the last evaluation that dp_debug_copy can read back. */
@@ -74,7 +81,10 @@ enum {
   DP_STAGE_ATOM_ENERGY = 4,/* f64 [nloc] */
   DP_STAGE_EDGE_GRAD = 5,  /* f64 [nloc][nnei][3] dE/d(x_j - x_i) */
   DP_STAGE_DEDD = 6,       /* f64 [nloc][M1*axis] dE/dD (fp32 values in mixed mode) */
-  DP_STAGE_EXT_TYPE = 7    /* int32 [nall] */
+  DP_STAGE_EXT_TYPE = 7,   /* int32 [nall] */
+  DP_STAGE_C4_MOMENTS = 8, /* DPA4C: f32 [nloc][44] raw sums: scalar [8], vector [3][4],
+                              tensor [5][4], sum env^2, sum env^4, 2 pad */
+  DP_STAGE_C4_COTANGENTS = 9 /* DPA4C: f32 [nloc][44] dE/d(raw sums), same layout */
 };
 
 /*
@@ -195,6 +205,32 @@ int dp_graph_stats(const dp_model* model, long* captures, long* replays);
  * otherwise. Stage times then refer to the last of them. No counterpart in the
  * reference, whose errors surface at the next synchronous call. */
 int dp_sync(dp_model* model);
+
+/*
+ * DPA4C evaluation of a compact canonical graph, all pointers device memory:
+ * d_atype [nall_nodes] int64 model types; edges sorted by destination, with
+ * d_destination_row_ptr [nall_nodes + 1] their CSR over destination nodes,
+ * d_source [edge_storage] the source node of each edge and d_edge_vec
+ * [edge_storage][3] fp32 x_source - x_destination; d_source_row_ptr /
+ * d_source_order the CSR of the same edges by source (positions into the edge
+ * arrays). Only local destinations (< nloc) carry model edges; slots past them
+ * are reserved. Writes d_atom_energy [nloc], d_force [nall_nodes][3] =
+ * sum(dst=n) g - sum(src=n) g and d_atom_virial [nall_nodes][9] = -sum(src=n)
+ * g (x) d with g = dE/dd, ghost contributions left in ghost slots; work is
+ * ordered on `stream` and complete when the call returns. Replaces
+ * DeepPot::compute_canonical_graph_gpu (deepmd-op/overlays/api_cc/include/
+ * DeepPot.h:430-442, DeepPotPTExpt.cc:2747-2908, same argument meanings and
+ * the same dimension checks); forces follow
+ * deepmd-op/overlays/op/pt/edge_force_virial.cu:1-14. DP_ERR_MODEL for an
+ * se_e2_a model, DP_ERR_ARG for a type or source outside the model / graph.
+ */
+int dp_compute_canonical_graph_device(dp_model* model, double* d_atom_energy, double* d_force,
+                                      double* d_atom_virial, const int64_t* d_atype,
+                                      const uint32_t* d_source, const float* d_edge_vec,
+                                      const int64_t* d_destination_row_ptr,
+                                      const int64_t* d_source_row_ptr,
+                                      const uint32_t* d_source_order, int nloc, int nall_nodes,
+                                      int64_t edge_storage, void* stream);
 
 /* Copy a stage buffer of the last evaluation (DP_STAGE_*) to host memory.
  * Returns the buffer's size in bytes (copies min(size, capacity) bytes);

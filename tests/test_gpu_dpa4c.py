@@ -1,0 +1,309 @@
+"""GPU parity of the DPA4C-Nano path through the C ABI against the fp64 CPU
+oracle (oracle/dpa4c_oracle.py).
+
+The HIP path computes the descriptor and the fitting net in fp32, as the
+reference does (fp64 energies); the bars are the reference's own
+mixed-precision acceptance limits (data/numeric-tolerances.json:3-9): energy
+per atom 2e-5 eV, force RMSE 4e-5 eV/A, force max-abs 5e-4 eV/A, stress
+max-abs 4e-4 GPa. Edge lists are bit-exact (the same (i, j) sets as the
+oracle's brute-force r^2 < rcut^2 search)."""
+import importlib
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from _pkg import load_dpa4c_oracle
+from cases import lammps_inputs
+
+pytestmark = pytest.mark.gpu
+
+C4 = load_dpa4c_oracle()
+E_TOL = 2e-5        # eV per atom
+F_RMSE = 4e-5       # eV/A
+F_MAX = 5e-4        # eV/A
+S_TOL = 4e-4        # GPa
+EV_A3_TO_GPA = 160.21766208
+
+
+def _systems(dp):
+    return {
+        "cu256": (dp.systems.fcc(4, 3.615, seed=7), "cu"),
+        "hea250": (dp.systems.bcc_hea(5, 3.2, seed=8), "hea"),
+        "water192": (dp.systems.build(0), "water"),
+        "water24_smallbox": (dp.systems.water(2, 6.21, seed=44), "water"),
+    }
+
+
+def _volume(box):
+    return abs(np.linalg.det(np.asarray(box, np.float64).reshape(3, 3)))
+
+
+def _check(ref, got, n, vol, nforce=None):
+    e, f, v, ae, av = got
+    assert abs(e - ref["energy"]) / n <= E_TOL, (e, ref["energy"])
+    assert np.abs(ae - ref["atom_energy"]).max() <= E_TOL
+    df = f - ref["force"]
+    assert np.sqrt((df ** 2).mean()) <= F_RMSE, np.sqrt((df ** 2).mean())
+    assert np.abs(df).max() <= F_MAX, np.abs(df).max()
+    if vol is not None:
+        assert np.abs(v - ref["virial"]).max() / vol * EV_A3_TO_GPA <= S_TOL
+    np.testing.assert_allclose(av.sum(0), v, atol=1e-9 * max(1.0, np.abs(v).max()))
+
+
+def _model(dp, kind, seed):
+    m = dp.dpa4c.random_model(kind, seed=seed)
+    mb = dp.dpa4c.to_bytes(m)
+    return m, mb, C4.Dpa4cOracle(mb)
+
+
+@pytest.mark.parametrize("case", ["cu256", "hea250", "water192", "water24_smallbox"])
+def test_standalone_parity(dp, case):
+    (coord, atype, box), kind = _systems(dp)[case]
+    m, mb, O = _model(dp, kind, 300)
+    ref = O.compute(coord, atype, box)
+    pot = dp.DeepPot(file_content=mb)
+    assert pot.model_kind == dp.MODEL_DPA4C
+    got = pot.compute(coord, atype, box, atomic=True)
+    n = len(atype)
+    _check(ref, got, n, _volume(box))
+    # edge lists: the extended atoms are the oracle's, and every centre's
+    # neighbour set is exactly the strict-cutoff set
+    nall = len(ref["ext_type"])
+    ext = pot.stage(dp.STAGE_EXT_COORD, np.float64, (nall, 3))
+    assert ext.tobytes() == ref["ext_coord"].tobytes()
+    nl = pot.stage(dp.STAGE_NLIST, np.int32, (n, pot.nnei))
+    for i in range(n):
+        row = nl[i][nl[i] >= 0]
+        assert sorted(row.tolist()) == sorted(ref["src"][ref["dst"] == i].tolist()), i
+
+
+@pytest.mark.parametrize("case", ["cu256", "hea250"])
+def test_moments_and_cotangents(dp, case):
+    """Stage parity: the 44 raw sums per atom and their cotangents dE/d(sums)
+    against the oracle (fp32 sums of ~80 edges: relative 2e-5 of the largest
+    entry of each block)."""
+    (coord, atype, box), kind = _systems(dp)[case]
+    m, mb, O = _model(dp, kind, 301)
+    ref = O.compute(coord, atype, box)
+    pot = dp.DeepPot(file_content=mb)
+    pot.compute(coord, atype, box)
+    n = len(atype)
+    mom = pot.stage(dp.STAGE_C4_MOMENTS, np.float32, (n, 44)).astype(np.float64)
+    cot = pot.stage(dp.STAGE_C4_COTANGENTS, np.float32, (n, 44)).astype(np.float64)
+    at = torch.as_tensor(ref["ext_type"], dtype=torch.long)
+    ev = torch.as_tensor(ref["edge_vec"])
+    src = torch.as_tensor(ref["src"], dtype=torch.long)
+    dst = torch.as_tensor(ref["dst"], dtype=torch.long)
+    parts = [p.detach().clone().requires_grad_(True) for p in O.moments(ev, src, dst, at, n)]
+    scal, vec, ten, ms, ma = parts
+    want = np.concatenate([scal.detach().numpy(), vec.detach().numpy().reshape(n, 12),
+                           ten.detach().numpy().reshape(n, 20), ms.detach().numpy()[:, None],
+                           ma.detach().numpy()[:, None]], 1)
+    raw = O.readout(scal, vec, ten, ms, ma, at[:n])
+    D = (raw - O.T["mean"]) * O.T["inv_std"]
+    E = O.fitting(D, at[:n]).sum()
+    grads = torch.autograd.grad(E, parts)
+    gwant = np.concatenate([grads[0].numpy(), grads[1].numpy().reshape(n, 12),
+                            grads[2].numpy().reshape(n, 20), grads[3].numpy()[:, None],
+                            grads[4].numpy()[:, None]], 1)
+    for lo, hi in ((0, 8), (8, 20), (20, 40), (40, 42)):
+        scale = np.abs(want[:, lo:hi]).max()
+        np.testing.assert_allclose(mom[:, lo:hi], want[:, lo:hi], rtol=0, atol=2e-5 * scale)
+        gscale = np.abs(gwant[:, lo:hi]).max()
+        np.testing.assert_allclose(cot[:, lo:hi], gwant[:, lo:hi], rtol=0, atol=2e-4 * gscale)
+    assert np.all(mom[:, 42:] == 0) and np.all(cot[:, 42:] == 0)
+
+
+def test_open_cluster(dp):
+    """box = NULL: a 60-atom alloy cluster; zero net force and torque."""
+    rng = np.random.default_rng(12)
+    x = rng.uniform(-5.0, 5.0, (60, 3))
+    keep = [0]
+    for k in range(1, len(x)):
+        if np.linalg.norm(x[keep] - x[k], axis=1).min() > 1.8:
+            keep.append(k)
+    x = x[keep]
+    atype = np.arange(len(x)) % 4
+    m, mb, O = _model(dp, "hea", 302)
+    ref = O.compute(x, atype, None)
+    pot = dp.DeepPot(file_content=mb)
+    got = pot.compute(x, atype, None, atomic=True)
+    _check(ref, got, len(x), None)
+    f = got[1]
+    assert np.abs(f.sum(0)).max() < 1e-9
+    assert np.abs(np.cross(x, f).sum(0)).max() < 1e-3 * np.abs(f).max() * 10
+
+
+def test_lammps_path(dp, orc):
+    """dp_compute_nlist with a DPA4C model: LAMMPS' full list with skin,
+    shuffled rows, ghosts after the locals; ghost forces stay in ghost slots."""
+    (coord, atype, box), kind = _systems(dp)["hea250"]
+    m, mb, O = _model(dp, kind, 303)
+    shim = types.SimpleNamespace(ghosts=orc.Oracle.ghosts, candidates=orc.Oracle.candidates,
+                                 m={"rcut": m["rcut"]})
+    ext, et, mp, ilist, numneigh, firstneigh = lammps_inputs(shim, coord, atype, box)
+    nloc, nall = len(atype), len(et)
+    # oracle: every (i local, j extended) pair with r^2 < rcut^2
+    dst, src = [], []
+    for i in range(nloc):
+        d = ext - ext[i]
+        r2 = d[:, 0] * d[:, 0] + d[:, 1] * d[:, 1] + d[:, 2] * d[:, 2]
+        js = np.nonzero((r2 < m["rcut"] ** 2) & (np.arange(nall) != i))[0]
+        dst += [i] * len(js)
+        src += js.tolist()
+    src, dst = np.array(src), np.array(dst)
+    ref = O.evaluate_graph(et, src, dst, ext[src] - ext[dst], nloc, nall)
+    pot = dp.DeepPot(file_content=mb)
+    got = pot.compute_nlist(ext, et, box, nall - nloc, ilist, numneigh, firstneigh, ago=0,
+                            atomic=True)
+    e, f, v, ae, av = got
+    _check(ref, (e, f, v, ae[:nloc], av), nloc, _volume(box))
+
+
+def _canonical(ref_ext, ref_et, src, dst, dv, nloc, extra=5):
+    """Compact canonical graph arrays (the reference's layout) of an edge set
+    sorted by destination."""
+    nall = len(ref_et)
+    order = np.lexsort((src, dst))
+    src, dst, dv = src[order], dst[order], dv[order]
+    E = len(src)
+    storage = E + extra
+    drow = np.zeros(nall + 1, np.int64)
+    np.add.at(drow, dst + 1, 1)
+    drow = np.cumsum(drow)
+    sorder = np.argsort(src, kind="stable").astype(np.uint32)
+    srow = np.zeros(nall + 1, np.int64)
+    np.add.at(srow, src + 1, 1)
+    srow = np.cumsum(srow)
+    ev = np.zeros((storage, 3), np.float32)
+    ev[:E] = dv.astype(np.float32)
+    ev[E:] = 1e6  # reserved slots hold garbage: never read as edges
+    source = np.zeros(storage, np.uint32)
+    source[:E] = src
+    sorder_full = np.zeros(storage, np.uint32)
+    sorder_full[:E] = sorder
+    return dict(atype=ref_et.astype(np.int64), source=source, edge_vec=ev, drow=drow, srow=srow,
+                sorder=sorder_full, storage=storage, src=src, dst=dst, nall=nall)
+
+
+def _run_canonical(dp, pot, g, nloc):
+    hip = importlib.import_module("dpamd.hip")
+    nall = g["nall"]
+    bufs = {k: hip.DeviceArray(np.ascontiguousarray(g[k]))
+            for k in ("atype", "source", "edge_vec", "drow", "srow", "sorder")}
+    ae, f, av = (hip.DeviceArray(nbytes=8 * max(nloc, 1)), hip.DeviceArray(nbytes=24 * nall),
+                 hip.DeviceArray(nbytes=72 * nall))
+    pot.compute_canonical_graph_device(ae.ptr, f.ptr, av.ptr, bufs["atype"].ptr,
+                                       bufs["source"].ptr, bufs["edge_vec"].ptr,
+                                       bufs["drow"].ptr, bufs["srow"].ptr, bufs["sorder"].ptr,
+                                       nloc, nall, g["storage"])
+    return (ae.to_host(np.float64, (max(nloc, 1),))[:nloc], f.to_host(np.float64, (nall, 3)),
+            av.to_host(np.float64, (nall, 9)))
+
+
+@pytest.mark.parametrize("case", ["cu256", "water24_smallbox"])
+def test_canonical_graph(dp, case):
+    """dp_compute_canonical_graph_device on the reference's compact canonical
+    graph (fp32 edge vectors, int64 types, uint32 sources, two CSR views)
+    against the oracle's evaluate_graph on the same fp32 vectors; forces and
+    atom virials unfolded over all nodes."""
+    (coord, atype, box), kind = _systems(dp)[case]
+    m, mb, O = _model(dp, kind, 304)
+    base = O.compute(coord, atype, box)
+    nloc = len(atype)
+    g = _canonical(base["ext_coord"], base["ext_type"], base["src"], base["dst"],
+                   base["edge_vec"], nloc)
+    ev64 = g["edge_vec"][:len(g["src"])].astype(np.float64)
+    ref = O.evaluate_graph(g["atype"], g["src"], g["dst"], ev64, nloc, g["nall"])
+    pot = dp.DeepPot(file_content=mb)
+    ae, f, av = _run_canonical(dp, pot, g, nloc)
+    assert np.abs(ae - ref["atom_energy"]).max() <= E_TOL
+    df = f - ref["force"]
+    assert np.sqrt((df ** 2).mean()) <= F_RMSE and np.abs(df).max() <= F_MAX
+    vol = _volume(box)
+    assert np.abs(av.sum(0) - ref["virial"]).max() / vol * EV_A3_TO_GPA <= S_TOL
+    # folding the ghost slots onto their owners gives the standalone result
+    mp = base["mapping"]
+    ff = np.zeros((nloc, 3))
+    np.add.at(ff, mp, f)
+    dff = ff - base["force"]
+    assert np.abs(dff).max() <= F_MAX
+    # a second call with the same arrays is bit-identical (deterministic)
+    ae2, f2, av2 = _run_canonical(dp, pot, g, nloc)
+    assert np.array_equal(f2, f) and np.array_equal(av2, av) and np.array_equal(ae2, ae)
+
+
+def test_canonical_graph_errors(dp):
+    """The reference's dimension check, a model of the wrong family, and an
+    out-of-range type (flagged by the kernels, which skip it and stay in
+    bounds) are reported as errors."""
+    (coord, atype, box), kind = _systems(dp)["cu256"]
+    m, mb, O = _model(dp, kind, 305)
+    base = O.compute(coord, atype, box)
+    nloc = len(atype)
+    g = _canonical(base["ext_coord"], base["ext_type"], base["src"], base["dst"],
+                   base["edge_vec"], nloc)
+    pot = dp.DeepPot(file_content=mb)
+    bad = dict(g)
+    bad["storage"] = 1
+    with pytest.raises(dp.DeepmdException, match="invalid compact canonical graph dimensions"):
+        _run_canonical(dp, pot, bad, nloc)
+    bad = dict(g)
+    bad["atype"] = g["atype"].copy()
+    bad["atype"][3] = 5
+    with pytest.raises(dp.DeepmdException, match="outside the model"):
+        _run_canonical(dp, pot, bad, nloc)
+    # the handle works normally afterwards
+    ae, f, av = _run_canonical(dp, pot, g, nloc)
+    assert np.isfinite(f).all()
+    sea = dp.DeepPot(file_content=dp.model.to_bytes(dp.model.random_model("cu", seed=1)))
+    with pytest.raises(dp.DeepmdException, match="requires a DPA4C model"):
+        _run_canonical(dp, sea, g, nloc)
+
+
+def test_strict_cutoff_and_sel_overflow(dp):
+    """A dimer at exactly rcut has no edge, one just inside has two; a sel too
+    small for the neighbourhood is an error, never a truncation."""
+    m, mb, O = _model(dp, "cu", 306)
+    pot = dp.DeepPot(file_content=mb)
+    rc = m["rcut"]
+    for dx, nedge in ((rc, 0), (np.nextafter(rc, 0.0), 1)):
+        x = np.array([[0.0, 0.0, 0.0], [dx, 0.0, 0.0]])
+        e, f, v = pot.compute(x, np.array([0, 0]), None)
+        nl = pot.stage(dp.STAGE_NLIST, np.int32, (2, pot.nnei))
+        assert (nl[0] >= 0).sum() == nedge
+        ref = O.compute(x, np.array([0, 0]), None)
+        assert abs(e - ref["energy"]) <= 2 * E_TOL
+    small = dp.dpa4c.random_model("cu", seed=306, sel=[40])
+    pot2 = dp.DeepPot(file_content=dp.dpa4c.to_bytes(small))
+    coord, atype, box = dp.systems.fcc(4, 3.615, seed=7)
+    with pytest.raises(dp.DeepmdException, match="sel holds"):
+        pot2.compute(coord, atype, box)
+
+
+def test_device_path_matches_host_path(dp):
+    """dp_compute_device and its asynchronous form with a DPA4C model give the
+    host path's numbers bit for bit."""
+    hip = importlib.import_module("dpamd.hip")
+    (coord, atype, box), kind = _systems(dp)["hea250"]
+    m, mb, O = _model(dp, kind, 307)
+    pot = dp.DeepPot(file_content=mb)
+    e, f, v, ae, av = pot.compute(coord, atype, box, atomic=True)
+    n = len(atype)
+    dc = hip.DeviceArray(np.ascontiguousarray(coord, np.float64))
+    da = hip.DeviceArray(atype.astype(np.int32))
+    outs = [hip.DeviceArray(nbytes=8), hip.DeviceArray(nbytes=24 * n), hip.DeviceArray(nbytes=72),
+            hip.DeviceArray(nbytes=8 * n), hip.DeviceArray(nbytes=72 * n)]
+    for asynchronous in (False, True):
+        if asynchronous:
+            pot.compute_device_async(dc.ptr, da.ptr, n, box, *[b.ptr for b in outs], ago=0)
+            pot.sync()
+        else:
+            pot.compute_device(dc.ptr, da.ptr, n, box, *[b.ptr for b in outs], ago=0)
+        assert outs[0].to_host(np.float64, (1,))[0] == e
+        assert np.array_equal(outs[1].to_host(np.float64, (n, 3)), f)
+        assert np.array_equal(outs[2].to_host(np.float64, (9,)), v)
+        assert np.array_equal(outs[3].to_host(np.float64, (n,)), ae)
+        assert np.array_equal(outs[4].to_host(np.float64, (n, 9)), av)
