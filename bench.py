@@ -21,7 +21,8 @@ entry point (coordinates in and forces out over PCIe each step). The roofline ob
 kernel, timed with HIP events on the stream it runs on over a second pass of
 the same queued steps (the events stay out of the headline pass);
 the CPU baseline is the repository's fp64 CPU restatement (oracle/) timed on a
-bounded sample of centres.
+bounded sample of centres. The DPA4C-Nano model family is measured the same
+way on Cu-Ni alloys of the reference's CuNi workload sizes (under "dpa4c").
 """
 from __future__ import annotations
 
@@ -161,6 +162,80 @@ def run_config(dp, hip, config, steps, warmup):
                 device_bytes=pot.device_bytes(), mb=mb, coord=coord, atype=atype, box=box)
 
 
+def c4_work(n, n_edges):
+    """Algorithmic HBM bytes of the DPA4C passes for one step: the moment and
+    edge-gradient passes read each edge's list index (4 B) and neighbour
+    coordinates (24 B) and the node's 44-float record (176 B); the edge pass
+    writes the fp64 gradient (24 B); the node pass reads the moments and
+    writes the cotangents and the energy."""
+    return {
+        "embed_fwd": ("byte", 28.0 * n_edges + 176.0 * n),
+        "fitting": ("byte", (176.0 * 2 + 8.0) * n),
+        "embed_bwd": ("byte", 52.0 * n_edges + 176.0 * n),
+        "force": ("byte", 28.0 * n_edges + 24.0 * n),
+        "nlist": ("byte", 4.0 * n_edges + 24.0 * n),
+    }
+
+
+C4_STAGE_NAMES = {"embed_fwd": "moments", "fitting": "node (readout + fitting + VJP)",
+                  "embed_bwd": "edge_grad"}
+
+
+def run_c4(dp, hip, name, steps, warmup):
+    """DPA4C-Nano on a Cu-Ni workload: the same queued device-resident step
+    (ghosts, cells, strict-cutoff list, moments, node pass, edge gradients,
+    force gather, reductions)."""
+    import numpy as np
+    coord, atype, box = dp.systems.build_c4(name)
+    n = len(atype)
+    mb = dp.dpa4c.to_bytes(dp.dpa4c.random_model("cuni", seed=2000))
+    pot = dp.DeepPot(file_content=mb, gpu_rank=0)
+    d_coord = hip.DeviceArray(coord.astype("float64"))
+    d_atype = hip.DeviceArray(atype.astype("int32"))
+    d_e, d_f, d_v = hip.DeviceArray(nbytes=8), hip.DeviceArray(nbytes=24 * n), hip.DeviceArray(nbytes=72)
+
+    def step(ago, queued=True):
+        f = pot.compute_device_async if queued else pot.compute_device
+        f(d_coord.ptr, d_atype.ptr, n, box, d_e.ptr, d_f.ptr, d_v.ptr, ago=ago)
+
+    for w in range(max(warmup, 1)):
+        step(0 if w == 0 else 1, queued=False)
+    nl = pot.stage(dp.STAGE_NLIST, np.int32, (n, pot.nnei))
+    n_edges = int((nl >= 0).sum())
+    pot.sync()
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(1)
+    pot.sync()
+    hip.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    pot.enable_stage_timing(True)
+    for _ in range(steps):
+        step(1)
+    pot.sync()
+    stage_ms = dict(pot.stage_times())
+    pot.enable_stage_timing(False)
+    work = c4_work(n, n_edges)
+    stages = {}
+    for k, t in stage_ms.items():
+        if k in ("descriptor", "dE_dT"):
+            continue  # the DPA4C path has no such stage
+        entry = {"ms": round(t, 4)}
+        if k in C4_STAGE_NAMES:
+            entry["kernel"] = C4_STAGE_NAMES[k]
+        if k in work and t > 0:
+            entry.update(gbs=round(work[k][1] / (t * 1e-3) / 1e9, 1),
+                         frac=round(work[k][1] / (t * 1e-3) / PEAK_HBM, 4))
+        stages[k] = entry
+    return {"workload": f"{name} DPA4C-Nano FCC Cu-Ni {n} atoms, rcut 6, 8 channels, "
+                        f"lmax 2, fitting 70-96-1",
+            "atoms": n, "edges": n_edges, "precision": "f32 nets / f64 energy, force, virial",
+            "us_per_step_atom": round(ms * 1e3 / n, 5), "ms_per_step": round(ms, 4),
+            "ns_per_day": round(1.0 * 1e-6 * 86400.0 / (ms * 1e-3), 4),
+            "device_bytes_peak": pot.device_bytes(), "stages": stages}
+
+
 def cpu_baseline(mb, coord, atype, box, target_s=12.0):
     """fp64 CPU restatement (oracle/) on a bounded sample of centres: ghosts for
     the whole box, then neighbour list + full evaluation of the first K centres."""
@@ -196,6 +271,8 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3, 4])
     ap.add_argument("--secondary", default="1,3,4",
                     help="comma-separated configs reported alongside (-1: none)")
+    ap.add_argument("--dpa4c", default="cuni32k,cuni500k",
+                    help="comma-separated DPA4C workloads reported alongside ('' : none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only copy this many bytes device-to-device twice (HBM counter calibration)")
@@ -287,6 +364,9 @@ def main():
             "device_bytes_peak": s["device_bytes"],
             "stages": s["stages"]})
         del s
+    c4 = [w for w in str(args.dpa4c).split(",") if w.strip()]
+    if c4:
+        out["dpa4c"] = [run_c4(dp, hip, w.strip(), args.steps, args.warmup) for w in c4]
     if not args.no_cpu_baseline:
         cb = cpu_baseline(main_r["mb"], main_r["coord"], main_r["atype"], main_r["box"])
         cb["gpu_speedup"] = round(cb["value"] / us_atom, 1)

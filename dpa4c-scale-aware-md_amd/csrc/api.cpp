@@ -519,9 +519,11 @@ void gather_and_reduce(dp_model* M, hipStream_t st, int nloc, int ntarget, const
 }
 
 // DPA4C-Nano on the sel-sorted list: moments, node pass (readout, fitting,
-// readout VJP), edge gradients, then the shared gather and reduction. Stage
-// timers: moments under embed_fwd, the node pass under fitting, the edge
-// gradients under embed_bwd.
+// readout VJP), then on the standalone path one edge pass straight into
+// forces and virials, on the LAMMPS path (ghost slots kept) edge gradients,
+// the shared gather and the reduction. Stage timers: moments under embed_fwd,
+// the node pass under fitting, edge gradients under embed_bwd, the fused
+// edge/force pass under force.
 void run_c4(dp_model* M, hipStream_t st, int nloc, const int* d_mapping, int ntarget,
             const Outputs& out) {
   const ModelHost& m = M->host;
@@ -536,13 +538,34 @@ void run_c4(dp_model* M, hipStream_t st, int nloc, const int* d_mapping, int nta
   float* mom = need<float>(M, M->c4_mom, (size_t)std::max(nloc, 1) * kC4Mom);
   float* cot = need<float>(M, M->c4_cot, (size_t)std::max(nloc, 1) * kC4Mom);
   double* e = need<double>(M, M->e_bucket, (size_t)std::max(nloc, 1));
-  double* eg = need<double>(M, M->edge_grad, (size_t)std::max(nloc, 1) * m.nnei * 3);
   launch_c4_moments(st, M->c4p, src, nloc, mom, status);
   record(M, st, kStEmbFwd + 1);
   record(M, st, kStDescr + 1);
   launch_c4_node(st, M->c4p, nloc, src.ext_type, mom, e, cot);
   record(M, st, kStFit + 1);
   record(M, st, kStDT + 1);
+  if (d_mapping) {
+    // standalone: the list is complete and folded onto owners, so both
+    // directions of each edge are evaluated by its centre (no reverse list)
+    record(M, st, kStEmbBwd + 1);
+    double* cpart = need<double>(M, M->cpart, (size_t)std::max(nloc, 1) * 12);
+    launch_c4_edge_force(st, M->c4p, src, nloc, d_mapping, cot, out.force, out.atom_virial,
+                         cpart);
+    record(M, st, kStForce + 1);
+    double* partials = need<double>(M, M->partials, 256 * 10);
+    double* out10 = need<double>(M, M->out10, 10);
+    launch_reduce_ev(st, nloc, nloc, e, cpart, partials, out10);
+    if (out.energy) DPAMD_HIP(hipMemcpyAsync(out.energy, out10, 8, hipMemcpyDeviceToDevice, st));
+    if (out.virial)
+      DPAMD_HIP(hipMemcpyAsync(out.virial, out10 + 1, 72, hipMemcpyDeviceToDevice, st));
+    if (out.atom_energy && nloc > 0)
+      DPAMD_HIP(hipMemcpyAsync(out.atom_energy, e, sizeof(double) * nloc,
+                               hipMemcpyDeviceToDevice, st));
+    record(M, st, kStReduce + 1);
+    (void)ntarget;
+    return;
+  }
+  double* eg = need<double>(M, M->edge_grad, (size_t)std::max(nloc, 1) * m.nnei * 3);
   launch_c4_edge_grad(st, M->c4p, src, nloc, cot, eg);
   record(M, st, kStEmbBwd + 1);
   gather_and_reduce(M, st, nloc, ntarget, d_mapping, e, nloc, nullptr, out);

@@ -20,9 +20,12 @@
 //                   to cotangents of the 42 raw sums.
 //   k_c4_edge_grad  G lanes per node recompute each edge and contract it with
 //                   the node's cotangents into dE/dd.
-// Forces then come from the shared gather (force.hip) on the sel-sorted list,
-// or from k_c4_graph_force over the caller's two CSR views on the canonical
-// graph path (deepmd-op/overlays/op/pt/edge_force_virial.cu:67-180 form:
+//   k_c4_edge_force on the standalone path (complete list folded onto
+//                   owners) both directions of every edge at once, straight
+//                   into forces and virials.
+// Forces otherwise come from the shared gather (force.hip) on the LAMMPS
+// path, or from k_c4_graph_force over the caller's two CSR views on the
+// canonical graph path (deepmd-op/overlays/op/pt/edge_force_virial.cu:67-180 form:
 // force[n] = sum(dst=n) g - sum(src=n) g, atom_virial[src] -= g (x) d).
 #include "fastmath.h"
 #include "kernels.h"
@@ -50,7 +53,7 @@ struct Geo {
 };
 
 __device__ __forceinline__ void geometry(const C4Params& p, const float d[3], Geo& g) {
-  const float sq = d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + p.eps2;
+  const float sq = fmaf(d[2], d[2], fmaf(d[1], d[1], fmaf(d[0], d[0], p.eps2)));
   g.ir = rsqrtf(sq);
   g.r = sq * g.ir;
 #pragma unroll
@@ -145,6 +148,11 @@ struct NlSrc {
   // returns false for an edge this pass must skip
   __device__ bool edge(const C4Params& p, const Node& nd, int k, float d[3], int& tj,
                        long& out) const {
+    int j;
+    return edge(p, nd, k, d, tj, out, j);
+  }
+  __device__ bool edge(const C4Params&, const Node& nd, int k, float d[3], int& tj, long& out,
+                       int& j) const {
     int kk = k, base = 0;
     bool found = false;
 #pragma unroll
@@ -159,7 +167,7 @@ struct NlSrc {
       }
     }
     out = nd.row + base + kk;
-    const int j = a.nlist[out];
+    j = a.nlist[out];
     tj = a.ext_type[j];
 #pragma unroll
     for (int c = 0; c < 3; ++c) d[c] = (float)(a.ext[3 * (long)j + c] - nd.x[c]);
@@ -683,6 +691,58 @@ __global__ __launch_bounds__(kBlock) void k_c4_node(C4Params p, int nnodes,
 }
 
 // ---- pass 3: edge gradients -------------------------------------------------
+// dE/dd of one edge seen from a centre with cotangents c: PairFiLM (fa, fb)
+// of (centre type, neighbour type), direction u from the centre, y = Y2(u),
+// the radial values / slopes and d env / dr of the edge's length. Every
+// operation is an explicit fmaf or product and contraction is off, so two
+// inlined copies produce the same bits for the same inputs: the reverse
+// direction of an edge evaluated by its other end then equals the forward
+// evaluation exactly (negating u commutes with every operation below), which
+// keeps sum F = 0 to fp64 rounding on the fused standalone path.
+__device__ __forceinline__ void contract(const float c[kC4Mom], const float fa[8],
+                                         const float fb[8], const Geo& g, const float u[3],
+                                         const float y[5], const float rad[8],
+                                         const float drad[8], float denv_dr, float out[3]) {
+#pragma clang fp contract(off)
+  const float env = g.env;
+  float denv = 0.f, dr = 0.f, du[3] = {0.f, 0.f, 0.f}, hy[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int cc = 0; cc < 8; ++cc) {
+    const float film = fmaf(fa[cc], rad[cc], fb[cc]);
+    const float amp = film * env;
+    float damp = c[kS + cc];
+    if (cc < 4) {
+      const float ang = amp * env;
+      float q = 0.f;
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        q = fmaf(c[kV + 4 * a + cc], u[a], q);
+        du[a] = fmaf(ang, c[kV + 4 * a + cc], du[a]);
+      }
+#pragma unroll
+      for (int m = 0; m < 5; ++m) {
+        q = fmaf(c[kT + 4 * m + cc], y[m], q);
+        hy[m] = fmaf(ang, c[kT + 4 * m + cc], hy[m]);
+      }
+      damp = fmaf(env, q, damp);
+      denv = fmaf(amp, q, denv);
+    }
+    denv = fmaf(damp, film, denv);
+    dr = fmaf((damp * env) * fa[cc], drad[cc], dr);
+  }
+  denv = fmaf(2.f * env, c[kMs], denv);
+  denv = fmaf(((4.f * env) * env) * env, c[kMa], denv);
+  dr = fmaf(denv, denv_dr, dr);
+  // harmonics: dY/du (graph_compress.cuh:702-713)
+  du[0] = fmaf(kSq3, fmaf(hy[4], u[0], fmaf(hy[3], u[2], hy[0] * u[1])), du[0]);
+  du[1] = fmaf(kSq3, fmaf(-hy[4], u[1], fmaf(hy[1], u[2], hy[0] * u[0])), du[1]);
+  du[2] = fmaf(3.f * hy[2], u[2], fmaf(kSq3, fmaf(hy[3], u[0], hy[1] * u[1]), du[2]));
+  const float dot = fmaf(u[2], du[2], fmaf(u[1], du[1], u[0] * du[0]));
+  // u = d / r with r = sqrt(|d|^2 + eps^2): du/dd = (I - u u^T) / r, dr/dd = u
+#pragma unroll
+  for (int a = 0; a < 3; ++a) out[a] = fmaf(fmaf(-u[a], dot, du[a]), g.ir, dr * u[a]);
+}
+
 template <class Src>
 __global__ __launch_bounds__(kBlock) void k_c4_edge_grad(C4Params p, Src src, int nnodes,
                                                         const float* __restrict__ cot,
@@ -715,44 +775,100 @@ __global__ __launch_bounds__(kBlock) void k_c4_edge_grad(C4Params p, Src src, in
     radial(p, g, rad, drad);
     film_of(p, ti * p.nt + tj, fa, fb);
     harm2(g.u, y);
-    const float env = g.env;
-    float denv = 0.f, dr = 0.f, du[3] = {0.f, 0.f, 0.f}, hy[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    float gr[3];
+    contract(c, fa, fb, g, g.u, y, rad, drad, env_deriv(p, g.r), gr);
 #pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
-      const float film = fmaf(fa[cc], rad[cc], fb[cc]);
-      const float amp = film * env;
-      float damp = c[kS + cc];
-      if (cc < 4) {
-        const float ang = amp * env;
-        float q = 0.f;
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-          q = fmaf(c[kV + 4 * a + cc], g.u[a], q);
-          du[a] = fmaf(ang, c[kV + 4 * a + cc], du[a]);
-        }
-#pragma unroll
-        for (int m = 0; m < 5; ++m) {
-          q = fmaf(c[kT + 4 * m + cc], y[m], q);
-          hy[m] = fmaf(ang, c[kT + 4 * m + cc], hy[m]);
-        }
-        damp = fmaf(env, q, damp);
-        denv = fmaf(amp, q, denv);
-      }
-      denv = fmaf(damp, film, denv);
-      dr = fmaf(damp * env * fa[cc], drad[cc], dr);
-    }
-    denv = fmaf(2.f * env, c[kMs], denv);
-    denv = fmaf(4.f * env * env * env, c[kMa], denv);
-    dr = fmaf(denv, env_deriv(p, g.r), dr);
-    // harmonics: dY/du (graph_compress.cuh:702-713)
-    du[0] += kSq3 * (hy[0] * g.u[1] + hy[3] * g.u[2] + hy[4] * g.u[0]);
-    du[1] += kSq3 * (hy[0] * g.u[0] + hy[1] * g.u[2] - hy[4] * g.u[1]);
-    du[2] += kSq3 * (hy[1] * g.u[1] + hy[3] * g.u[0]) + 3.f * hy[2] * g.u[2];
-    const float dot = g.u[0] * du[0] + g.u[1] * du[1] + g.u[2] * du[2];
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-      eg[3 * slot + a] = (double)fmaf(du[a] - g.u[a] * dot, g.ir, dr * g.u[a]);
+    for (int a = 0; a < 3; ++a) eg[3 * slot + a] = (double)gr[a];
   }
+}
+
+// Both directions of every edge in one pass, for a complete (never
+// truncated) list folded onto owners: the edge t -> j (owner i) has the
+// reverse i -> image of t with vector -d, whose gradient is i's cotangents
+// contracted with the same geometry (the degree-two harmonics are even in u,
+// the radial and envelope terms depend on r only) under the swapped pair
+// (tj, ti). So, per centre t and with no reverse list, atomics or scatter:
+//   force[t]       = sum_e g(t->j) - g(i->t)
+//   atom_virial[t] = -sum over edges into t of g (x) d_in = sum_e g(i->t) (x) d
+//   cpart[t]       = (sum_e g(t->j), -sum_e g(t->j) (x) d), the centre-side
+//                    force and frame-virial partials the reduction sums.
+// Sums run in a fixed order (lane stride, then a butterfly): deterministic.
+__global__ __launch_bounds__(kBlock) void k_c4_edge_force(
+    C4Params p, NlSrc src, int nnodes, const int* __restrict__ mapping,
+    const float* __restrict__ cot, double* __restrict__ force, double* __restrict__ atom_virial,
+    double* __restrict__ cpart) {
+  const int lane = threadIdx.x & (kG - 1);
+  const int node = (int)(((long)blockIdx.x * kBlock + threadIdx.x) / kG);
+  double f[3] = {0.0, 0.0, 0.0}, fo[3] = {0.0, 0.0, 0.0};
+  double vo[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  double av[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+  const int ti = node < nnodes ? src.node_type(node) : -1;
+  if (ti >= 0 && ti < p.nt) {
+    NlSrc::Node nd;
+    src.open(p, node, nd);
+    float c[kC4Mom];
+    load_mom(cot + (long)node * kC4Mom, c);
+    for (int k = lane; k < nd.n; k += kG) {
+      float d[3];
+      int tj, j;
+      long slot;
+      src.edge(p, nd, k, d, tj, slot, j);
+      const int i = mapping[j];
+      Geo g;
+      geometry(p, d, g);
+      float rad[8], drad[8], fa[8], fb[8], y[5];
+      radial(p, g, rad, drad);
+      harm2(g.u, y);
+      const float de = env_deriv(p, g.r);
+      float gf[3], gb[3];
+      film_of(p, ti * p.nt + tj, fa, fb);
+      contract(c, fa, fb, g, g.u, y, rad, drad, de, gf);
+      {
+        float cn[kC4Mom];
+        load_mom(cot + (long)i * kC4Mom, cn);
+        film_of(p, tj * p.nt + ti, fa, fb);
+        const float um[3] = {-g.u[0], -g.u[1], -g.u[2]};
+        contract(cn, fa, fb, g, um, y, rad, drad, de, gb);
+      }
+      double dd[3];
+#pragma unroll
+      for (int a = 0; a < 3; ++a) dd[a] = src.a.ext[3 * (long)j + a] - nd.x[a];
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        fo[a] += (double)gf[a];
+        f[a] += (double)gf[a] - (double)gb[a];
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+          vo[3 * a + b] = fma(-(double)gf[a], dd[b], vo[3 * a + b]);
+          av[3 * a + b] = fma((double)gb[a], dd[b], av[3 * a + b]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < kG; off <<= 1) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      f[a] += __shfl_xor(f[a], off, kWave);
+      fo[a] += __shfl_xor(fo[a], off, kWave);
+    }
+#pragma unroll
+    for (int a = 0; a < 9; ++a) {
+      vo[a] += __shfl_xor(vo[a], off, kWave);
+      av[a] += __shfl_xor(av[a], off, kWave);
+    }
+  }
+  if (node >= nnodes || lane != 0) return;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    force[3 * (long)node + a] = f[a];
+    cpart[12 * (long)node + a] = fo[a];
+  }
+#pragma unroll
+  for (int a = 0; a < 9; ++a) cpart[12 * (long)node + 3 + a] = vo[a];
+  if (atom_virial)
+#pragma unroll
+    for (int a = 0; a < 9; ++a) atom_virial[9 * (long)node + a] = av[a];
 }
 
 // ---- canonical graph force / virial -------------------------------------
@@ -867,6 +983,15 @@ void launch_c4_edge_grad(hipStream_t st, const C4Params& p, const C4Graph& s, in
   if (n <= 0) return;
   hipLaunchKernelGGL(k_c4_edge_grad<GraphSrc>, group_grid(n), dim3(kBlock), 0, st, p,
                      GraphSrc{s}, n, cot, eg);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_c4_edge_force(hipStream_t st, const C4Params& p, const C4Nlist& s, int n,
+                          const int* mapping, const float* cot, double* force,
+                          double* atom_virial, double* cpart) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_c4_edge_force, group_grid(n), dim3(kBlock), 0, st, p, NlSrc{s}, n, mapping,
+                     cot, force, atom_virial, cpart);
   DPAMD_LAUNCH_CHECK();
 }
 

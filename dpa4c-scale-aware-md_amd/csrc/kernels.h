@@ -246,6 +246,11 @@ void launch_c4_edge_grad(hipStream_t, const C4Params&, const C4Nlist&, int nnode
                          const float* cot, double* eg);
 void launch_c4_edge_grad(hipStream_t, const C4Params&, const C4Graph&, int nnodes,
                          const float* cot, double* eg);
+// standalone path: forces, atom virials (folded onto owners) and the
+// centre-side partials cpart [nloc][12] from both directions of every edge
+void launch_c4_edge_force(hipStream_t, const C4Params&, const C4Nlist&, int nnodes,
+                          const int* mapping, const float* cot, double* force,
+                          double* atom_virial, double* cpart);
 void launch_c4_zero_tail(hipStream_t, const long* drow, int nloc, long storage, double* eg);
 void launch_c4_graph_force(hipStream_t, int nall, const long* drow, const long* srow,
                            const unsigned* sorder, const float* edge_vec, const double* eg,

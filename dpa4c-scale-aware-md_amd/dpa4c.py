@@ -76,6 +76,7 @@ KINDS = {
     "cu": dict(type_map=["Cu"], sel=[128]),
     "water": dict(type_map=["O", "H"], sel=[64, 128]),
     "hea": dict(type_map=["Co", "Cr", "Fe", "Ni"], sel=[48, 48, 48, 48]),
+    "cuni": dict(type_map=["Cu", "Ni"], sel=[80, 80]),
 }
 
 

@@ -110,6 +110,39 @@ def bcc_hea(n_cells: int, a: float, seed: int, ntypes: int = 4, sigma: float = 0
     return coord, atype, cubic_box(n_cells * a)
 
 
+def fcc_alloy(cells, a: float, seed: int, ntypes: int = 2, sigma: float = 0.05):
+    """FCC supercell of cells = (nx, ny, nz) conventional cells (orthorhombic
+    box), species at exactly 1/ntypes each by a seeded permutation, plus
+    N(0, sigma^2) displacements."""
+    basis = np.array([[0, 0, 0], [0.5, 0.5, 0], [0.5, 0, 0.5], [0, 0.5, 0.5]])
+    nx, ny, nz = cells
+    grid = np.stack(np.meshgrid(np.arange(nx, dtype=np.float64), np.arange(ny, dtype=np.float64),
+                                np.arange(nz, dtype=np.float64), indexing="ij"), axis=-1)
+    coord = ((grid.reshape(-1, 1, 3) + basis[None]) * a).reshape(-1, 3)
+    n = len(coord)
+    coord = coord + sigma * Stream(seed, 1).normal(coord.size).reshape(-1, 3)
+    atype = np.repeat(np.arange(ntypes, dtype=np.int32), n // ntypes)
+    atype = np.concatenate([atype, np.arange(n - len(atype), dtype=np.int32)])
+    atype = atype[Stream(seed, 2).permutation(n)].astype(np.int32)
+    box = np.array([nx * a, 0, 0, 0, ny * a, 0, 0, 0, nz * a], dtype=np.float64)
+    return coord, atype, box
+
+
+# DPA4C workloads: Cu-Ni FCC alloys with the atom counts of the reference's
+# CuNi-small / -medium / -large runs (data/workload.csv:2-4: 2,016, 31,920 and
+# 499,800 atoms = 4 x 8x7x9, 4 x 20x21x19 and 4 x 50x49x51 cells), a = 3.56 A
+C4_WORKLOADS = {
+    "cuni2k": dict(cells=(8, 7, 9), kind="cuni"),
+    "cuni32k": dict(cells=(20, 21, 19), kind="cuni"),
+    "cuni500k": dict(cells=(50, 49, 51), kind="cuni"),
+}
+
+
+def build_c4(name: str, seed: int = 5):
+    w = C4_WORKLOADS[name]
+    return fcc_alloy(w["cells"], 3.56, seed=seed)
+
+
 # (system builder, model kind) per benchmark configuration
 CONFIGS = {
     0: dict(name="water192", kind="water", build=lambda: water(4, 12.42, seed=0)),

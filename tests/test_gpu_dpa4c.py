@@ -49,7 +49,12 @@ def _check(ref, got, n, vol, nforce=None):
     assert np.abs(df).max() <= F_MAX, np.abs(df).max()
     if vol is not None:
         assert np.abs(v - ref["virial"]).max() / vol * EV_A3_TO_GPA <= S_TOL
-    np.testing.assert_allclose(av.sum(0), v, atol=1e-9 * max(1.0, np.abs(v).max()))
+    # the atom virials sum to the virial to fp32 rounding (the standalone
+    # path forms them from the two directions of each edge separately)
+    np.testing.assert_allclose(av.sum(0), v, atol=1e-6 * max(1.0, np.abs(v).max()))
+    if "atom_virial" in ref:
+        scale = max(1.0, np.abs(ref["atom_virial"]).max())
+        assert np.abs(av - ref["atom_virial"]).max() <= 1e-5 * scale * 50
 
 
 def _model(dp, kind, seed):
