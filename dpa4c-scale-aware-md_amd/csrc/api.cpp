@@ -949,6 +949,7 @@ void upload_c4(dp_model* M) {
   p.floor = (float)c.floor;
   p.stride = (float)c.stride;
   p.inv_stride = (float)(1.0 / c.stride);
+  p.ncu = M->ncu;
 }
 
 }  // namespace

@@ -27,6 +27,8 @@
 // path, or from k_c4_graph_force over the caller's two CSR views on the
 // canonical graph path (deepmd-op/overlays/op/pt/edge_force_virial.cu:67-180 form:
 // force[n] = sum(dst=n) g - sum(src=n) g, atom_virial[src] -= g (x) d).
+#include <algorithm>
+
 #include "fastmath.h"
 #include "kernels.h"
 
@@ -34,7 +36,9 @@ namespace dpamd {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kG = 16;  // lanes per node in the edge passes
+constexpr int kEdgeBlock = 512;  // persistent edge passes: 32 nodes per block sweep
+constexpr int kG = 16;           // lanes per node in the edge passes
+constexpr int kLdsTableMax = 64 * 1024;
 constexpr float kSq2 = 1.41421356237309505f;
 constexpr float kSq3 = 1.73205080756887729f;
 constexpr float kInvSq2 = 0.70710678118654752f;
@@ -90,9 +94,8 @@ __device__ __forceinline__ void harm2(const float u[3], float y[5]) {
 }
 
 // radial_c(x) for the 8 channels from the interval's [6][8] coefficients
-__device__ __forceinline__ void radial(const C4Params& p, const Geo& g, float rad[8],
-                                       float* drad) {
-  const f4* row = reinterpret_cast<const f4*>(p.table + (long)g.idx * 48);
+__device__ __forceinline__ void radial(const f4* tab, const Geo& g, float rad[8], float* drad) {
+  const f4* row = tab + g.idx * 12;
   f4 c[12];
 #pragma unroll
   for (int q = 0; q < 12; ++q) c[q] = row[q];
@@ -110,8 +113,8 @@ __device__ __forceinline__ void radial(const C4Params& p, const Geo& g, float ra
     }
 }
 
-__device__ __forceinline__ void film_of(const C4Params& p, int pair, float a[8], float b[8]) {
-  const f4* fr = reinterpret_cast<const f4*>(p.film + (long)pair * 16);
+__device__ __forceinline__ void film_of(const f4* flm, int pair, float a[8], float b[8]) {
+  const f4* fr = flm + pair * 4;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const f4 v = fr[q];
@@ -119,6 +122,28 @@ __device__ __forceinline__ void film_of(const C4Params& p, int pair, float a[8],
     b[2 * q] = v[1];
     a[2 * q + 1] = v[2];
     b[2 * q + 1] = v[3];
+  }
+}
+
+// The radial table and the PairFiLM rows every edge reads: staged once per
+// block into LDS when they fit (each lane reads a random 192-byte table row,
+// which from L2 would cost more than the edge's arithmetic), else read from
+// global memory.
+template <bool Lds>
+__device__ __forceinline__ void stage_tables(const C4Params& p, const f4*& tab, const f4*& flm) {
+  if constexpr (Lds) {
+    extern __shared__ f4 c4_lds[];
+    const int n1 = p.n_int * 12, n2 = p.nt * p.nt * 4;
+    const f4* gt = reinterpret_cast<const f4*>(p.table);
+    const f4* gf = reinterpret_cast<const f4*>(p.film);
+    for (int q = threadIdx.x; q < n1; q += blockDim.x) c4_lds[q] = gt[q];
+    for (int q = threadIdx.x; q < n2; q += blockDim.x) c4_lds[n1 + q] = gf[q];
+    __syncthreads();
+    tab = c4_lds;
+    flm = c4_lds + n1;
+  } else {
+    tab = reinterpret_cast<const f4*>(p.table);
+    flm = reinterpret_cast<const f4*>(p.film);
   }
 }
 
@@ -215,11 +240,17 @@ struct GraphSrc {
 };
 
 // ---- pass 1: moments --------------------------------------------------------
-template <class Src>
-__global__ __launch_bounds__(kBlock) void k_c4_moments(C4Params p, Src src, int nnodes,
-                                                      float* __restrict__ mom, int* status) {
+// Persistent blocks (grid of a few blocks per CU, the tables staged once):
+// block b serves nodes b*gpb + g, then strides by the grid.
+template <class Src, bool Lds>
+__global__ __launch_bounds__(kEdgeBlock) void k_c4_moments(C4Params p, Src src, int nnodes,
+                                                          float* __restrict__ mom, int* status) {
+  const f4 *tab, *flm;
+  stage_tables<Lds>(p, tab, flm);
   const int lane = threadIdx.x & (kG - 1);
-  const int node = (int)(((long)blockIdx.x * kBlock + threadIdx.x) / kG);
+  constexpr int gpb = kEdgeBlock / kG;
+  for (int base = blockIdx.x * gpb; base < nnodes; base += gridDim.x * gpb) {
+  const int node = base + (int)threadIdx.x / kG;
   float S[8], V[3][4], T[5][4], ms = 0.f, ma = 0.f;
 #pragma unroll
   for (int c = 0; c < 8; ++c) S[c] = 0.f;
@@ -246,8 +277,8 @@ __global__ __launch_bounds__(kBlock) void k_c4_moments(C4Params p, Src src, int 
       Geo g;
       geometry(p, d, g);
       float rad[8], fa[8], fb[8], y[5];
-      radial(p, g, rad, nullptr);
-      film_of(p, ti * p.nt + tj, fa, fb);
+      radial(tab, g, rad, nullptr);
+      film_of(flm, ti * p.nt + tj, fa, fb);
       harm2(g.u, y);
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
@@ -283,15 +314,17 @@ __global__ __launch_bounds__(kBlock) void k_c4_moments(C4Params p, Src src, int 
     ms += __shfl_xor(ms, off, kWave);
     ma += __shfl_xor(ma, off, kWave);
   }
-  if (node >= nnodes || lane != 0) return;
-  f4* o = reinterpret_cast<f4*>(mom + (long)node * kC4Mom);
-  o[0] = f4{S[0], S[1], S[2], S[3]};
-  o[1] = f4{S[4], S[5], S[6], S[7]};
+  if (node < nnodes && lane == 0) {
+    f4* o = reinterpret_cast<f4*>(mom + (long)node * kC4Mom);
+    o[0] = f4{S[0], S[1], S[2], S[3]};
+    o[1] = f4{S[4], S[5], S[6], S[7]};
 #pragma unroll
-  for (int k = 0; k < 3; ++k) o[2 + k] = f4{V[k][0], V[k][1], V[k][2], V[k][3]};
+    for (int k = 0; k < 3; ++k) o[2 + k] = f4{V[k][0], V[k][1], V[k][2], V[k][3]};
 #pragma unroll
-  for (int m = 0; m < 5; ++m) o[5 + m] = f4{T[m][0], T[m][1], T[m][2], T[m][3]};
-  o[10] = f4{ms, ma, 0.f, 0.f};
+    for (int m = 0; m < 5; ++m) o[5 + m] = f4{T[m][0], T[m][1], T[m][2], T[m][3]};
+    o[10] = f4{ms, ma, 0.f, 0.f};
+  }
+  }
 }
 
 // ---- pass 2: readout, fitting, readout VJP (one thread per node) ---------
@@ -743,18 +776,22 @@ __device__ __forceinline__ void contract(const float c[kC4Mom], const float fa[8
   for (int a = 0; a < 3; ++a) out[a] = fmaf(fmaf(-u[a], dot, du[a]), g.ir, dr * u[a]);
 }
 
-template <class Src>
-__global__ __launch_bounds__(kBlock) void k_c4_edge_grad(C4Params p, Src src, int nnodes,
-                                                        const float* __restrict__ cot,
-                                                        double* __restrict__ eg) {
+template <class Src, bool Lds>
+__global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_grad(C4Params p, Src src, int nnodes,
+                                                            const float* __restrict__ cot,
+                                                            double* __restrict__ eg) {
+  const f4 *tab, *flm;
+  stage_tables<Lds>(p, tab, flm);
   const int lane = threadIdx.x & (kG - 1);
-  const int node = (int)(((long)blockIdx.x * kBlock + threadIdx.x) / kG);
-  if (node >= nnodes) return;
+  constexpr int gpb = kEdgeBlock / kG;
+  for (int base = blockIdx.x * gpb; base < nnodes; base += gridDim.x * gpb) {
+  const int node = base + (int)threadIdx.x / kG;
+  if (node >= nnodes) continue;
   const int ti = src.node_type(node);
   const bool valid = ti >= 0 && ti < p.nt;
   typename Src::Node nd;
   src.open(p, node, nd);
-  if (nd.n == 0) return;
+  if (nd.n == 0) continue;
   float c[kC4Mom];
   load_mom(cot + (long)node * kC4Mom, c);
   for (int k = lane; k < nd.n; k += kG) {
@@ -772,13 +809,14 @@ __global__ __launch_bounds__(kBlock) void k_c4_edge_grad(C4Params p, Src src, in
     Geo g;
     geometry(p, d, g);
     float rad[8], drad[8], fa[8], fb[8], y[5];
-    radial(p, g, rad, drad);
-    film_of(p, ti * p.nt + tj, fa, fb);
+    radial(tab, g, rad, drad);
+    film_of(flm, ti * p.nt + tj, fa, fb);
     harm2(g.u, y);
     float gr[3];
     contract(c, fa, fb, g, g.u, y, rad, drad, env_deriv(p, g.r), gr);
 #pragma unroll
     for (int a = 0; a < 3; ++a) eg[3 * slot + a] = (double)gr[a];
+  }
   }
 }
 
@@ -793,12 +831,17 @@ __global__ __launch_bounds__(kBlock) void k_c4_edge_grad(C4Params p, Src src, in
 //   cpart[t]       = (sum_e g(t->j), -sum_e g(t->j) (x) d), the centre-side
 //                    force and frame-virial partials the reduction sums.
 // Sums run in a fixed order (lane stride, then a butterfly): deterministic.
-__global__ __launch_bounds__(kBlock) void k_c4_edge_force(
+template <bool Lds>
+__global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_force(
     C4Params p, NlSrc src, int nnodes, const int* __restrict__ mapping,
     const float* __restrict__ cot, double* __restrict__ force, double* __restrict__ atom_virial,
     double* __restrict__ cpart) {
+  const f4 *tab, *flm;
+  stage_tables<Lds>(p, tab, flm);
   const int lane = threadIdx.x & (kG - 1);
-  const int node = (int)(((long)blockIdx.x * kBlock + threadIdx.x) / kG);
+  constexpr int gpb = kEdgeBlock / kG;
+  for (int base = blockIdx.x * gpb; base < nnodes; base += gridDim.x * gpb) {
+  const int node = base + (int)threadIdx.x / kG;
   double f[3] = {0.0, 0.0, 0.0}, fo[3] = {0.0, 0.0, 0.0};
   double vo[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
   double av[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
@@ -817,16 +860,16 @@ __global__ __launch_bounds__(kBlock) void k_c4_edge_force(
       Geo g;
       geometry(p, d, g);
       float rad[8], drad[8], fa[8], fb[8], y[5];
-      radial(p, g, rad, drad);
+      radial(tab, g, rad, drad);
       harm2(g.u, y);
       const float de = env_deriv(p, g.r);
       float gf[3], gb[3];
-      film_of(p, ti * p.nt + tj, fa, fb);
+      film_of(flm, ti * p.nt + tj, fa, fb);
       contract(c, fa, fb, g, g.u, y, rad, drad, de, gf);
       {
         float cn[kC4Mom];
         load_mom(cot + (long)i * kC4Mom, cn);
-        film_of(p, tj * p.nt + ti, fa, fb);
+        film_of(flm, tj * p.nt + ti, fa, fb);
         const float um[3] = {-g.u[0], -g.u[1], -g.u[2]};
         contract(cn, fa, fb, g, um, y, rad, drad, de, gb);
       }
@@ -858,17 +901,19 @@ __global__ __launch_bounds__(kBlock) void k_c4_edge_force(
       av[a] += __shfl_xor(av[a], off, kWave);
     }
   }
-  if (node >= nnodes || lane != 0) return;
+  if (node < nnodes && lane == 0) {
 #pragma unroll
-  for (int a = 0; a < 3; ++a) {
-    force[3 * (long)node + a] = f[a];
-    cpart[12 * (long)node + a] = fo[a];
+    for (int a = 0; a < 3; ++a) {
+      force[3 * (long)node + a] = f[a];
+      cpart[12 * (long)node + a] = fo[a];
+    }
+#pragma unroll
+    for (int a = 0; a < 9; ++a) cpart[12 * (long)node + 3 + a] = vo[a];
+    if (atom_virial)
+#pragma unroll
+      for (int a = 0; a < 9; ++a) atom_virial[9 * (long)node + a] = av[a];
   }
-#pragma unroll
-  for (int a = 0; a < 9; ++a) cpart[12 * (long)node + 3 + a] = vo[a];
-  if (atom_virial)
-#pragma unroll
-    for (int a = 0; a < 9; ++a) atom_virial[9 * (long)node + a] = av[a];
+  }
 }
 
 // ---- canonical graph force / virial -------------------------------------
@@ -936,22 +981,56 @@ __global__ void k_c4_zero_tail(const long* __restrict__ drow, int nloc, long sto
 
 inline dim3 group_grid(long n) { return dim3((unsigned)((n * kG + kBlock - 1) / kBlock)); }
 
+// LDS bytes of the staged tables (0: they do not fit and stay in global memory)
+size_t table_lds_bytes(const C4Params& p) {
+  const size_t b = ((size_t)p.n_int * 12 + (size_t)p.nt * p.nt * 4) * sizeof(f4);
+  return b <= (size_t)kLdsTableMax ? b : 0;
+}
+
+// persistent grid: `per_cu` blocks per compute unit, fewer if the nodes run out
+dim3 edge_grid(const C4Params& p, long n, int per_cu) {
+  const long need = (n + kEdgeBlock / kG - 1) / (kEdgeBlock / kG);
+  return dim3((unsigned)std::max<long>(1, std::min<long>(need, (long)p.ncu * per_cu)));
+}
+
+template <class Src>
+void moments_launch(hipStream_t st, const C4Params& p, const Src& src, int n, float* mom,
+                    int* status) {
+  if (n <= 0) return;
+  const size_t lds = table_lds_bytes(p);
+  if (lds)
+    hipLaunchKernelGGL((k_c4_moments<Src, true>), edge_grid(p, n, 2), dim3(kEdgeBlock), lds, st,
+                       p, src, n, mom, status);
+  else
+    hipLaunchKernelGGL((k_c4_moments<Src, false>), edge_grid(p, n, 2), dim3(kEdgeBlock), 0, st,
+                       p, src, n, mom, status);
+  DPAMD_LAUNCH_CHECK();
+}
+
+template <class Src>
+void edge_grad_launch(hipStream_t st, const C4Params& p, const Src& src, int n, const float* cot,
+                      double* eg) {
+  if (n <= 0) return;
+  const size_t lds = table_lds_bytes(p);
+  if (lds)
+    hipLaunchKernelGGL((k_c4_edge_grad<Src, true>), edge_grid(p, n, 1), dim3(kEdgeBlock), lds, st,
+                       p, src, n, cot, eg);
+  else
+    hipLaunchKernelGGL((k_c4_edge_grad<Src, false>), edge_grid(p, n, 1), dim3(kEdgeBlock), 0, st,
+                       p, src, n, cot, eg);
+  DPAMD_LAUNCH_CHECK();
+}
+
 }  // namespace
 
 void launch_c4_moments(hipStream_t st, const C4Params& p, const C4Nlist& s, int n, float* mom,
                        int* status) {
-  if (n <= 0) return;
-  hipLaunchKernelGGL(k_c4_moments<NlSrc>, group_grid(n), dim3(kBlock), 0, st, p, NlSrc{s}, n, mom,
-                     status);
-  DPAMD_LAUNCH_CHECK();
+  moments_launch(st, p, NlSrc{s}, n, mom, status);
 }
 
 void launch_c4_moments(hipStream_t st, const C4Params& p, const C4Graph& s, int n, float* mom,
                        int* status) {
-  if (n <= 0) return;
-  hipLaunchKernelGGL(k_c4_moments<GraphSrc>, group_grid(n), dim3(kBlock), 0, st, p, GraphSrc{s},
-                     n, mom, status);
-  DPAMD_LAUNCH_CHECK();
+  moments_launch(st, p, GraphSrc{s}, n, mom, status);
 }
 
 void launch_c4_node(hipStream_t st, const C4Params& p, int n, const int* type, const float* mom,
@@ -972,26 +1051,25 @@ void launch_c4_node(hipStream_t st, const C4Params& p, int n, const long* type, 
 
 void launch_c4_edge_grad(hipStream_t st, const C4Params& p, const C4Nlist& s, int n,
                          const float* cot, double* eg) {
-  if (n <= 0) return;
-  hipLaunchKernelGGL(k_c4_edge_grad<NlSrc>, group_grid(n), dim3(kBlock), 0, st, p, NlSrc{s}, n,
-                     cot, eg);
-  DPAMD_LAUNCH_CHECK();
+  edge_grad_launch(st, p, NlSrc{s}, n, cot, eg);
 }
 
 void launch_c4_edge_grad(hipStream_t st, const C4Params& p, const C4Graph& s, int n,
                          const float* cot, double* eg) {
-  if (n <= 0) return;
-  hipLaunchKernelGGL(k_c4_edge_grad<GraphSrc>, group_grid(n), dim3(kBlock), 0, st, p,
-                     GraphSrc{s}, n, cot, eg);
-  DPAMD_LAUNCH_CHECK();
+  edge_grad_launch(st, p, GraphSrc{s}, n, cot, eg);
 }
 
 void launch_c4_edge_force(hipStream_t st, const C4Params& p, const C4Nlist& s, int n,
                           const int* mapping, const float* cot, double* force,
                           double* atom_virial, double* cpart) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_c4_edge_force, group_grid(n), dim3(kBlock), 0, st, p, NlSrc{s}, n, mapping,
-                     cot, force, atom_virial, cpart);
+  const size_t lds = table_lds_bytes(p);
+  if (lds)
+    hipLaunchKernelGGL(k_c4_edge_force<true>, edge_grid(p, n, 1), dim3(kEdgeBlock), lds, st, p,
+                       NlSrc{s}, n, mapping, cot, force, atom_virial, cpart);
+  else
+    hipLaunchKernelGGL(k_c4_edge_force<false>, edge_grid(p, n, 1), dim3(kEdgeBlock), 0, st, p,
+                       NlSrc{s}, n, mapping, cot, force, atom_virial, cpart);
   DPAMD_LAUNCH_CHECK();
 }
 

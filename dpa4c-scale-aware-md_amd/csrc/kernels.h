@@ -213,6 +213,7 @@ struct C4Params {
   float bh;            // head bias
   int nt, n_int, H, act, resnet;
   float rcut, inv_rcut, eps2, floor, stride, inv_stride;
+  int ncu;  // compute units: sizes the persistent edge-pass grids
 };
 // edges of a node from the sel-sorted list (standalone and LAMMPS paths)
 struct C4Nlist {
