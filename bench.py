@@ -273,6 +273,8 @@ def main():
                     help="comma-separated configs reported alongside (-1: none)")
     ap.add_argument("--dpa4c", default="cuni32k,cuni500k",
                     help="comma-separated DPA4C workloads reported alongside ('' : none)")
+    ap.add_argument("--dpa4c-only", action="store_true",
+                    help="measure only the --dpa4c workloads (profiling runs); prints their list")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only copy this many bytes device-to-device twice (HBM counter calibration)")
@@ -296,6 +298,11 @@ def main():
         print(json.dumps({"copy_probe_bytes": args.copy_probe}))
         return
 
+    if args.dpa4c_only:
+        c4 = [w.strip() for w in str(args.dpa4c).split(",") if w.strip()]
+        print(json.dumps({"dpa4c": [run_c4(dp, hip, w, args.steps, args.warmup) for w in c4]}),
+              flush=True)
+        return
     main_r = run_config(dp, hip, args.config, args.steps, args.warmup)
     n = main_r["n"]
     us_atom = main_r["ms"] * 1e3 / n

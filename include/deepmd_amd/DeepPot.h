@@ -17,6 +17,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <stdexcept>
+#include <cstdint>
 #include <string>
 #include <vector>
 
@@ -185,6 +186,27 @@ class DeepPot {
     require_init();
     check(dp_sync(h_));
   }
+
+  // DPA4C models: the compact canonical graph entry, same signature and
+  // argument meaning as DeepPot::compute_canonical_graph_gpu
+  // (deepmd-op/overlays/api_cc/include/DeepPot.h:430-442); dp_compute_canonical_graph_device.
+  void compute_canonical_graph_gpu(double* d_atom_energy, double* d_force, double* d_atom_virial,
+                                   const std::int64_t* d_atype, const std::uint32_t* d_source,
+                                   const float* d_edge_vec,
+                                   const std::int64_t* d_destination_row_ptr,
+                                   const std::int64_t* d_source_row_ptr,
+                                   const std::uint32_t* d_source_order, const int nloc,
+                                   const int nall_nodes, const std::int64_t edge_storage,
+                                   void* stream = nullptr) {
+    require_init();
+    check(dp_compute_canonical_graph_device(h_, d_atom_energy, d_force, d_atom_virial, d_atype,
+                                            d_source, d_edge_vec, d_destination_row_ptr,
+                                            d_source_row_ptr, d_source_order, nloc, nall_nodes,
+                                            edge_storage, stream));
+  }
+  bool uses_canonical_graph_inference() const { return info_.model_kind == DP_MODEL_DPA4C; }
+  bool uses_fp32_edge_vectors() const { return info_.model_kind == DP_MODEL_DPA4C; }
+  bool supports_device_edge_inference() const { return info_.model_kind == DP_MODEL_DPA4C; }
 
   dp_model* handle() const { return h_; }
 

@@ -38,9 +38,12 @@ for one and two edges with identity readout matrices; the C3 envelope's value
 and derivatives at 0 and rcut; C2 continuity of the radial table across
 knots; |Y2(u)| = 1 and STF(Y2(u)) = sqrt(3/2)(uu^T - I/3); rotation,
 translation and permutation invariance of all 70 descriptor entries; F =
--dE/dx and W = -dE/d(strain) by central differences; sum F = 0. The Bis222
-normalisation constant kappa is the reference's value
-(graph_compress.cuh:34-38) and is pinned only by that citation.
+-dE/dx and W = -dE/d(strain) by central differences; sum F = 0; the
+magnitudes of the Bis112 and Bis222 couplings (1/sqrt5, sqrt(12/35)) as the
+unit-Frobenius normalisations of the Cartesian Gaunt tensors in the packed
+STF basis. Their signs are the reference's convention
+(graph_compress.cuh:34-38, graph_compress_kernel.cuh:581-584) and are pinned
+only by that citation: parity unpinned for the two signs.
 """
 from __future__ import annotations
 

@@ -215,3 +215,20 @@ def test_strict_cutoff(dp):
         x = np.array([[0.0, 0.0, 0.0], [dx, 0.0, 0.0]])
         out = O.compute(x, np.array([0, 0]), None)
         assert len(out["src"]) == n_edges
+
+
+def test_gaunt_normalisations():
+    """The coupling constants are the unit-Frobenius normalisations of the
+    Cartesian Gaunt tensors in the packed STF basis (graph_compress.cuh:34-38):
+    with S_a = STF(e_a), sum_a |S_a|_F^2 = 5, so the 112 coupling is 1/sqrt5 in
+    magnitude, and sum_abc tr(S_a S_b S_c)^2 = 35/12, so the 222 coupling is
+    sqrt(12/35) in magnitude. (Their signs are the reference's convention.)"""
+    E = torch.eye(5, dtype=torch.float64)
+    S = C4.stf(E)                                  # [5, 3, 3]
+    np.testing.assert_allclose((S * S).sum(), 5.0, rtol=1e-15)
+    t3 = torch.einsum("aij,bjk,cki->abc", S, S, S)
+    np.testing.assert_allclose((t3 * t3).sum(), 35.0 / 12.0, rtol=1e-14)
+    assert abs(abs(C4.KAPPA_222) - math.sqrt(12.0 / 35.0)) < 1e-15
+    # the packed basis is orthonormal under the Frobenius product
+    gram = torch.einsum("aij,bij->ab", S, S)
+    np.testing.assert_allclose(gram, torch.eye(5, dtype=torch.float64), atol=1e-15)
