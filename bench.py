@@ -236,6 +236,27 @@ def run_c4(dp, hip, name, steps, warmup):
             "device_bytes_peak": pot.device_bytes(), "stages": stages}
 
 
+def cpu_baseline_c4(name):
+    """The DPA4C oracle (torch fp64 on the host cores, autograd gradients) on
+    the whole `name` workload, one evaluation: ghosts, strict-cutoff edges,
+    descriptor, fitting, forces."""
+    import torch
+    sys.path.insert(0, ROOT)
+    from _pkg import load_pkg
+    from oracle import dpa4c_oracle
+    dp = load_pkg()
+    coord, atype, box = dp.systems.build_c4(name)
+    O = dpa4c_oracle.Dpa4cOracle(dp.dpa4c.to_bytes(dp.dpa4c.random_model("cuni", seed=2000)))
+    t0 = time.perf_counter()
+    O.compute(coord, atype, box)
+    t = time.perf_counter() - t0
+    n = len(atype)
+    return {"value": round(t * 1e6 / n, 3), "unit": "us/step/atom",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"DPA4C oracle (torch fp64, CPU) on all {n} atoms of {name}, one "
+                      f"evaluation ({t:.1f} s)"}
+
+
 def cpu_baseline(mb, coord, atype, box, target_s=12.0):
     """fp64 CPU restatement (oracle/) on a bounded sample of centres: ghosts for
     the whole box, then neighbour list + full evaluation of the first K centres."""
@@ -374,6 +395,11 @@ def main():
     c4 = [w for w in str(args.dpa4c).split(",") if w.strip()]
     if c4:
         out["dpa4c"] = [run_c4(dp, hip, w.strip(), args.steps, args.warmup) for w in c4]
+        if not args.no_cpu_baseline:
+            first = out["dpa4c"][0]
+            cb = cpu_baseline_c4(c4[0].strip())
+            cb["gpu_speedup"] = round(cb["value"] / first["us_per_step_atom"], 1)
+            first["cpu_baseline"] = cb
     if not args.no_cpu_baseline:
         cb = cpu_baseline(main_r["mb"], main_r["coord"], main_r["atype"], main_r["box"])
         cb["gpu_speedup"] = round(cb["value"] / us_atom, 1)
