@@ -94,8 +94,12 @@ __device__ __forceinline__ void harm2(const float u[3], float y[5]) {
 }
 
 // radial_c(x) for the 8 channels from the interval's [6][8] coefficients
-__device__ __forceinline__ void radial(const f4* tab, const Geo& g, float rad[8], float* drad) {
-  const f4* row = tab + g.idx * 12;
+// Rows of `stride` float4 (12 in global memory; 13 in LDS, where a 12-float4
+// stride puts every row on one of only 4 bank groups and the lanes' random
+// rows collide, while 13 is coprime to the 16 float4 bank slots).
+__device__ __forceinline__ void radial(const f4* tab, int stride, const Geo& g, float rad[8],
+                                       float* drad) {
+  const f4* row = tab + g.idx * stride;
   f4 c[12];
 #pragma unroll
   for (int q = 0; q < 12; ++q) c[q] = row[q];
@@ -129,6 +133,13 @@ __device__ __forceinline__ void film_of(const f4* flm, int pair, float a[8], flo
 // block into LDS when they fit (each lane reads a random 192-byte table row,
 // which from L2 would cost more than the edge's arithmetic), else read from
 // global memory.
+constexpr int kLdsRow = 13;  // float4 per table row in LDS
+
+template <bool Lds>
+__device__ __forceinline__ int table_stride() {
+  return Lds ? kLdsRow : 12;
+}
+
 template <bool Lds>
 __device__ __forceinline__ void stage_tables(const C4Params& p, const f4*& tab, const f4*& flm) {
   if constexpr (Lds) {
@@ -136,11 +147,12 @@ __device__ __forceinline__ void stage_tables(const C4Params& p, const f4*& tab, 
     const int n1 = p.n_int * 12, n2 = p.nt * p.nt * 4;
     const f4* gt = reinterpret_cast<const f4*>(p.table);
     const f4* gf = reinterpret_cast<const f4*>(p.film);
-    for (int q = threadIdx.x; q < n1; q += blockDim.x) c4_lds[q] = gt[q];
-    for (int q = threadIdx.x; q < n2; q += blockDim.x) c4_lds[n1 + q] = gf[q];
+    for (int q = threadIdx.x; q < n1; q += blockDim.x) c4_lds[(q / 12) * kLdsRow + q % 12] = gt[q];
+    const int t1 = p.n_int * kLdsRow;
+    for (int q = threadIdx.x; q < n2; q += blockDim.x) c4_lds[t1 + q] = gf[q];
     __syncthreads();
     tab = c4_lds;
-    flm = c4_lds + n1;
+    flm = c4_lds + t1;
   } else {
     tab = reinterpret_cast<const f4*>(p.table);
     flm = reinterpret_cast<const f4*>(p.film);
@@ -277,7 +289,7 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_moments(C4Params p, Src src, 
       Geo g;
       geometry(p, d, g);
       float rad[8], fa[8], fb[8], y[5];
-      radial(tab, g, rad, nullptr);
+      radial(tab, table_stride<Lds>(), g, rad, nullptr);
       film_of(flm, ti * p.nt + tj, fa, fb);
       harm2(g.u, y);
 #pragma unroll
@@ -809,7 +821,7 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_grad(C4Params p, Src src
     Geo g;
     geometry(p, d, g);
     float rad[8], drad[8], fa[8], fb[8], y[5];
-    radial(tab, g, rad, drad);
+    radial(tab, table_stride<Lds>(), g, rad, drad);
     film_of(flm, ti * p.nt + tj, fa, fb);
     harm2(g.u, y);
     float gr[3];
@@ -860,7 +872,7 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_force(
       Geo g;
       geometry(p, d, g);
       float rad[8], drad[8], fa[8], fb[8], y[5];
-      radial(tab, g, rad, drad);
+      radial(tab, table_stride<Lds>(), g, rad, drad);
       harm2(g.u, y);
       const float de = env_deriv(p, g.r);
       float gf[3], gb[3];
@@ -983,7 +995,7 @@ inline dim3 group_grid(long n) { return dim3((unsigned)((n * kG + kBlock - 1) / 
 
 // LDS bytes of the staged tables (0: they do not fit and stay in global memory)
 size_t table_lds_bytes(const C4Params& p) {
-  const size_t b = ((size_t)p.n_int * 12 + (size_t)p.nt * p.nt * 4) * sizeof(f4);
+  const size_t b = ((size_t)p.n_int * kLdsRow + (size_t)p.nt * p.nt * 4) * sizeof(f4);
   return b <= (size_t)kLdsTableMax ? b : 0;
 }
 
