@@ -596,6 +596,16 @@ NlParams nl_params(const dp_model* M) {
   return np;
 }
 
+// DPA4C sums over a centre's edges in list order, which need not be by
+// distance, only reproducible: the standalone list keeps candidate order over
+// cell-ordered atoms (no rank pass). The LAMMPS list, whose candidate order is
+// the caller's, stays sorted.
+NlParams nl_params_cells(const dp_model* M) {
+  NlParams np = nl_params(M);
+  np.unsorted = M->kind == dp_model::kDpa4c ? 1 : 0;
+  return np;
+}
+
 // Ghosts + cells + nlist for the standalone path, with no host round trip:
 // the extended arrays are sized for every ghost candidate (nshift images of
 // each local atom, the most the box can produce), the number of ghosts is
@@ -641,8 +651,9 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
     exclusive_scan_int(st, ccount, cstart, ncell + 1, tmp, tb);
   }
   launch_cell_scatter(st, nall, nall_d, cell_of, crank, cstart, ext, ext_type, sorted);
+  const NlParams np = nl_params_cells(M);
+  if (np.unsorted) launch_cell_order(st, ncell, cstart, sorted);
   record(M, st, kStGeom + 1);
-  const NlParams np = nl_params(M);
   int* nlist = need<int>(M, M->nlist, (size_t)std::max(nloc, 1) * m.nnei);
   int* nreal = need<int>(M, M->nreal, (size_t)std::max(nloc, 1) * m.ntypes);
   launch_nlist_cells(st, nloc, bp, np, ext, ext_type, cell_of, cstart, sorted, nlist, nreal,

@@ -30,6 +30,7 @@ struct NlParams {
   int sec[kMaxTypes + 1];
   double rc2;
   int sel_strict;  // a section holding more than sel[t] atoms raises kStatusSelOverflow
+  int unsorted;    // place candidates in candidate order instead of (type, r2, j) order
 };
 
 struct CellAtom {
@@ -103,6 +104,8 @@ void launch_cell_assign(hipStream_t, int cap, const int* d_count, const BoxParam
 void launch_cell_scatter(hipStream_t, int cap, const int* d_count, const int* cell_of,
                          const int* cell_rank, const int* cell_start, const double* ext,
                          const int* ext_type, CellAtom* sorted);
+// atoms of each cell in ascending index order (reproducible candidate order)
+void launch_cell_order(hipStream_t, int ncell, const int* cell_start, CellAtom* sorted);
 // nall = nloc + number of flagged ghost candidates, from the flags and their
 // exclusive scan, into device memory
 void launch_ghost_total(hipStream_t, int nloc, long nf, const int* flags, const int* pos,

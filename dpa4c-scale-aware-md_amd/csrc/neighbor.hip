@@ -141,6 +141,40 @@ __global__ void k_cell_scatter(int cap, const int* __restrict__ d_count,
   sorted[p] = a;
 }
 
+// Atoms of a cell in ascending index order (the scatter's order comes from
+// atomic ranks): one wave per cell reads the cell's records into registers,
+// ranks them by index and writes them back, so candidate order -- and with it
+// an unsorted neighbour list -- is reproducible. Cells of more than
+// kCellSortMax atoms keep the scatter's order (every access stays in bounds).
+constexpr int kCellSortK = 8;
+constexpr int kCellSortMax = 64 * kCellSortK;
+__global__ __launch_bounds__(256) void k_cell_order(int ncell, const int* __restrict__ cell_start,
+                                                   CellAtom* __restrict__ sorted) {
+  const int lane = threadIdx.x & 63;
+  const int c = (int)(((long)blockIdx.x * 256 + threadIdx.x) >> 6);
+  if (c >= ncell) return;
+  const int beg = cell_start[c], cnt = cell_start[c + 1] - beg;
+  if (cnt <= 1 || cnt > kCellSortMax) return;
+  CellAtom a[kCellSortK];
+  int rank[kCellSortK];
+#pragma unroll
+  for (int k = 0; k < kCellSortK; ++k) {
+    rank[k] = 0;
+    a[k].idx = 0x7fffffff;
+    if (lane + 64 * k < cnt) a[k] = sorted[beg + lane + 64 * k];
+  }
+  for (int m = 0; m < cnt; ++m) {
+    const int om = sorted[beg + m].idx;
+#pragma unroll
+    for (int k = 0; k < kCellSortK; ++k) rank[k] += om < a[k].idx ? 1 : 0;
+  }
+  // the wave's loads above all complete before its stores below (the stores
+  // write the loaded records at addresses computed from loaded indices)
+#pragma unroll
+  for (int k = 0; k < kCellSortK; ++k)
+    if (lane + 64 * k < cnt) sorted[beg + rank[k]] = a[k];
+}
+
 // ---------------------------------------------------------------------------
 // sel formatting shared by the cell and the CSR front ends. One wave per
 // centre; candidates within rcut are compacted into LDS, ranked by
@@ -268,6 +302,25 @@ __device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s, int* 
     first[t] = acc;
     acc += cnt[t];
   }
+  if (np.unsorted) {
+    // candidate order (reproducible with cell-ordered atoms), each type's
+    // candidates compacted into its section
+    int put[kMaxTypes];
+#pragma unroll
+    for (int t = 0; t < kMaxTypes; ++t) put[t] = 0;
+    for (int base = 0; base < n; base += kWave) {
+      const int q = base + lane;
+      const int tq = q < n ? s[q].t : -1;
+      const int jq = q < n ? s[q].j : -1;
+#pragma unroll
+      for (int t = 0; t < kMaxTypes; ++t) {
+        const unsigned long long m = __ballot(tq == t);
+        const int pos = put[t] + __popcll(m & ((1ull << lane) - 1ull));
+        if (tq == t && pos < np.sel[t]) row[np.sec[t] + pos] = jq;
+        put[t] += __popcll(m);
+      }
+    }
+  } else {
   // rank of each candidate in (key, j) order: one pass over the list ranks
   // every candidate this lane holds (q = lane + 64k, k < K)
   switch ((n + kWave - 1) / kWave) {
@@ -277,6 +330,7 @@ __device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s, int* 
     case 3: nl_rank_place<3>(np, n, s, claim, first, row); break;
     case 4: nl_rank_place<4>(np, n, s, claim, first, row); break;
     default: nl_rank_place<kMaxCand / kWave>(np, n, s, claim, first, row); break;
+  }
   }
   for (int t = 0; t < np.ntypes; ++t) {
     if (np.sel_strict && cnt[t] > np.sel[t] && lane == 0) atomicOr(status, kStatusSelOverflow);
@@ -450,6 +504,13 @@ void launch_cell_scatter(hipStream_t st, int cap, const int* d_count, const int*
   if (cap <= 0) return;
   hipLaunchKernelGGL(k_cell_scatter, dim3((cap + 255) / 256), dim3(256), 0, st, cap, d_count,
                      cell_of, cell_rank, cell_start, ext, ext_type, sorted);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_cell_order(hipStream_t st, int ncell, const int* cell_start, CellAtom* sorted) {
+  if (ncell <= 0) return;
+  hipLaunchKernelGGL(k_cell_order, dim3((unsigned)(((long)ncell * 64 + 255) / 256)), dim3(256), 0,
+                     st, ncell, cell_start, sorted);
   DPAMD_LAUNCH_CHECK();
 }
 

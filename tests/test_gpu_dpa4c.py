@@ -82,6 +82,13 @@ def test_standalone_parity(dp, case):
     for i in range(n):
         row = nl[i][nl[i] >= 0]
         assert sorted(row.tolist()) == sorted(ref["src"][ref["dst"] == i].tolist()), i
+    # the list keeps candidate order over cell-ordered atoms, not distance
+    # order: a fresh handle reproduces the list and every output bit for bit
+    pot2 = dp.DeepPot(file_content=mb)
+    got2 = pot2.compute(coord, atype, box, atomic=True)
+    assert np.array_equal(pot2.stage(dp.STAGE_NLIST, np.int32, (n, pot.nnei)), nl)
+    for a, b in zip(got, got2):
+        assert np.array_equal(np.asarray(a), np.asarray(b))
 
 
 @pytest.mark.parametrize("case", ["cu256", "hea250"])
