@@ -245,8 +245,11 @@ class Dpa4cOracle:
         s = torch.as_tensor(np.asarray(src), dtype=torch.long)
         d = torch.as_tensor(np.asarray(dst), dtype=torch.long)
         ev = torch.as_tensor(np.asarray(edge_vec, np.float64)).clone().requires_grad_(True)
-        D = self.descriptor(ev, s, d, at, nloc)
-        e = self.fitting(D, at[:nloc])
+        # virtual atoms (type < 0) carry no energy; callers give them no edges
+        real = at[:nloc] >= 0
+        atc = torch.clamp(at, min=0)
+        D = self.descriptor(ev, s, d, atc, nloc)
+        e = torch.where(real, self.fitting(D, atc[:nloc]), torch.zeros((), dtype=torch.float64))
         E = e.sum()
         g = torch.autograd.grad(E, ev)[0] if len(s) else torch.zeros((0, 3), dtype=torch.float64)
         g = g.numpy()

@@ -148,6 +148,22 @@ def test_open_cluster(dp):
     assert np.abs(np.cross(x, f).sum(0)).max() < 1e-3 * np.abs(f).max() * 10
 
 
+def test_virtual_atoms(dp):
+    """Atoms of type -1 are absent: no energy, no force, never a neighbour
+    (the oracle gives them no edges and zero energy)."""
+    (coord, atype, box), kind = _systems(dp)["hea250"]
+    atype = atype.copy()
+    atype[[3, 77, 150]] = -1
+    m, mb, O = _model(dp, kind, 308)
+    ref = O.compute(coord, atype, box)
+    assert not np.isin(ref["src"], np.nonzero(atype < 0)[0]).any()
+    pot = dp.DeepPot(file_content=mb)
+    got = pot.compute(coord, atype, box, atomic=True)
+    _check(ref, got, len(atype), _volume(box))
+    e, f, v, ae, av = got
+    assert np.all(ae[atype < 0] == 0.0) and np.all(f[atype < 0] == 0.0)
+
+
 def test_lammps_path(dp, orc):
     """dp_compute_nlist with a DPA4C model: LAMMPS' full list with skin,
     shuffled rows, ghosts after the locals; ghost forces stay in ghost slots."""
