@@ -152,7 +152,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
       for (int t = 0; t < S::NT2; ++t) acc2[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
-        const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::L2P + c;
+        const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::W2LD + c;
 #pragma unroll
         for (int t = 0; t < S::NT2; ++t) acc2[t] = mfma_f32(W2[16 * t], x1[q], acc2[t]);
       }
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
 #pragma unroll
         for (int q = 0; q < NQ3F; ++q) {
           const float av = x2[q >> 2][q & 3];
-          const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::L3P + 16 * u0 + c;
+          const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::W3LD + 16 * u0 + c;
 #pragma unroll
           for (int uu = 0; uu < kU3F; ++uu)
             if (u0 + uu < S::NU3) acc3[uu] = mfma_f32(av, W3[16 * uu], acc3[uu]);
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       for (int t = 0; t < S::NT2; ++t) acc2t[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
-        const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::L2P + c;
+        const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::W2LD + c;
 #pragma unroll
         for (int t = 0; t < S::NT2; ++t) acc2t[t] = mfma_f32(W2[16 * t], x1t[q], acc2t[t]);
       }
@@ -443,7 +443,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 #pragma unroll
         for (int q = 0; q < NQ3F; ++q) {
           const float bv = x2t[q >> 2][q & 3];
-          const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::L3P + 16 * u0 + c;
+          const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::W3LD + 16 * u0 + c;
 #pragma unroll
           for (int uu = 0; uu < kU3B; ++uu)
             if (u0 + uu < S::NU3) acc3t[uu] = mfma_f32(W3[16 * uu], bv, acc3t[uu]);

@@ -185,10 +185,10 @@ void pack_embedding(const ModelHost& m, const EmbLayout& e, std::vector<double>&
       Q[e.off_b1 + f] = b1[f];
     }
     for (int k = 0; k < L1; ++k)
-      for (int n = 0; n < L2; ++n) Q[e.off_w2 + k * e.L2P + n] = W2[(long)k * L2 + n];
+      for (int n = 0; n < L2; ++n) Q[e.off_w2 + k * e.W2LD + n] = W2[(long)k * L2 + n];
     for (int n = 0; n < L2; ++n) Q[e.off_b2 + n] = b2[n];
     for (int k = 0; k < L2; ++k)
-      for (int n = 0; n < L3; ++n) Q[e.off_w3 + k * e.L3P + n] = W3[(long)k * L3 + n];
+      for (int n = 0; n < L3; ++n) Q[e.off_w3 + k * e.W3LD + n] = W3[(long)k * L3 + n];
     for (int n = 0; n < L3; ++n) Q[e.off_b3 + n] = b3[n];
     for (int q = 0; q < 4; ++q) {
       envp[(size_t)p * 8 + q] = m.davg[(size_t)p * 4 + q];
