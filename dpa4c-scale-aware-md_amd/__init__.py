@@ -32,7 +32,8 @@ MODEL_SE_E2_A, MODEL_DPA4C = 0, 1
 
 EXPORTED = ("dp_create", "dp_destroy", "dp_get_info", "dp_last_error", "dp_compute",
             "dp_compute_nlist", "dp_compute_device", "dp_compute_device_async", "dp_sync",
-            "dp_graph_stats", "dp_compute_canonical_graph_device",
+            "dp_graph_stats", "dp_compute_canonical_graph_device", "dp_compute_edges_device",
+            "dp_compute_edges_device_f32",
             "dp_debug_copy", "dp_stage_times", "dp_device_bytes")
 
 
@@ -70,6 +71,8 @@ def lib():
         L.dp_graph_stats.argtypes = [P, C.POINTER(C.c_long), C.POINTER(C.c_long)]
         L.dp_compute_canonical_graph_device.argtypes = [P, P, P, P, P, P, P, P, P, P, I, I,
                                                         C.c_int64, P]
+        L.dp_compute_edges_device.argtypes = [P, P, P, P, P, P, P, P, I, I, I, P]
+        L.dp_compute_edges_device_f32.argtypes = [P, P, P, P, P, P, P, P, I, I, I, P]
         L.dp_debug_copy.argtypes = [P, I, P, C.c_size_t]
         L.dp_debug_copy.restype = C.c_long
         L.dp_stage_times.argtypes = [P, I, P, I, P, C.c_size_t]
@@ -221,6 +224,17 @@ class DeepPot:
             self._h, d_atom_energy or None, d_force, d_atom_virial, d_atype, d_source, d_edge_vec,
             d_destination_row_ptr, d_source_row_ptr, d_source_order, nloc, nall_nodes,
             edge_storage, stream or None))
+
+    def compute_edges_device(self, d_atom_energy: int, d_force: int, d_atom_virial: int,
+                             d_coord: int, d_atype: int, d_edge_index: int, d_edge_vec: int,
+                             nloc: int, nedge: int, nall_nodes: int = 0, fp32: bool = False,
+                             stream: int = 0):
+        """Evaluation of a device edge graph on raw device pointers
+        (dp_compute_edges_device[_f32], mirroring DeepPot::compute_edges_gpu)."""
+        f = lib().dp_compute_edges_device_f32 if fp32 else lib().dp_compute_edges_device
+        self._check(f(self._h, d_atom_energy or None, d_force, d_atom_virial, d_coord or None,
+                      d_atype, d_edge_index or None, d_edge_vec or None, nloc, nedge, nall_nodes,
+                      stream or None))
 
     def sync(self):
         """Wait for the queued asynchronous evaluations (dp_sync)."""

@@ -525,7 +525,7 @@ void gather_and_reduce(dp_model* M, hipStream_t st, int nloc, int ntarget, const
 // the node pass under fitting, edge gradients under embed_bwd, the fused
 // edge/force pass under force.
 void run_c4(dp_model* M, hipStream_t st, int nloc, const int* d_mapping, int ntarget,
-            const Outputs& out) {
+            const Outputs& out, bool complete) {
   const ModelHost& m = M->host;
   C4Nlist src{};
   src.nlist = static_cast<const int*>(M->nlist.p);
@@ -544,7 +544,7 @@ void run_c4(dp_model* M, hipStream_t st, int nloc, const int* d_mapping, int nta
   launch_c4_node(st, M->c4p, nloc, src.ext_type, mom, e, cot);
   record(M, st, kStFit + 1);
   record(M, st, kStDT + 1);
-  if (d_mapping) {
+  if (complete) {
     // standalone: the list is complete and folded onto owners, so both
     // directions of each edge are evaluated by its centre (no reverse list)
     record(M, st, kStEmbBwd + 1);
@@ -571,9 +571,13 @@ void run_c4(dp_model* M, hipStream_t st, int nloc, const int* d_mapping, int nta
   gather_and_reduce(M, st, nloc, ntarget, d_mapping, e, nloc, nullptr, out);
 }
 
+// complete: the list holds every neighbour within rcut of every centre and
+// maps onto local owners (the standalone path), which the DPA4C fused force
+// pass relies on
 void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_mapping, int ntarget,
-               const Outputs& out) {
-  if (M->kind == dp_model::kDpa4c) return run_c4(M, st, nloc, d_mapping, ntarget, out);
+               const Outputs& out, bool complete) {
+  if (M->kind == dp_model::kDpa4c)
+    return run_c4(M, st, nloc, d_mapping, ntarget, out, complete && d_mapping && ntarget == nloc);
   if (M->precision == DP_PREC_MIXED) run_model_t<float>(M, st, nloc, nall, d_mapping, ntarget, out);
   else run_model_t<double>(M, st, nloc, nall, d_mapping, ntarget, out);
 }
@@ -883,7 +887,7 @@ void device_step(dp_model* M, int natoms, const double* d_coord, const int* d_at
   // the evaluation proper: no host synchronisation, no allocation once sized
   auto body = [&](hipStream_t s) {
     const int nall = build_standalone_nlist(M, s, natoms, d_coord, d_atype, bp);
-    run_model(M, s, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o);
+    run_model(M, s, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o, true);
     if (async) DPAMD_HIP(hipMemcpyAsync(M->status_host, M->status.p, 4, hipMemcpyDeviceToHost, s));
     M->last_nall = nall;
   };
@@ -908,6 +912,77 @@ void device_step(dp_model* M, int natoms, const double* d_coord, const int* d_at
   } else {
     finish(M, st);
   }
+}
+
+// se_e2_a groups centres by type on the host: the edge entry points carry no
+// `ago`, so the local types are read back on every call (nloc ints) and the
+// grouping is rebuilt only when they changed. DPA4C needs no grouping.
+void edges_types(dp_model* M, const int* d_atype, int nloc, hipStream_t st) {
+  if (M->kind != dp_model::kSeA) return;
+  DPAMD_HIP(hipSetDevice(M->device));
+  settle_async(M);
+  std::vector<int> at(std::max(nloc, 0));
+  if (nloc > 0) {
+    if (!d_atype) throw ApiError{DP_ERR_ARG, "null device pointer"};
+    DPAMD_HIP(hipMemcpyAsync(at.data(), d_atype, sizeof(int) * nloc, hipMemcpyDeviceToHost, st));
+  }
+  DPAMD_HIP(hipStreamSynchronize(st));
+  update_buckets(M, nloc, at.data(), st);
+}
+
+// The compute_edges_gpu path (dp_compute_edges_device*): the caller's edge
+// graph becomes extended atoms (edges.hip), its candidate CSR by centre is
+// sel-formatted by the LAMMPS-list kernel, and the model runs with forces
+// gathered onto the edges' source nodes.
+template <class T>
+void edges_step(dp_model* M, double* d_atom_energy, double* d_force, double* d_atom_virial,
+                const int* d_atype, const int* d_edge_index, const T* d_edge_vec, int nloc,
+                int nedge, int nall_nodes, hipStream_t st) {
+  const int nnode = nall_nodes > 0 ? nall_nodes : nloc;
+  if (nloc < 0 || nedge < 0 || nnode < nloc)
+    throw ApiError{DP_ERR_ARG, "invalid edge graph dimensions"};
+  if ((nnode > 0 && (!d_atype || !d_force || !d_atom_virial)) ||
+      (nedge > 0 && (!d_edge_index || !d_edge_vec)) || (nloc > 0 && !d_atom_energy))
+    throw ApiError{DP_ERR_ARG, "null device pointer"};
+  if ((long)nloc + nedge >= (1L << 31) - 1) throw ApiError{DP_ERR_CAPACITY, "too many edges"};
+  begin(M, st);
+  const ModelHost& m = M->host;
+  int* status = static_cast<int*>(M->status.p);
+  const int nall = nloc + nedge;
+  double* ext = need<double>(M, M->ext, (size_t)std::max(nall, 1) * 3);
+  int* ext_type = need<int>(M, M->ext_type, (size_t)std::max(nall, 1));
+  int* mapping = need<int>(M, M->mapping, (size_t)std::max(nall, 1));
+  int* count = need<int>(M, M->cell_count, (size_t)nloc + 1);
+  int* off = need<int>(M, M->cell_start, (size_t)nloc + 1);
+  int* rank = need<int>(M, M->cell_rank, (size_t)std::max(nedge, 1));
+  long* cand_off = need<long>(M, M->cand_off, (size_t)nloc + 1);
+  int* cand = need<int>(M, M->cand, (size_t)std::max(nedge, 1));
+  launch_fill_int(st, (long)nloc + 1, 0, count);
+  launch_edges_ext<T>(st, nloc, nedge, nnode, d_edge_index, d_edge_vec, d_atype, ext, ext_type,
+                      mapping, count, rank, status);
+  {
+    const size_t tb = scan_temp_bytes(nloc + 1);
+    void* tmp = need<char>(M, M->scan_tmp, tb);
+    exclusive_scan_int(st, count, off, nloc + 1, tmp, tb);
+  }
+  launch_edges_fill(st, nloc, nedge, nnode, d_edge_index, off, rank, cand_off, cand);
+  record(M, st, kStGeom + 1);
+  const NlParams np = nl_params(M);
+  int* nlist = need<int>(M, M->nlist, (size_t)std::max(nloc, 1) * m.nnei);
+  int* nreal = need<int>(M, M->nreal, (size_t)std::max(nloc, 1) * m.ntypes);
+  launch_nlist_csr(st, nloc, np, ext, ext_type, cand_off, cand, nlist, nreal, status);
+  record(M, st, kStNlist + 1);
+  // atom energies go through a workspace over every node (the gather zeroes
+  // ntarget of them), of which the first nloc are the caller's
+  double* ae = need<double>(M, M->ae_ws, (size_t)std::max(nnode, 1));
+  Outputs o{nullptr, d_force, nullptr, ae, d_atom_virial};
+  run_model(M, st, nloc, nall, mapping, nnode, o, false);
+  if (nloc > 0)
+    DPAMD_HIP(hipMemcpyAsync(d_atom_energy, ae, sizeof(double) * nloc, hipMemcpyDeviceToDevice, st));
+  M->last_nloc = nloc;
+  M->last_nall = nall;
+  M->last_standalone = false;
+  finish(M, st);
 }
 
 // Packs every DPA4C parameter array into one device allocation (each array
@@ -1165,7 +1240,7 @@ int dp_compute(dp_model* M, int natoms, const double* coord, const int* atype, c
     double* ae = atom_energy ? need<double>(M, M->ae_ws, (size_t)std::max(natoms, 1)) : nullptr;
     double* o10 = need<double>(M, M->out10, 10);
     Outputs o{nullptr, f, nullptr, ae, av};
-    run_model(M, st, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o);
+    run_model(M, st, natoms, nall, static_cast<const int*>(M->mapping.p), natoms, o, true);
     M->last_nloc = natoms;
     M->last_nall = nall;
     M->last_standalone = true;
@@ -1243,7 +1318,7 @@ int dp_compute_nlist(dp_model* M, int nall, int nghost, const double* coord, con
     double* ae = atom_energy ? need<double>(M, M->ae_ws, (size_t)std::max(nall, 1)) : nullptr;
     double* o10 = need<double>(M, M->out10, 10);
     Outputs o{nullptr, f, nullptr, ae, av};
-    run_model(M, st, nloc, nall, nullptr, nall, o);
+    run_model(M, st, nloc, nall, nullptr, nall, o, false);
     M->last_nloc = nloc;
     M->last_nall = nall;
     M->last_standalone = false;
@@ -1309,6 +1384,30 @@ int dp_compute_canonical_graph_device(dp_model* M, double* d_atom_energy, double
     M->last_nall = nall_nodes;
     M->last_standalone = false;
     finish(M, st);
+  });
+}
+
+int dp_compute_edges_device(dp_model* M, double* d_atom_energy, double* d_force,
+                            double* d_atom_virial, const double* d_coord, const int* d_atype,
+                            const int* d_edge_index, const double* d_edge_vec, int nloc,
+                            int nedge, int nall_nodes, void* stream) {
+  (void)d_coord;
+  return guarded(M, [&]() {
+    edges_types(M, d_atype, nloc, static_cast<hipStream_t>(stream));
+    edges_step<double>(M, d_atom_energy, d_force, d_atom_virial, d_atype, d_edge_index,
+                       d_edge_vec, nloc, nedge, nall_nodes, static_cast<hipStream_t>(stream));
+  });
+}
+
+int dp_compute_edges_device_f32(dp_model* M, double* d_atom_energy, double* d_force,
+                                double* d_atom_virial, const double* d_coord, const int* d_atype,
+                                const int* d_edge_index, const float* d_edge_vec, int nloc,
+                                int nedge, int nall_nodes, void* stream) {
+  (void)d_coord;
+  return guarded(M, [&]() {
+    edges_types(M, d_atype, nloc, static_cast<hipStream_t>(stream));
+    edges_step<float>(M, d_atom_energy, d_force, d_atom_virial, d_atype, d_edge_index, d_edge_vec,
+                      nloc, nedge, nall_nodes, static_cast<hipStream_t>(stream));
   });
 }
 

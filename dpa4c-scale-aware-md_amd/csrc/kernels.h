@@ -1,6 +1,8 @@
 // Kernel-side argument structs and host launchers of every pipeline stage.
 #pragma once
 
+#include <algorithm>
+
 #include "common.h"
 #include "emb_shape.h"
 
@@ -117,6 +119,16 @@ void launch_nlist_cells(hipStream_t, int nloc, const BoxParams&, const NlParams&
                         const CellAtom* sorted, int* nlist, int* nreal, int* status);
 void launch_nlist_csr(hipStream_t, int nloc, const NlParams&, const double* ext, const int* ext_type,
                       const long* cand_off, const int* cand, int* nlist, int* nreal, int* status);
+
+// Edge-list front end (edges.hip): extended atoms nloc + e at the bond
+// vectors, owners = source nodes, and the per-centre candidate counts
+// (count must start at zero) and ranks; then the candidate CSR by centre.
+template <class T>
+void launch_edges_ext(hipStream_t, int nloc, int nedge, int nnode, const int* edge_index,
+                      const T* edge_vec, const int* atype, double* ext, int* ext_type,
+                      int* mapping, int* count, int* rank, int* status);
+void launch_edges_fill(hipStream_t, int nloc, int nedge, int nnode, const int* edge_index,
+                       const int* off, const int* rank, long* cand_off, int* cand);
 
 // Scans (hipCUB)
 size_t scan_temp_bytes(int n);

@@ -204,9 +204,41 @@ class DeepPot {
                                             d_source_row_ptr, d_source_order, nloc, nall_nodes,
                                             edge_storage, stream));
   }
+  // Device edge-graph entry, same overloads and argument meaning as
+  // DeepPot::compute_edges_gpu (deepmd-op/overlays/api_cc/include/DeepPot.h:395-429):
+  // edge_index [2][nedge] holds the source node in row 0 and the destination
+  // centre (< nloc) in row 1, edge_vec = r_source - r_centre. Both model kinds
+  // take no fparam / aparam and exchange no node features between ranks, so
+  // comm_nlist is not read. dp_compute_edges_device / _f32.
+  void compute_edges_gpu(double* d_atom_energy, double* d_force, double* d_atom_virial,
+                         const double* d_coord, const int* d_atype, const int* d_edge_index,
+                         const double* d_edge_vec, const int nloc, const int nedge) {
+    edges_impl(d_atom_energy, d_force, d_atom_virial, d_coord, d_atype, d_edge_index, d_edge_vec,
+               nloc, nedge, nloc);
+  }
+  void compute_edges_gpu(double* d_atom_energy, double* d_force, double* d_atom_virial,
+                         const double* d_coord, const int* d_atype, const int* d_edge_index,
+                         const double* d_edge_vec, const int nloc, const int nedge,
+                         const std::vector<double>& fparam, const std::vector<double>& aparam,
+                         const int nall_nodes, const InputNlist* comm_nlist) {
+    (void)comm_nlist;
+    no_params(fparam, aparam, std::vector<double>());
+    edges_impl(d_atom_energy, d_force, d_atom_virial, d_coord, d_atype, d_edge_index, d_edge_vec,
+               nloc, nedge, nall_nodes);
+  }
+  void compute_edges_gpu(double* d_atom_energy, double* d_force, double* d_atom_virial,
+                         const double* d_coord, const int* d_atype, const int* d_edge_index,
+                         const float* d_edge_vec, const int nloc, const int nedge,
+                         const std::vector<double>& fparam, const std::vector<double>& aparam,
+                         const int nall_nodes, const InputNlist* comm_nlist) {
+    (void)comm_nlist;
+    no_params(fparam, aparam, std::vector<double>());
+    edges_impl(d_atom_energy, d_force, d_atom_virial, d_coord, d_atype, d_edge_index, d_edge_vec,
+               nloc, nedge, nall_nodes);
+  }
   bool uses_canonical_graph_inference() const { return info_.model_kind == DP_MODEL_DPA4C; }
   bool uses_fp32_edge_vectors() const { return info_.model_kind == DP_MODEL_DPA4C; }
-  bool supports_device_edge_inference() const { return info_.model_kind == DP_MODEL_DPA4C; }
+  bool supports_device_edge_inference() const { return true; }
 
   dp_model* handle() const { return h_; }
 
@@ -224,7 +256,19 @@ class DeepPot {
   static void no_params(const std::vector<V>& fparam, const std::vector<V>& aparam,
                         const std::vector<double>& cs) {
     if (!fparam.empty() || !aparam.empty() || !cs.empty())
-      throw deepmd_exception("se_e2_a model takes no fparam / aparam / charge_spin");
+      throw deepmd_exception("se_e2_a and DPA4C-Nano models take no fparam / aparam / charge_spin");
+  }
+  void edges_impl(double* ae, double* f, double* av, const double* coord, const int* atype,
+                  const int* ei, const double* vec, int nloc, int nedge, int nall_nodes) {
+    require_init();
+    check(dp_compute_edges_device(h_, ae, f, av, coord, atype, ei, vec, nloc, nedge, nall_nodes,
+                                  nullptr));
+  }
+  void edges_impl(double* ae, double* f, double* av, const double* coord, const int* atype,
+                  const int* ei, const float* vec, int nloc, int nedge, int nall_nodes) {
+    require_init();
+    check(dp_compute_edges_device_f32(h_, ae, f, av, coord, atype, ei, vec, nloc, nedge,
+                                      nall_nodes, nullptr));
   }
   template <typename V>
   static std::vector<double> to_double(const std::vector<V>& v) {

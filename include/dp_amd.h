@@ -232,6 +232,34 @@ int dp_compute_canonical_graph_device(dp_model* model, double* d_atom_energy, do
                                       const uint32_t* d_source_order, int nloc, int nall_nodes,
                                       int64_t edge_storage, void* stream);
 
+/*
+ * Device-resident evaluation of a caller-built edge graph, all arrays device
+ * memory, work ordered on `stream` and complete on return. Replaces
+ * DeepPot::compute_edges_gpu (deepmd-op/overlays/api_cc/include/DeepPot.h:
+ * 395-429; backend DeepPotPTExpt.cc:2402-2740; called by the Kokkos pair,
+ * lmp/pair_deepmd_kokkos.cpp:586-597), with its argument meanings:
+ * d_edge_index int32 [2][nedge], row 0 the neighbour (source) node and row 1
+ * the centre (destination, < nloc); d_edge_vec [nedge][3] = r_neighbour -
+ * r_centre (fp64, or fp32 in the _f32 form); d_atype int32 [nall_nodes]
+ * model types; nall_nodes = nloc folds every edge onto local source nodes
+ * (single domain), nall_nodes > nloc keeps ghost nodes whose forces the
+ * caller's reverse communication folds. Edges beyond rcut (a skin) are
+ * filtered; d_coord is accepted for the signature and not read (the edge
+ * vectors carry the geometry). Outputs: d_atom_energy [nloc], d_force
+ * [nall_nodes][3], d_atom_virial [nall_nodes][9] (charged to the source
+ * node). Works for both model families; an edge naming a node outside the
+ * graph gives DP_ERR_ARG. For se_e2_a the local types are read back each call
+ * (nloc ints) to group centres by type.
+ */
+int dp_compute_edges_device(dp_model* model, double* d_atom_energy, double* d_force,
+                            double* d_atom_virial, const double* d_coord, const int* d_atype,
+                            const int* d_edge_index, const double* d_edge_vec, int nloc,
+                            int nedge, int nall_nodes, void* stream);
+int dp_compute_edges_device_f32(dp_model* model, double* d_atom_energy, double* d_force,
+                                double* d_atom_virial, const double* d_coord, const int* d_atype,
+                                const int* d_edge_index, const float* d_edge_vec, int nloc,
+                                int nedge, int nall_nodes, void* stream);
+
 /* Copy a stage buffer of the last evaluation (DP_STAGE_*) to host memory.
  * Returns the buffer's size in bytes (copies min(size, capacity) bytes);
  * negative on error. No counterpart in the reference: parity tests use it to
