@@ -48,8 +48,16 @@ constexpr int nq3() {
   return n;
 }
 
-constexpr int kU3F = 4;  // layer-3 output tiles per group, forward
-constexpr int kU3B = 8;  // backward
+// Layer-3 output tiles per group (MFMA accumulators in flight). Both kernels
+// are latency-bound on short neighbour sections (one or two tiles per item),
+// so registers go to occupancy rather than to accumulators: the forward is
+// held to 128 VGPRs (4 waves per SIMD), the backward fits 168 (3 waves). An
+// accumulation chain into one register issues back to back, so one or two
+// tiles keep the matrix pipe fed (measured on the 128,000-atom HEA step:
+// forward 3.76 -> 3.27 ms, backward 4.14 -> 3.65 ms against 4 and 8 tiles at
+// 2 waves per SIMD).
+constexpr int kU3F = 1;  // forward
+constexpr int kU3B = 2;  // backward
 
 template <class S>
 constexpr int lds_params() {
@@ -71,7 +79,8 @@ constexpr int bwd_lds_floats(int waves) {
 }
 
 template <class S, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void k_embed_fwd32(EmbArgs a) {
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void
+k_embed_fwd32(EmbArgs a) {
   static_assert(S::L1 > 2, "layer-1 residual not supported");
   static_assert(S::K3P == S::L2P, "fp32 layout expected");
   extern __shared__ float lds32[];
@@ -319,28 +328,22 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
     const f4* act2 = reinterpret_cast<const f4*>(act) + lane;  // (t) at act2[64t]
     // (u, r) at act3[256u + 4r]
     const float* act3 = act + 16 * S::L2P + 64 * (c >> 2) + 16 * g + (c & 3);
-    // activations and neighbour coordinates of tile k+1 fetched during tile k,
-    // the neighbour index one tile earlier
-    f4 nth2[S::NT2];
-    float nth3[S::NU3][4];
+    // neighbour coordinates of tile k+1 fetched during tile k, the neighbour
+    // index one tile earlier; the saved activations are loaded at the start
+    // of their own tile (holding the next tile's 48 values in registers would
+    // cost a wave per SIMD, worth more than the hidden latency)
     double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
     int jn = 0;
-    auto prefetch = [&](int tile, const f4* p2, const float* p3) {
+    auto prefetch = [&](int tile) {
       if (tile + c < nr) {
         nx0 = a.ext[3 * (long)jn];
         nx1 = a.ext[3 * (long)jn + 1];
         nx2 = a.ext[3 * (long)jn + 2];
       }
       jn = tile + 16 + c < nr ? row[tile + 16 + c] : 0;
-#pragma unroll
-      for (int t = 0; t < S::NT2; ++t) nth2[t] = p2[64 * t];
-#pragma unroll
-      for (int u = 0; u < S::NU3; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) nth3[u][r] = p3[256 * u + 4 * r];
     };
     jn = c < nr ? row[c] : 0;
-    if (nr > 0) prefetch(0, act2, act3);
+    if (nr > 0) prefetch(0);
 
     for (int tile = 0; tile < nr; tile += 16, act2 += BLK / 4, act3 += BLK) {
       const int slot = tile + c;
@@ -348,11 +351,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       f4 th2[S::NT2];
       float th3[S::NU3][4];
 #pragma unroll
-      for (int t = 0; t < S::NT2; ++t) th2[t] = nth2[t];
+      for (int t = 0; t < S::NT2; ++t) th2[t] = act2[64 * t];
 #pragma unroll
       for (int u = 0; u < S::NU3; ++u)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) th3[u][r] = nth3[u][r];
+        for (int r = 0; r < 4; ++r) th3[u][r] = act3[256 * u + 4 * r];
       double d0 = 0.0, d1 = 0.0, d2 = 0.0;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
       if (valid) {
@@ -361,7 +364,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
         d2 = nx2 - zi;
         env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
       }
-      if (tile + 16 < nr) prefetch(tile + 16, act2 + BLK / 4, act3 + BLK);
+      if (tile + 16 < nr) prefetch(tile + 16);
       const float s = (float)Rn[0];
 
       // layer 1 (recomputed) and its tangent
@@ -502,7 +505,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 using ShapeWater32 = EmbShape<25, 50, 100, true>;
 using ShapeMetal32 = EmbShape<32, 64, 128, true>;
 constexpr int kFwdWaves32 = 8;
-constexpr int kBwdWaves32 = 4;
+constexpr int kBwdWaves32 = 8;  // LDS then admits 4 waves per SIMD (2 blocks per CU)
 
 template <class S>
 void fwd32_impl(hipStream_t st, const EmbArgs& a, int nblocks) {
