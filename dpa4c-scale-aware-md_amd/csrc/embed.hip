@@ -37,10 +37,14 @@
 
 namespace dpamd {
 
-// layer-3 output tiles per group: independent MFMA accumulation chains in
-// flight (both kernels run two waves per SIMD)
-constexpr int kU3 = 4;
-constexpr int kU3B = 4;
+// Layer-3 output tiles per group: MFMA accumulation chains in flight. Both
+// kernels run two waves per SIMD (LDS holds one block of eight waves per CU);
+// an accumulation chain into one register issues back to back, so fewer
+// chains cost no matrix throughput and free registers: with 4 chains the
+// forward spilled (192 bytes per lane for 25-50-100). Measured on 12,288-atom
+// water: forward 0.672 -> 0.634 ms, backward 0.616 -> 0.603 ms; Cu unchanged.
+constexpr int kU3 = 2;
+constexpr int kU3B = 1;
 
 // LDS: padded net | env statistics of the pair (8) | per-wave scratch
 template <class S>
