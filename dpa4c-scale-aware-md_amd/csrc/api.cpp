@@ -1101,7 +1101,8 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
     upload(M->d_tpad, tpad);
     if (mixed) {
       // the nets are evaluated in fp32: round the parameters once here
-      const std::vector<float> emb32(emb.begin(), emb.end());
+      std::vector<float> emb32(emb.begin(), emb.end());
+      pack_embedding_bf16(m, M->el, emb32);
       const std::vector<float> fit32(m.fit_params.begin(), m.fit_params.end());
       upload(M->d_emb, emb32);
       upload(M->d_fit, fit32);

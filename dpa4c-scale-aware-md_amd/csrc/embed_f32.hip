@@ -1,18 +1,26 @@
 // Mixed-precision embedding kernels: the fp32 counterparts of the fp64
-// forward and backward in embed.hip, on v_mfma_f32_16x16x4f32. The env row
-// of each slot, its gradient and the edge gradient written for the force
-// stage stay fp64; the nets, the T contraction, the saved activations and the
-// u/v dot products are fp32 (reference precision rule for the mixed mode:
-// fp32 embedding/fitting, fp64 env matrix, force and virial).
+// forward and backward in embed.hip. The env row of each slot, its gradient
+// and the edge gradient written for the force stage stay fp64; the nets, the
+// T contraction, the saved activations and the u/v dot products are fp32
+// (reference precision rule for the mixed mode: fp32 embedding/fitting, fp64
+// env matrix, force and virial).
+//
+// The layer-2 and layer-3 products run on v_mfma_f32_16x16x32_bf16 at fp32
+// accuracy: each fp32 operand is split exactly into three bf16 pieces and the
+// six products that reach fp32 precision are accumulated in fp32 (mfma3). The
+// weights are split once on the host (emb_shape.h), the activations and
+// tangents in registers. On gfx950 the bf16 form does 8x the work of
+// v_mfma_f32_16x16x4f32 in 0.65x its time.
 //
 // Work decomposition, tiles and the saved-activation scheme are those of the
 // fp64 kernels. What differs is the MFMA output layout: register r of lane
 // (g, c) holds row 4g + r (fp64: g + 4r). Every layer therefore takes its
-// k-steps in the order that layout leaves the previous layer in registers:
-// in k-step q, lane group g supplies feature 16(q/4) + 4g + q%4 (kf3 below),
-// and the weight rows are read in that order. Layer 1 (computed per lane)
-// uses the same order when L1 is a multiple of 16, which keeps the layer-2
-// [x, x] residual in the lane's own registers.
+// k elements in the order that layout leaves the previous layer in
+// registers: element e of 32-wide k chunk h of lane group g is feature
+// 32h + 16(e/4) + 4g + e%4 (kf3 below with q = 8h + e), and the weights are
+// packed in that order. Layer 1 (computed per lane) uses the same order when
+// L1 is a multiple of 16, which keeps the layer-2 [x, x] residual in the
+// lane's own registers.
 //
 // Saved activations, per tile of 16 slots, float:
 //   layer 2: element (t, r) of lane L at [256t + 4L + r] (same layout in
@@ -39,13 +47,67 @@ __device__ __forceinline__ int kf1(int q, int g) {
   else return 4 * q + g;
 }
 
-// layer-3 k-steps that hold at least one real layer-2 feature: q < nq3
+// bf16 operands of v_mfma_f32_16x16x32_bf16: lane 16g + c holds A[c][8g + e]
+// and B[8g + e][c], e = 0..7; D register r holds D[4g + r][c], as in the fp32
+// 16x16x4 form (checked on MI355X).
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f4 mfma_bf16(bf8 a, bf8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// An fp32 operand as three bf16 pieces, x = h + m + l exactly: h = bf16(x)
+// leaves a remainder of at most 16 significant bits, m = bf16 of that one of
+// at most 8, which l holds exactly (round to nearest even throughout).
+struct Split3 {
+  bf8 h, m, l;
+};
+
+__device__ __forceinline__ Split3 split3(const float* v) {
+  Split3 s;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 h = (__bf16)v[e];
+    const float r1 = v[e] - (float)h;
+    const __bf16 m = (__bf16)r1;
+    s.h[e] = h;
+    s.m[e] = m;
+    s.l[e] = (__bf16)(r1 - (float)m);
+  }
+  return s;
+}
+
+// (a_h + a_m + a_l)(b_h + b_m + b_l) to fp32 accuracy: the six products down
+// to 2^-18 of the leading one (the three dropped are below 2^-26), smallest
+// first. Six bf16 MFMAs of K 32 take about half the time of the eight fp32
+// 16x16x4 MFMAs they replace (measured on MI355X: 9.4 vs 14.4 ns each).
+__device__ __forceinline__ f4 mfma3(const Split3& a, const Split3& b, f4 c) {
+  c = mfma_bf16(a.m, b.m, c);
+  c = mfma_bf16(a.l, b.h, c);
+  c = mfma_bf16(a.h, b.l, c);
+  c = mfma_bf16(a.m, b.h, c);
+  c = mfma_bf16(a.h, b.m, c);
+  return mfma_bf16(a.h, b.h, c);
+}
+
+// pre-split weights of (output tile, k chunk) block idx from LDS: three
+// 16-byte reads, consecutive lanes on consecutive addresses
+__device__ __forceinline__ Split3 wpieces(const float* region, int idx, int lane) {
+  const bf8* w = reinterpret_cast<const bf8*>(region) + idx * 3 * 64 + lane;
+  return Split3{w[0], w[64], w[128]};
+}
+
+// layer-3 input pieces of chunk h: element e is layer-2 result row
+// 16(e/4) + 4g + e%4 of tile 2h + e/4 (x2[tile][row % 4] in the lane)
 template <class S>
-constexpr int nq3() {
-  int n = 0;
-  for (int q = 0; q < S::NT2 * 4; ++q)
-    if (16 * (q >> 2) + (q & 3) < S::L2) n = q + 1;
-  return n;
+__device__ __forceinline__ Split3 x2_pieces(const float (&x2)[S::NT2][4], int h) {
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int t = 2 * h + (e >> 2);
+    v[e] = t < S::NT2 ? x2[t][e & 3] : 0.0f;
+  }
+  return split3(v);
 }
 
 // Layer-3 output tiles per group (MFMA accumulators in flight). Both kernels
@@ -53,9 +115,7 @@ constexpr int nq3() {
 // so registers go to occupancy rather than to accumulators: the forward is
 // held to 128 VGPRs (4 waves per SIMD), the backward fits 168 (3 waves). An
 // accumulation chain into one register issues back to back, so one or two
-// tiles keep the matrix pipe fed (measured on the 128,000-atom HEA step:
-// forward 3.76 -> 3.27 ms, backward 4.14 -> 3.65 ms against 4 and 8 tiles at
-// 2 waves per SIMD).
+// tiles keep the matrix pipe fed.
 constexpr int kU3F = 1;  // forward
 constexpr int kU3B = 2;  // backward
 
@@ -83,10 +143,9 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(4, 4
 k_embed_fwd32(EmbArgs a) {
   static_assert(S::L1 > 2, "layer-1 residual not supported");
   static_assert(S::K3P == S::L2P, "fp32 layout expected");
-  extern __shared__ float lds32[];
+  extern __shared__ __align__(16) float lds32[];
   constexpr int PS = lds_params<S>();
   constexpr int X2LD = x2_ld<S>();
-  constexpr int NQ3F = nq3<S>();
   float* P = lds32;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   double* EnvS = reinterpret_cast<double*>(lds32 + PS);  // PS is a multiple of 64
@@ -148,22 +207,27 @@ k_embed_fwd32(EmbArgs a) {
       }
       const float s = (float)Rn[0];
 
-      // layer 1 -> B operand of layer 2 (feature kf1(q, g) of slot c)
-      float x1[S::NQ2];
+      // layer 1 -> B operand of layer 2: element e of k chunk h is feature
+      // kf1(8h + e, g) of slot c
+      float x1[8 * S::KC2];
 #pragma unroll
-      for (int q = 0; q < S::NQ2; ++q) {
+      for (int q = 0; q < 8 * S::KC2; ++q) {
         const int f = kf1<S>(q, g);
         x1[q] = (f < S::L1) ? tanh_f32(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0f;
       }
       // layer 2, transposed: register r of tile t is feature 16t + 4g + r
       f4 acc2[S::NT2];
+      {
+        Split3 xb[S::KC2];
 #pragma unroll
-      for (int t = 0; t < S::NT2; ++t) acc2[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int h = 0; h < S::KC2; ++h) xb[h] = split3(x1 + 8 * h);
 #pragma unroll
-      for (int q = 0; q < S::NQ2; ++q) {
-        const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::W2LD + c;
+        for (int t = 0; t < S::NT2; ++t) {
+          acc2[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int t = 0; t < S::NT2; ++t) acc2[t] = mfma_f32(W2[16 * t], x1[q], acc2[t]);
+          for (int h = 0; h < S::KC2; ++h)
+            acc2[t] = mfma3(wpieces(P + S::OFF_W2, t * S::KC2 + h, lane), xb[h], acc2[t]);
+        }
       }
       float x2[S::NT2][4];
 #pragma unroll
@@ -195,6 +259,9 @@ k_embed_fwd32(EmbArgs a) {
       }
       wave_lds_sync();
       // layer 3, non-transposed: register r of tile u is slot 4g + r, feature 16u + c
+      Split3 xa[S::KC3];
+#pragma unroll
+      for (int h = 0; h < S::KC3; ++h) xa[h] = x2_pieces<S>(x2, h);
 #pragma unroll
       for (int u0 = 0; u0 < S::NU3; u0 += kU3F) {
         __builtin_amdgcn_sched_barrier(0);
@@ -202,13 +269,11 @@ k_embed_fwd32(EmbArgs a) {
 #pragma unroll
         for (int uu = 0; uu < kU3F; ++uu) acc3[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int q = 0; q < NQ3F; ++q) {
-          const float av = x2[q >> 2][q & 3];
-          const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::W3LD + 16 * u0 + c;
+        for (int h = 0; h < S::KC3; ++h)
 #pragma unroll
           for (int uu = 0; uu < kU3F; ++uu)
-            if (u0 + uu < S::NU3) acc3[uu] = mfma_f32(av, W3[16 * uu], acc3[uu]);
-        }
+            if (u0 + uu < S::NU3)
+              acc3[uu] = mfma3(xa[h], wpieces(P + S::OFF_W3, (u0 + uu) * S::KC3 + h, lane), acc3[uu]);
 #pragma unroll
         for (int uu = 0; uu < kU3F; ++uu) {
           const int u = u0 + uu;
@@ -272,9 +337,8 @@ template <class S, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
   static_assert(S::L1 > 2, "layer-1 residual not supported");
   static_assert(S::K3P == S::L2P, "fp32 layout expected");
-  extern __shared__ float lds32[];
+  extern __shared__ __align__(16) float lds32[];
   constexpr int PS = lds_params<S>();
-  constexpr int NQ3F = nq3<S>();
   float* P = lds32;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   double* EnvS = reinterpret_cast<double*>(lds32 + PS);  // PS is a multiple of 64
@@ -329,9 +393,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
     // (u, r) at act3[256u + 4r]
     const float* act3 = act + 16 * S::L2P + 64 * (c >> 2) + 16 * g + (c & 3);
     // neighbour coordinates of tile k+1 fetched during tile k, the neighbour
-    // index one tile earlier; the saved activations are loaded at the start
-    // of their own tile (holding the next tile's 48 values in registers would
-    // cost a wave per SIMD, worth more than the hidden latency)
+    // index one tile earlier; the saved activations are loaded where they are
+    // used, layer 3's per output tile (holding them, or the next tile's, in
+    // registers costs occupancy or spills, worth more than the hidden latency)
     double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
     int jn = 0;
     auto prefetch = [&](int tile) {
@@ -349,13 +413,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       const int slot = tile + c;
       const bool valid = slot < nr;
       f4 th2[S::NT2];
-      float th3[S::NU3][4];
+
 #pragma unroll
       for (int t = 0; t < S::NT2; ++t) th2[t] = act2[64 * t];
-#pragma unroll
-      for (int u = 0; u < S::NU3; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) th3[u][r] = act3[256 * u + 4 * r];
+
       double d0 = 0.0, d1 = 0.0, d2 = 0.0;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
       if (valid) {
@@ -368,9 +429,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       const float s = (float)Rn[0];
 
       // layer 1 (recomputed) and its tangent
-      float x1[S::NQ2], x1t[S::NQ2];
+      float x1[8 * S::KC2], x1t[8 * S::KC2];
 #pragma unroll
-      for (int q = 0; q < S::NQ2; ++q) {
+      for (int q = 0; q < 8 * S::KC2; ++q) {
         const int f = kf1<S>(q, g);
         if (f < S::L1) {
           const float wv = P[S::OFF_W1 + f];
@@ -384,13 +445,17 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       }
       // layer 2 tangent (transposed); tanh of the primal from the forward
       f4 acc2t[S::NT2];
+      {
+        Split3 xb[S::KC2];
 #pragma unroll
-      for (int t = 0; t < S::NT2; ++t) acc2t[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int h = 0; h < S::KC2; ++h) xb[h] = split3(x1t + 8 * h);
 #pragma unroll
-      for (int q = 0; q < S::NQ2; ++q) {
-        const float* W2 = P + S::OFF_W2 + kf1<S>(q, g) * S::W2LD + c;
+        for (int t = 0; t < S::NT2; ++t) {
+          acc2t[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int t = 0; t < S::NT2; ++t) acc2t[t] = mfma_f32(W2[16 * t], x1t[q], acc2t[t]);
+          for (int h = 0; h < S::KC2; ++h)
+            acc2t[t] = mfma3(wpieces(P + S::OFF_W2, t * S::KC2 + h, lane), xb[h], acc2t[t]);
+        }
       }
       float x2[S::NT2][4], x2t[S::NT2][4];
 #pragma unroll
@@ -437,6 +502,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
           }
       }
       // layer 3 tangent, transposed: register r of tile u is feature 16u + 4g + r
+      Split3 xt[S::KC3];
+#pragma unroll
+      for (int h = 0; h < S::KC3; ++h) xt[h] = x2_pieces<S>(x2t, h);
 #pragma unroll
       for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
         __builtin_amdgcn_sched_barrier(0);
@@ -444,13 +512,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 #pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int q = 0; q < NQ3F; ++q) {
-          const float bv = x2t[q >> 2][q & 3];
-          const float* W3 = P + S::OFF_W3 + kf3(q, g) * S::W3LD + 16 * u0 + c;
+        for (int h = 0; h < S::KC3; ++h)
 #pragma unroll
           for (int uu = 0; uu < kU3B; ++uu)
-            if (u0 + uu < S::NU3) acc3t[uu] = mfma_f32(W3[16 * uu], bv, acc3t[uu]);
-        }
+            if (u0 + uu < S::NU3)
+              acc3t[uu] = mfma3(wpieces(P + S::OFF_W3, (u0 + uu) * S::KC3 + h, lane), xt[h], acc3t[uu]);
 #pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) {
           const int u = u0 + uu;
@@ -458,7 +524,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int f = 16 * u + 4 * g + r;
-              const float th = th3[u][r];
+              const float th = act3[256 * u + 4 * r];
               const float tt = (1.0f - th * th) * acc3t[uu][r];
 #pragma unroll
               for (int m = 0; m < 4; ++m) {
@@ -504,8 +570,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 
 using ShapeWater32 = EmbShape<25, 50, 100, true>;
 using ShapeMetal32 = EmbShape<32, 64, 128, true>;
-constexpr int kFwdWaves32 = 8;
-constexpr int kBwdWaves32 = 8;  // LDS then admits 4 waves per SIMD (2 blocks per CU)
+// One block per CU holds the pre-split nets (about 61 KB) once: 16 waves
+// (4 per SIMD) for the forward, 12 (3 per SIMD, its register budget) for the
+// backward.
+constexpr int kFwdWaves32 = 16;
+constexpr int kBwdWaves32 = 12;
 
 template <class S>
 void fwd32_impl(hipStream_t st, const EmbArgs& a, int nblocks) {

@@ -184,11 +184,13 @@ void pack_embedding(const ModelHost& m, const EmbLayout& e, std::vector<double>&
       Q[e.off_w1 + f] = W1[f];
       Q[e.off_b1 + f] = b1[f];
     }
-    for (int k = 0; k < L1; ++k)
-      for (int n = 0; n < L2; ++n) Q[e.off_w2 + k * e.W2LD + n] = W2[(long)k * L2 + n];
+    if (!e.f32) {  // the fp32 layout's W2 / W3 are bf16 pieces (pack_embedding_bf16)
+      for (int k = 0; k < L1; ++k)
+        for (int n = 0; n < L2; ++n) Q[e.off_w2 + k * e.W2LD + n] = W2[(long)k * L2 + n];
+      for (int k = 0; k < L2; ++k)
+        for (int n = 0; n < L3; ++n) Q[e.off_w3 + k * e.W3LD + n] = W3[(long)k * L3 + n];
+    }
     for (int n = 0; n < L2; ++n) Q[e.off_b2 + n] = b2[n];
-    for (int k = 0; k < L2; ++k)
-      for (int n = 0; n < L3; ++n) Q[e.off_w3 + k * e.W3LD + n] = W3[(long)k * L3 + n];
     for (int n = 0; n < L3; ++n) Q[e.off_b3 + n] = b3[n];
     for (int q = 0; q < 4; ++q) {
       envp[(size_t)p * 8 + q] = m.davg[(size_t)p * 4 + q];
@@ -200,6 +202,60 @@ void pack_embedding(const ModelHost& m, const EmbLayout& e, std::vector<double>&
     embed_host(m, P, Rpad[0], G);
     for (int q = 0; q < 4; ++q)
       for (int f = 0; f < L3; ++f) tpad[((size_t)p * 4 + q) * L3 + f] = Rpad[q] * G[f];
+  }
+}
+
+namespace {
+uint16_t bf16_rne(float x) {  // round to nearest even (finite x)
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+float bf16_value(uint16_t h) {
+  const uint32_t u = (uint32_t)h << 16;
+  float x;
+  std::memcpy(&x, &u, 4);
+  return x;
+}
+// w = hi + mid + lo exactly (each rounding leaves at most 16, then 8 bits)
+void split3(float w, uint16_t out[3]) {
+  out[0] = bf16_rne(w);
+  const float r1 = w - bf16_value(out[0]);
+  out[1] = bf16_rne(r1);
+  const float r2 = r1 - bf16_value(out[1]);
+  out[2] = bf16_rne(r2);
+}
+// one net's pre-split weights W [K][N] (row-major, fp64) into a bf16 region
+// [tiles][chunks][3][64][8] with the given k order; entries past K or N are 0
+void pack_pieces(const double* W, int K, int N, int tiles, int chunks, bool row_order,
+                 uint16_t* dst) {
+  for (int t = 0; t < tiles; ++t)
+    for (int h = 0; h < chunks; ++h)
+      for (int lane = 0; lane < 64; ++lane) {
+        const int g = lane >> 4, c = lane & 15, n = 16 * t + c;
+        for (int e = 0; e < 8; ++e) {
+          const int k = bf16_kperm(h, g, e, row_order);
+          const float w = (k < K && n < N) ? (float)W[(long)k * N + n] : 0.0f;
+          uint16_t pc[3];
+          split3(w, pc);
+          for (int q = 0; q < 3; ++q)
+            dst[((((long)t * chunks + h) * 3 + q) * 64 + lane) * 8 + e] = pc[q];
+        }
+      }
+}
+}  // namespace
+
+void pack_embedding_bf16(const ModelHost& m, const EmbLayout& e, std::vector<float>& emb32) {
+  const int np = m.ntypes * m.ntypes;
+  const int L1 = m.emb[0], L2 = m.emb[1], L3 = m.emb[2];
+  for (int p = 0; p < np; ++p) {
+    const double* P = m.emb_params.data() + (size_t)p * m.emb_block;
+    const double* W2 = P + 2 * L1;
+    const double* W3 = W2 + (long)L1 * L2 + L2;
+    float* Q = emb32.data() + (size_t)p * e.stride;
+    pack_pieces(W2, L1, L2, e.NT2, e.KC2, L1 % 16 == 0,
+                reinterpret_cast<uint16_t*>(Q + e.off_w2));
+    pack_pieces(W3, L2, L3, e.NU3, e.KC3, true, reinterpret_cast<uint16_t*>(Q + e.off_w3));
   }
 }
 

@@ -33,6 +33,12 @@ std::string parse_model(const unsigned char* buf, size_t len, ModelHost& m);
 void pack_embedding(const ModelHost& m, const EmbLayout& e, std::vector<double>& emb,
                     std::vector<double>& envp, std::vector<double>& tpad);
 
+// fp32 layout only: fills the W2 / W3 regions of the fp32-rounded packed nets
+// (pack_embedding's output converted to float) with the weights rounded to
+// fp32 and split exactly into three bf16 pieces, in the lane order the
+// mixed-precision kernels read (emb_shape.h).
+void pack_embedding_bf16(const ModelHost& m, const EmbLayout& e, std::vector<float>& emb32);
+
 // Offsets (in doubles) of each fitting layer inside a type's block.
 struct FitOffsets {
   long W[3], b[3], idt[3], Wo, bo;

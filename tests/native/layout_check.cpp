@@ -45,6 +45,39 @@ static int check(bool f32) {
           ++bad;
         }
       }
+    eq("KC2", e.KC2, S::KC2);
+    eq("KC3", e.KC3, S::KC3);
+    // the bf16 weight regions are read 16 bytes per lane
+    if (e.off_w2 % 4 || e.off_w3 % 4) {
+      std::printf("bf16 regions not 16-byte aligned: %d %d\n", e.off_w2, e.off_w3);
+      ++bad;
+    }
+    // each k chunk's (g, e) -> k map is a bijection onto its 32 k values, and
+    // the layer-3 one is the order of layer 2's result rows (tile 2h + e/4,
+    // row 4g + e%4), which the kernels split as the A / B operand
+    for (int row_order = 0; row_order < 2; ++row_order)
+      for (int h = 0; h < 2; ++h) {
+        int seen[32] = {0};
+        for (int g = 0; g < 4; ++g)
+          for (int ee = 0; ee < 8; ++ee) {
+            const int k = dpamd::bf16_kperm(h, g, ee, row_order != 0);
+            if (k < 32 * h || k >= 32 * h + 32) {
+              std::printf("kperm(%d,%d,%d) = %d outside its chunk\n", h, g, ee, k);
+              ++bad;
+            } else {
+              ++seen[k - 32 * h];
+            }
+            if (row_order && k != 16 * (2 * h + (ee >> 2)) + 4 * g + (ee & 3)) {
+              std::printf("layer-3 kperm(%d,%d,%d) = %d not a layer-2 row\n", h, g, ee, k);
+              ++bad;
+            }
+          }
+        for (int k = 0; k < 32; ++k)
+          if (seen[k] != 1) {
+            std::printf("kperm chunk %d covers k %d %d times\n", h, k, seen[k]);
+            ++bad;
+          }
+      }
   }
   return bad;
 }
