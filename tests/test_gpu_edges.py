@@ -160,3 +160,21 @@ def test_edges_empty_graph(dp, orc, kind):
     ae, f, av = _run(dp, pot, ei, vec, t, 3, 3)
     assert np.abs(ae - ref["atom_energy"]).max() <= tol
     assert not f.any() and not av.any()
+
+
+def test_edges_mixed_precision(dp, orc):
+    """A mixed-precision se_e2_a handle through the edge entry point, at the
+    reference's mixed-precision limits (energy/atom 2e-5 eV, force RMSE 4e-5
+    and max 5e-4 eV/A)."""
+    (coord, atype, box), m = CASES["hea1024"]()
+    mb = model_bytes(m)
+    O = orc.Oracle(mb)
+    ref = O.compute(coord, atype, box)
+    ext, et, mp, ei, vec = _edges(orc, coord, atype, box, O.m["rcut"])
+    n = len(atype)
+    pot = dp.DeepPot(file_content=mb, precision=dp.PREC_MIXED)
+    ae, f, av = _run(dp, pot, ei, vec, atype, n, n)
+    assert np.abs(ae - ref["atom_energy"]).max() <= 2e-5
+    df = f - ref["force"]
+    assert np.sqrt((df ** 2).mean()) <= 4e-5 and np.abs(df).max() <= 5e-4
+    assert np.abs(df).max() > 0.0  # the fp32 nets ran
