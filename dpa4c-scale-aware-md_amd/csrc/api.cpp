@@ -81,6 +81,10 @@ struct dp_model {
   double* d_envp = nullptr;
   double* d_tpad = nullptr;
   void* d_fit = nullptr;
+  // mixed precision: per type and fitting layer, byte offsets into d_fitf of
+  // the pre-split W (forward) and W^T (backward) fragments, -1 if absent
+  void* d_fitf = nullptr;
+  long fitf_off[kMaxTypes][3][2];
   FitOffsets fo{};
   void* blas = nullptr;  // rocBLAS handle for the plain input-gradient GEMM
   // With several centre types the per-type fitting chains run concurrently,
@@ -438,6 +442,11 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
       net.L[k].idt = M->fo.idt[k] >= 0 ? P + M->fo.idt[k] : nullptr;
       net.L[k].in = ins[k];
       net.L[k].out = m.fit[k];
+      if (f32 && M->d_fitf) {
+        const char* fb = static_cast<const char*>(M->d_fitf);
+        net.L[k].Wf = M->fitf_off[t][k][0] >= 0 ? fb + M->fitf_off[t][k][0] : nullptr;
+        net.L[k].WfT = M->fitf_off[t][k][1] >= 0 ? fb + M->fitf_off[t][k][1] : nullptr;
+      }
     }
     net.Wo = P + M->fo.Wo;
     net.bo = m.fit_params[(size_t)t * m.fit_block + M->fo.bo];
@@ -1106,6 +1115,22 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
       const std::vector<float> fit32(m.fit_params.begin(), m.fit_params.end());
       upload(M->d_emb, emb32);
       upload(M->d_fit, fit32);
+      // fitting GEMM operands pre-split for the bf16 matrix cores: W0 forward
+      // (its backward dE/dD is rocBLAS sgemm), W1 / W2 forward and transposed
+      const FitOffsets fo = fit_offsets(m);
+      const int ins[3] = {m.emb[2] * m.axis, m.fit[0], m.fit[1]};
+      std::vector<uint16_t> frag;
+      for (int t = 0; t < m.ntypes; ++t)
+        for (int k = 0; k < 3; ++k)
+          for (int tr = 0; tr < 2; ++tr) {
+            M->fitf_off[t][k][tr] = -1;
+            if (k == 0 && tr == 1) continue;  // dE/dD: rocBLAS sgemm (faster there)
+            frag.resize((frag.size() + 127) / 128 * 128);  // 256-byte aligned blocks
+            M->fitf_off[t][k][tr] = (long)(frag.size() * sizeof(uint16_t));
+            pack_gemm_bf16(m.fit_params.data() + (size_t)t * m.fit_block + fo.W[k], ins[k],
+                           m.fit[k], tr == 1, frag);
+          }
+      upload(M->d_fitf, frag);
     } else {
       upload(M->d_emb, emb);
       upload(M->d_fit, m.fit_params);
@@ -1132,7 +1157,7 @@ void dp_destroy(dp_model* M) {
   for (Buf* b : M->bufs)
     if (b->p) (void)hipFree(b->p);
   for (void* p : {M->d_emb, static_cast<void*>(M->d_envp), static_cast<void*>(M->d_tpad), M->d_fit,
-                  M->d_c4})
+                  M->d_fitf, M->d_c4})
     if (p) (void)hipFree(p);
   if (M->async_pending) (void)hipStreamSynchronize(M->async_stream);
   for (auto& set : M->ev)

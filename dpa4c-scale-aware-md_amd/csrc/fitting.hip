@@ -13,6 +13,7 @@
 // fused tile analog is deepmd-op/overlays/op/pt/tiled_fitting.cuh:4-60.
 #include <rocblas/rocblas.h>
 
+#include "bf16x3.h"
 #include "fastmath.h"
 #include "kernels.h"
 
@@ -44,7 +45,66 @@ struct GemmArgs {
   // epilogue kernel sums the slices in order
   int split;
   T* ws;
+  // fp32 only: B pre-split into bf16 fragments (pack_gemm_bf16 layout), which
+  // selects the bf16 three-piece kernel k_gemm3; null for the fp32 / fp64 MFMA
+  const void* Bf;
 };
+
+// Block tile output: the split-K slice store, or the layer epilogue (plain,
+// forward: bias + tanh + residual, backward: (dH_in + acc) idt (1 - t^2)).
+// acc[n] register r of wave w holds C[row0 + 16w + Frag::row(g, r)][col0 + 16n + c].
+template <class T, int NT>
+__device__ __forceinline__ void gemm_store(const GemmArgs<T>& a, const typename Frag<T>::V (&acc)[NT],
+                                           int row0, int col0, int w, int g, int c) {
+  if (a.split > 1) {
+    T* out = a.ws + (long)blockIdx.z * a.M * a.ldc;
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = row0 + 16 * w + Frag<T>::row(g, r);
+        if (row < a.M) out[(long)row * a.ldc + col0 + 16 * n + c] = acc[n][r];
+      }
+    return;
+  }
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int col = col0 + 16 * n + c;
+    // forward epilogue: the four tanh of this column at once (fp64: shared
+    // reciprocal; rows past M hold zeros and are not stored)
+    T th[4];
+    if (a.epi == 1) {
+      T z[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
+      if constexpr (sizeof(T) == 8) {
+        tanh_fast4(z, th);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) th[r] = tanh_act(z[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + 16 * w + Frag<T>::row(g, r);
+      if (row >= a.M) continue;
+      const long o = (long)row * a.ldc + col;
+      const T v = acc[n][r];
+      if (a.epi == 0) {
+        a.C[o] = v;
+      } else if (a.epi == 1) {
+        const T t = th[r];
+        if (a.T_out) a.T_out[o] = t;
+        a.C[o] = a.idt ? a.A[(long)row * a.lda + col] + a.idt[col] * t : t;
+      } else {
+        const T dh = v + (a.dHin ? a.dHin[(long)row * a.ld_dhin + col] : T(0));
+        if (a.dH_out) a.dH_out[o] = dh;
+        const T tk = a.Tk[o];
+        a.C[o] = dh * (a.idt ? a.idt[col] : T(1)) * (T(1) - tk * tk);
+      }
+    }
+  }
+}
 
 // C = epi(A[MxK] B[KxN]); B(k,n) = TRANSB ? B[n*ldb + k] : B[k*ldb + n].
 // Block tile 64 x 16*NT: wave w owns rows 16w..16w+15 and all NT column tiles,
@@ -162,54 +222,108 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
     if (kc + 1 < nk) stash(buf ^ 1);
     __syncthreads();
   }
+  gemm_store<T, NT>(a, acc, row0, col0, w, g, c);
+}
+
+// fp32 GEMM on the bf16 matrix cores at fp32 accuracy (mixed precision):
+// C = epi(A[MxK] B[KxN]) with B pre-split on the host into fragments
+// a.Bf [ceil(K/32)][N/16][3][64 lanes] (8 bf16 each: lane 16g + c of (chunk
+// h, column tile n) holds the pieces of B(32h + 8g + e, 16n + c), e = 0..7,
+// zero past K). Block tile 64 x 16 NT, wave w rows 16w..16w+15 as in k_gemm;
+// K advances 32 at a time: the A chunk (fp32) and the block's B fragments
+// (NT tiles) go through two LDS buffers, each wave splits its A fragment
+// (row 16w + c, k 8g..8g+7) once per chunk and runs six bf16 MFMAs per column
+// tile (mfma3). On gfx950 the fp32 16x16x4 MFMA is barely faster than the
+// VALU; the bf16 form with the six-product split does about twice its work
+// per unit time. AT: A is D = T^T T[:, :16] formed while staging; chunk kc
+// holds D columns 32kc.. 32kc + 31 (a = 2kc, 2kc + 1), thread (row, part)
+// stages columns 8 part .. 8 part + 7 and keeps T[m][8 (part % 2) + e].
+template <int NT, bool AT>
+__global__ __launch_bounds__(256) void k_gemm3(GemmArgs<float> a) {
+  constexpr int BM = 64, BK = 32, BN = 16 * NT, ALD = BK + 4;
+  __shared__ __align__(16) float As[2][BM * ALD];
+  __shared__ __align__(16) bf8 Bs[2][NT * 3 * 64];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
+  const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+  const int ntile = a.N / 16, tile0 = col0 / 16;
+  const bf8* Bf = static_cast<const bf8*>(a.Bf);
+  // staging share: row sr, k columns sk .. sk + 7 of the chunk
+  const int sr = tid >> 2, part = tid & 3, sk = 8 * part;
+  const int grow = row0 + sr;
+  const float* arow = grow < a.M ? (AT ? a.Tt + 4 * (long)grow : a.A + (long)grow * a.lda) : nullptr;
+  float tb[4][8];
+  if constexpr (AT) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        tb[m][e] = arow ? arow[(8 * (part & 1) + e) * a.ldt + m] : 0.0f;
+  }
+  float ra[8];
+  bf8 rb[(NT * 3 * 64 + 255) / 256];
+  auto fetch = [&](int kc) {
+    if constexpr (AT) {
+      // ra[m] = T[m][a] of this row, a = 2 kc + part / 2
+      const int ac = 2 * kc + (part >> 1);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) ra[m] = arow ? arow[(long)ac * a.ldt + m] : 0.0f;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = 32 * kc + sk + e;
+        ra[e] = (arow && k < a.K) ? arow[k] : 0.0f;
+      }
+    }
+    const bf8* src = Bf + ((long)kc * ntile + tile0) * 192;
+#pragma unroll
+    for (int u = 0; u < (NT * 192 + 255) / 256; ++u) {
+      const int q = tid + 256 * u;
+      if (q < NT * 192) rb[u] = src[q];
+    }
+  };
+  auto stash = [&](int buf) {
+    float* dst = As[buf] + sr * ALD + sk;
+    if constexpr (AT) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        dst[e] = ra[0] * tb[0][e] + ra[1] * tb[1][e] + ra[2] * tb[2][e] + ra[3] * tb[3][e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e] = ra[e];
+    }
+#pragma unroll
+    for (int u = 0; u < (NT * 192 + 255) / 256; ++u) {
+      const int q = tid + 256 * u;
+      if (q < NT * 192) Bs[buf][q] = rb[u];
+    }
+  };
+  f4 acc[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) acc[n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  int kc0 = 0, nk = (a.K + BK - 1) / BK;
   if (a.split > 1) {
-    T* out = a.ws + (long)blockIdx.z * a.M * a.ldc;
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = row0 + 16 * w + Frag<T>::row(g, r);
-        if (row < a.M) out[(long)row * a.ldc + col0 + 16 * n + c] = acc[n][r];
-      }
-    return;
+    const int per = (nk + a.split - 1) / a.split;
+    kc0 = blockIdx.z * per;
+    nk = min(nk, kc0 + per);
   }
-#pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    const int col = col0 + 16 * n + c;
-    // forward epilogue: the four tanh of this column at once (fp64: shared
-    // reciprocal; rows past M hold zeros and are not stored)
-    T th[4];
-    if (a.epi == 1) {
-      T z[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
-      if constexpr (sizeof(T) == 8) {
-        tanh_fast4(z, th);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) th[r] = tanh_act(z[r]);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = row0 + 16 * w + Frag<T>::row(g, r);
-      if (row >= a.M) continue;
-      const long o = (long)row * a.ldc + col;
-      const T v = acc[n][r];
-      if (a.epi == 0) {
-        a.C[o] = v;
-      } else if (a.epi == 1) {
-        const T t = th[r];
-        if (a.T_out) a.T_out[o] = t;
-        a.C[o] = a.idt ? a.A[(long)row * a.lda + col] + a.idt[col] * t : t;
-      } else {
-        const T dh = v + (a.dHin ? a.dHin[(long)row * a.ld_dhin + col] : T(0));
-        if (a.dH_out) a.dH_out[o] = dh;
-        const T tk = a.Tk[o];
-        a.C[o] = dh * (a.idt ? a.idt[col] : T(1)) * (T(1) - tk * tk);
-      }
-    }
+  if (kc0 < nk) {
+    fetch(kc0);
+    stash(kc0 & 1);
   }
+  __syncthreads();
+  for (int kc = kc0; kc < nk; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < nk) fetch(kc + 1);
+    const Split3 xa = split3(As[buf] + (16 * w + c) * ALD + 8 * g);
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const bf8* b = Bs[buf] + n * 192 + lane;
+      acc[n] = mfma3(xa, Split3{b[0], b[64], b[128]}, acc[n]);
+    }
+    if (kc + 1 < nk) stash(buf ^ 1);
+    __syncthreads();
+  }
+  gemm_store<float, NT>(a, acc, row0, col0, w, g, c);
 }
 
 // Split-K forward epilogue of a layer without residual: C = tanh(sum over
@@ -366,6 +480,13 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
 template <class T, int NT, bool TRANSB, bool AT = false>
 static void gemm_nt(hipStream_t st, const GemmArgs<T>& a) {
   dim3 grid(a.N / (16 * NT), (a.M + 63) / 64, a.split > 1 ? a.split : 1);
+  if constexpr (sizeof(T) == 4) {
+    if (a.Bf) {  // B pre-split: the bf16 three-piece kernel (B's orientation is in the fragments)
+      hipLaunchKernelGGL((k_gemm3<NT, AT>), grid, dim3(256), 0, st, a);
+      DPAMD_LAUNCH_CHECK();
+      return;
+    }
+  }
   hipLaunchKernelGGL((k_gemm<T, NT, TRANSB, AT>), grid, dim3(256), 0, st, a);
   DPAMD_LAUNCH_CHECK();
 }
@@ -440,7 +561,7 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   // forward
   g = G{};
   g.M = rows; g.N = F0; g.K = Dn; g.A = D; g.lda = Dn; g.B = net.L[0].W; g.ldb = F0;
-  g.epi = 1; g.bias = net.L[0].b; g.idt = nullptr; g.C = b.H0; g.ldc = F0;
+  g.epi = 1; g.bias = net.L[0].b; g.idt = nullptr; g.C = b.H0; g.ldc = F0; g.Bf = net.L[0].Wf;
   if (b.split > 1) {
     g.split = b.split;
     g.ws = b.ws;
@@ -463,10 +584,12 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   g = G{};
   g.M = rows; g.N = F1; g.K = F0; g.A = b.H0; g.lda = F0; g.B = net.L[1].W; g.ldb = F1;
   g.epi = 1; g.bias = net.L[1].b; g.idt = net.L[1].idt; g.C = b.H1; g.ldc = F1; g.T_out = b.T1;
+  g.Bf = net.L[1].Wf;
   gemm<false>(st, g);
   g = G{};
   g.M = rows; g.N = F2; g.K = F1; g.A = b.H1; g.lda = F1; g.B = net.L[2].W; g.ldb = F2;
   g.epi = 1; g.bias = net.L[2].b; g.idt = net.L[2].idt; g.C = b.H2; g.ldc = F2; g.T_out = b.T2;
+  g.Bf = net.L[2].Wf;
   gemm<false>(st, g);
   hipLaunchKernelGGL(k_head<T>, dim3((rows + 3) / 4), dim3(256), 0, st, rows, F2, b.H2, b.T2, net.Wo,
                      net.L[2].idt, net.bo, net.bias, e_bucket, b.dZa);
@@ -476,12 +599,14 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   g.M = rows; g.N = F1; g.K = F2; g.A = b.dZa; g.lda = F2; g.B = net.L[2].W; g.ldb = F2;
   g.epi = 2; g.idt = net.L[1].idt; g.C = b.dZb; g.ldc = F1;
   g.dHin = net.L[2].idt ? net.Wo : nullptr; g.ld_dhin = 0; g.dH_out = b.dH; g.Tk = b.T1;
+  g.Bf = net.L[2].WfT;
   gemm<true>(st, g);
   // dH0 = [res1] dH1 + dZ1 W1^T, dZ0 = dH0 (1 - H0^2)
   g = G{};
   g.M = rows; g.N = F0; g.K = F1; g.A = b.dZb; g.lda = F1; g.B = net.L[1].W; g.ldb = F1;
   g.epi = 2; g.idt = nullptr; g.C = b.dZa; g.ldc = F0;
   g.dHin = net.L[1].idt ? b.dH : nullptr; g.ld_dhin = F1; g.dH_out = nullptr; g.Tk = b.H0;
+  g.Bf = net.L[1].WfT;
   gemm<true>(st, g);
   // dD = dZ0 W0^T
   if (blas) {

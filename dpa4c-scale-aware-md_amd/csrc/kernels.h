@@ -157,6 +157,10 @@ struct FitLayer {
   const T* b;    // [out]
   const T* idt;  // [out] or null
   int in, out;
+  // mixed precision: W (forward) and W^T (backward) pre-split into bf16
+  // fragments for the fp32 GEMM on the bf16 matrix cores; null otherwise
+  const void* Wf;
+  const void* WfT;
 };
 template <class T>
 struct FitNet {

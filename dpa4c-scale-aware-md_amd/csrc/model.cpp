@@ -245,6 +245,27 @@ void pack_pieces(const double* W, int K, int N, int tiles, int chunks, bool row_
 }
 }  // namespace
 
+void pack_gemm_bf16(const double* W, int rows, int cols, bool trans, std::vector<uint16_t>& out) {
+  const int K = trans ? cols : rows, N = trans ? rows : cols;
+  const int chunks = (K + 31) / 32, tiles = N / 16;
+  const size_t base = out.size();
+  out.resize(base + (size_t)chunks * tiles * 3 * 64 * 8, 0);
+  uint16_t* dst = out.data() + base;
+  for (int h = 0; h < chunks; ++h)
+    for (int t = 0; t < tiles; ++t)
+      for (int lane = 0; lane < 64; ++lane) {
+        const int g = lane >> 4, c = lane & 15, n = 16 * t + c;
+        for (int e = 0; e < 8; ++e) {
+          const int k = 32 * h + 8 * g + e;
+          const double v = k < K ? (trans ? W[(long)n * cols + k] : W[(long)k * cols + n]) : 0.0;
+          uint16_t pc[3];
+          split3((float)v, pc);
+          for (int q = 0; q < 3; ++q)
+            dst[((((size_t)h * tiles + t) * 3 + q) * 64 + lane) * 8 + e] = pc[q];
+        }
+      }
+}
+
 void pack_embedding_bf16(const ModelHost& m, const EmbLayout& e, std::vector<float>& emb32) {
   const int np = m.ntypes * m.ntypes;
   const int L1 = m.emb[0], L2 = m.emb[1], L3 = m.emb[2];

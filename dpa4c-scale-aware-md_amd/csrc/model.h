@@ -39,6 +39,13 @@ void pack_embedding(const ModelHost& m, const EmbLayout& e, std::vector<double>&
 // mixed-precision kernels read (emb_shape.h).
 void pack_embedding_bf16(const ModelHost& m, const EmbLayout& e, std::vector<float>& emb32);
 
+// Appends the fragments of the fp32 GEMM operand B [K][N] (B(k, n) = W[k][n],
+// or W[n][k] when `trans`; W row-major [rows][cols] fp64, rounded to fp32 and
+// split exactly into three bf16 pieces) in the layout the bf16 GEMM reads:
+// [ceil(K/32)][N/16][3][64 lanes][8], lane 16g + c of (chunk h, tile n)
+// holding B(32h + 8g + e, 16n + c), e = 0..7, zero past K. N % 16 == 0.
+void pack_gemm_bf16(const double* W, int rows, int cols, bool trans, std::vector<uint16_t>& out);
+
 // Offsets (in doubles) of each fitting layer inside a type's block.
 struct FitOffsets {
   long W[3], b[3], idt[3], Wo, bo;
