@@ -415,15 +415,23 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
   __shared__ T Ts[kDtWaves][4 * 128];
   __shared__ T F16[kDtWaves][4 * AX];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  const int pos = blockIdx.x * kDtWaves + w;
+  const int pos0 = blockIdx.x * kDtWaves, pos = pos0 + w;
+  // T of the block's positions from the column-major copy (element (pos, a,
+  // m) at Tt[a * 4 nb + 4 pos + m]): column a of the kDtWaves consecutive
+  // positions is one contiguous run of 4 kDtWaves values, read by as many
+  // consecutive threads (a wave alone would use a quarter of each line)
+  {
+    constexpr int RUN = 4 * kDtWaves;
+    const int k = threadIdx.x % RUN, pw = k >> 2, m = k & 3;
+    if (pos0 + pw < nb) {
+      const T* src = Tt + 4 * (long)pos0 + k;
+      for (int a = threadIdx.x / RUN; a < L3; a += kDtWaves * 64 / RUN)
+        Ts[pw][m * L3 + a] = src[(long)a * 4 * nb];
+    }
+  }
+  __syncthreads();
   if (pos >= nb) return;
   const int i = items[pos];
-  // T of this position from the column-major copy: element (a, m) at
-  // Tt[a * 4 nb + 4 pos + m]
-  const T* Ti = Tt + 4 * (long)pos;
-  for (int q = lane; q < 4 * L3; q += 64)
-    Ts[w][(q & 3) * L3 + (q >> 2)] = Ti[(long)(q >> 2) * 4 * nb + (q & 3)];
-  wave_lds_sync();
   const T tb0 = Ts[w][c], tb1 = Ts[w][L3 + c], tb2 = Ts[w][2 * L3 + c], tb3 = Ts[w][3 * L3 + c];
   const bool hi8 = (c & 8) != 0, hi4 = (c & 4) != 0;
   const int mine = c >> 2;  // the m whose first-term sum this lane ends with
