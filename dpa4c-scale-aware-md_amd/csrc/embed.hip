@@ -41,8 +41,10 @@ namespace dpamd {
 // kernels run two waves per SIMD (LDS holds one block of eight waves per CU);
 // an accumulation chain into one register issues back to back, so fewer
 // chains cost no matrix throughput and free registers: with 4 chains the
-// forward spilled (192 bytes per lane for 25-50-100). Measured on 12,288-atom
-// water: forward 0.672 -> 0.634 ms, backward 0.616 -> 0.603 ms; Cu unchanged.
+// forward spilled 192 bytes per lane (25-50-100) and 116 (32-64-128), with 2
+// it spills 52 / 36 and with 1 none, but 2 measured fastest. Measured on
+// 12,288-atom water: forward 0.672 -> 0.634 ms, backward 0.616 -> 0.603 ms;
+// Cu unchanged.
 constexpr int kU3 = 2;
 constexpr int kU3B = 1;
 
