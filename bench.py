@@ -17,7 +17,10 @@ memory high-water mark) are measured in the same run and reported under
 (dp_compute_device_async, the form an MD loop with device-resident data
 uses); `ms_per_step_sync` times the synchronous entry point (one host round
 trip per step) on the same system and `ms_per_step_host_arrays` the host-array
-entry point (coordinates in and forces out over PCIe each step). The roofline object describes the dominant
+entry point (coordinates in and forces out over PCIe each step); the water
+line's `ms_per_step_lammps_list` times the call `pair_style deepmd` makes,
+dp_compute_nlist with a LAMMPS-style full list (1 A skin) cached between
+list rebuilds, host arrays in and out. The roofline object describes the dominant
 kernel, timed with HIP events on the stream it runs on over a second pass of
 the same queued steps (the events stay out of the headline pass);
 the CPU baseline is the repository's fp64 CPU restatement (oracle/) timed on a
@@ -78,6 +81,48 @@ def flops_bytes(pot, n_real, nloc, nb_edges, mixed=False):
         # reads the section sums, writes T (the first fitting GEMM forms D from T)
         work["descriptor"] = ("byte", es * nloc * (nt * 4 * L3 + 4 * L3))
     return work
+
+
+def lammps_list_ms(dp, config, mb, mixed, energy_ref, steps):
+    """The `pair_style deepmd` call itself: dp_compute_nlist with host arrays
+    (coordinates of the local and ghost atoms up, forces of all of them down
+    over PCIe each step) and a LAMMPS-style full list with a 1 A skin, built
+    once on the host (systems.lammps_list) and uploaded with ago = 0; the
+    timed steps pass ago = 1, so the cached candidates are re-filtered by
+    distance every step as the reference does between list rebuilds."""
+    import ctypes as C
+    import numpy as np
+    coord, atype, box = dp.systems.build(config)
+    pot = dp.DeepPot(file_content=mb, gpu_rank=0,
+                     precision=dp.PREC_MIXED if mixed else dp.PREC_FP64)
+    ext, et, nghost, off, nb = dp.systems.lammps_list(coord, atype, box, pot.cutoff() + 1.0)
+    nloc, nall = len(atype), len(et)
+    ext = np.ascontiguousarray(ext, np.float64)
+    et = np.ascontiguousarray(et, np.int32)
+    ilist = np.arange(nloc, dtype=np.int32)
+    numneigh = np.ascontiguousarray(np.diff(off), np.int32)
+    nb = np.ascontiguousarray(nb, np.int32)
+    ptrs = (C.c_void_p * nloc)(*[nb.ctypes.data + 4 * int(o) for o in off[:-1]])
+    boxa = np.ascontiguousarray(box, np.float64).reshape(9)
+    e = C.c_double()
+    f = np.zeros((nall, 3))
+    v = np.zeros(9)
+    lib = dp.lib()
+
+    def call(ago):
+        pot._check(lib.dp_compute_nlist(pot._h, nall, nghost, ext.ctypes.data, et.ctypes.data,
+                                        boxa.ctypes.data, nloc, ilist.ctypes.data,
+                                        numneigh.ctypes.data, C.cast(ptrs, C.c_void_p), 0, ago,
+                                        C.byref(e), f.ctypes.data, v.ctypes.data, None, None))
+
+    call(0)
+    call(1)
+    if abs(e.value - energy_ref) > 1e-6 * max(1.0, abs(energy_ref)):
+        raise RuntimeError(f"LAMMPS-list energy {e.value} differs from {energy_ref}")
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call(1)
+    return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def run_config(dp, hip, config, steps, warmup):
@@ -297,6 +342,9 @@ def main():
     ap.add_argument("--dpa4c-only", action="store_true",
                     help="measure only the --dpa4c workloads (profiling runs); prints their list")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--lammps-list", default="1",
+                    help="secondary configs whose line also times the LAMMPS-list entry point "
+                         "(dp_compute_nlist, host arrays, 1 A skin list): ms_per_step_lammps_list")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only copy this many bytes device-to-device twice (HBM counter calibration)")
     args = ap.parse_args()
@@ -376,6 +424,7 @@ def main():
         "stages": main_r["stages"],
         "device_bytes_peak": main_r["device_bytes"],
     }
+    lammps_cfgs = {int(x) for x in str(args.lammps_list).split(",") if x.strip()}
     secondary = [int(x) for x in str(args.secondary).split(",") if x.strip()]
     secondary = [c for c in secondary if c >= 0 and c != args.config]
     if secondary:
@@ -391,6 +440,9 @@ def main():
             "ns_per_day": round(DT_FS[cfg] * 1e-6 * 86400.0 / (s["ms"] * 1e-3), 4),
             "device_bytes_peak": s["device_bytes"],
             "stages": s["stages"]})
+        if cfg in lammps_cfgs:
+            out["secondary"][-1]["ms_per_step_lammps_list"] = round(
+                lammps_list_ms(dp, cfg, s["mb"], s["mixed"], s["energy"], max(1, min(args.steps, 10))), 4)
         del s
     c4 = [w for w in str(args.dpa4c).split(",") if w.strip()]
     if c4:

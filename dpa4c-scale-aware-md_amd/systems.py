@@ -156,3 +156,69 @@ CONFIGS = {
 def build(config: int):
     """(coord [n,3] f64, atype [n] i32, box [9] f64) of benchmark configuration `config`."""
     return CONFIGS[config]["build"]()
+
+
+def lammps_list(coord, atype, box, cutoff: float):
+    """A LAMMPS-style full neighbour list for an orthorhombic periodic box, as
+    `pair_style deepmd` hands it to the model: ghost atoms (periodic images
+    within `cutoff` of the box, appended after the local atoms) and, for every
+    local atom, all other atoms within `cutoff` (rcut + skin), as a CSR
+    (offsets [nloc + 1], neighbours). Returns (ext_coord [nall, 3], ext_type
+    [nall], nghost, offsets, neighbours). Built with a cell grid, one stencil
+    offset at a time, so memory stays at a few candidate arrays."""
+    coord = np.ascontiguousarray(coord, np.float64).reshape(-1, 3)
+    atype = np.ascontiguousarray(atype, np.int32)
+    h = np.asarray(box, np.float64).reshape(3, 3)
+    if np.any(np.abs(h - np.diag(np.diag(h))) > 0):
+        raise ValueError("lammps_list: orthorhombic boxes only")
+    L = np.diag(h)
+    if np.any(L <= 2 * cutoff):
+        raise ValueError("lammps_list: box edge must exceed twice the cutoff")
+    nloc = len(coord)
+    x = coord - np.floor(coord / L) * L
+    ext, et = [x], [atype]
+    for s in np.ndindex(3, 3, 3):
+        sh = np.array(s) - 1
+        if not sh.any():
+            continue
+        y = x + sh * L
+        keep = np.all((y >= -cutoff) & (y < L + cutoff), axis=1)
+        ext.append(y[keep])
+        et.append(atype[keep])
+    ext = np.concatenate(ext)
+    et = np.concatenate(et).astype(np.int32)
+    nall = len(ext)
+    nc = np.maximum(1, np.floor((L + 2 * cutoff) / cutoff).astype(np.int64))
+    cw = (L + 2 * cutoff) / nc
+    cidx = np.minimum(((ext + cutoff) / cw).astype(np.int64), nc - 1)
+    cell = (cidx[:, 2] * nc[1] + cidx[:, 1]) * nc[0] + cidx[:, 0]
+    order = np.argsort(cell, kind="stable")
+    ncell = int(nc.prod())
+    cnt = np.bincount(cell, minlength=ncell)
+    start = np.concatenate([[0], np.cumsum(cnt)])
+    ci = cidx[:nloc]
+    rc2 = cutoff * cutoff
+    pi, pj = [], []
+    for o in np.ndindex(3, 3, 3):
+        cc = ci + np.array(o) - 1
+        ok = np.all((cc >= 0) & (cc < nc), axis=1)
+        centres = np.nonzero(ok)[0]
+        cid = (cc[ok, 2] * nc[1] + cc[ok, 1]) * nc[0] + cc[ok, 0]
+        k = cnt[cid]
+        tot = int(k.sum())
+        if tot == 0:
+            continue
+        i = np.repeat(centres, k)
+        first = np.repeat(start[cid], k)
+        run = np.arange(tot) - np.repeat(np.cumsum(k) - k, k)
+        j = order[first + run]
+        d = ext[j] - ext[i]
+        m = (np.einsum("ij,ij->i", d, d) < rc2) & (j != i)
+        pi.append(i[m])
+        pj.append(j[m])
+    pi = np.concatenate(pi)
+    pj = np.concatenate(pj)
+    srt = np.lexsort((pj, pi))
+    pi, pj = pi[srt], pj[srt]
+    off = np.concatenate([[0], np.cumsum(np.bincount(pi, minlength=nloc))]).astype(np.int64)
+    return ext, et, nall - nloc, off, pj.astype(np.int32)
