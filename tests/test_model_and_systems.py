@@ -58,3 +58,32 @@ def test_benchmark_systems(dp, cfg, natoms, edge):
         a = 3.615
         frac = coord / a * 2
         assert np.abs(frac - np.rint(frac)).max() < 0.2 * 2 / a * 3  # jitter sigma 0.05 A
+
+
+def test_lammps_list_matches_brute_force(dp):
+    """The host-side LAMMPS-style list (ghosts appended after the local atoms,
+    all atoms within the cutoff of each local atom): neighbour sets equal a
+    brute-force search over the extended atoms, counts equal the minimum
+    image's, ghosts are images of local atoms."""
+    coord, atype, box = dp.systems.build(1)
+    cut = 7.0
+    ext, et, nghost, off, nb = dp.systems.lammps_list(coord, atype, box, cut)
+    n = len(atype)
+    assert len(et) == n + nghost and off[0] == 0 and off[-1] == len(nb)
+    L = np.diag(np.asarray(box, np.float64).reshape(3, 3))
+    # ghosts are periodic images of local atoms of the same type
+    assert nghost > 0
+    rng = np.random.default_rng(0)
+    for gi in rng.choice(nghost, 20, replace=False):
+        dg = coord - ext[n + gi]
+        dg -= np.round(dg / L) * L
+        k = int(np.argmin(np.einsum("ij,ij->i", dg, dg)))
+        assert np.abs(dg[k]).max() < 1e-9 and atype[k] == et[n + gi]
+    for i in rng.choice(n, 12, replace=False):
+        dd = np.linalg.norm(ext - ext[i], axis=1)
+        want = set(np.nonzero(dd < cut)[0].tolist()) - {int(i)}
+        assert want == set(nb[off[i]:off[i + 1]].tolist())
+        m = coord - coord[i]
+        m -= np.round(m / L) * L
+        assert int((np.einsum("ij,ij->i", m, m) < cut * cut).sum()) - 1 == off[i + 1] - off[i]
+    assert np.all(et[n:] >= 0)
