@@ -293,7 +293,10 @@ __device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s, int* 
     const int q = base + lane;
     const int tq = q < n ? s[q].t : -1;
 #pragma unroll
-    for (int t = 0; t < kMaxTypes; ++t) cnt[t] += __popcll(__ballot(tq == t));
+    for (int t = 0; t < kMaxTypes; ++t) {
+      if (t >= np.ntypes) break;  // wave-uniform: the arrays stay in registers
+      cnt[t] += __popcll(__ballot(tq == t));
+    }
   }
   int first[kMaxTypes];  // candidates of lower types
   int acc = 0;
@@ -314,6 +317,7 @@ __device__ void nl_place(const NlParams& np, int i, int n, const NlKey* s, int* 
       const int jq = q < n ? s[q].j : -1;
 #pragma unroll
       for (int t = 0; t < kMaxTypes; ++t) {
+        if (t >= np.ntypes) break;
         const unsigned long long m = __ballot(tq == t);
         const int pos = put[t] + __popcll(m & ((1ull << lane) - 1ull));
         if (tq == t && pos < np.sel[t]) row[np.sec[t] + pos] = jq;
