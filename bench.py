@@ -41,6 +41,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 PEAK_FP64_MFMA = 78.6e12   # FLOP/s, MI355X dense FP64 matrix
 PEAK_HBM = 8.0e12          # B/s
 PEAK_FP32_MFMA = 157.3e12  # FLOP/s, MI355X dense FP32 matrix
+PEAK_FP32_VALU = 157.3e12  # FLOP/s, MI355X FP32 vector
 DT_FS = {0: 0.5, 1: 0.5, 2: 1.0, 3: 1.0, 4: 0.5}
 KIND = {0: "water", 1: "water", 2: "cu", 3: "hea", 4: "water"}
 # config 3 is specified in mixed precision (fp32 nets, fp64 env/force/virial)
@@ -191,13 +192,7 @@ def run_config(dp, hip, config, steps, warmup):
     for k, t in stage_ms.items():
         entry = {"ms": round(t, 4)}
         if k in work and t > 0:
-            kind, amount = work[k]
-            if kind == "flop":
-                entry.update(tflops=round(amount / (t * 1e-3) / 1e12, 3),
-                             frac=round(amount / (t * 1e-3) / peak_mfma, 4))
-            else:
-                entry.update(gbs=round(amount / (t * 1e-3) / 1e9, 1),
-                             frac=round(amount / (t * 1e-3) / PEAK_HBM, 4))
+            priced(entry, *work[k], t, peak_mfma)
         stages[k] = entry
     return dict(n=n, ms=ms, ms_sync=ms_sync, ms_host=ms_host, stage_ms=stage_ms, stages=stages,
                 work=work,
@@ -207,23 +202,45 @@ def run_config(dp, hip, config, steps, warmup):
                 device_bytes=pot.device_bytes(), mb=mb, coord=coord, atype=atype, box=box)
 
 
-def c4_work(n, n_edges):
-    """Algorithmic HBM bytes of the DPA4C passes for one step: the moment and
-    edge-gradient passes read each edge's list index (4 B) and neighbour
-    coordinates (24 B) and the node's 44-float record (176 B); the edge pass
-    writes the fp64 gradient (24 B); the node pass reads the moments and
-    writes the cotangents and the energy."""
+def c4_work(n, n_edges, hidden):
+    """Algorithmic work of the DPA4C passes for one step on the standalone
+    path. Bytes are the unique data a pass must move: the list (4 B per edge),
+    coordinates (24 B per atom), the 44-float moment / cotangent records
+    (176 B per atom), forces (24 B), atom virials (72 B) and the centre-side
+    partials (96 B) per atom; neighbour records re-read per edge come from
+    the caches. The node pass (readout, fitting forward and input gradient,
+    readout VJP; one thread per atom) is priced against the FP32 vector peak
+    with the fitting's 2 (70 H + H) multiply-adds each way per atom. The edge
+    gradients have no pass of their own here: the fused edge/force kernel
+    (under "force") evaluates both directions of every edge."""
     return {
-        "embed_fwd": ("byte", 28.0 * n_edges + 176.0 * n),
-        "fitting": ("byte", (176.0 * 2 + 8.0) * n),
-        "embed_bwd": ("byte", 52.0 * n_edges + 176.0 * n),
-        "force": ("byte", 28.0 * n_edges + 24.0 * n),
+        "embed_fwd": ("byte", 4.0 * n_edges + (24.0 + 176.0) * n),
+        "fitting": ("valu", 2.0 * 2.0 * (70.0 * hidden + hidden) * n),
+        "force": ("byte", 4.0 * n_edges + (24.0 + 176.0 + 24.0 + 72.0 + 96.0) * n),
         "nlist": ("byte", 4.0 * n_edges + 24.0 * n),
     }
 
 
 C4_STAGE_NAMES = {"embed_fwd": "moments", "fitting": "node (readout + fitting + VJP)",
-                  "embed_bwd": "edge_grad"}
+                  "force": "fused edge gradient + force / virial (both directions)"}
+
+
+def priced(entry, kind, amount, t_ms, peak_mfma):
+    """Achieved rate and fraction of the bounding peak; a fraction above 1
+    means the timed interval does not contain that work, and is not reported
+    as one."""
+    t = t_ms * 1e-3
+    if kind == "flop":
+        entry.update(tflops=round(amount / t / 1e12, 3), frac=round(amount / t / peak_mfma, 4))
+    elif kind == "valu":
+        entry.update(tflops=round(amount / t / 1e12, 3), bound="fp32 valu",
+                     frac=round(amount / t / PEAK_FP32_VALU, 4))
+    else:
+        entry.update(gbs=round(amount / t / 1e9, 1), frac=round(amount / t / PEAK_HBM, 4))
+    if entry["frac"] > 1.0:
+        entry["frac"] = None
+        entry["error"] = "above peak: the timed interval does not hold this work"
+    return entry
 
 
 def run_c4(dp, hip, name, steps, warmup):
@@ -261,17 +278,16 @@ def run_c4(dp, hip, name, steps, warmup):
     pot.sync()
     stage_ms = dict(pot.stage_times())
     pot.enable_stage_timing(False)
-    work = c4_work(n, n_edges)
+    work = c4_work(n, n_edges, pot.info.fit[0])
     stages = {}
     for k, t in stage_ms.items():
-        if k in ("descriptor", "dE_dT"):
-            continue  # the DPA4C path has no such stage
+        if k in ("descriptor", "dE_dT", "embed_bwd"):
+            continue  # no such pass on the DPA4C standalone path
         entry = {"ms": round(t, 4)}
         if k in C4_STAGE_NAMES:
             entry["kernel"] = C4_STAGE_NAMES[k]
         if k in work and t > 0:
-            entry.update(gbs=round(work[k][1] / (t * 1e-3) / 1e9, 1),
-                         frac=round(work[k][1] / (t * 1e-3) / PEAK_HBM, 4))
+            priced(entry, *work[k], t, PEAK_FP32_MFMA)
         stages[k] = entry
     return {"workload": f"{name} DPA4C-Nano FCC Cu-Ni {n} atoms, rcut 6, 8 channels, "
                         f"lmax 2, fitting 70-96-1",
@@ -281,10 +297,33 @@ def run_c4(dp, hip, name, steps, warmup):
             "device_bytes_peak": pot.device_bytes(), "stages": stages}
 
 
+def cpu_model():
+    """The host CPU's model name (first /proc/cpuinfo entry)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def timed_median(fn, runs=3):
+    """One untimed warm-up call, then the median of `runs` timed calls (s)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2], ts
+
+
 def cpu_baseline_c4(name):
     """The DPA4C oracle (torch fp64 on the host cores, autograd gradients) on
-    the whole `name` workload, one evaluation: ghosts, strict-cutoff edges,
-    descriptor, fitting, forces."""
+    the whole `name` workload: ghosts, strict-cutoff edges, descriptor,
+    fitting, forces; one warm-up and the median of three evaluations."""
     import torch
     sys.path.insert(0, ROOT)
     from _pkg import load_pkg
@@ -292,41 +331,42 @@ def cpu_baseline_c4(name):
     dp = load_pkg()
     coord, atype, box = dp.systems.build_c4(name)
     O = dpa4c_oracle.Dpa4cOracle(dp.dpa4c.to_bytes(dp.dpa4c.random_model("cuni", seed=2000)))
-    t0 = time.perf_counter()
-    O.compute(coord, atype, box)
-    t = time.perf_counter() - t0
+    t, ts = timed_median(lambda: O.compute(coord, atype, box))
     n = len(atype)
     return {"value": round(t * 1e6 / n, 3), "unit": "us/step/atom",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"DPA4C oracle (torch fp64, CPU) on all {n} atoms of {name}, one "
-                      f"evaluation ({t:.1f} s)"}
+            "cores": torch.get_num_threads(), "kind": "port", "cpu": cpu_model(),
+            "sample": f"DPA4C oracle (torch fp64, CPU) on all {n} atoms of {name}: one warm-up, "
+                      f"median of 3 evaluations ({', '.join(f'{x:.2f}' for x in ts)} s)"}
 
 
-def cpu_baseline(mb, coord, atype, box, target_s=12.0):
-    """fp64 CPU restatement (oracle/) on a bounded sample of centres: ghosts for
-    the whole box, then neighbour list + full evaluation of the first K centres."""
+def cpu_baseline(mb, coord, atype, box, target_s=4.0):
+    """fp64 CPU restatement (oracle/, C + OpenMP over centres) on a bounded
+    sample of centres: ghosts for the whole box, then neighbour list + full
+    evaluation of the first K centres, K sized for about target_s seconds;
+    one warm-up and the median of three timed samples."""
     from _pkg import load_oracle
     orc = load_oracle()
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
     O = orc.Oracle(mb)
 
     def sample(K):
-        t0 = time.perf_counter()
         ext, et, _ = O.ghosts(coord, atype, box, O.m["rcut"])
         off, cand = O.candidates(K, ext, et, O.m["rcut"], "cell")
         nl = O.format_nlist(K, ext, et, off, cand)
         O.eval_ext(K, ext, et, nl, nthreads=threads, want_atomic=False)
-        return time.perf_counter() - t0
 
     n = len(atype)
     k0 = min(n, 256)
-    t0 = sample(k0)
+    t0 = time.perf_counter()
+    sample(k0)
+    t0 = time.perf_counter() - t0
     K = int(min(n, max(k0, k0 * target_s / max(t0, 1e-6))))
-    t = sample(K)
+    t, ts = timed_median(lambda: sample(K))
     return {"value": round(t * 1e6 / K, 3), "unit": "us/step/atom", "cores": threads,
-            "kind": "port",
+            "kind": "port", "cpu": cpu_model(),
             "sample": f"oracle fp64 se_e2_a: ghosts of all {n} atoms + nlist and full "
-                      f"evaluation of the first {K} centres ({t:.1f} s), per centre"}
+                      f"evaluation of the first {K} centres; one warm-up, median of 3 "
+                      f"({', '.join(f'{x:.2f}' for x in ts)} s), per centre"}
 
 
 def main():

@@ -107,9 +107,11 @@ struct dp_model {
   int type_off[kMaxTypes + 1] = {0};
   int nbucket = 0;
   bool buckets_valid = false;
-  // LAMMPS candidate cache
+  // LAMMPS candidate cache: the caller's list uploaded at ago == 0, valid
+  // for the same nloc and nall until a rebuild (the edge entry points reuse
+  // the same buffers and invalidate it)
   bool cand_valid = false;
-  int cand_nloc = -1;
+  int cand_nloc = -1, cand_nall = -1;
   // last evaluation sizes (debug copies); on the standalone path last_nall is
   // the capacity of the extended arrays and the count itself is in nall_d
   int last_nloc = 0, last_nall = 0;
@@ -966,6 +968,8 @@ void edges_step(dp_model* M, double* d_atom_energy, double* d_force, double* d_a
   int* rank = need<int>(M, M->cell_rank, (size_t)std::max(nedge, 1));
   long* cand_off = need<long>(M, M->cand_off, (size_t)nloc + 1);
   int* cand = need<int>(M, M->cand, (size_t)std::max(nedge, 1));
+  // the edge graph's candidates overwrite a cached LAMMPS list
+  M->cand_valid = false;
   launch_fill_int(st, (long)nloc + 1, 0, count);
   launch_edges_ext<T>(st, nloc, nedge, nnode, d_edge_index, d_edge_vec, d_atype, ext, ext_type,
                       mapping, count, rank, status);
@@ -1304,7 +1308,7 @@ int dp_compute_nlist(dp_model* M, int nall, int nghost, const double* coord, con
       DPAMD_HIP(hipMemcpyAsync(ext, coord, sizeof(double) * 3 * nall, hipMemcpyHostToDevice, st));
       DPAMD_HIP(hipMemcpyAsync(ext_type, atype, sizeof(int) * nall, hipMemcpyHostToDevice, st));
     }
-    if (ago == 0 || !M->cand_valid || M->cand_nloc != nloc) {
+    if (ago == 0 || !M->cand_valid || M->cand_nloc != nloc || M->cand_nall != nall) {
       std::vector<long> off(nloc + 1, 0);
       std::vector<int> cnt(nloc, 0);
       for (int ii = 0; ii < inum; ++ii) {
@@ -1330,6 +1334,7 @@ int dp_compute_nlist(dp_model* M, int nall, int nghost, const double* coord, con
       DPAMD_HIP(hipStreamSynchronize(st));
       M->cand_valid = true;
       M->cand_nloc = nloc;
+      M->cand_nall = nall;
     }
     record(M, st, kStGeom + 1);
     const NlParams np = nl_params(M);

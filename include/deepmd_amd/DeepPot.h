@@ -1,9 +1,10 @@
 // deepmd_amd/DeepPot.h — header-only C++ façade over dp_amd.h that keeps the
-// surface `pair_style deepmd` calls on the reference's deepmd::DeepPot
-// (deepmd-op/overlays/api_cc/include/DeepPot.h:451-926) and the upstream
-// InputNlist type (fields evidenced at lammps-deepmd-plugin/src/pair_deepmd.cpp:355-364).
-// Failures throw deepmd::deepmd_exception, which the pair style turns into
-// error->one (pair_deepmd.cpp:372-374).
+// surface `pair_style deepmd` calls on the reference's deepmd::DeepPot and
+// deepmd::DeepPotModelDevi (deepmd-op/overlays/api_cc/include/DeepPot.h:451-926,
+// :928-1104), on top of the model-base types of DeepBaseModel.h. pair_deepmd.h
+// of the reference plugin (lammps-deepmd-plugin/src/pair_deepmd.h:16-28,
+// :55-56) includes this header under that name and declares a
+// deepmd_compat::DeepPot and a deepmd_compat::DeepPotModelDevi.
 //
 // Link with -ldpamd. The interface is double precision; the float overloads
 // convert at the boundary, as the reference's compute<float> does. The
@@ -12,71 +13,26 @@
 // precision is a property of the trained model, so init() keeps the
 // reference's three arguments and reads the choice from the environment
 // variable DPAMD_PRECISION ("fp64" or "mixed") unless it is passed explicitly.
+//
+// Frames: the std::vector<ENERGYTYPE> overloads take nframes configurations
+// back to back (coord nframes x natoms x 3, box nframes x 9 or empty) and
+// evaluate them one after another; compute_mixed_type also takes per-frame
+// types (atype nframes x natoms). With a neighbour list every frame uses the
+// caller's list, the first with the caller's `ago`, the others as cached
+// (ago = 1: re-filtered on that frame's positions).
 #pragma once
 
-#include <cstdlib>
-#include <cstring>
-#include <stdexcept>
-#include <cstdint>
-#include <string>
-#include <vector>
-
-#include "../dp_amd.h"
+#include "DeepBaseModel.h"
 
 namespace deepmd {
 
-typedef double ENERGYTYPE;
-
-class deepmd_exception : public std::runtime_error {
- public:
-  explicit deepmd_exception(const std::string& msg) : std::runtime_error(msg) {}
-};
-
-// LAMMPS neighbour list handed to the model (full list, with skin). The
-// communication fields are carried for source compatibility; this build is
-// single-rank and does not read them.
-struct InputNlist {
-  int inum = 0;
-  int* ilist = nullptr;
-  int* numneigh = nullptr;
-  int** firstneigh = nullptr;
-  int nswap = 0;
-  int* sendnum = nullptr;
-  int* recvnum = nullptr;
-  int* firstrecv = nullptr;
-  int** sendlist = nullptr;
-  int* sendproc = nullptr;
-  int* recvproc = nullptr;
-  void* world = nullptr;
-  int nprocs = 1;
-  int mask = 0;
-  int* mapping = nullptr;
-  InputNlist() = default;
-  InputNlist(int inum_, int* ilist_, int* numneigh_, int** firstneigh_)
-      : inum(inum_), ilist(ilist_), numneigh(numneigh_), firstneigh(firstneigh_) {}
-  InputNlist(int inum_, int* ilist_, int* numneigh_, int** firstneigh_, int nswap_,
-             int* sendnum_, int* recvnum_, int* firstrecv_, int** sendlist_, int* sendproc_,
-             int* recvproc_, void* world_, int nprocs_ = 1)
-      : inum(inum_), ilist(ilist_), numneigh(numneigh_), firstneigh(firstneigh_),
-        nswap(nswap_), sendnum(sendnum_), recvnum(recvnum_), firstrecv(firstrecv_),
-        sendlist(sendlist_), sendproc(sendproc_), recvproc(recvproc_), world(world_),
-        nprocs(nprocs_) {}
-  void set_mask(int m) { mask = m; }
-  void set_mapping(int* m) { mapping = m; }
-};
-
-class DeepPot {
+class DeepPot : public DeepBaseModel {
  public:
   DeepPot() = default;
   DeepPot(const std::string& model, const int& gpu_rank = 0,
           const std::string& file_content = "") {
     init(model, gpu_rank, file_content);
   }
-  ~DeepPot() {
-    if (h_) dp_destroy(h_);
-  }
-  DeepPot(const DeepPot&) = delete;
-  DeepPot& operator=(const DeepPot&) = delete;
 
   void init(const std::string& model, const int& gpu_rank = 0,
             const std::string& file_content = "", int precision = -1) {
@@ -104,18 +60,11 @@ class DeepPot {
     dp_get_info(h_, &info_);
   }
 
-  double cutoff() const { return info_.rcut; }
-  int numb_types() const { return info_.ntypes; }
-  int numb_types_spin() const { return 0; }
-  int dim_fparam() const { return info_.dim_fparam; }
-  int dim_aparam() const { return info_.dim_aparam; }
-  int dim_chg_spin() const { return 0; }
-  void get_type_map(std::string& type_map) const {
-    type_map.clear();
-    for (int t = 0; t < info_.ntypes; ++t) {
-      if (t) type_map += " ";
-      type_map += info_.type_map[t];
-    }
+  // Neither model family has a charge / spin input (dim_chg_spin() == 0):
+  // only the empty condition is accepted.
+  void set_charge_spin(const std::vector<double>& charge_spin) {
+    if (!charge_spin.empty())
+      throw deepmd_exception("DeePMD-kit (MI355X): the model has no charge/spin input");
   }
 
   // compute(ener, force, virial, coord, atype, box[, fparam, aparam, charge_spin])
@@ -165,6 +114,112 @@ class DeepPot {
                const std::vector<double>& charge_spin = std::vector<double>()) {
     compute_nlist_impl(ener, force, virial, atom_energy, atom_virial, true, coord, atype, box,
                        nghost, lmp_list, ago, fparam, aparam, charge_spin);
+  }
+
+  // Frames back to back: ener[nframes], force nframes x natoms x 3, virial
+  // nframes x 9 (DeepPot.h:492-502, :539-549, :577-587, :631-644 of the
+  // reference api_cc/include).
+  template <typename VALUETYPE>
+  void compute(std::vector<ENERGYTYPE>& ener, std::vector<VALUETYPE>& force,
+               std::vector<VALUETYPE>& virial, const std::vector<VALUETYPE>& coord,
+               const std::vector<int>& atype, const std::vector<VALUETYPE>& box,
+               const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    std::vector<VALUETYPE> ae, av;
+    frames_impl(ener, force, virial, ae, av, false, coord, atype, false, box, nullptr, 0, 0,
+                fparam, aparam, charge_spin);
+  }
+  template <typename VALUETYPE>
+  void compute(std::vector<ENERGYTYPE>& ener, std::vector<VALUETYPE>& force,
+               std::vector<VALUETYPE>& virial, std::vector<VALUETYPE>& atom_energy,
+               std::vector<VALUETYPE>& atom_virial, const std::vector<VALUETYPE>& coord,
+               const std::vector<int>& atype, const std::vector<VALUETYPE>& box,
+               const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    frames_impl(ener, force, virial, atom_energy, atom_virial, true, coord, atype, false, box,
+                nullptr, 0, 0, fparam, aparam, charge_spin);
+  }
+  template <typename VALUETYPE>
+  void compute(std::vector<ENERGYTYPE>& ener, std::vector<VALUETYPE>& force,
+               std::vector<VALUETYPE>& virial, const std::vector<VALUETYPE>& coord,
+               const std::vector<int>& atype, const std::vector<VALUETYPE>& box,
+               const int nghost, const InputNlist& lmp_list, const int& ago,
+               const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    std::vector<VALUETYPE> ae, av;
+    frames_impl(ener, force, virial, ae, av, false, coord, atype, false, box, &lmp_list, nghost,
+                ago, fparam, aparam, charge_spin);
+  }
+  template <typename VALUETYPE>
+  void compute(std::vector<ENERGYTYPE>& ener, std::vector<VALUETYPE>& force,
+               std::vector<VALUETYPE>& virial, std::vector<VALUETYPE>& atom_energy,
+               std::vector<VALUETYPE>& atom_virial, const std::vector<VALUETYPE>& coord,
+               const std::vector<int>& atype, const std::vector<VALUETYPE>& box,
+               const int nghost, const InputNlist& lmp_list, const int& ago,
+               const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    frames_impl(ener, force, virial, atom_energy, atom_virial, true, coord, atype, false, box,
+                &lmp_list, nghost, ago, fparam, aparam, charge_spin);
+  }
+  // Per-frame types (atype nframes x natoms), DeepPot.h:700-760 of the
+  // reference api_cc/include; the scalar-energy forms take one frame.
+  template <typename VALUETYPE>
+  void compute_mixed_type(ENERGYTYPE& ener, std::vector<VALUETYPE>& force,
+                          std::vector<VALUETYPE>& virial, const int& nframes,
+                          const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+                          const std::vector<VALUETYPE>& box,
+                          const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+                          const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+                          const std::vector<double>& charge_spin = std::vector<double>()) {
+    std::vector<ENERGYTYPE> e;
+    std::vector<VALUETYPE> ae, av;
+    one_frame(nframes);
+    frames_impl(e, force, virial, ae, av, false, coord, atype, true, box, nullptr, 0, 0, fparam,
+                aparam, charge_spin);
+    ener = e[0];
+  }
+  template <typename VALUETYPE>
+  void compute_mixed_type(std::vector<ENERGYTYPE>& ener, std::vector<VALUETYPE>& force,
+                          std::vector<VALUETYPE>& virial, const int& nframes,
+                          const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+                          const std::vector<VALUETYPE>& box,
+                          const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+                          const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+                          const std::vector<double>& charge_spin = std::vector<double>()) {
+    std::vector<VALUETYPE> ae, av;
+    frames_impl(ener, force, virial, ae, av, false, coord, atype, true, box, nullptr, 0, 0,
+                fparam, aparam, charge_spin, nframes);
+  }
+  template <typename VALUETYPE>
+  void compute_mixed_type(ENERGYTYPE& ener, std::vector<VALUETYPE>& force,
+                          std::vector<VALUETYPE>& virial, std::vector<VALUETYPE>& atom_energy,
+                          std::vector<VALUETYPE>& atom_virial, const int& nframes,
+                          const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+                          const std::vector<VALUETYPE>& box,
+                          const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+                          const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+                          const std::vector<double>& charge_spin = std::vector<double>()) {
+    std::vector<ENERGYTYPE> e;
+    one_frame(nframes);
+    frames_impl(e, force, virial, atom_energy, atom_virial, true, coord, atype, true, box,
+                nullptr, 0, 0, fparam, aparam, charge_spin);
+    ener = e[0];
+  }
+  template <typename VALUETYPE>
+  void compute_mixed_type(std::vector<ENERGYTYPE>& ener, std::vector<VALUETYPE>& force,
+                          std::vector<VALUETYPE>& virial, std::vector<VALUETYPE>& atom_energy,
+                          std::vector<VALUETYPE>& atom_virial, const int& nframes,
+                          const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+                          const std::vector<VALUETYPE>& box,
+                          const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+                          const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+                          const std::vector<double>& charge_spin = std::vector<double>()) {
+    frames_impl(ener, force, virial, atom_energy, atom_virial, true, coord, atype, true, box,
+                nullptr, 0, 0, fparam, aparam, charge_spin, nframes);
   }
 
   // Device-resident step on device pointers (dp_compute_device, or with
@@ -240,17 +295,63 @@ class DeepPot {
   bool uses_fp32_edge_vectors() const { return info_.model_kind == DP_MODEL_DPA4C; }
   bool supports_device_edge_inference() const { return true; }
 
-  dp_model* handle() const { return h_; }
-
  private:
-  dp_model* h_ = nullptr;
-  dp_model_info info_{};
-
-  void check(int rc) const {
-    if (rc != DP_OK) throw deepmd_exception(std::string("DeePMD-kit (MI355X): ") + dp_last_error(h_));
+  static void one_frame(int nframes) {
+    if (nframes != 1)
+      throw deepmd_exception("DeePMD-kit (MI355X): a scalar energy holds one frame, got " +
+                             std::to_string(nframes));
   }
-  void require_init() const {
-    if (!h_) throw deepmd_exception("DeePMD-kit (MI355X): model not initialised");
+  // nframes_given > 0 (mixed-type form): atype holds nframes x natoms types;
+  // otherwise the types are shared and nframes follows from coord.
+  template <typename V>
+  void frames_impl(std::vector<ENERGYTYPE>& ener, std::vector<V>& force, std::vector<V>& virial,
+                   std::vector<V>& atom_energy, std::vector<V>& atom_virial, bool atomic,
+                   const std::vector<V>& coord, const std::vector<int>& atype, bool typed_frames,
+                   const std::vector<V>& box, const InputNlist* nl, int nghost, int ago,
+                   const std::vector<V>& fparam, const std::vector<V>& aparam,
+                   const std::vector<double>& cs, int nframes_given = 1) {
+    require_init();
+    size_t nframes = 1, natoms = atype.size();
+    if (typed_frames) {
+      if (nframes_given <= 0 || atype.size() % (size_t)nframes_given)
+        throw deepmd_exception("atype size must be nframes * natoms");
+      nframes = (size_t)nframes_given;
+      natoms = atype.size() / nframes;
+    } else if (natoms > 0) {
+      if (coord.size() % (3 * natoms)) throw deepmd_exception("coord size must be nframes * natoms * 3");
+      nframes = coord.size() / (3 * natoms);
+    } else if (!box.empty()) {
+      nframes = box.size() / 9;
+    }
+    if (coord.size() != nframes * natoms * 3)
+      throw deepmd_exception("coord size must be nframes * natoms * 3");
+    if (!box.empty() && box.size() != 9 * nframes)
+      throw deepmd_exception("box size must be nframes * 9");
+    ener.assign(nframes, 0.0);
+    force.clear();
+    virial.clear();
+    atom_energy.clear();
+    atom_virial.clear();
+    for (size_t f = 0; f < nframes; ++f) {
+      const std::vector<V> c(coord.begin() + f * natoms * 3, coord.begin() + (f + 1) * natoms * 3);
+      const std::vector<int> t = typed_frames
+          ? std::vector<int>(atype.begin() + f * natoms, atype.begin() + (f + 1) * natoms)
+          : atype;
+      const std::vector<V> b = box.empty() ? std::vector<V>()
+                                           : std::vector<V>(box.begin() + f * 9, box.begin() + (f + 1) * 9);
+      std::vector<V> ff, vv, ae, av;
+      if (nl)
+        compute_nlist_impl(ener[f], ff, vv, ae, av, atomic, c, t, b, nghost, *nl, f ? 1 : ago,
+                           fparam, aparam, cs);
+      else
+        compute_impl(ener[f], ff, vv, ae, av, atomic, c, t, b, fparam, aparam, cs);
+      force.insert(force.end(), ff.begin(), ff.end());
+      virial.insert(virial.end(), vv.begin(), vv.end());
+      if (atomic) {
+        atom_energy.insert(atom_energy.end(), ae.begin(), ae.end());
+        atom_virial.insert(atom_virial.end(), av.begin(), av.end());
+      }
+    }
   }
   template <typename V>
   static void no_params(const std::vector<V>& fparam, const std::vector<V>& aparam,
@@ -334,6 +435,117 @@ class DeepPot {
       from_double(atom_energy, ae);
       from_double(atom_virial, av);
     }
+  }
+};
+
+// Several models on the same configuration (pair_deepmd.cpp:426-442 calls
+// compute with every model's outputs, :493-530 the deviation statistics).
+class DeepPotModelDevi : public DeepBaseModelDevi {
+ public:
+  DeepPotModelDevi() = default;
+  DeepPotModelDevi(const std::vector<std::string>& models, const int& gpu_rank = 0,
+                   const std::vector<std::string>& file_contents = std::vector<std::string>()) {
+    init(models, gpu_rank, file_contents);
+  }
+  // Every model is loaded onto the same GPU; they must agree on the cutoff
+  // and the number of types, as one neighbour list serves them all.
+  void init(const std::vector<std::string>& models, const int& gpu_rank = 0,
+            const std::vector<std::string>& file_contents = std::vector<std::string>()) {
+    if (models.empty()) throw deepmd_exception("DeePMD-kit (MI355X): no models given");
+    if (!file_contents.empty() && file_contents.size() != models.size())
+      throw deepmd_exception("DeePMD-kit (MI355X): one file content per model expected");
+    dps.clear();
+    dpbases.clear();
+    for (size_t k = 0; k < models.size(); ++k) {
+      auto p = std::make_shared<DeepPot>();
+      p->init(models[k], gpu_rank, file_contents.empty() ? std::string() : file_contents[k]);
+      if (k && (p->cutoff() != dps[0]->cutoff() || p->numb_types() != dps[0]->numb_types()))
+        throw deepmd_exception("DeePMD-kit (MI355X): models differ in cutoff or type count");
+      dps.push_back(p);
+      dpbases.push_back(p);
+    }
+    numb_models = (unsigned)dps.size();
+  }
+  int dim_chg_spin() const { return numb_models > 0 ? dps[0]->dim_chg_spin() : 0; }
+  void set_charge_spin(const std::vector<double>& charge_spin) {
+    for (auto& p : dps) p->set_charge_spin(charge_spin);
+  }
+
+  template <typename VALUETYPE>
+  void compute(std::vector<ENERGYTYPE>& all_ener, std::vector<std::vector<VALUETYPE>>& all_force,
+               std::vector<std::vector<VALUETYPE>>& all_virial,
+               const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+               const std::vector<VALUETYPE>& box,
+               const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    each(all_ener, all_force, all_virial, [&](DeepPot& d, ENERGYTYPE& e, std::vector<VALUETYPE>& f,
+                                              std::vector<VALUETYPE>& v, size_t) {
+      d.compute(e, f, v, coord, atype, box, fparam, aparam, charge_spin);
+    });
+  }
+  template <typename VALUETYPE>
+  void compute(std::vector<ENERGYTYPE>& all_ener, std::vector<std::vector<VALUETYPE>>& all_force,
+               std::vector<std::vector<VALUETYPE>>& all_virial,
+               std::vector<std::vector<VALUETYPE>>& all_atom_energy,
+               std::vector<std::vector<VALUETYPE>>& all_atom_virial,
+               const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+               const std::vector<VALUETYPE>& box,
+               const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    all_atom_energy.assign(models(), {});
+    all_atom_virial.assign(models(), {});
+    each(all_ener, all_force, all_virial, [&](DeepPot& d, ENERGYTYPE& e, std::vector<VALUETYPE>& f,
+                                              std::vector<VALUETYPE>& v, size_t k) {
+      d.compute(e, f, v, all_atom_energy[k], all_atom_virial[k], coord, atype, box, fparam,
+                aparam, charge_spin);
+    });
+  }
+  template <typename VALUETYPE>
+  void compute(std::vector<ENERGYTYPE>& all_ener, std::vector<std::vector<VALUETYPE>>& all_force,
+               std::vector<std::vector<VALUETYPE>>& all_virial,
+               const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+               const std::vector<VALUETYPE>& box, const int nghost, const InputNlist& lmp_list,
+               const int& ago, const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    each(all_ener, all_force, all_virial, [&](DeepPot& d, ENERGYTYPE& e, std::vector<VALUETYPE>& f,
+                                              std::vector<VALUETYPE>& v, size_t) {
+      d.compute(e, f, v, coord, atype, box, nghost, lmp_list, ago, fparam, aparam, charge_spin);
+    });
+  }
+  template <typename VALUETYPE>
+  void compute(std::vector<ENERGYTYPE>& all_ener, std::vector<std::vector<VALUETYPE>>& all_force,
+               std::vector<std::vector<VALUETYPE>>& all_virial,
+               std::vector<std::vector<VALUETYPE>>& all_atom_energy,
+               std::vector<std::vector<VALUETYPE>>& all_atom_virial,
+               const std::vector<VALUETYPE>& coord, const std::vector<int>& atype,
+               const std::vector<VALUETYPE>& box, const int nghost, const InputNlist& lmp_list,
+               const int& ago, const std::vector<VALUETYPE>& fparam = std::vector<VALUETYPE>(),
+               const std::vector<VALUETYPE>& aparam = std::vector<VALUETYPE>(),
+               const std::vector<double>& charge_spin = std::vector<double>()) {
+    all_atom_energy.assign(models(), {});
+    all_atom_virial.assign(models(), {});
+    each(all_ener, all_force, all_virial, [&](DeepPot& d, ENERGYTYPE& e, std::vector<VALUETYPE>& f,
+                                              std::vector<VALUETYPE>& v, size_t k) {
+      d.compute(e, f, v, all_atom_energy[k], all_atom_virial[k], coord, atype, box, nghost,
+                lmp_list, ago, fparam, aparam, charge_spin);
+    });
+  }
+
+ protected:
+  std::vector<std::shared_ptr<DeepPot>> dps;
+
+ private:
+  template <typename V, class Fn>
+  void each(std::vector<ENERGYTYPE>& all_ener, std::vector<std::vector<V>>& all_force,
+            std::vector<std::vector<V>>& all_virial, Fn&& fn) {
+    if (dps.empty()) throw deepmd_exception("DeePMD-kit (MI355X): no models initialised");
+    all_ener.assign(dps.size(), 0.0);
+    all_force.assign(dps.size(), {});
+    all_virial.assign(dps.size(), {});
+    for (size_t k = 0; k < dps.size(); ++k) fn(*dps[k], all_ener[k], all_force[k], all_virial[k], k);
   }
 };
 

@@ -178,3 +178,26 @@ def test_edges_mixed_precision(dp, orc):
     df = f - ref["force"]
     assert np.sqrt((df ** 2).mean()) <= 4e-5 and np.abs(df).max() <= 5e-4
     assert np.abs(df).max() > 0.0  # the fp32 nets ran
+
+
+def test_edges_then_cached_lammps_list(dp, orc):
+    """The edge entry points build their candidates in the buffers that cache
+    a LAMMPS list between rebuilds; a list call with ago > 0 after an edge
+    call on the same handle must not format the edge graph's candidates
+    against the caller's atoms (it re-uploads the caller's list instead)."""
+    from cases import lammps_inputs
+    (coord, atype, box), m = CASES["water192"]()
+    mb = model_bytes(m)
+    O = orc.Oracle(mb)
+    ext, et, mp, ilist, numneigh, firstneigh = lammps_inputs(O, coord, atype, box)
+    nloc, nall = len(atype), len(et)
+    pot = dp.DeepPot(file_content=mb)
+    e0, f0, v0 = pot.compute_nlist(ext, et, box, nall - nloc, ilist, numneigh, firstneigh, ago=0)
+    nl0 = pot.stage(dp.STAGE_NLIST, np.int32, (nloc, O.nnei)).copy()
+    # an edge call with the same nloc in between
+    _, _, _, ei, vec = _edges(orc, coord, atype, box, O.m["rcut"])
+    _run(dp, pot, ei, vec, atype, nloc, nloc)
+    e1, f1, v1 = pot.compute_nlist(ext, et, box, nall - nloc, ilist, numneigh, firstneigh, ago=1)
+    assert np.array_equal(pot.stage(dp.STAGE_NLIST, np.int32, (nloc, O.nnei)), nl0)
+    assert e1 == e0
+    assert np.array_equal(f1, f0) and np.array_equal(v1, v0)

@@ -2,8 +2,9 @@
 
 Full-size parity: neighbour lists bit-exact against the oracle's cell list,
 full E/F/V against the oracle on the 12,288-atom water box, and on the large
-systems atom energies of a sample of centres plus size-independent properties
-(sum of forces, virial symmetry, sum of atom virials). Tolerances as in
+systems the atom energies and edge gradients of the first and last 512
+centres plus size-independent properties (sum of forces, virial symmetry,
+sum of atom virials). Tolerances as in
 test_gpu_parity.py (fp64: 1e-10 eV/atom, 1e-8 eV/A, 1e-8 eV)."""
 import hashlib
 import importlib
@@ -15,7 +16,7 @@ import numpy as np
 import pytest
 
 from cases import CASES, model_bytes
-from test_native import build_facade, write_input
+from test_native import build_facade, build_pair_shape, write_input
 
 pytestmark = pytest.mark.gpu
 
@@ -80,6 +81,44 @@ def test_cpp_facade_on_gpu(dp, orc, tmp_path):
     assert abs(float.fromhex(lines["ENL"][0]) - ref2["energy"]) / len(atype) <= E_TOL
 
 
+def test_pair_style_shape_on_gpu(dp, orc, tmp_path):
+    """The pair style's model members driven through every branch it takes
+    (single model with and without a list, model deviation of two models):
+    energies against the oracle, deviation statistics against numpy on the
+    oracle's forces and virials of both models."""
+    exe = build_pair_shape(tmp_path)
+    (coord, atype, box), m = CASES["water192"]()
+    m2 = dict(m)
+    m2["fit_params"] = m["fit_params"] * 1.01
+    pa, pb = tmp_path / "a.dp", tmp_path / "b.dp"
+    dp.model.write_model(str(pa), m)
+    dp.model.write_model(str(pb), m2)
+    write_input(tmp_path / "in.bin", coord, atype, box)
+    r = subprocess.run([str(exe), "run", str(pa), str(pb), str(tmp_path / "in.bin")],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    out = {ln.split()[0]: ln.split()[1:] for ln in r.stdout.splitlines() if ln[:1].isupper()}
+    n = len(atype)
+    ref = orc.Oracle(model_bytes(m)).compute(coord, atype, box)
+    assert abs(float.fromhex(out["E"][0]) - ref["energy"]) / n <= E_TOL
+    # list path: the input taken as an open system (no ghosts)
+    res = []
+    for mm in (m, m2):
+        O = orc.Oracle(model_bytes(mm))
+        off, cand = O.candidates(n, coord, atype, O.m["rcut"], "brute")
+        res.append(O.eval_ext(n, coord, atype, O.format_nlist(n, coord, atype, off, cand)))
+    assert abs(float.fromhex(out["ENL"][0]) - res[0]["energy"]) / n <= E_TOL
+    ea, eb = (float.fromhex(x) for x in out["DEVI_E"])
+    assert abs(ea - res[0]["energy"]) / n <= E_TOL and abs(eb - res[1]["energy"]) / n <= E_TOL
+    fs = np.stack([x["force"] for x in res])
+    std_f = np.sqrt(((fs - fs.mean(0)) ** 2).sum(2).mean(0))
+    fmax, fmean = (float.fromhex(x) for x in out["DEVI_F"])
+    assert fmax == pytest.approx(std_f.max(), rel=1e-6) and fmean == pytest.approx(std_f.mean(), rel=1e-6)
+    vs = np.stack([x["virial"] for x in res]) / n
+    assert float.fromhex(out["DEVI_V"][0]) == pytest.approx(
+        (np.sqrt(((vs - vs.mean(0)) ** 2).mean(0)) / (np.abs(vs.mean(0)) + 0.1)).max(), rel=1e-6)
+
+
 def _full(dp, orc, cfg):
     coord, atype, box = dp.systems.build(cfg)
     mb = dp.model.to_bytes(dp.model.random_model(KIND[cfg], seed=1000 + cfg))
@@ -89,11 +128,11 @@ def _full(dp, orc, cfg):
     ext, et, mp, nl = O.neighbor_list(coord, atype, box)
     gnl = pot.stage(dp.STAGE_NLIST, np.int32, nl.shape)
     assert np.array_equal(gnl, nl), "full-size neighbour list differs"
-    return O, (coord, atype, box), (e, f, v, ae, av), (ext, et, mp, nl)
+    return O, pot, (coord, atype, box), (e, f, v, ae, av), (ext, et, mp, nl)
 
 
 def test_full_water12k_all_outputs(dp, orc):
-    O, (coord, atype, box), (e, f, v, ae, av), _ = _full(dp, orc, 1)
+    O, _, (coord, atype, box), (e, f, v, ae, av), _ = _full(dp, orc, 1)
     ref = O.compute(coord, atype, box)
     n = len(atype)
     assert abs(e - ref["energy"]) / n <= E_TOL
@@ -103,13 +142,34 @@ def test_full_water12k_all_outputs(dp, orc):
     assert np.abs(av - ref["atom_virial"]).max() <= V_TOL
 
 
+def _sample(O, ext, et, nl, idx):
+    """Oracle evaluation of the centres idx alone: copies of them are put
+    first in the extended arrays and their neighbour indices shifted past the
+    copies, so eval_ext sees them as its K local atoms."""
+    K = len(idx)
+    ext2 = np.concatenate([ext[idx], ext])
+    et2 = np.concatenate([et[idx], et]).astype(np.int32)
+    nl2 = np.where(nl[idx] >= 0, nl[idx] + K, -1).astype(np.int32)
+    return O.eval_ext(K, ext2, et2, nl2)
+
+
+def sample_centres(n, K=512):
+    """The first and the last K centres: the top of the index range exercises
+    the largest offsets into the per-slot buffers."""
+    return np.concatenate([np.arange(K), np.arange(n - K, n)])
+
+
 @pytest.mark.parametrize("cfg", [2, 3, 4])
 def test_full_size_sample_and_invariants(dp, orc, cfg):
-    O, (coord, atype, box), (e, f, v, ae, av), (ext, et, mp, nl) = _full(dp, orc, cfg)
-    K = 1024
-    sample = O.eval_ext(K, ext, et, nl[:K])
-    assert np.abs(ae[:K] - sample["atom_energy"]).max() <= E_TOL
+    """Atom energies and edge gradients (the backward's output, per slot) of
+    1,024 centres against the oracle, plus the size-independent properties."""
+    O, pot, (coord, atype, box), (e, f, v, ae, av), (ext, et, mp, nl) = _full(dp, orc, cfg)
     n = len(atype)
+    idx = sample_centres(n)
+    ref = _sample(O, ext, et, nl, idx)
+    assert np.abs(ae[idx] - ref["atom_energy"]).max() <= E_TOL
+    eg = pot.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))[idx]
+    assert np.abs(eg - ref["edge_grad"]).max() <= 1e-11
     assert np.abs(f.sum(0)).max() <= 1e-12 * n
     W = v.reshape(3, 3)
     assert np.abs(W - W.T).max() <= 1e-9 * max(1.0, np.abs(W).max())

@@ -106,18 +106,34 @@ def test_mixed_lammps_path(dp, orc):
     _check(nloc, _volume(box), got, ref, "hea1024/lammps")
 
 
-def test_mixed_full_size_hea128k(dp):
+def test_mixed_full_size_hea128k(dp, orc):
     """Config 3 at its full size (128,000-atom HEA, the configuration the
     mixed mode is specified for): mixed against this library's fp64 result,
-    which the fp64 tests hold to the oracle, to the same limits."""
+    which the fp64 tests hold to the oracle, to the same limits; and the atom
+    energies and edge gradients of the first and last 512 centres against
+    the fp64 oracle itself (edge gradients to the force limits)."""
+    from test_gpu_fullsize import _sample, sample_centres
     coord, atype, box = dp.systems.build(3)
     mb = dp.model.to_bytes(dp.model.random_model("hea", seed=1003))
     ref64 = dp.DeepPot(file_content=mb).compute(coord, atype, box, atomic=True)
     ref = {"energy": ref64[0], "force": ref64[1], "virial": ref64[2], "atom_energy": ref64[3]}
-    got = dp.DeepPot(file_content=mb, precision=dp.PREC_MIXED).compute(coord, atype, box,
-                                                                       atomic=True)
+    pot = dp.DeepPot(file_content=mb, precision=dp.PREC_MIXED)
+    got = pot.compute(coord, atype, box, atomic=True)
     _check(len(atype), _volume(box), got, ref, "hea128k")
     assert np.abs(got[1].sum(0)).max() <= 1e-10 * len(atype)
+    O = orc.Oracle(mb)
+    ext, et, mp, nl = O.neighbor_list(coord, atype, box)
+    n = len(atype)
+    assert np.array_equal(pot.stage(dp.STAGE_NLIST, np.int32, nl.shape), nl)
+    idx = sample_centres(n)
+    r = _sample(O, ext, et, nl, idx)
+    dae = float(np.abs(got[3][idx] - r["atom_energy"]).max())
+    deg = pot.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))[idx] - r["edge_grad"]
+    print(f"hea128k sample vs oracle: atom energy max {dae:.2e} eV, edge grad rmse "
+          f"{np.sqrt((deg ** 2).mean()):.2e} max {np.abs(deg).max():.2e} eV/A", flush=True)
+    assert dae <= E_ATOM
+    assert np.sqrt((deg ** 2).mean()) <= F_RMSE and np.abs(deg).max() <= F_MAX
+    assert np.abs(deg).max() > 0.0
 
 
 def test_mixed_device_entry_point_and_reproducible(dp):

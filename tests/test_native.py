@@ -89,6 +89,26 @@ def build_facade(tmp_path):
     return exe
 
 
+def build_pair_shape(tmp_path):
+    """The pair-style member check, compiled the way the reference plugin is
+    (LMPPLUGIN: headers found by their bare names on the include path)."""
+    exe = tmp_path / "pair_shape_check"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-Wall", "-Werror",
+                    "-I", os.path.join(ROOT, "include", "deepmd_amd"),
+                    os.path.join(ROOT, "tests", "native", "pair_shape_check.cpp"), "-o", str(exe),
+                    "-L", PKG_DIR, "-ldpamd", f"-Wl,-rpath,{PKG_DIR}"], check=True)
+    return exe
+
+
+def test_pair_style_members_compile_and_deviation_statistics(tmp_path):
+    """The façade hosts pair_base.h / pair_deepmd.h's model members (the
+    translation unit compiles only if every bound type and called method
+    exists) and the model-deviation statistics match their closed forms."""
+    exe = build_pair_shape(tmp_path)
+    r = subprocess.run([str(exe), "stats"], capture_output=True, text=True)
+    assert r.returncode == 0 and "STATS OK" in r.stdout, r.stdout + r.stderr
+
+
 def write_input(path, coord, atype, box):
     with open(path, "wb") as f:
         f.write(np.int32(len(atype)).tobytes())

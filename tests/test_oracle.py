@@ -196,6 +196,58 @@ def test_virial_is_minus_strain_derivative(orc, case):
     assert np.abs(out["force"].sum(0)).max() < 1e-10
 
 
+def test_atom_virial_split_and_orientation(dp, orc):
+    """Per-atom virial pinned element by element, not only through its sum.
+
+    One oxygen centre carries all the energy: the hydrogen fitting net and its
+    bias_atom_e are zero, so every hydrogen's atom energy is exactly 0 and so
+    are the gradients of the edges it centres. Each edge (0 -> j) then carries
+    g_j = dE/d(x_j - x_0) = -F_j, and F_j is taken here by central differences
+    of the energy, independently of the oracle's backward. The reference
+    charges -g (x) d to the edge's neighbour (source) atom with row = gradient
+    component (deepmd-op/overlays/op/pt/edge_force_virial.cu:8-9, :138-146),
+    so atom_virial[j][3c + d] = F_j[c] (x_j - x_0)[d] and the centre gets 0.
+    Charging the centre, or transposing the 3x3, fails here: the expected
+    matrices are far from symmetric because se_e2_a edge gradients are not
+    radial."""
+    m = dp.model.random_model("water", seed=11)
+    m["fit_params"][1, :] = 0.0
+    m["bias_atom_e"][1] = 0.0
+    O = orc.Oracle(model_bytes(m))
+    ext0 = np.array([[0.0, 0.0, 0.0],
+                     [0.93, 0.31, -0.22],
+                     [-0.41, 1.17, 0.35],
+                     [2.10, -1.30, 1.90],
+                     [-1.70, -2.40, -0.80],
+                     [0.60, 3.10, -2.70]])
+    et = np.array([0, 1, 1, 1, 1, 1], np.int32)
+    n = len(et)
+
+    def run(ext):
+        off, cand = O.candidates(n, ext, et, O.m["rcut"], "brute")
+        return O.eval_ext(n, ext, et, O.format_nlist(n, ext, et, off, cand))
+
+    out = run(ext0)
+    assert np.all(out["atom_energy"][1:] == 0.0)
+    av = out["atom_virial"].reshape(n, 3, 3)
+    assert np.all(av[0] == 0.0)
+    h = 1e-5
+    asym = 0.0
+    for j in range(1, n):
+        fj = np.zeros(3)
+        for c in range(3):
+            ep = ext0.copy(); ep[j, c] += h
+            em = ext0.copy(); em[j, c] -= h
+            fj[c] = -(run(ep)["energy"] - run(em)["energy"]) / (2 * h)
+        np.testing.assert_allclose(out["force"][j], fj, rtol=0, atol=1e-7)
+        expect = np.outer(fj, ext0[j] - ext0[0])
+        np.testing.assert_allclose(av[j], expect, rtol=0, atol=1e-6)
+        asym = max(asym, np.abs(expect - expect.T).max())
+    # the transposed split would miss by far more than the tolerance
+    assert asym > 100 * 1e-6
+    np.testing.assert_allclose(av.sum(0).reshape(9), out["virial"], rtol=0, atol=1e-12)
+
+
 def test_invariances(dp, orc, water):
     O, coord, atype, box = water
     e0 = O.compute(coord, atype, box)
