@@ -74,8 +74,14 @@ def flops_bytes(pot, n_real, nloc, nb_edges, mixed=False):
         "fitting": ("flop", fit * nloc),
         # reads dE/dD and T, writes dE/dT
         "dE_dT": ("byte", es * nloc * (Dn + 4 * L3 + 4 * L3)),
-        # edge gradient (24 B) + reverse index (4 B) per edge, force 24 B per atom
-        "force": ("byte", 28.0 * nb_edges + 24.0 * nloc),
+        # fp64: the edges are scattered inside the embedding backward (fixed
+        # point); this stage folds ghost sums onto owners and assembles per
+        # atom the section sums (96 B per section), the fixed-point force
+        # (24 B), the force (24 B) and the centre partials (96 B). Mixed: the
+        # reverse-list gather reads each edge gradient (24 B) and its index
+        # (4 B) and writes the force (24 B per atom)
+        "force": ("byte", 28.0 * nb_edges + 24.0 * nloc) if mixed else
+                 ("byte", (96.0 * nt + 24.0 + 24.0 + 96.0) * nloc),
         "nlist": ("byte", 4.0 * nloc * pot.nnei + 24.0 * nloc),
     }
     if nt > 1:
@@ -339,7 +345,7 @@ def cpu_baseline_c4(name):
                       f"median of 3 evaluations ({', '.join(f'{x:.2f}' for x in ts)} s)"}
 
 
-def cpu_baseline(mb, coord, atype, box, target_s=4.0):
+def cpu_baseline(mb, coord, atype, box, target_s=6.0):
     """fp64 CPU restatement (oracle/, C + OpenMP over centres) on a bounded
     sample of centres: ghosts for the whole box, then neighbour list + full
     evaluation of the first K centres, K sized for about target_s seconds;

@@ -34,7 +34,7 @@ EXPORTED = ("dp_create", "dp_destroy", "dp_get_info", "dp_last_error", "dp_compu
             "dp_compute_nlist", "dp_compute_device", "dp_compute_device_async", "dp_sync",
             "dp_graph_stats", "dp_compute_canonical_graph_device", "dp_compute_edges_device",
             "dp_compute_edges_device_f32",
-            "dp_debug_copy", "dp_stage_times", "dp_device_bytes")
+            "dp_debug_copy", "dp_debug_keep", "dp_stage_times", "dp_device_bytes")
 
 
 class DeepmdException(RuntimeError):
@@ -75,6 +75,7 @@ def lib():
         L.dp_compute_edges_device_f32.argtypes = [P, P, P, P, P, P, P, P, I, I, I, P]
         L.dp_debug_copy.argtypes = [P, I, P, C.c_size_t]
         L.dp_debug_copy.restype = C.c_long
+        L.dp_debug_keep.argtypes = [P, I]
         L.dp_stage_times.argtypes = [P, I, P, I, P, C.c_size_t]
         L.dp_device_bytes.argtypes = [P]
         L.dp_device_bytes.restype = C.c_size_t
@@ -257,6 +258,11 @@ class DeepPot:
         if got < 0:
             self._check(int(got))
         return out
+
+    def keep_stages(self, on=True):
+        """Store the per-slot edge gradients of the evaluations that follow, so
+        stage(STAGE_EDGE_GRAD) can return them (dp_debug_keep)."""
+        self._check(lib().dp_debug_keep(self._h, 1 if on else 0))
 
     def enable_stage_timing(self, on=True):
         times = (C.c_double * 16)()

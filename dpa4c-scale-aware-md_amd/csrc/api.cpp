@@ -99,7 +99,8 @@ struct dp_model {
   Buf coord_in, atype_in, sfrac, flags, gpos, ext, ext_type, mapping, cell_of, cell_count,
       cell_start, cell_rank, sorted, nlist, nreal, cand_off, cand, items, Tsec, Tt, D, dD, dT,
       fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_rank, rev, force_ws, av_ws,
-      ae_ws, partials, out10, status, scan_tmp, act, nall_d, split_ws, c4_mom, c4_cot;
+      ae_ws, partials, out10, status, scan_tmp, act, nall_d, split_ws, c4_mom, c4_cot, facc, vacc,
+      cpsec, ftgt, vtgt;
   size_t bytes_now = 0, bytes_peak = 0;
   // type buckets
   std::vector<int> atype_cache;
@@ -133,6 +134,11 @@ struct dp_model {
   int graph_warm = 0;
   long graph_captures = 0, graph_replays = 0;
   unsigned long buf_gen = 0, bucket_gen = 0;  // bumped by any reallocation / rebucketing
+  // dp_debug_keep: store the per-slot edge gradients (which the se_e2_a
+  // backward otherwise scatters without writing) for dp_debug_copy;
+  // eg_valid: the last evaluation left them in edge_grad
+  bool keep_edge_grad = false;
+  bool eg_valid = false;
   // stage timers
   bool timing = false;
   // one event set per evaluation in a ring, so that evaluations queued by
@@ -152,7 +158,7 @@ struct dp_model {
             &dD,       &dT,       &fitb,      &e_bucket, &edge_grad,  &cpart,     &rev_count,
             &rev_off,  &rev_rank, &rev,       &force_ws, &av_ws,      &ae_ws,     &partials,
             &out10,    &status,   &scan_tmp, &act,       &nall_d,    &split_ws,  &c4_mom,
-            &c4_cot};
+            &c4_cot,   &facc,     &vacc,      &cpsec,      &ftgt,      &vtgt};
   }
 };
 
@@ -310,10 +316,14 @@ DescArgs desc_args(dp_model* M, void* Tt, void* D) {
 
 void gather_and_reduce(dp_model* M, hipStream_t st, int nloc, int ntarget, const int* d_mapping,
                        const double* e_vals, int ne, const int* items, const Outputs& out);
+void reduce_outputs(dp_model* M, hipStream_t st, int nloc, int ntarget, const double* e_vals,
+                    int ne, const int* items, const Outputs& out);
 
+// nall: extended atoms, or (d_nall non-null, standalone path) their
+// capacity with the count itself on the device.
 template <class E>
-void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_mapping,
-                 int ntarget, const Outputs& out) {
+void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_nall,
+                 const int* d_mapping, int ntarget, const Outputs& out) {
   constexpr bool f32 = sizeof(E) == 4;
   const ModelHost& m = M->host;
   const int nt = m.ntypes, nnei = m.nnei, L3 = m.emb[2], axis = m.axis, Dn = L3 * axis;
@@ -334,7 +344,18 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   const int Fmax = std::max(m.fit[0], std::max(m.fit[1], m.fit[2]));
   E* fitb = need<E>(M, M->fitb, (size_t)8 * std::max(nb, 1) * Fmax);
   double* e_bucket = need<double>(M, M->e_bucket, (size_t)std::max(nb, 1));
-  double* edge_grad = need<double>(M, M->edge_grad, (size_t)nloc * nnei * 3);
+  // fp64: the backward scatters each edge's forces itself (fixed point) and
+  // stores g only when kept; fp32 (mixed): the backward stores g and the
+  // reverse-list gather assembles the forces (a separate atomic pass was
+  // slower there: global atomics run at ~30 G/s on this device, and inside
+  // the fp32 backward they hold up its just-in-time activation loads)
+  double* edge_grad = (f32 || M->keep_edge_grad)
+                          ? need<double>(M, M->edge_grad, (size_t)std::max(nloc, 1) * nnei * 3)
+                          : nullptr;
+  const size_t nfix = (size_t)std::max(std::max(nall, ntarget), 1);
+  auto* facc = f32 ? nullptr : need<unsigned long long>(M, M->facc, nfix * 3);
+  auto* vacc = (!f32 && out.atom_virial) ? need<unsigned long long>(M, M->vacc, nfix * 9) : nullptr;
+  double* cpsec = f32 ? nullptr : need<double>(M, M->cpsec, (size_t)std::max(nloc, 1) * nt * 12);
 
   EmbArgs ea{};
   ea.ntypes = nt;
@@ -358,6 +379,9 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   ea.Tsec = Tsec;
   ea.dT = dT;
   ea.edge_grad = edge_grad;
+  ea.facc = facc;
+  ea.vacc = vacc;
+  ea.cpsec = cpsec;
   ea.Tt = nt == 1 ? static_cast<void*>(Tt) : nullptr;
   ea.ldt = 4L * nb;
   ea.tpad = M->d_tpad;
@@ -476,16 +500,54 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_m
   launch_dT(st, nb, L3, axis, items, Tt, dD, dT);
   record(M, st, kStDT + 1);
 
+  if (f32) {
+    nblk = block_table(embed_waves_bwd(M->el, f32));
+    launch_embed_bwd(st, M->el, ea, nblk, f32);
+    M->eg_valid = true;
+    record(M, st, kStEmbBwd + 1);
+    gather_and_reduce(M, st, nloc, ntarget, d_mapping, e_bucket, nb, items, out);
+    (void)nall;
+    return;
+  }
+  // the fixed-point sums start at zero (a kernel, so that the step can be
+  // captured in a graph); on the standalone path over the ghosts counted on
+  // the device
+  const long nzero = std::max(nall, ntarget);
+  launch_zero_u64(st, nzero, d_nall, 3, facc);
+  if (vacc) launch_zero_u64(st, nzero, d_nall, 9, vacc);
   nblk = block_table(embed_waves_bwd(M->el, f32));
   launch_embed_bwd(st, M->el, ea, nblk, f32);
+  M->eg_valid = edge_grad != nullptr;
   record(M, st, kStEmbBwd + 1);
-  gather_and_reduce(M, st, nloc, ntarget, d_mapping, e_bucket, nb, items, out);
+  const int nsec = nt;
+  double* cpart = need<double>(M, M->cpart, (size_t)std::max(nloc, 1) * 12);
+  const unsigned long long *fsum = facc, *vsum = vacc;
+  if (d_mapping && ntarget == nloc) {
+    // every owner is local: ghost sums folded in place
+    launch_fold_fixed(st, nloc, nall, d_nall, d_mapping, facc, vacc, facc, vacc);
+  } else if (d_mapping) {
+    // owners beyond the locals (the edge graph's kept ghost nodes) share
+    // indices with extended atoms: fold every atom into separate target sums
+    auto* ft = need<unsigned long long>(M, M->ftgt, (size_t)std::max(ntarget, 1) * 3);
+    auto* vt = vacc ? need<unsigned long long>(M, M->vtgt, (size_t)std::max(ntarget, 1) * 9) : nullptr;
+    launch_zero_u64(st, ntarget, nullptr, 3, ft);
+    if (vt) launch_zero_u64(st, ntarget, nullptr, 9, vt);
+    launch_fold_fixed(st, 0, nall, d_nall, d_mapping, facc, vacc, ft, vt);
+    fsum = ft;
+    vsum = vt;
+  }
+  launch_force_finalize(st, ntarget, nloc, nsec, static_cast<const int*>(M->ext_type.p), cpsec,
+                        fsum, vsum, out.force, out.atom_virial, cpart);
+  record(M, st, kStForce + 1);
+  reduce_outputs(M, st, nloc, ntarget, e_bucket, nb, items, out);
   (void)nall;
 }
 
-// Reverse list + force / atom-virial gather from the edge gradients, then the
-// energy / virial reduction. Atom energies e_vals[0..ne) are in bucket order
-// (items maps a position to its atom) or, with items null, in atom order.
+// Reverse list + force / atom-virial gather from stored edge gradients (the
+// mixed-precision se_e2_a path and the DPA4C edge-gradient paths), then the
+// energy / virial reduction. Atom
+// energies e_vals[0..ne) are in bucket order (items maps a position to its
+// atom) or, with items null, in atom order.
 void gather_and_reduce(dp_model* M, hipStream_t st, int nloc, int ntarget, const int* d_mapping,
                        const double* e_vals, int ne, const int* items, const Outputs& out) {
   const int nnei = M->host.nnei;
@@ -510,7 +572,14 @@ void gather_and_reduce(dp_model* M, hipStream_t st, int nloc, int ntarget, const
   launch_force_gather(st, ntarget, nloc, nnei, roff, rev, nlist, ext, edge_grad, cpart,
                       out.force, out.atom_virial, status);
   record(M, st, kStForce + 1);
+  reduce_outputs(M, st, nloc, ntarget, e_vals, ne, items, out);
+}
 
+// Energy and frame virial from the atom energies and the centre partials
+// cpart, copied into the caller's outputs.
+void reduce_outputs(dp_model* M, hipStream_t st, int nloc, int ntarget, const double* e_vals,
+                    int ne, const int* items, const Outputs& out) {
+  const double* cpart = static_cast<const double*>(M->cpart.p);
   double* partials = need<double>(M, M->partials, 256 * 10);
   double* out10 = need<double>(M, M->out10, 10);
   launch_reduce_ev(st, ne, nloc, e_vals, cpart, partials, out10);
@@ -562,6 +631,7 @@ void run_c4(dp_model* M, hipStream_t st, int nloc, const int* d_mapping, int nta
     double* cpart = need<double>(M, M->cpart, (size_t)std::max(nloc, 1) * 12);
     launch_c4_edge_force(st, M->c4p, src, nloc, d_mapping, cot, out.force, out.atom_virial,
                          cpart);
+    M->eg_valid = false;
     record(M, st, kStForce + 1);
     double* partials = need<double>(M, M->partials, 256 * 10);
     double* out10 = need<double>(M, M->out10, 10);
@@ -578,6 +648,7 @@ void run_c4(dp_model* M, hipStream_t st, int nloc, const int* d_mapping, int nta
   }
   double* eg = need<double>(M, M->edge_grad, (size_t)std::max(nloc, 1) * m.nnei * 3);
   launch_c4_edge_grad(st, M->c4p, src, nloc, cot, eg);
+  M->eg_valid = true;
   record(M, st, kStEmbBwd + 1);
   gather_and_reduce(M, st, nloc, ntarget, d_mapping, e, nloc, nullptr, out);
 }
@@ -589,8 +660,12 @@ void run_model(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_map
                const Outputs& out, bool complete) {
   if (M->kind == dp_model::kDpa4c)
     return run_c4(M, st, nloc, d_mapping, ntarget, out, complete && d_mapping && ntarget == nloc);
-  if (M->precision == DP_PREC_MIXED) run_model_t<float>(M, st, nloc, nall, d_mapping, ntarget, out);
-  else run_model_t<double>(M, st, nloc, nall, d_mapping, ntarget, out);
+  // the standalone path counts its ghosts on the device
+  const int* d_nall = complete ? static_cast<const int*>(M->nall_d.p) : nullptr;
+  if (M->precision == DP_PREC_MIXED)
+    run_model_t<float>(M, st, nloc, nall, d_nall, d_mapping, ntarget, out);
+  else
+    run_model_t<double>(M, st, nloc, nall, d_nall, d_mapping, ntarget, out);
 }
 
 // Neighbour-list parameters of the model. DPA4C keeps r^2 < rcut^2 (strict,
@@ -1405,6 +1480,7 @@ int dp_compute_canonical_graph_device(dp_model* M, double* d_atom_energy, double
     record(M, st, kStDT + 1);
     launch_c4_edge_grad(st, M->c4p, g, nloc, cot, eg);
     launch_c4_zero_tail(st, g.row_ptr, nloc, edge_storage, eg);
+    M->eg_valid = true;
     record(M, st, kStEmbBwd + 1);
     launch_c4_graph_force(st, nall_nodes, g.row_ptr, reinterpret_cast<const long*>(d_source_row_ptr),
                           d_source_order, d_edge_vec, eg, edge_storage, d_force, d_atom_virial,
@@ -1513,7 +1589,13 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
         break;
       case DP_STAGE_C4_MOMENTS: copy(M->c4_mom.p, (size_t)nloc * kC4Mom * 4); break;
       case DP_STAGE_C4_COTANGENTS: copy(M->c4_cot.p, (size_t)nloc * kC4Mom * 4); break;
-      case DP_STAGE_EDGE_GRAD: copy(M->edge_grad.p, (size_t)nloc * m.nnei * 24); break;
+      case DP_STAGE_EDGE_GRAD:
+        if (!M->eg_valid)
+          throw ApiError{DP_ERR_ARG,
+                         "edge gradients were not stored: call dp_debug_keep(handle, 1) before "
+                         "the evaluation"};
+        copy(M->edge_grad.p, (size_t)nloc * m.nnei * 24);
+        break;
       default: throw ApiError{DP_ERR_ARG, "unknown stage"};
     }
   });
@@ -1542,5 +1624,11 @@ int dp_stage_times(dp_model* M, int enable, double* times, int n, char* names, s
 }
 
 size_t dp_device_bytes(const dp_model* M) { return M ? M->bytes_peak : 0; }
+
+int dp_debug_keep(dp_model* M, int keep) {
+  if (!M) return DP_ERR_ARG;
+  M->keep_edge_grad = keep != 0;
+  return DP_OK;
+}
 
 }  // extern "C"

@@ -61,10 +61,12 @@ constexpr int x1_stash_doubles() {
   return (S::RES2 != 0 && !S::X1_ALIGNED) ? 16 * (S::K2P + 1) : 0;
 }
 
+// ... | per wave: section-sum cells [16 slot lanes][12] (edge_out) and the
+// neighbour indices of the current and the next tile, int [2][16]
 template <class S>
 constexpr int bwd_lds_doubles(int waves) {
   return (S::SIZE + 31) / 32 * 32 + 8 + waves * 4 * (S::L3P + S::L2P) +
-         waves * x1_stash_doubles<S>();
+         waves * x1_stash_doubles<S>() + waves * (16 * 12 + 16);
 }
 
 template <class S, int WAVES>
@@ -312,6 +314,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   // layer-1 stash (see x1_stash_doubles)
   double* X1s = lds + PS + 8 + WAVES * 4 * (S::L3P + S::L2P) + w * x1_stash_doubles<S>();
   constexpr int X1LD = S::K2P + 1;
+  double* own_w = lds + PS + 8 + WAVES * 4 * (S::L3P + S::L2P) + WAVES * x1_stash_doubles<S>() +
+                  w * (16 * 12 + 16);
+  int* jbuf = reinterpret_cast<int*>(own_w + 16 * 12);
 
   const int p = find_pair(a);
   const int ti = p / a.ntypes, tj = p % a.ntypes;
@@ -319,6 +324,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     const double* src = static_cast<const double*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
     if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
+    for (int q = lane; q < 16 * 12; q += 64) own_w[q] = 0.0;
   }
   __syncthreads();
   const int nitems = a.type_off[ti + 1] - a.type_off[ti];
@@ -364,6 +370,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     // consumed after the layer-2 and layer-3 products: their latency is covered
     // by those products and by the other wave of the SIMD. Holding them a whole
     // tile ahead would need the registers of that second wave.
+    // The neighbour index of each slot is parked in LDS (jbuf, by tile
+    // parity) when its coordinates are fetched, for the slot's output.
     double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
     int jn = c < nr ? row[c] : 0;
     if (c < nr) {
@@ -371,9 +379,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       nx1 = a.ext[3 * (long)jn + 1];
       nx2 = a.ext[3 * (long)jn + 2];
     }
+    if (g == 0) jbuf[c] = jn;
     jn = 16 + c < nr ? row[16 + c] : 0;
 
     for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
+      const int par = (tile >> 4) & 1;
       const int slot = tile + c;
       const bool valid = slot < nr;
       double th2[S::NT2][4], th3[S::NU3][4];
@@ -397,6 +407,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         nx0 = a.ext[3 * (long)jn];
         nx1 = a.ext[3 * (long)jn + 1];
         nx2 = a.ext[3 * (long)jn + 2];
+        if (g == 0) jbuf[16 * (par ^ 1) + c] = jn;
       }
       jn = slot + 32 < nr ? row[slot + 32] : 0;
       const double s = Rn[0];
@@ -551,19 +562,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         nd[0] += (Rn[0] * vp[0] + Rn[1] * vp[1] + Rn[2] * vp[2] + Rn[3] * vp[3]) * a.inv_nnei;
         double gv[3];
         env_grad(d0, d1, d2, a.rcut_smth, a.rcut, sd, nd, gv);
-        double* eg = a.edge_grad + (ebase + slot) * 3;
-        eg[0] = gv[0];
-        eg[1] = gv[1];
-        eg[2] = gv[2];
+        const double dv[3] = {d0, d1, d2};
+        edge_out(a, ebase + slot, jbuf[16 * par + c], dv, gv, own_w + 12 * c);
       }
     }
-    // padded slots carry no gradient
-    for (int sl = nr + lane; sl < a.sel[tj]; sl += 64) {
-      double* eg = a.edge_grad + (ebase + sl) * 3;
-      eg[0] = 0.0;
-      eg[1] = 0.0;
-      eg[2] = 0.0;
-    }
+    own_flush(a, i, tj, nr, ebase, own_w, lane);
   }
 }
 

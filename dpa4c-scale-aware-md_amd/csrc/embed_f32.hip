@@ -508,6 +508,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
         nd[0] += (Rn[0] * (double)vp[0] + Rn[1] * (double)vp[1] + Rn[2] * (double)vp[2] +
                   Rn[3] * (double)vp[3]) *
                  a.inv_nnei;
+        // stored (coalesced); the forces are scattered from them by a
+        // streaming pass afterwards (launch_edge_scatter): atomics here would
+        // hold up the just-in-time activation loads behind them in the
+        // in-order memory counter
         double gv[3];
         env_grad(d0, d1, d2, a.rcut_smth, a.rcut, sd, nd, gv);
         double* eg = a.edge_grad + (ebase + slot) * 3;

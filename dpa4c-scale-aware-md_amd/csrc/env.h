@@ -4,6 +4,7 @@
 // kernels' block table.
 #pragma once
 
+#include "fixed.h"
 #include "kernels.h"
 
 namespace dpamd {
@@ -63,6 +64,67 @@ __device__ __forceinline__ void env_grad(double d0, double d1, double d2, double
   for (int mm = 0; mm < 3; ++mm) {
     const double ur = d[mm] * inv_r;
     gv[mm] = w0 * dR0_dr * ur + w[mm] * q + wd * dq_dr * ur;
+  }
+}
+
+// Output of one slot of the embedding backward, from the lane that holds the
+// slot's edge gradient g = dE/d(x_j - x_i), d = x_j - x_i, neighbour j
+// (extended-atom index). The centre side (force += g, frame virial -= g (x) d)
+// goes into the lane's private LDS cells own[12], added in tile order; the
+// neighbour side (force -= g, atom virial -= g (x) d, charged to the
+// neighbour as in deepmd-op/overlays/op/pt/edge_force_virial.cu:138-146) is
+// scattered in fixed point onto slot j. g itself is stored only when the
+// caller keeps edge gradients.
+__device__ __forceinline__ void edge_out(const EmbArgs& a, long e, int t, const double d[3],
+                                         const double gv[3], double* own) {
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    __hip_atomic_fetch_add(own + c, gv[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+      __hip_atomic_fetch_add(own + 3 + 3 * c + q, -gv[c] * d[q], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WAVEFRONT);
+  }
+  unsigned long long* fa = a.facc + 3L * t;
+  fixed_add(fa, gv[0]);
+  fixed_add(fa + 1, gv[1]);
+  fixed_add(fa + 2, gv[2]);
+  if (a.vacc) {
+    unsigned long long* va = a.vacc + 9L * t;
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) fixed_add(va + 3 * c + q, -gv[c] * d[q]);
+  }
+  if (a.edge_grad) {
+    double* eg = a.edge_grad + e * 3;
+    eg[0] = gv[0];
+    eg[1] = gv[1];
+    eg[2] = gv[2];
+  }
+}
+
+// End of an item (centre i, section tj): sums the 16 slot lanes' cells in a
+// fixed order into cpsec[i][tj][12] and clears them for the next item; zeroes
+// the kept edge gradients of the section's padded slots.
+__device__ __forceinline__ void own_flush(const EmbArgs& a, int i, int tj, int nr, long ebase,
+                                         double* own_w, int lane) {
+  wave_lds_sync();
+  if (lane < 12) {
+    double s = 0.0;
+    for (int k = 0; k < 16; ++k) s += own_w[12 * k + lane];
+    a.cpsec[((long)i * a.ntypes + tj) * 12 + lane] = s;
+  }
+  wave_lds_sync();
+  for (int q = lane; q < 16 * 12; q += 64) own_w[q] = 0.0;
+  wave_lds_sync();
+  if (a.edge_grad) {
+    for (int sl = nr + lane; sl < a.sel[tj]; sl += 64) {
+      double* eg = a.edge_grad + (ebase + sl) * 3;
+      eg[0] = 0.0;
+      eg[1] = 0.0;
+      eg[2] = 0.0;
+    }
   }
 }
 

@@ -13,9 +13,101 @@
 // :138-146 (dual-CSR gather, one warp per node there, one 64-lane wave here);
 // the frame virial is summed per centre from its own row. The frame sums
 // follow the fixed two-stage fp64 reduction of edge_force_virial.cu:187-256.
+#include "fixed.h"
 #include "kernels.h"
 
 namespace dpamd {
+
+// se_e2_a: the embedding backward leaves each centre's own-row sums per
+// neighbour section in cpsec [nloc][nsec][12] (fp64) and scatters every
+// edge's target side into fixed-point sums facc / vacc. One thread per target
+// atom: force = own sums (sections in order) - incoming sum; atom virial =
+// the incoming sum (charged to the neighbour); cpart = the own sums, which
+// the reduction turns into the frame virial. Centres of a negative type
+// (absent, "virtual" atoms) have no sections.
+__global__ __launch_bounds__(256) void k_force_finalize(int ntarget, int nloc, int nsec,
+                                                        const int* __restrict__ type,
+                                                        const double* __restrict__ cpsec,
+                                                        const unsigned long long* __restrict__ facc,
+                                                        const unsigned long long* __restrict__ vacc,
+                                                        double* __restrict__ force,
+                                                        double* __restrict__ atom_virial,
+                                                        double* __restrict__ cpart) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= ntarget) return;
+  double own[12];
+#pragma unroll
+  for (int q = 0; q < 12; ++q) own[q] = 0.0;
+  if (t < nloc) {
+    const int ns = type[t] >= 0 ? nsec : 0;
+    for (int sec = 0; sec < ns; ++sec) {
+      const double* cp = cpsec + ((long)t * nsec + sec) * 12;
+#pragma unroll
+      for (int q = 0; q < 12; ++q) own[q] += cp[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 12; ++q) cpart[(long)t * 12 + q] = own[q];
+  }
+#pragma unroll
+  for (int c = 0; c < 3; ++c) force[3L * t + c] = own[c] - from_fixed(facc[3L * t + c]);
+  if (atom_virial) {
+#pragma unroll
+    for (int q = 0; q < 9; ++q) atom_virial[9L * t + q] = from_fixed(vacc[9L * t + q]);
+  }
+}
+
+// Sums of extended atoms j in [j0, n) added onto their owners mapping[j] in
+// dst (which may be src itself when every owner is below j0).
+__global__ __launch_bounds__(256) void k_fold_fixed(int j0, int cap, const int* __restrict__ d_count,
+                                                    const int* __restrict__ mapping,
+                                                    const unsigned long long* src_f,
+                                                    const unsigned long long* src_v,
+                                                    unsigned long long* dst_f,
+                                                    unsigned long long* dst_v) {
+  const int n = d_count ? *d_count : cap;
+  const int j = j0 + blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const long t = mapping[j];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) atomicAdd(dst_f + 3 * t + c, src_f[3L * j + c]);
+  if (src_v) {
+#pragma unroll
+    for (int q = 0; q < 9; ++q) atomicAdd(dst_v + 9 * t + q, src_v[9L * j + q]);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_zero_u64(long cap, const int* __restrict__ d_count,
+                                                  int per, unsigned long long* __restrict__ p) {
+  const long n = (d_count ? (long)*d_count : cap) * per;
+  for (long q = (long)blockIdx.x * blockDim.x + threadIdx.x; q < n; q += (long)gridDim.x * blockDim.x)
+    p[q] = 0ull;
+}
+
+void launch_fold_fixed(hipStream_t st, int j0, int cap, const int* d_count, const int* mapping,
+                       const unsigned long long* src_f, const unsigned long long* src_v,
+                       unsigned long long* dst_f, unsigned long long* dst_v) {
+  if (cap <= j0 || !mapping) return;
+  hipLaunchKernelGGL(k_fold_fixed, dim3((cap - j0 + 255) / 256), dim3(256), 0, st, j0, cap, d_count,
+                     mapping, src_f, src_v, dst_f, dst_v);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_zero_u64(hipStream_t st, long cap, const int* d_count, int per, unsigned long long* p) {
+  if (cap <= 0) return;
+  const long blocks = std::min<long>((cap * per + 255) / 256, 2048);
+  hipLaunchKernelGGL(k_zero_u64, dim3((unsigned)blocks), dim3(256), 0, st, cap, d_count, per, p);
+  DPAMD_LAUNCH_CHECK();
+}
+
+void launch_force_finalize(hipStream_t st, int ntarget, int nloc, int nsec, const int* type,
+                           const double* cpsec, const unsigned long long* facc,
+                           const unsigned long long* vacc, double* force, double* atom_virial,
+                           double* cpart) {
+  if (ntarget <= 0) return;
+  hipLaunchKernelGGL(k_force_finalize, dim3((ntarget + 255) / 256), dim3(256), 0, st, ntarget,
+                     nloc, nsec, type, cpsec, facc, vacc, force, atom_virial, cpart);
+  DPAMD_LAUNCH_CHECK();
+}
 
 // The count keeps each edge's rank among the edges into its target (the value
 // its increment returned), so the fill is a plain scatter; that order is

@@ -59,7 +59,17 @@ struct EmbArgs {
   const int* items;    // centres grouped by type
   void* Tsec;          // forward out [nloc][ntypes][4][L3]
   const void* dT;      // backward in [nloc][4][L3]
-  double* edge_grad;   // backward out [nloc][nnei][3]
+  // Backward outputs. Each slot's edge gradient goes to its centre's
+  // section sums cpsec [nloc][ntypes][12] (force 3, frame virial 9, fp64)
+  // and, in fixed point (fixed.h), to its neighbour's extended-atom slot j:
+  // facc [nall][3] and, when non-null, vacc [nall][9]; both must start at
+  // zero (launch_fold_fixed then moves ghost sums onto their owners).
+  // edge_grad [nloc][nnei][3] is written only when non-null (kept for
+  // inspection).
+  double* edge_grad;
+  unsigned long long* facc;
+  unsigned long long* vacc;
+  double* cpsec;
   // Saved activations: per (centre, tile of 16 slots) a block of
   // 16*(L2P + L3P) doubles holding tanh of layers 2 and 3 in the backward's
   // register order; tiles of section tj start at tile_off[tj], tiles_per_atom
@@ -202,6 +212,23 @@ void launch_rev_count(hipStream_t, long nedge, int nnei, const int* nlist, const
                       int* count, int* rank);
 void launch_rev_fill(hipStream_t, long nedge, int nnei, const int* nlist, const int* mapping,
                      const int* off, const int* rank, int* rev);
+// Fixed-point sums src of extended atoms j in [j0, n) added onto their
+// owners mapping[j] in dst (integer atomics: order-independent); dst may be
+// src when every owner lies below j0. n = *d_count when d_count is given (a
+// count on the device, at most cap), else cap; src_v / dst_v may be null.
+void launch_fold_fixed(hipStream_t, int j0, int cap, const int* d_count, const int* mapping,
+                       const unsigned long long* src_f, const unsigned long long* src_v,
+                       unsigned long long* dst_f, unsigned long long* dst_v);
+// p[0 .. per * n) = 0 for 64-bit words, n = *d_count (at most cap) or cap
+void launch_zero_u64(hipStream_t, long cap, const int* d_count, int per, unsigned long long* p);
+// se_e2_a: forces, atom virials and the centre partials cpart [nloc][12]
+// from the embedding backward's section sums cpsec [nloc][nsec][12] and the
+// fixed-point target sums facc [ntarget][3], vacc [ntarget][9] (or null);
+// type [nloc]: centres of a negative type have no sections.
+void launch_force_finalize(hipStream_t, int ntarget, int nloc, int nsec, const int* type,
+                           const double* cpsec, const unsigned long long* facc,
+                           const unsigned long long* vacc, double* force, double* atom_virial,
+                           double* cpart);
 // cpart [nloc][12]: each centre's own-row force (3) and frame virial (9),
 // written by the gather and summed by the reduction.
 void launch_force_gather(hipStream_t, int ntarget, int nloc, int nnei, const int* rev_off,

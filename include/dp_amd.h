@@ -267,6 +267,13 @@ int dp_compute_edges_device_f32(dp_model* model, double* d_atom_energy, double* 
  * analogue is its DPA_DUMP_FRAME hook, graph_compress.cu:1354-1378). */
 long dp_debug_copy(dp_model* model, int stage, void* dst, size_t capacity);
 
+/* keep != 0: the evaluations that follow also store their per-slot edge
+ * gradients, so dp_debug_copy can return DP_STAGE_EDGE_GRAD (the se_e2_a
+ * force stage otherwise scatters them into the forces without writing them);
+ * keep == 0 (the default) switches that off again. No counterpart in the
+ * reference: a parity-test hook, like dp_debug_copy. */
+int dp_debug_keep(dp_model* model, int keep);
+
 /* Per-stage GPU time in milliseconds (hipEvent pairs) of the last synchronous
  * evaluation, or the mean over the evaluations queued by
  * dp_compute_device_async up to the last dp_sync, filled into times[0..n-1] in

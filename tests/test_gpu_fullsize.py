@@ -124,6 +124,7 @@ def _full(dp, orc, cfg):
     mb = dp.model.to_bytes(dp.model.random_model(KIND[cfg], seed=1000 + cfg))
     O = orc.Oracle(mb)
     pot = dp.DeepPot(file_content=mb)
+    pot.keep_stages(True)
     e, f, v, ae, av = pot.compute(coord, atype, box, atomic=True)
     ext, et, mp, nl = O.neighbor_list(coord, atype, box)
     gnl = pot.stage(dp.STAGE_NLIST, np.int32, nl.shape)

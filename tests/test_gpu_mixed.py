@@ -78,6 +78,7 @@ def test_mixed_stages(dp, orc, case):
     O = orc.Oracle(mb)
     ref = O.compute(coord, atype, box, want_internals=True)
     pot = dp.DeepPot(file_content=mb, precision=dp.PREC_MIXED)
+    pot.keep_stages(True)
     pot.compute(coord, atype, box)
     n = len(atype)
     d = pot.stage(dp.STAGE_DESCRPT, np.float64, (n, O.ndescrpt))
@@ -118,6 +119,7 @@ def test_mixed_full_size_hea128k(dp, orc):
     ref64 = dp.DeepPot(file_content=mb).compute(coord, atype, box, atomic=True)
     ref = {"energy": ref64[0], "force": ref64[1], "virial": ref64[2], "atom_energy": ref64[3]}
     pot = dp.DeepPot(file_content=mb, precision=dp.PREC_MIXED)
+    pot.keep_stages(True)
     got = pot.compute(coord, atype, box, atomic=True)
     _check(len(atype), _volume(box), got, ref, "hea128k")
     assert np.abs(got[1].sum(0)).max() <= 1e-10 * len(atype)

@@ -16,12 +16,14 @@ F_TOL = 1e-8    # eV/A
 V_TOL = 1e-8    # eV
 
 
-def _run(dp, orc, case):
+def _run(dp, orc, case, keep=False):
     (coord, atype, box), m = CASES[case]()
     mb = model_bytes(m)
     O = orc.Oracle(mb)
     ref = O.compute(coord, atype, box, want_internals=True)
     pot = dp.DeepPot(file_content=mb)
+    if keep:
+        pot.keep_stages(True)
     e, f, v, ae, av = pot.compute(coord, atype, box, atomic=True)
     return O, ref, pot, (e, f, v, ae, av), (coord, atype, box)
 
@@ -53,7 +55,7 @@ def test_energy_force_virial(dp, orc, case):
 
 @pytest.mark.parametrize("case", ["water192", "cu864"])
 def test_stage_parity(dp, orc, case):
-    O, ref, pot, _, (coord, atype, box) = _run(dp, orc, case)
+    O, ref, pot, (e, f, v, ae, av), (coord, atype, box) = _run(dp, orc, case, keep=True)
     n = len(atype)
     d = pot.stage(dp.STAGE_DESCRPT, np.float64, (n, O.ndescrpt))
     np.testing.assert_allclose(d, ref["descrpt"], rtol=0, atol=1e-12)
@@ -61,6 +63,13 @@ def test_stage_parity(dp, orc, case):
     np.testing.assert_allclose(dd, ref["dE_dD"], rtol=0, atol=1e-11)
     eg = pot.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))
     np.testing.assert_allclose(eg, ref["edge_grad"], rtol=0, atol=1e-11)
+    # keeping the edge gradients changes no output
+    pot2 = dp.DeepPot(file_content=model_bytes(CASES[case]()[1]))
+    e2, f2, v2, ae2, av2 = pot2.compute(coord, atype, box, atomic=True)
+    assert e2 == e and np.array_equal(f2, f) and np.array_equal(v2, v)
+    assert np.array_equal(av2, av)
+    with pytest.raises(dp.DeepmdException, match="dp_debug_keep"):
+        pot2.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))
 
 
 @pytest.mark.parametrize("case", ["water192", "hea1024"])
