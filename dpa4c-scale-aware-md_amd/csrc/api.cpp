@@ -81,6 +81,9 @@ struct dp_model {
   double* d_envp = nullptr;
   double* d_tpad = nullptr;
   void* d_fit = nullptr;
+  // fp64: the first fitting layer's weights of every type transposed,
+  // [nt][F0][L3 axis] (the fused dE/dD -> dE/dT kernel's operand), or null
+  double* d_w0t = nullptr;
   // mixed precision: per type and fitting layer, byte offsets into d_fitf of
   // the pre-split W (forward) and W^T (backward) fragments, -1 if absent
   void* d_fitf = nullptr;
@@ -139,6 +142,7 @@ struct dp_model {
   // eg_valid: the last evaluation left them in edge_grad
   bool keep_edge_grad = false;
   bool eg_valid = false;
+  bool dd_valid = false;  // dE/dD of the last evaluation is in dD
   // stage timers
   bool timing = false;
   // one event set per evaluation in a ring, so that evaluations queued by
@@ -339,7 +343,11 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   E* Tt = need<E>(M, M->Tt, (size_t)std::max(nb, 1) * 4 * L3);
   const bool d_from_t = axis == 16;
   E* D = d_from_t ? nullptr : need<E>(M, M->D, (size_t)std::max(nb, 1) * Dn);
-  E* dD = need<E>(M, M->dD, (size_t)std::max(nb, 1) * Dn);
+  // fp64 with the fused input-gradient kernel: dE/dD is not stored (only
+  // when kept for inspection)
+  const bool fused_ddt = !f32 && M->d_w0t && d_from_t;
+  E* dD = (!fused_ddt || M->keep_edge_grad) ? need<E>(M, M->dD, (size_t)std::max(nb, 1) * Dn)
+                                            : nullptr;
   E* dT = need<E>(M, M->dT, (size_t)nloc * 4 * L3);
   const int Fmax = std::max(m.fit[0], std::max(m.fit[1], m.fit[2]));
   E* fitb = need<E>(M, M->fitb, (size_t)8 * std::max(nb, 1) * Fmax);
@@ -487,9 +495,18 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
     E** slots[8] = {&fb.H0, &fb.T1, &fb.H1, &fb.T2, &fb.H2, &fb.dZa, &fb.dZb, &fb.dH};
     // slab q holds [rows][F] of every type back to back; F <= Fmax
     for (int q = 0; q < 8; ++q) *slots[q] = base + q * slab + r0 * (size_t)Fmax;
+    FitDdt ddt{};
+    if (fused_ddt) {
+      ddt.W0T = M->d_w0t + (size_t)t * m.fit[0] * Dn;
+      ddt.items = items;
+      ddt.pos0 = (int)r0;
+      ddt.dT = reinterpret_cast<double*>(dT);
+      ddt.dD = dD ? reinterpret_cast<double*>(dD) + r0 * Dn : nullptr;
+      ddt.ncu = M->ncu;
+    }
     launch_fitting(fst, net, rows, d_from_t ? nullptr : D + r0 * Dn,
-                   d_from_t ? Tt + r0 * 4 : nullptr, 4L * nb, L3, fb, dD + r0 * Dn,
-                   e_bucket + r0, blas);
+                   d_from_t ? Tt + r0 * 4 : nullptr, 4L * nb, L3, fb, dD ? dD + r0 * Dn : nullptr,
+                   e_bucket + r0, blas, fused_ddt ? &ddt : nullptr);
     if (fork) {
       DPAMD_HIP(hipEventRecord(M->join_ev[t], fst));
       DPAMD_HIP(hipStreamWaitEvent(st, M->join_ev[t], 0));
@@ -497,7 +514,8 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   }
   record(M, st, kStFit + 1);
 
-  launch_dT(st, nb, L3, axis, items, Tt, dD, dT);
+  if (!fused_ddt) launch_dT(st, nb, L3, axis, items, Tt, dD, dT);
+  M->dd_valid = dD != nullptr;
   record(M, st, kStDT + 1);
 
   if (f32) {
@@ -1213,6 +1231,17 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
     } else {
       upload(M->d_emb, emb);
       upload(M->d_fit, m.fit_params);
+      const int Dn = m.emb[2] * m.axis, F0 = m.fit[0];
+      if (ddt_supported(F0, m.emb[2], m.axis)) {
+        const FitOffsets fo = fit_offsets(m);
+        std::vector<double> w0t((size_t)m.ntypes * F0 * Dn);
+        for (int t = 0; t < m.ntypes; ++t) {
+          const double* W = m.fit_params.data() + (size_t)t * m.fit_block + fo.W[0];
+          for (int n = 0; n < Dn; ++n)
+            for (int k = 0; k < F0; ++k) w0t[((size_t)t * F0 + k) * Dn + n] = W[(size_t)n * F0 + k];
+        }
+        upload(M->d_w0t, w0t);
+      }
     }
     M->bytes_peak = M->bytes_now;
     M->fo = fit_offsets(m);
@@ -1236,7 +1265,7 @@ void dp_destroy(dp_model* M) {
   for (Buf* b : M->bufs)
     if (b->p) (void)hipFree(b->p);
   for (void* p : {M->d_emb, static_cast<void*>(M->d_envp), static_cast<void*>(M->d_tpad), M->d_fit,
-                  M->d_fitf, M->d_c4})
+                  M->d_fitf, M->d_c4, static_cast<void*>(M->d_w0t)})
     if (p) (void)hipFree(p);
   if (M->async_pending) (void)hipStreamSynchronize(M->async_stream);
   for (auto& set : M->ev)
@@ -1581,6 +1610,10 @@ long dp_debug_copy(dp_model* M, int stage, void* dst, size_t capacity) {
       case DP_STAGE_DEDD:
         if (M->kind == dp_model::kDpa4c)
           throw ApiError{DP_ERR_ARG, "the DPA4C path keeps dE/dD in registers"};
+        if (!M->dd_valid)
+          throw ApiError{DP_ERR_ARG,
+                         "dE/dD was not stored: call dp_debug_keep(handle, 1) before the "
+                         "evaluation"};
         copy_bucket(M->dD.p, Dn, net_esize);
         break;
       case DP_STAGE_ATOM_ENERGY:

@@ -485,6 +485,187 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
   }
 }
 
+// Input gradient of the first fitting layer fused with the descriptor
+// backward (fp64): for the rows (atoms of one type) of a block,
+//   dD[a][b] = sum_k dZ0[k] W0[16a + b][k]         (FP64 MFMA, in registers)
+//   dT[m][a] = sum_b dD[a][b] T[m][b] + (a < 16) sum_a' dD[a'][a] T[m][a']
+// so dD is never stored. Wave w owns rows 16w .. 16w + 15 of the block and
+// keeps their dZ0 rows in registers as MFMA B operands for the whole K = 4 NQ
+// (60 k-steps for F0 = 240); the block walks the column groups a (16 columns
+// b each) with W0^T[k][16a .. 16a + 15] staged in LDS (double-buffered, shared
+// by all waves). Each MFMA tile is computed transposed, D'[b][row] =
+// W0 dZ0^T, so register r of lane (g, c) holds dD[row c][a][b = g + 4r]:
+//   first term  lane-local over r (T[row c][m][g + 4r] held in registers),
+//               then over the four lane groups (xor 16, 32); lane (g, c)
+//               keeps m = g and parks it in an LDS buffer of 16 columns,
+//               flushed as 128-byte runs of dT[atom][m][a];
+//   second term lane-local: acc2[r][m] += dD[row][a][b] T[row][m][a], with
+//               T[row][m][a] of the block's rows staged in LDS per a.
+// The column groups run 16 .. L3-1 and then 0 .. 15, so the last buffer holds
+// the first term of a < 16 when the second term is complete; the two are
+// added and written at the end. T is the column-major copy (element (pos, a,
+// m) at Tt[a ldt + 4 pos + m]) with Tt pointing at the type's first row
+// (bucket position pos0); dT is in atom order (items[pos0 + row] is the atom
+// of a row); dD (inspection only) is written when non-null.
+// Reference analog of the fused forward + gradient fitting entry:
+// deepmd-op/overlays/op/pt/graph_fitting.cu:728-757.
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+struct DdtArgs {
+  int rows, K, L3;
+  const double* dZ;   // [rows][K]
+  const double* W0T;  // [K][16 L3]
+  const double* Tt;
+  long ldt;
+  int pos0;
+  const int* items;
+  double* dT;  // [atoms][4][L3]
+  double* dD;  // [rows][16 L3] or null
+};
+
+template <int WAVES, int NQ>
+__global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
+  constexpr int BM = 16 * WAVES, K = 4 * NQ;
+  extern __shared__ double lds[];
+  double* Bs = lds;                   // [2][K][16]
+  double* Ts = Bs + 2 * K * 16;       // [2][BM][4]
+  double* Ob = Ts + 2 * BM * 4;       // [WAVES][16 rows][4 m][16 columns]
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int row0 = blockIdx.x * BM, wrow = row0 + 16 * w + c;  // this lane's row
+  const bool rowok = wrow < p.rows;
+  const int Dn = 16 * p.L3;
+  double* Obw = Ob + w * 16 * 4 * 16;
+  // dZ0 row of this lane as MFMA B operands: element k = 4q + g
+  double Zb[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) Zb[q] = rowok ? p.dZ[(long)wrow * K + 4 * q + g] : 0.0;
+  // T[row][m][b = g + 4r] of this lane's row (first term)
+  const long tpos = 4L * wrow;
+  // atom of this lane's row (rows of the wave are broadcast from lane c)
+  const int my_atom = rowok ? p.items[p.pos0 + wrow] : 0;
+  double Tc[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) Tc[r][m] = rowok ? p.Tt[(long)(g + 4 * r) * p.ldt + tpos + m] : 0.0;
+  double acc2[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc2[r][m] = 0.0;
+
+  // Staging of column group a through the LDS DMA (global_load_lds, 16 bytes
+  // per lane, lane L's granule at base + 16 L; no registers): W0^T rows k,
+  // columns 16a .. 16a + 15 (granule q: k = q / 8, columns 2 (q % 8) + 0, 1),
+  // and T column a of the block's rows (granule q: row q / 2, m 2 (q % 2) + 0,
+  // 1; rows past the type's end read its last row and are not used).
+  constexpr int NGB = K * 8, NGT = BM * 2;  // granules per group
+  auto issue = [&](int buf, int a) {
+    for (int i = w; 64 * i < NGB; i += WAVES) {
+      const int q = 64 * i + lane;
+      if (q < NGB)
+        __builtin_amdgcn_global_load_lds(p.W0T + (long)(q >> 3) * Dn + 16 * a + 2 * (q & 7),
+                                         LDS_PTR(Bs + buf * K * 16 + 128 * i), 16, 0, 0);
+    }
+    for (int i = w; 64 * i < NGT; i += WAVES) {
+      const int q = 64 * i + lane;
+      const int r = min(row0 + (q >> 1), p.rows - 1);
+      __builtin_amdgcn_global_load_lds(p.Tt + (long)a * p.ldt + 4L * r + 2 * (q & 1),
+                                       LDS_PTR(Ts + buf * BM * 4 + 128 * i), 16, 0, 0);
+    }
+  };
+  auto col_of = [&](int i) { return i + 16 < p.L3 ? i + 16 : i + 16 - p.L3; };
+
+  issue(0, col_of(0));
+  for (int i = 0; i < p.L3; ++i) {
+    const int a = col_of(i), buf = i & 1;
+    // group i has landed (each wave waits for its own transfers, then the
+    // barrier), and no wave still reads the buffer group i + 1 goes to
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (i + 1 < p.L3) issue(buf ^ 1, col_of(i + 1));
+    // D'[b][row] over K: register r of lane (g, c) = dD[row c][a][g + 4r]
+    // two independent accumulation chains (the halves of K), operands read
+    // from LDS two k-steps ahead
+    const double* B = Bs + buf * K * 16 + g * 16 + c;
+    constexpr int H = NQ / 2;
+    static_assert(NQ % 2 == 0, "K halves");
+    d4 acc0 = d4{0.0, 0.0, 0.0, 0.0}, acc1 = d4{0.0, 0.0, 0.0, 0.0};
+    double b0[3], b1[3];
+    b0[0] = B[0];
+    b1[0] = B[64 * H];
+    b0[1] = B[64];
+    b1[1] = B[64 * (H + 1)];
+#pragma unroll
+    for (int q = 0; q < H; ++q) {
+      if (q + 2 < H) {
+        b0[(q + 2) % 3] = B[64 * (q + 2)];
+        b1[(q + 2) % 3] = B[64 * (H + q + 2)];
+      }
+      acc0 = mfma_f64(b0[q % 3], Zb[q], acc0);
+      acc1 = mfma_f64(b1[q % 3], Zb[H + q], acc1);
+    }
+    d4 acc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = acc0[r] + acc1[r];
+    // first term: sum over b = g + 4r (lane-local over r, then the groups)
+    double s[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      double v = acc[0] * Tc[0][m];
+      v = fma(acc[1], Tc[1][m], v);
+      v = fma(acc[2], Tc[2][m], v);
+      v = fma(acc[3], Tc[3][m], v);
+      v += shfl_xor_d(v, 16);
+      v += shfl_xor_d(v, 32);
+      s[m] = v;
+    }
+    Obw[(c * 4 + g) * 16 + (a & 15)] = g == 0 ? s[0] : g == 1 ? s[1] : g == 2 ? s[2] : s[3];
+    // second term: T[row][m][a]
+    const double* tr = Ts + buf * BM * 4 + (16 * w + c) * 4;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const double t = tr[m];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc2[r][m] = fma(acc[r], t, acc2[r][m]);
+    }
+    if (p.dD && rowok) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p.dD[(long)wrow * Dn + 16 * a + g + 4 * r] = acc[r];
+    }
+    // a column group is complete: flush it (the group a < 16 stays for the end)
+    if (a >= 16 && ((a & 15) == 15 || a == p.L3 - 1)) {
+      wave_lds_sync();
+      const int abase = a & ~15, na = a - abase + 1;
+#pragma unroll
+      for (int rl = 0; rl < 16; ++rl) {
+        // pass rl: row rl of the wave, lane = (m, al)
+        const int atom = __shfl(my_atom, rl, 64);
+        const int m = lane >> 4, al = lane & 15;
+        if (al < na && row0 + 16 * w + rl < p.rows)
+          p.dT[((long)atom * 4 + m) * p.L3 + abase + al] = Obw[64 * rl + lane];
+      }
+      wave_lds_sync();
+    }
+  }
+  // a < 16: first term from the buffer + second term
+  wave_lds_sync();
+  if (rowok) {
+    double* out = p.dT + (long)my_atom * 4 * p.L3;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int b = g + 4 * r;
+        out[m * p.L3 + b] = Obw[(c * 4 + m) * 16 + b] + acc2[r][m];
+      }
+  }
+}
+
+template <int WAVES>
+static size_t ddt_lds_bytes(int K) {
+  return sizeof(double) * (2 * K * 16 + 2 * 16 * WAVES * 4 + WAVES * 16 * 4 * 16);
+}
+
 template <class T, int NT, bool TRANSB, bool AT = false>
 static void gemm_nt(hipStream_t st, const GemmArgs<T>& a) {
   dim3 grid(a.N / (16 * NT), (a.M + 63) / 64, a.split > 1 ? a.split : 1);
@@ -561,7 +742,8 @@ void blas_destroy(void* h) {
 
 template <class T>
 void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, const T* Tt,
-                    long ldt, int L3, const FitBufs<T>& b, T* dD, double* e_bucket, void* blas) {
+                    long ldt, int L3, const FitBufs<T>& b, T* dD, double* e_bucket, void* blas,
+                    const FitDdt* ddt) {
   using G = GemmArgs<T>;
   if (rows <= 0) return;
   const int Dn = net.L[0].in, F0 = net.L[0].out, F1 = net.L[1].out, F2 = net.L[2].out;
@@ -616,7 +798,14 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   g.dHin = net.L[1].idt ? b.dH : nullptr; g.ld_dhin = F1; g.dH_out = nullptr; g.Tk = b.H0;
   g.Bf = net.L[1].WfT;
   gemm<true>(st, g);
-  // dD = dZ0 W0^T
+  // dD = dZ0 W0^T, or (fp64) straight on to dE/dT
+  if constexpr (sizeof(T) == 8) {
+    if (ddt) {
+      launch_dDdT(st, rows, F0, L3, b.dZa, ddt->W0T, Tt, ldt, ddt->pos0, ddt->items, ddt->dT, ddt->dD,
+                  ddt->ncu);
+      return;
+    }
+  }
   if (blas) {
     blas_gemm_nt(blas, st, rows, Dn, F0, b.dZa, net.L[0].W, dD);
     return;
@@ -625,6 +814,30 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   g.M = rows; g.N = Dn; g.K = F0; g.A = b.dZa; g.lda = F0; g.B = net.L[0].W; g.ldb = F0;
   g.epi = 0; g.C = dD; g.ldc = Dn;
   gemm<true>(st, g);
+}
+
+bool ddt_supported(int K, int L3, int axis) { return K == 240 && axis == 16 && L3 >= 16 && L3 <= 128; }
+
+void launch_dDdT(hipStream_t st, int rows, int K, int L3, const double* dZ, const double* W0T,
+                 const double* Tt, long ldt, int pos0, const int* items, double* dT, double* dD,
+                 int ncu) {
+  if (rows <= 0) return;
+  if (K != 240) throw HipError{hipErrorInvalidValue, "fused dE/dD kernel needs F0 = 240"};
+  DdtArgs p{rows, K, L3, dZ, W0T, Tt, ldt, pos0, items, dT, dD};
+  // eight waves (128 rows) per block when that still gives every compute
+  // unit two blocks; four (64 rows) otherwise
+  if ((rows + 127) / 128 >= 2 * ncu) {
+    const size_t bytes = ddt_lds_bytes<8>(K);
+    DPAMD_HIP(hipFuncSetAttribute((const void*)k_dDdT<8, 60>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    hipLaunchKernelGGL((k_dDdT<8, 60>), dim3((rows + 127) / 128), dim3(512), bytes, st, p);
+  } else {
+    const size_t bytes = ddt_lds_bytes<4>(K);
+    DPAMD_HIP(hipFuncSetAttribute((const void*)k_dDdT<4, 60>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    hipLaunchKernelGGL((k_dDdT<4, 60>), dim3((rows + 63) / 64), dim3(256), bytes, st, p);
+  }
+  DPAMD_LAUNCH_CHECK();
 }
 
 template <class T>
@@ -640,10 +853,10 @@ void launch_dT(hipStream_t st, int nloc, int L3, int axis, const int* items, con
 
 template void launch_fitting<double>(hipStream_t, const FitNet<double>&, int, const double*,
                                      const double*, long, int, const FitBufs<double>&, double*,
-                                     double*, void*);
+                                     double*, void*, const FitDdt*);
 template void launch_fitting<float>(hipStream_t, const FitNet<float>&, int, const float*,
                                     const float*, long, int, const FitBufs<float>&, float*,
-                                    double*, void*);
+                                    double*, void*, const FitDdt*);
 template void launch_dT<double>(hipStream_t, int, int, int, const int*, const double*,
                                 const double*, double*);
 template void launch_dT<float>(hipStream_t, int, int, int, const int*, const float*, const float*,

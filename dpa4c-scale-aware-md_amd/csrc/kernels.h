@@ -195,9 +195,25 @@ int fit_splits(int rows, int N, int K, int ncu);
 // D may be null.
 // blas: a rocBLAS handle (blas_create) for the plain input-gradient GEMM, or
 // null for this library's own GEMM kernel.
+// fp64: the first layer's input gradient fused with the descriptor backward
+// (launch_dDdT); when given, launch_fitting computes dE/dT of its rows
+// instead of dE/dD.
+struct FitDdt {
+  const double* W0T;  // [F0][16 L3] first-layer weights, transposed
+  const int* items;   // bucket position -> atom
+  int pos0;           // bucket position of the type's first row
+  double* dT;         // [atoms][4][L3]
+  double* dD;         // [rows][16 L3] when kept for inspection, else null
+  int ncu;
+};
+bool ddt_supported(int F0, int L3, int axis);
+void launch_dDdT(hipStream_t, int rows, int K, int L3, const double* dZ, const double* W0T,
+                 const double* Tt, long ldt, int pos0, const int* items, double* dT, double* dD,
+                 int ncu);
 template <class T>
 void launch_fitting(hipStream_t, const FitNet<T>&, int rows, const T* D, const T* Tt, long ldt,
-                    int L3, const FitBufs<T>&, T* dD, double* e_bucket, void* blas);
+                    int L3, const FitBufs<T>&, T* dD, double* e_bucket, void* blas,
+                    const FitDdt* ddt = nullptr);
 void* blas_create();
 void blas_destroy(void* handle);
 // Tt column-major in bucket order (element (pos, a, m) at Tt[a * 4 nloc +
