@@ -377,6 +377,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   ea.stride = M->el.stride;
   ea.rcut = m.rcut;
   ea.rcut_smth = m.rcut_smth;
+  ea.inv_sw = 1.0 / (m.rcut - m.rcut_smth);
   ea.inv_nnei = 1.0 / (double)nnei;
   ea.emb = M->d_emb;
   ea.envp = M->d_envp;

@@ -48,10 +48,28 @@ namespace dpamd {
 constexpr int kU3 = 2;
 constexpr int kU3B = 1;
 
-// LDS: padded net | env statistics of the pair (8) | per-wave scratch
+// LDS: padded net | env statistics of the pair (8) | exp2 table of the tanh
+// (kTanhTab) | per-wave scratch
+constexpr int kTanhTab = 128;
 template <class S>
 constexpr int fwd_lds_doubles(int waves) {
-  return (S::SIZE + 31) / 32 * 32 + 8 + waves * 16 * (S::L2P + 2) + waves * 64;
+  return (S::SIZE + 31) / 32 * 32 + 8 + kTanhTab + waves * 16 * (S::L2P + 2) + waves * 64;
+}
+
+// tanh of n values (groups of four sharing a reciprocal, the tail padded
+// with zeros, which evaluate to 0)
+template <int N>
+__device__ __forceinline__ void tanh_n(const double* z, double* y, const double* tab) {
+#pragma unroll
+  for (int q0 = 0; q0 < N; q0 += 4) {
+    double zz[4], yy[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) zz[j] = q0 + j < N ? z[q0 + j] : 0.0;
+    tanh_tab4(zz, yy, tab);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (q0 + j < N) y[q0 + j] = yy[j];
+  }
 }
 
 // layer-1 stash [16 slots][K2P + 1] per wave, for a layer-2 [x, x] residual
@@ -65,7 +83,7 @@ constexpr int x1_stash_doubles() {
 // neighbour indices of the current and the next tile, int [2][16]
 template <class S>
 constexpr int bwd_lds_doubles(int waves) {
-  return (S::SIZE + 31) / 32 * 32 + 8 + waves * 4 * (S::L3P + S::L2P) +
+  return (S::SIZE + 31) / 32 * 32 + 8 + kTanhTab + waves * 4 * (S::L3P + S::L2P) +
          waves * x1_stash_doubles<S>() + waves * (16 * 12 + 16);
 }
 
@@ -78,15 +96,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
   double* P = lds;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   double* EnvS = lds + PS;
-  double* X2s = lds + PS + 8 + w * 16 * X2LD;
-  double* Rs = lds + PS + 8 + WAVES * 16 * X2LD + w * 64;
+  double* Tab = lds + PS + 8;
+  double* X2s = lds + PS + 8 + kTanhTab + w * 16 * X2LD;
+  double* Rs = lds + PS + 8 + kTanhTab + WAVES * 16 * X2LD + w * 64;
 
   const int p = find_pair(a);
   const int ti = p / a.ntypes, tj = p % a.ntypes;
   {
     const double* src = static_cast<const double*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
-    if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
+    if (threadIdx.x < 8) {
+      const double v = a.envp[p * 8 + threadIdx.x];
+      EnvS[threadIdx.x] = threadIdx.x < 4 ? v : 1.0 / v;  // avg[4], 1 / dstd[4]
+    }
+    for (int q = threadIdx.x; q < kTanhTab; q += WAVES * 64) Tab[q] = kExp2Tab128[q];
   }
   __syncthreads();
   const int nitems = a.type_off[ti + 1] - a.type_off[ti];
@@ -100,7 +123,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     // ordered behind the activation traffic by the in-order vector memory
     // counter
     const double* avg = EnvS;
-    const double* sd = EnvS + 4;
+    const double* sd = EnvS + 4;  // 1 / dstd
     const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
 
     double Tacc[S::NU3 * 4];
@@ -130,7 +153,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
       const int slot = tile + c;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
-      if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, avg, sd, Rn);
+      if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, a.inv_sw, avg, sd, Rn);
       if (slot + 16 < nr) {
         nx0 = a.ext[3 * (long)jn];
         nx1 = a.ext[3 * (long)jn + 1];
@@ -143,26 +166,17 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       }
       const double s = Rn[0];
 
-      // layer 1 -> B operand of layer 2 (feature 4q+g of slot c); four at a
-      // time (shared reciprocal) when every feature is real
+      // layer 1 -> B operand of layer 2 (feature 4q+g of slot c), four at a
+      // time (shared reciprocal); padded features have zero weights and bias
       double x1[S::NQ2];
-      if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
-#pragma unroll
-        for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
-          double z[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int f = 4 * (q0 + j) + g;
-            z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
-          }
-          tanh_fast4(z, x1 + q0);
-        }
-      } else {
+      {
+        double z[S::NQ2];
 #pragma unroll
         for (int q = 0; q < S::NQ2; ++q) {
           const int f = 4 * q + g;
-          x1[q] = (f < S::L1) ? tanh_fast(s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f]) : 0.0;
+          z[q] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
         }
+        tanh_n<S::NQ2>(z, x1, Tab);
       }
       // a residual feature f % L1 lives in another lane group: stash layer 1
       // in this wave's X2 buffer (overwritten by X2 only after every read)
@@ -188,7 +202,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
         double z2[4], th2v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) z2[r] = acc2[t][r] + P[S::OFF_B2 + 16 * t + 4 * r + g];
-        tanh_fast4(z2, th2v);
+        tanh_tab4(z2, th2v, Tab);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int f = 16 * t + 4 * r + g;
@@ -247,7 +261,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
             const double b3 = P[S::OFF_B3 + f];
 #pragma unroll
             for (int r = 0; r < 4; ++r) z3[r] = acc3[uu][r] + b3;
-            tanh_fast4(z3, th3v);
+            tanh_tab4(z3, th3v, Tab);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int sl = g + 4 * r;
@@ -309,13 +323,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   double* P = lds;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   double* EnvS = lds + PS;
-  double* dTs = lds + PS + 8 + w * 4 * (S::L3P + S::L2P);
+  double* Tab = lds + PS + 8;
+  double* dTs = lds + PS + 8 + kTanhTab + w * 4 * (S::L3P + S::L2P);
   double* dTf = dTs + 4 * S::L3P;
   // layer-1 stash (see x1_stash_doubles)
-  double* X1s = lds + PS + 8 + WAVES * 4 * (S::L3P + S::L2P) + w * x1_stash_doubles<S>();
+  double* X1s =
+      lds + PS + 8 + kTanhTab + WAVES * 4 * (S::L3P + S::L2P) + w * x1_stash_doubles<S>();
   constexpr int X1LD = S::K2P + 1;
-  double* own_w = lds + PS + 8 + WAVES * 4 * (S::L3P + S::L2P) + WAVES * x1_stash_doubles<S>() +
-                  w * (16 * 12 + 16);
+  double* own_w = lds + PS + 8 + kTanhTab + WAVES * 4 * (S::L3P + S::L2P) +
+                  WAVES * x1_stash_doubles<S>() + w * (16 * 12 + 16);
   int* jbuf = reinterpret_cast<int*>(own_w + 16 * 12);
 
   const int p = find_pair(a);
@@ -323,8 +339,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   {
     const double* src = static_cast<const double*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
-    if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
+    if (threadIdx.x < 8) {
+      const double v = a.envp[p * 8 + threadIdx.x];
+      EnvS[threadIdx.x] = threadIdx.x < 4 ? v : 1.0 / v;  // avg[4], 1 / dstd[4]
+    }
     for (int q = lane; q < 16 * 12; q += 64) own_w[q] = 0.0;
+    for (int q = threadIdx.x; q < kTanhTab; q += WAVES * 64) Tab[q] = kExp2Tab128[q];
   }
   __syncthreads();
   const int nitems = a.type_off[ti + 1] - a.type_off[ti];
@@ -339,7 +359,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     // ordered behind the activation traffic by the in-order vector memory
     // counter
     const double* avg = EnvS;
-    const double* sd = EnvS + 4;
+    const double* sd = EnvS + 4;  // 1 / dstd
     const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
     constexpr int BLK = 16 * (S::L2P + S::L3P);
     const double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
@@ -401,7 +421,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         d0 = nx0 - xi;
         d1 = nx1 - yi;
         d2 = nx2 - zi;
-        env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
+        env_value(d0, d1, d2, a.rcut_smth, a.rcut, a.inv_sw, avg, sd, Rn);
       }
       if (slot + 16 < nr) {
         nx0 = a.ext[3 * (long)jn];
@@ -412,38 +432,19 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       jn = slot + 32 < nr ? row[slot + 32] : 0;
       const double s = Rn[0];
 
-      // layer 1 (recomputed, elementwise) and its tangent
+      // layer 1 (recomputed, elementwise) and its tangent; padded features
+      // have zero weights and bias (tanh 0, tangent 0)
       double x1[S::NQ2], x1t[S::NQ2];
-      if constexpr (S::L1 == S::K2P && S::NQ2 % 4 == 0) {
-#pragma unroll
-        for (int q0 = 0; q0 < S::NQ2; q0 += 4) {
-          double z[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int f = 4 * (q0 + j) + g;
-            z[j] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
-          }
-          tanh_fast4(z, x1 + q0);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const double th = x1[q0 + j];
-            x1t[q0 + j] = (1.0 - th * th) * P[S::OFF_W1 + 4 * (q0 + j) + g];
-          }
-        }
-      } else {
+      {
+        double z[S::NQ2];
 #pragma unroll
         for (int q = 0; q < S::NQ2; ++q) {
           const int f = 4 * q + g;
-          if (f < S::L1) {
-            const double wv = P[S::OFF_W1 + f];
-            const double th = tanh_fast(s * wv + P[S::OFF_B1 + f]);
-            x1[q] = th;
-            x1t[q] = (1.0 - th * th) * wv;
-          } else {
-            x1[q] = 0.0;
-            x1t[q] = 0.0;
-          }
+          z[q] = s * P[S::OFF_W1 + f] + P[S::OFF_B1 + f];
         }
+        tanh_n<S::NQ2>(z, x1, Tab);
+#pragma unroll
+        for (int q = 0; q < S::NQ2; ++q) x1t[q] = (1.0 - x1[q] * x1[q]) * P[S::OFF_W1 + 4 * q + g];
       }
       if constexpr (S::RES2 != 0 && !S::X1_ALIGNED) {
 #pragma unroll
@@ -561,7 +562,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         for (int m = 0; m < 4; ++m) nd[m] = up[m] * a.inv_nnei;
         nd[0] += (Rn[0] * vp[0] + Rn[1] * vp[1] + Rn[2] * vp[2] + Rn[3] * vp[3]) * a.inv_nnei;
         double gv[3];
-        env_grad(d0, d1, d2, a.rcut_smth, a.rcut, sd, nd, gv);
+        env_grad(d0, d1, d2, a.rcut_smth, a.rcut, a.inv_sw, sd, nd, gv);
         const double dv[3] = {d0, d1, d2};
         edge_out(a, ebase + slot, jbuf[16 * par + c], dv, gv, own_w + 12 * c);
       }

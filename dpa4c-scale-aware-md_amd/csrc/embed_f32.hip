@@ -115,7 +115,10 @@ k_embed_fwd32(EmbArgs a) {
   {
     const float* src = static_cast<const float*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
-    if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
+    if (threadIdx.x < 8) {
+      const double v = a.envp[p * 8 + threadIdx.x];
+      EnvS[threadIdx.x] = threadIdx.x < 4 ? v : 1.0 / v;  // avg[4], 1 / dstd[4]
+    }
   }
   __syncthreads();
   const int nitems = a.type_off[ti + 1] - a.type_off[ti];
@@ -129,7 +132,7 @@ k_embed_fwd32(EmbArgs a) {
     // ordered behind the activation traffic by the in-order vector memory
     // counter
     const double* avg = EnvS;
-    const double* sd = EnvS + 4;
+    const double* sd = EnvS + 4;  // 1 / dstd
     const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
 
     float Tacc[S::NU3 * 4];
@@ -152,7 +155,7 @@ k_embed_fwd32(EmbArgs a) {
     for (int tile = 0; tile < nr; tile += 16, act2 += BLK / 4, act3 += BLK / 4) {
       const int slot = tile + c;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
-      if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, avg, sd, Rn);
+      if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, a.inv_sw, avg, sd, Rn);
       if (slot + 16 < nr) {
         nx0 = a.ext[3 * (long)jn];
         nx1 = a.ext[3 * (long)jn + 1];
@@ -308,7 +311,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
   {
     const float* src = static_cast<const float*>(a.emb) + (long)p * a.stride;
     for (int q = threadIdx.x; q < S::SIZE; q += WAVES * 64) P[q] = src[q];
-    if (threadIdx.x < 8) EnvS[threadIdx.x] = a.envp[p * 8 + threadIdx.x];
+    if (threadIdx.x < 8) {
+      const double v = a.envp[p * 8 + threadIdx.x];
+      EnvS[threadIdx.x] = threadIdx.x < 4 ? v : 1.0 / v;  // avg[4], 1 / dstd[4]
+    }
   }
   __syncthreads();
   const int nitems = a.type_off[ti + 1] - a.type_off[ti];
@@ -323,7 +329,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
     // ordered behind the activation traffic by the in-order vector memory
     // counter
     const double* avg = EnvS;
-    const double* sd = EnvS + 4;
+    const double* sd = EnvS + 4;  // 1 / dstd
     const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
     constexpr int BLK = 16 * (S::L2P + S::L3P);
     const float* act =
@@ -381,7 +387,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
         d0 = nx0 - xi;
         d1 = nx1 - yi;
         d2 = nx2 - zi;
-        env_value(d0, d1, d2, a.rcut_smth, a.rcut, avg, sd, Rn);
+        env_value(d0, d1, d2, a.rcut_smth, a.rcut, a.inv_sw, avg, sd, Rn);
       }
       if (tile + 16 < nr) prefetch(tile + 16);
       const float s = (float)Rn[0];
@@ -466,6 +472,16 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 #pragma unroll
       for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
         __builtin_amdgcn_sched_barrier(0);
+        // this output tile's saved activations, issued ahead of its products
+        // (which cover their latency) and pinned there: left to itself the
+        // scheduler may sink each load to its use and wait on it alone
+        float th3v[kU3B][4];
+#pragma unroll
+        for (int uu = 0; uu < kU3B; ++uu)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            th3v[uu][r] = u0 + uu < S::NU3 ? act3[256 * (u0 + uu) + 4 * r] : 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
         f4 acc3t[kU3B];
 #pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -482,7 +498,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int f = 16 * u + 4 * g + r;
-              const float th = act3[256 * u + 4 * r];
+              const float th = th3v[uu][r];
               const float tt = (1.0f - th * th) * acc3t[uu][r];
 #pragma unroll
               for (int m = 0; m < 4; ++m) {
@@ -513,7 +529,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
         // hold up the just-in-time activation loads behind them in the
         // in-order memory counter
         double gv[3];
-        env_grad(d0, d1, d2, a.rcut_smth, a.rcut, sd, nd, gv);
+        env_grad(d0, d1, d2, a.rcut_smth, a.rcut, a.inv_sw, sd, nd, gv);
         double* eg = a.edge_grad + (ebase + slot) * 3;
         eg[0] = gv[0];
         eg[1] = gv[1];

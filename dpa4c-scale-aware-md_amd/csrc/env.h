@@ -9,55 +9,79 @@
 
 namespace dpamd {
 
-// spline5 switch and the normalised env row [sw/r, sw x/r^2, sw y/r^2, sw z/r^2].
+// The kernels keep a pair's env statistics as avg[4] and isd[4] = 1 / dstd
+// (staged once per block), and EmbArgs carries inv_sw = 1 / (rcut -
+// rcut_smth), so no IEEE division is left per slot; 1/r comes from the
+// hardware reciprocal square root refined by two Newton steps (relative
+// error at the rounding level). The oracle divides; the two agree to a few
+// ulp, far inside the fp64 tolerances.
+__device__ __forceinline__ double inv_sqrt(double x) {
+  double y = __builtin_amdgcn_rsq(x);
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const double e = fma(-x * y, y, 1.0);  // 1 - x y^2
+    y = fma(0.5 * y, e, y);
+  }
+  return y;
+}
+
+// spline5 switch sw(r) and its derivative over the window [rs, rc)
+__device__ __forceinline__ double switch5(double r, double rs, double rc, double inv_sw,
+                                          double* dsw) {
+  if (r < rs) {
+    *dsw = 0.0;
+    return 1.0;
+  }
+  if (r >= rc) {
+    *dsw = 0.0;
+    return 0.0;
+  }
+  const double u = (r - rs) * inv_sw;
+  const double u2 = u * u, u3 = u2 * u;
+  *dsw = (3.0 * u2 * (-6.0 * u2 + 15.0 * u - 10.0) + u3 * (-12.0 * u + 15.0)) * inv_sw;
+  return u3 * (-6.0 * u2 + 15.0 * u - 10.0) + 1.0;
+}
+
+// The normalised env row [sw/r, sw x/r^2, sw y/r^2, sw z/r^2] of one slot.
 __device__ __forceinline__ void env_value(double d0, double d1, double d2, double rs, double rc,
-                                          const double* avg, const double* sd, double* Rn) {
+                                          double inv_sw, const double* avg, const double* isd,
+                                          double* Rn) {
   const double r2 = d0 * d0 + d1 * d1 + d2 * d2;
-  const double r = sqrt(r2);
+  const double inv_r = inv_sqrt(r2);
+  const double r = r2 * inv_r;
   double sw;
   if (r < rs) {
     sw = 1.0;
   } else if (r >= rc) {
     sw = 0.0;
   } else {
-    const double u = (r - rs) / (rc - rs);
+    const double u = (r - rs) * inv_sw;
     const double u2 = u * u, u3 = u2 * u;
     sw = u3 * (-6.0 * u2 + 15.0 * u - 10.0) + 1.0;
   }
-  const double inv_r = 1.0 / r;
-  const double inv_r2 = inv_r * inv_r;
-  Rn[0] = (sw * inv_r - avg[0]) / sd[0];
-  Rn[1] = (sw * d0 * inv_r2 - avg[1]) / sd[1];
-  Rn[2] = (sw * d1 * inv_r2 - avg[2]) / sd[2];
-  Rn[3] = (sw * d2 * inv_r2 - avg[3]) / sd[3];
+  const double q = sw * inv_r * inv_r;
+  Rn[0] = (sw * inv_r - avg[0]) * isd[0];
+  Rn[1] = (q * d0 - avg[1]) * isd[1];
+  Rn[2] = (q * d1 - avg[2]) * isd[2];
+  Rn[3] = (q * d2 - avg[3]) * isd[3];
 }
 
 // Edge gradient g = sum_m nd[m] * d(Rn_m)/dd for one slot.
 __device__ __forceinline__ void env_grad(double d0, double d1, double d2, double rs, double rc,
-                                         const double* sd, const double* nd, double* gv) {
+                                         double inv_sw, const double* isd, const double* nd,
+                                         double* gv) {
   const double d[3] = {d0, d1, d2};
   const double r2 = d0 * d0 + d1 * d1 + d2 * d2;
-  const double r = sqrt(r2);
-  double sw, dsw;
-  if (r < rs) {
-    sw = 1.0;
-    dsw = 0.0;
-  } else if (r >= rc) {
-    sw = 0.0;
-    dsw = 0.0;
-  } else {
-    const double u = (r - rs) / (rc - rs);
-    const double u2 = u * u, u3 = u2 * u;
-    sw = u3 * (-6.0 * u2 + 15.0 * u - 10.0) + 1.0;
-    dsw = (3.0 * u2 * (-6.0 * u2 + 15.0 * u - 10.0) + u3 * (-12.0 * u + 15.0)) / (rc - rs);
-  }
-  const double inv_r = 1.0 / r;
+  const double inv_r = inv_sqrt(r2);
+  const double r = r2 * inv_r;
+  double dsw;
+  const double sw = switch5(r, rs, rc, inv_sw, &dsw);
   const double inv_r2 = inv_r * inv_r;
   const double dR0_dr = dsw * inv_r - sw * inv_r2;
   const double q = sw * inv_r2;
   const double dq_dr = dsw * inv_r2 - 2.0 * sw * inv_r2 * inv_r;
-  const double w0 = nd[0] / sd[0];
-  const double w[3] = {nd[1] / sd[1], nd[2] / sd[2], nd[3] / sd[3]};
+  const double w0 = nd[0] * isd[0];
+  const double w[3] = {nd[1] * isd[1], nd[2] * isd[2], nd[3] * isd[3]};
   // sum_c w_c d_c, used by the radial part of R_1..3
   const double wd = w[0] * d[0] + w[1] * d[1] + w[2] * d[2];
 #pragma unroll

@@ -49,6 +49,7 @@ struct EmbArgs {
   int block_off[kMaxPairs + 1];  // first block of each (ti, tj) pair
   int stride;                    // doubles per padded net
   double rcut, rcut_smth, inv_nnei;
+  double inv_sw;                 // 1 / (rcut - rcut_smth)
   // Precision-dependent arrays (double in fp64 mode, float in mixed mode):
   // emb, Tsec, dT and act; everything else is fp64 in both modes.
   const void* emb;     // [npair][stride] padded nets

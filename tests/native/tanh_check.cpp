@@ -47,5 +47,29 @@ int main() {
   dpamd::tanh_fast4(zx, z4);
   const bool zeros = z4[0] == 0.0 && z4[1] == 0.0;
   std::printf("tanh_fast4 max_abs %.3e, tanh(0) exact %d\n", max_abs4, (int)zeros);
-  return (max_abs <= 4e-15 && max_abs4 <= 4e-15 && zeros) ? 0 : 1;
+  // table-driven form (the embedding kernels): dense grid, random mixed
+  // magnitudes, the clamp, exact zeros and odd symmetry
+  double max_tab = 0;
+  auto tab4 = [&](const double* x) {
+    double y[4];
+    dpamd::tanh_tab4(x, y, dpamd::kExp2Tab128);
+    for (int k = 0; k < 4; ++k) max_tab = std::fmax(max_tab, std::fabs(y[k] - std::tanh(x[k])));
+  };
+  for (int i = -2000000; i <= 2000000; i += 4) {
+    const double x[4] = {i * 1e-5, (i + 1) * 1e-5, (i + 2) * 1e-5, (i + 3) * 1e-5};
+    tab4(x);
+  }
+  for (int i = 0; i < 2000000; ++i) {
+    double x[4];
+    for (int k = 0; k < 4; ++k) x[k] = (i % 3 == 0) ? U(g) : W(g) * std::pow(10.0, (i % 7) - 4);
+    if (i % 11 == 0) x[i % 4] = (i % 2 ? 25.0 : -30.0);
+    if (i % 13 == 0) x[(i + 1) % 4] = 0.0;
+    tab4(x);
+  }
+  double t4[4], tx[4] = {0.0, -0.0, 1e-300, -3.0}, tn[4], txn[4] = {0.0, 0.0, -1e-300, 3.0};
+  dpamd::tanh_tab4(tx, t4, dpamd::kExp2Tab128);
+  dpamd::tanh_tab4(txn, tn, dpamd::kExp2Tab128);
+  const bool tzero = t4[0] == 0.0 && t4[1] == 0.0 && std::signbit(t4[1]) && t4[3] == -tn[3];
+  std::printf("tanh_tab4 max_abs %.3e, zeros / odd symmetry %d\n", max_tab, (int)tzero);
+  return (max_abs <= 4e-15 && max_abs4 <= 4e-15 && zeros && max_tab <= 4e-15 && tzero) ? 0 : 1;
 }
