@@ -31,7 +31,8 @@ PREC_FP64, PREC_MIXED = 0, 1
 MODEL_SE_E2_A, MODEL_DPA4C = 0, 1
 
 EXPORTED = ("dp_create", "dp_destroy", "dp_get_info", "dp_last_error", "dp_compute",
-            "dp_compute_nlist", "dp_compute_device", "dp_compute_device_async", "dp_sync",
+            "dp_compute_nlist", "dp_compute_device", "dp_compute_device_async",
+            "dp_compute_device_noalloc", "dp_sync",
             "dp_graph_stats", "dp_compute_canonical_graph_device", "dp_compute_edges_device",
             "dp_compute_edges_device_f32",
             "dp_debug_copy", "dp_debug_keep", "dp_stage_times", "dp_device_bytes")
@@ -67,6 +68,7 @@ def lib():
         L.dp_compute_nlist.argtypes = [P, I, I, P, P, P, I, P, P, P, I, I, P, P, P, P, P]
         L.dp_compute_device.argtypes = [P, I, P, P, P, I, P, P, P, P, P, P]
         L.dp_compute_device_async.argtypes = [P, I, P, P, P, I, P, P, P, P, P, P]
+        L.dp_compute_device_noalloc.argtypes = [P, I, P, P, P, P, P, P, P, P, P]
         L.dp_sync.argtypes = [P]
         L.dp_graph_stats.argtypes = [P, C.POINTER(C.c_long), C.POINTER(C.c_long)]
         L.dp_compute_canonical_graph_device.argtypes = [P, P, P, P, P, P, P, P, P, P, I, I,
@@ -201,6 +203,17 @@ class DeepPot:
         self._check(lib().dp_compute_device(self._h, natoms, d_coord, d_atype, _ptr(boxa), ago,
                                             d_energy, d_force, d_virial, d_atom_energy or None,
                                             d_atom_virial or None, stream or None))
+
+    def compute_device_noalloc(self, d_coord: int, d_atype: int, natoms: int, box,
+                               d_energy: int, d_force: int, d_virial: int,
+                               d_atom_energy: int = 0, d_atom_virial: int = 0, stream: int = 0):
+        """dp_compute_device_noalloc: the device-resident evaluation with
+        every work buffer in the library's static per-GPU scratch."""
+        boxa = np.ascontiguousarray(box, np.float64).reshape(9)
+        self._check(lib().dp_compute_device_noalloc(self._h, natoms, d_coord, d_atype,
+                                                    _ptr(boxa), d_energy, d_force, d_virial,
+                                                    d_atom_energy or None, d_atom_virial or None,
+                                                    stream or None))
 
     def compute_device_async(self, d_coord: int, d_atype: int, natoms: int, box, d_energy: int,
                              d_force: int, d_virial: int, d_atom_energy: int = 0,

@@ -105,6 +105,12 @@ struct dp_model {
       ae_ws, partials, out10, status, scan_tmp, act, nall_d, split_ws, c4_mom, c4_cot, facc, vacc,
       cpsec, ftgt, vtgt;
   size_t bytes_now = 0, bytes_peak = 0;
+  // dp_compute_device_noalloc: buffers are carved from the device's static
+  // scratch (noalloc.hip) instead of allocated; no stream forks, no vendor
+  // library calls
+  bool arena_on = false;
+  char* arena_base = nullptr;
+  size_t arena_cap = 0, arena_used = 0;
   // type buckets
   std::vector<int> atype_cache;
   std::vector<int> items_h;
@@ -168,9 +174,23 @@ struct dp_model {
 
 namespace {
 
+struct ApiError;
+[[noreturn]] void arena_full(dp_model* M, size_t bytes);
+
 template <class T>
 T* need(dp_model* M, Buf& b, size_t count) {
   const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+  if (M->arena_on) {
+    // carve from the static scratch (256-byte aligned); a buffer asked for
+    // again with a larger size gets a new region
+    if (b.p && bytes <= b.cap) return static_cast<T*>(b.p);
+    const size_t off = (M->arena_used + 255) & ~size_t(255);
+    if (off + bytes > M->arena_cap) arena_full(M, off + bytes);
+    b.p = M->arena_base + off;
+    b.cap = bytes;
+    M->arena_used = off + bytes;
+    return static_cast<T*>(b.p);
+  }
   if (bytes > b.cap) {
     if (b.p) {
       // queued asynchronous evaluations may still use the old buffer
@@ -194,6 +214,14 @@ struct ApiError {
   int code;
   std::string msg;
 };
+
+void arena_full(dp_model* M, size_t bytes) {
+  throw ApiError{DP_ERR_CAPACITY,
+                 "the system needs more than the " + std::to_string(M->arena_cap >> 20) +
+                     " MiB of static scratch of dp_compute_device_noalloc (at least " +
+                     std::to_string((bytes + (1 << 20) - 1) >> 20) +
+                     " MiB); use dp_compute_device"};
+}
 
 // LAMMPS-shaped periodic box; formulas identical to the oracle's box_geometry.
 BoxParams make_box(const double* box, double rcut) {
@@ -447,7 +475,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   // split-K slices of the first layer, one region per type (the chains run
   // concurrently)
   E* split_ws = ws_need ? need<E>(M, M->split_ws, ws_need) : nullptr;
-  const bool fork = active > 1;
+  const bool fork = active > 1 && !M->arena_on;
   if (fork) {
     if (!M->fork_ev) DPAMD_HIP(hipEventCreateWithFlags(&M->fork_ev, hipEventDisableTiming));
     DPAMD_HIP(hipEventRecord(M->fork_ev, st));
@@ -456,7 +484,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
     const int rows = M->type_off[t + 1] - M->type_off[t];
     if (rows <= 0) continue;
     hipStream_t fst = st;
-    void* blas = M->blas;
+    void* blas = M->arena_on ? nullptr : M->blas;
     if (fork) {
       if (!M->fit_st[t]) {
         DPAMD_HIP(hipStreamCreateWithFlags(&M->fit_st[t], hipStreamNonBlocking));
@@ -1185,6 +1213,9 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
       throw ApiError{DP_ERR_NO_GPU, std::string("device is ") + prop.gcnArchName +
                                         ", this library is built for gfx950"};
+    // the device's static scratch of the no-allocation entry point (its
+    // address, looked up once per device)
+    M->arena_base = static_cast<char*>(noalloc_scratch_init(M->device));
     if (c4) {
       // DPA4C nets are fp32 by definition (fp64 energies, forces and virials)
       M->precision = DP_PREC_MIXED;
@@ -1335,6 +1366,55 @@ int dp_compute_device_async(dp_model* M, int natoms, const double* d_coord, cons
   return guarded(M, [&]() {
     device_step(M, natoms, d_coord, d_atype, box, ago, d_energy, d_force, d_virial, d_atom_energy,
                 d_atom_virial, static_cast<hipStream_t>(stream), true);
+  });
+}
+
+// The evaluation of dp_compute_device with every buffer carved from the
+// device's static scratch: the handle's own buffers are set aside for the
+// call and restored after it, and the state that refers to buffer contents
+// (type buckets, stage copies) is invalidated, since the scratch is shared by
+// every handle on the device.
+int dp_compute_device_noalloc(dp_model* M, int natoms, const double* d_coord, const int* d_atype,
+                              const double* box, double* d_energy, double* d_force,
+                              double* d_virial, double* d_atom_energy, double* d_atom_virial,
+                              void* stream) {
+  return guarded(M, [&]() {
+    DPAMD_HIP(hipSetDevice(M->device));
+    settle_async(M);
+    if (!M->arena_base) throw ApiError{DP_ERR_NO_GPU, "no static scratch on this device"};
+    std::vector<Buf> saved;
+    saved.reserve(M->bufs.size());
+    for (Buf* b : M->bufs) {
+      saved.push_back(*b);
+      *b = Buf{};
+    }
+    const bool timing = M->timing;
+    M->timing = false;
+    M->arena_on = true;
+    M->arena_cap = noalloc_scratch_bytes();
+    M->arena_used = 0;
+    M->buckets_valid = false;
+    auto restore = [&]() {
+      for (size_t k = 0; k < M->bufs.size(); ++k) *M->bufs[k] = saved[k];
+      M->arena_on = false;
+      M->timing = timing;
+      M->buckets_valid = false;
+      M->last_nloc = 0;
+      M->last_nall = 0;
+      M->last_standalone = false;
+      M->eg_valid = false;
+      M->dd_valid = false;
+    };
+    try {
+      device_step(M, natoms, d_coord, d_atype, box, 0, d_energy, d_force, d_virial, d_atom_energy,
+                  d_atom_virial, static_cast<hipStream_t>(stream), false);
+    } catch (...) {
+      // kernels already queued only touch the scratch: let them finish
+      (void)hipStreamSynchronize(static_cast<hipStream_t>(stream));
+      restore();
+      throw;
+    }
+    restore();
   });
 }
 

@@ -141,6 +141,12 @@ void launch_edges_ext(hipStream_t, int nloc, int nedge, int nnode, const int* ed
 void launch_edges_fill(hipStream_t, int nloc, int nedge, int nnode, const int* edge_index,
                        const int* off, const int* rank, long* cand_off, int* cand);
 
+// Static workspace of the no-allocation entry point (noalloc.hip): its size,
+// and its address on `device` (which must be current), looked up once per
+// device with hipGetSymbolAddress.
+size_t noalloc_scratch_bytes();
+void* noalloc_scratch_init(int device);
+
 // Scans (hipCUB)
 size_t scan_temp_bytes(int n);
 void exclusive_scan_int(hipStream_t, const int* in, int* out, int n, void* temp, size_t temp_bytes);

@@ -188,6 +188,29 @@ int dp_compute_device_async(dp_model* model, int natoms, const double* d_coord,
                             double* d_force, double* d_virial, double* d_atom_energy,
                             double* d_atom_virial, void* stream);
 
+/*
+ * dp_compute_device (with ago == 0) that allocates nothing: every work
+ * buffer of the evaluation is carved from a static scratch array of
+ * DP_NOALLOC_SCRATCH_BYTES (128 MiB) that the library holds on each GPU it
+ * runs on until the process ends, and no hipMalloc, hipFree or allocating
+ * library routine is called (no vendor GEMM either: the plain GEMMs run as
+ * this library's own kernels, and the per-type chains on `stream` alone).
+ * The caller passes inputs and outputs; the handle's own buffers are left as
+ * they were. A system whose work buffers exceed the scratch is rejected
+ * with DP_ERR_CAPACITY (the outputs are then unspecified; the handle keeps
+ * working). Every handle on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (from several host threads, or queued on different
+ * streams) race, and must be serialised by the caller. Returns when the
+ * outputs are complete. No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops and harnesses that forbid hipMalloc).
+ */
+#define DP_NOALLOC_SCRATCH_BYTES (128u << 20)
+int dp_compute_device_noalloc(dp_model* model, int natoms, const double* d_coord,
+                              const int* d_atype, const double* box, double* d_energy,
+                              double* d_force, double* d_virial, double* d_atom_energy,
+                              double* d_atom_virial, void* stream);
+
 /* With the environment variable DPAMD_GRAPH=1 set when the handle is
  * created, dp_compute_device_async replays the evaluation as a HIP graph: the
  * first call with a given key (natoms, every pointer, the box, the stream)
