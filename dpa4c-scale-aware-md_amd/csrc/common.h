@@ -85,6 +85,49 @@ __device__ __forceinline__ float shfl_xor_d(float v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
 
+// v + shfl_xor(v, 16) and v + shfl_xor(v, 32) on the VALU, with no LDS round
+// trip: v_permlane16_swap trades the odd 16-lane rows of its first operand
+// with the even rows of its second, v_permlane32_swap the upper half of the
+// first with the lower half of the second. With both operands = v, each lane
+// then holds its own value and its xor partner's (in either order), and the
+// sum equals v + shfl_xor(v, mask) exactly (addition commutes). Every lane of
+// the wave must be active. The two results are copied to scalars before any
+// bit cast: __builtin_bit_cast applied to an element of the returned vector
+// has been compiled as a cast of element 0.
+__device__ __forceinline__ unsigned lo32(double v) {
+  return (unsigned)__builtin_bit_cast(unsigned long long, v);
+}
+__device__ __forceinline__ unsigned hi32(double v) {
+  return (unsigned)(__builtin_bit_cast(unsigned long long, v) >> 32);
+}
+__device__ __forceinline__ double from32(unsigned hi, unsigned lo) {
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double add_xor16(double v) {
+  const auto l = __builtin_amdgcn_permlane16_swap(lo32(v), lo32(v), true, false);
+  const auto h = __builtin_amdgcn_permlane16_swap(hi32(v), hi32(v), true, false);
+  const unsigned l0 = l[0], l1 = l[1], h0 = h[0], h1 = h[1];
+  return from32(h0, l0) + from32(h1, l1);
+}
+__device__ __forceinline__ double add_xor32(double v) {
+  const auto l = __builtin_amdgcn_permlane32_swap(lo32(v), lo32(v), true, false);
+  const auto h = __builtin_amdgcn_permlane32_swap(hi32(v), hi32(v), true, false);
+  const unsigned l0 = l[0], l1 = l[1], h0 = h[0], h1 = h[1];
+  return from32(h0, l0) + from32(h1, l1);
+}
+__device__ __forceinline__ float add_xor16(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto s = __builtin_amdgcn_permlane16_swap(u, u, true, false);
+  const unsigned a = s[0], b = s[1];
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto s = __builtin_amdgcn_permlane32_swap(u, u, true, false);
+  const unsigned a = s[0], b = s[1];
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
 // Status word bits raised by kernels and checked by the host after a step.
 enum StatusBit : int {
   kStatusNeighbourOverflow = 1,  // > kMaxCand candidates within rcut of a centre

@@ -261,8 +261,7 @@ k_embed_fwd32(EmbArgs a) {
 #pragma unroll
     for (int q = 0; q < S::NU3 * 4; ++q) {
       float v = Tacc[q];
-      v += shfl_xor_d(v, 16);
-      v += shfl_xor_d(v, 32);
+      v = add_xor32(add_xor16(v));
       Tacc[q] = v;
     }
     if (g == 0 && a.Tt) {
@@ -512,10 +511,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       }
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        up[m] += shfl_xor_d(up[m], 16);
-        up[m] += shfl_xor_d(up[m], 32);
-        vp[m] += shfl_xor_d(vp[m], 16);
-        vp[m] += shfl_xor_d(vp[m], 32);
+        up[m] = add_xor32(add_xor16(up[m]));
+        vp[m] = add_xor32(add_xor16(vp[m]));
       }
       if (valid && g == 0) {
         double nd[4];

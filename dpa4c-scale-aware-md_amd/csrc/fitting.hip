@@ -468,14 +468,10 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
       }
     }
   }
-  s0 += shfl_xor_d(s0, 16);
-  s0 += shfl_xor_d(s0, 32);
-  s1 += shfl_xor_d(s1, 16);
-  s1 += shfl_xor_d(s1, 32);
-  s2 += shfl_xor_d(s2, 16);
-  s2 += shfl_xor_d(s2, 32);
-  s3 += shfl_xor_d(s3, 16);
-  s3 += shfl_xor_d(s3, 32);
+  s0 = add_xor32(add_xor16(s0));
+  s1 = add_xor32(add_xor16(s1));
+  s2 = add_xor32(add_xor16(s2));
+  s3 = add_xor32(add_xor16(s3));
   wave_lds_sync();
   if (g == 0) {
     out[c] = F16[w][c] + s0;
@@ -615,8 +611,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
       v = fma(acc[1], Tc[1][m], v);
       v = fma(acc[2], Tc[2][m], v);
       v = fma(acc[3], Tc[3][m], v);
-      v += shfl_xor_d(v, 16);
-      v += shfl_xor_d(v, 32);
+      v = add_xor32(add_xor16(v));
       s[m] = v;
     }
     Obw[(c * 4 + g) * 16 + (a & 15)] = g == 0 ? s[0] : g == 1 ? s[1] : g == 2 ? s[2] : s[3];
