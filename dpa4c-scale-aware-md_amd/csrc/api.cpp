@@ -32,6 +32,7 @@
 #include <vector>
 
 #include "../../include/dp_amd.h"
+#include "fixed.h"
 #include "kernels.h"
 #include "model.h"
 
@@ -406,6 +407,8 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   ea.rcut = m.rcut;
   ea.rcut_smth = m.rcut_smth;
   ea.inv_sw = 1.0 / (m.rcut - m.rcut_smth);
+  ea.status = static_cast<int*>(M->status.p);
+  ea.fix_gmax = fixed_gmax(m.rcut);
   ea.inv_nnei = 1.0 / (double)nnei;
   ea.emb = M->d_emb;
   ea.envp = M->d_envp;
@@ -811,6 +814,10 @@ void throw_status(int s) {
                    "more neighbours of one type within rcut than the model's sel holds"};
   if (s & kStatusBadInput)
     throw ApiError{DP_ERR_ARG, "atom type or edge source outside the model / graph"};
+  if (s & kStatusFixedRange)
+    throw ApiError{DP_ERR_CAPACITY,
+                   "an edge's force is outside the fixed-point force accumulators' range "
+                   "(|dE/dd| > 8192 eV/A / max(1, rcut), or not finite)"};
 }
 
 void check_status(dp_model* M, hipStream_t st) {

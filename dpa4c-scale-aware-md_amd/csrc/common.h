@@ -134,6 +134,7 @@ enum StatusBit : int {
   kStatusReverseOverflow = 2,    // > kMaxRev edges pointing at one atom
   kStatusBadInput = 4,           // atom type or source index outside the model / graph
   kStatusSelOverflow = 8,        // more neighbours of one type than a strict sel holds
+  kStatusFixedRange = 16,        // an edge gradient beyond the fixed-point accumulators' range
 };
 
 }  // namespace dpamd

@@ -109,6 +109,10 @@ __device__ __forceinline__ void edge_out(const EmbArgs& a, long e, int t, const 
       __hip_atomic_fetch_add(own + 3 + 3 * c + q, -gv[c] * d[q], __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_WAVEFRONT);
   }
+  // range guard of the fixed point: a NaN or an out-of-range gradient would
+  // wrap silently in the integer sums
+  const double gm = fmax(fabs(gv[0]), fmax(fabs(gv[1]), fabs(gv[2])));
+  if (!(gm <= a.fix_gmax)) atomicOr(a.status, kStatusFixedRange);
   unsigned long long* fa = a.facc + 3L * t;
   fixed_add(fa, gv[0]);
   fixed_add(fa + 1, gv[1]);

@@ -71,6 +71,10 @@ struct EmbArgs {
   unsigned long long* facc;
   unsigned long long* vacc;
   double* cpsec;
+  // status word, and the largest |component| of an edge gradient the fixed
+  // point accepts (raising kStatusFixedRange above it or on NaN)
+  int* status;
+  double fix_gmax;
   // Saved activations: per (centre, tile of 16 slots) a block of
   // 16*(L2P + L3P) doubles holding tanh of layers 2 and 3 in the backward's
   // register order; tiles of section tj start at tile_off[tj], tiles_per_atom

@@ -223,3 +223,22 @@ def test_bitwise_reproducible(dp):
     assert r1[0] == r2[0]
     for a, b in zip(r1[1:], r2[1:]):
         assert a.tobytes() == b.tobytes()
+
+
+def test_fixed_point_range_guard(dp):
+    """The fp64 force stage sums edge forces in 64-bit fixed point; an edge
+    gradient large enough to wrap those sums (here: the energy head scaled by
+    1e9) is reported as a capacity error instead of giving wrong forces, and
+    the flag does not outlive the evaluation that raised it."""
+    (coord, atype, box), m = CASES["water192"]()
+    m = dict(m)
+    fp = m["fit_params"].copy()
+    F2 = int(m["fit"][2])
+    fp[:, -(F2 + 1):-1] *= 1e9
+    m["fit_params"] = fp
+    pot = dp.DeepPot(file_content=model_bytes(m))
+    with pytest.raises(dp.DeepmdException, match="fixed-point"):
+        pot.compute(coord, atype, box)
+    # two atoms farther apart than rcut: no edges, nothing to overflow
+    e, f, v = pot.compute(np.array([[0.0, 0.0, 0.0], [9.0, 0.0, 0.0]]), np.array([0, 1]), None)
+    assert np.all(f == 0.0) and np.isfinite(e)
