@@ -128,6 +128,22 @@ __device__ __forceinline__ float add_xor32(float v) {
   return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
 
+// The hardware deals a grid's workgroups to the XCDs round robin in linear-id
+// order (x fastest), and each XCD has its own L2. xcd_swizzle() remaps the
+// linear id so that consecutive logical blocks run on the same XCD: with x
+// the column blocks of one row block, the blocks that read the same rows of
+// A share one L2 instead of each XCD fetching them from HBM. A bijection on
+// the grid for any block count.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int3 xcd_swizzle() {
+  const int nx = gridDim.x, ny = gridDim.y;
+  const int nb = nx * ny * (int)gridDim.z;
+  const int L = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+  const int q = nb / kXcds, r = nb % kXcds, x = L % kXcds;
+  const int id = x * q + (x < r ? x : r) + L / kXcds;
+  return int3{id % nx, (id / nx) % ny, id / (nx * ny)};
+}
+
 // Status word bits raised by kernels and checked by the host after a step.
 enum StatusBit : int {
   kStatusNeighbourOverflow = 1,  // > kMaxCand candidates within rcut of a centre

@@ -55,9 +55,9 @@ struct GemmArgs {
 // acc[n] register r of wave w holds C[row0 + 16w + Frag::row(g, r)][col0 + 16n + c].
 template <class T, int NT>
 __device__ __forceinline__ void gemm_store(const GemmArgs<T>& a, const typename Frag<T>::V (&acc)[NT],
-                                           int row0, int col0, int w, int g, int c) {
+                                           int row0, int col0, int zs, int w, int g, int c) {
   if (a.split > 1) {
-    T* out = a.ws + (long)blockIdx.z * a.M * a.ldc;
+    T* out = a.ws + (long)zs * a.M * a.ldc;
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -125,7 +125,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
   __shared__ T As[2][BM * ALD];
   __shared__ T Bs[2][BK * BLD];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
-  const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+  const int3 bid = xcd_swizzle();
+  const int row0 = bid.y * BM, col0 = bid.x * BN;
   // AT: this thread's row and column quarter, and T[m][4 part + j] of the row
   const int at_r = tid >> 2, at_part = tid & 3;
   const T* at_row = nullptr;  // T[.][0][row] of this thread's row
@@ -199,7 +200,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
   int kc0 = 0, nk = a.K / BK;
   if (a.split > 1) {
     const int per = (nk + a.split - 1) / a.split;
-    kc0 = blockIdx.z * per;
+    kc0 = bid.z * per;
     nk = min(nk, kc0 + per);
   }
   // (a slice past the end of K keeps zeros: it is still stored, and summed)
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
     if (kc + 1 < nk) stash(buf ^ 1);
     __syncthreads();
   }
-  gemm_store<T, NT>(a, acc, row0, col0, w, g, c);
+  gemm_store<T, NT>(a, acc, row0, col0, bid.z, w, g, c);
 }
 
 // fp32 GEMM on the bf16 matrix cores at fp32 accuracy (mixed precision):
@@ -244,7 +245,8 @@ __global__ __launch_bounds__(256) void k_gemm3(GemmArgs<float> a) {
   __shared__ __align__(16) float As[2][BM * ALD];
   __shared__ __align__(16) bf8 Bs[2][NT * 3 * 64];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
-  const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+  const int3 bid = xcd_swizzle();
+  const int row0 = bid.y * BM, col0 = bid.x * BN;
   const int ntile = a.N / 16, tile0 = col0 / 16;
   const bf8* Bf = static_cast<const bf8*>(a.Bf);
   // staging share: row sr, k columns sk .. sk + 7 of the chunk
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(256) void k_gemm3(GemmArgs<float> a) {
   int kc0 = 0, nk = (a.K + BK - 1) / BK;
   if (a.split > 1) {
     const int per = (nk + a.split - 1) / a.split;
-    kc0 = blockIdx.z * per;
+    kc0 = bid.z * per;
     nk = min(nk, kc0 + per);
   }
   if (kc0 < nk) {
@@ -323,7 +325,7 @@ __global__ __launch_bounds__(256) void k_gemm3(GemmArgs<float> a) {
     if (kc + 1 < nk) stash(buf ^ 1);
     __syncthreads();
   }
-  gemm_store<float, NT>(a, acc, row0, col0, w, g, c);
+  gemm_store<float, NT>(a, acc, row0, col0, bid.z, w, g, c);
 }
 
 // Split-K forward epilogue of a layer without residual: C = tanh(sum over
