@@ -104,7 +104,7 @@ struct dp_model {
       cell_start, cell_rank, sorted, nlist, nreal, cand_off, cand, items, Tsec, Tt, D, dD, dT,
       fitb, e_bucket, edge_grad, cpart, rev_count, rev_off, rev_rank, rev, force_ws, av_ws,
       ae_ws, partials, out10, status, scan_tmp, act, nall_d, split_ws, c4_mom, c4_cot, facc, vacc,
-      cpsec, ftgt, vtgt;
+      cpsec, ftgt, vtgt, ddt_ws;
   size_t bytes_now = 0, bytes_peak = 0;
   // dp_compute_device_noalloc: buffers are carved from the device's static
   // scratch (noalloc.hip) instead of allocated; no stream forks, no vendor
@@ -169,7 +169,7 @@ struct dp_model {
             &dD,       &dT,       &fitb,      &e_bucket, &edge_grad,  &cpart,     &rev_count,
             &rev_off,  &rev_rank, &rev,       &force_ws, &av_ws,      &ae_ws,     &partials,
             &out10,    &status,   &scan_tmp, &act,       &nall_d,    &split_ws,  &c4_mom,
-            &c4_cot,   &facc,     &vacc,      &cpsec,      &ftgt,      &vtgt};
+            &c4_cot,   &facc,     &vacc,      &cpsec,      &ftgt,      &vtgt,      &ddt_ws};
   }
 };
 
@@ -468,13 +468,17 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   record(M, st, kStDescr + 1);
 
   int active = 0;
-  size_t ws_need = 0, ws_off = 0;
+  size_t ws_need = 0, ws_off = 0, ddt_need = 0, ddt_off = 0;
   for (int t = 0; t < nt; ++t) {
     const int rows = M->type_off[t + 1] - M->type_off[t];
     active += rows > 0;
     const int sp = rows > 0 ? fit_splits(rows, m.fit[0], Dn, M->ncu) : 1;
     if (sp > 1) ws_need += (size_t)sp * rows * m.fit[0];
+    const int ds = (fused_ddt && rows > 0) ? ddt_splits(rows, L3, M->ncu) : 1;
+    if (ds > 1) ddt_need += (size_t)(ds + 1) * rows * 64;
   }
+  // the fused input-gradient kernel's split partials, one region per type
+  double* ddt_ws = ddt_need ? need<double>(M, M->ddt_ws, ddt_need) : nullptr;
   // split-K slices of the first layer, one region per type (the chains run
   // concurrently)
   E* split_ws = ws_need ? need<E>(M, M->split_ws, ws_need) : nullptr;
@@ -535,6 +539,9 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
       ddt.dT = reinterpret_cast<double*>(dT);
       ddt.dD = dD ? reinterpret_cast<double*>(dD) + r0 * Dn : nullptr;
       ddt.ncu = M->ncu;
+      ddt.nsplit = ddt_splits(rows, L3, M->ncu);
+      ddt.ws = ddt.nsplit > 1 ? ddt_ws + ddt_off : nullptr;
+      if (ddt.nsplit > 1) ddt_off += (size_t)(ddt.nsplit + 1) * rows * 64;
     }
     launch_fitting(fst, net, rows, d_from_t ? nullptr : D + r0 * Dn,
                    d_from_t ? Tt + r0 * 4 : nullptr, 4L * nb, L3, fb, dD ? dD + r0 * Dn : nullptr,

@@ -13,6 +13,8 @@
 // fused tile analog is deepmd-op/overlays/op/pt/tiled_fitting.cuh:4-60.
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
+
 #include "bf16x3.h"
 #include "fastmath.h"
 #include "kernels.h"
@@ -519,6 +521,12 @@ struct DdtArgs {
   const int* items;
   double* dT;  // [atoms][4][L3]
   double* dD;  // [rows][16 L3] or null
+  // column-group split (blockIdx.y of nsplit; 1: no split): the split's
+  // second-term partials go to ws[s][rows][4 m][16 b], the last split's
+  // first terms of a < 16 to ws[nsplit][rows][4][16], and k_ddt_combine
+  // assembles dT[.][m][b < 16] from them
+  int nsplit;
+  double* ws;
 };
 
 template <int WAVES, int NQ>
@@ -533,6 +541,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
   const bool rowok = wrow < p.rows;
   const int Dn = 16 * p.L3;
   double* Obw = Ob + w * 16 * 4 * 16;
+  // this block's column groups: split s takes i in [i0, i1), the boundaries
+  // 16-aligned within the a >= 16 groups (so every flush stays whole), the
+  // last split also the 16 groups a < 16
+  const int S = p.nsplit, s = blockIdx.y, R = p.L3 - 16;
+  auto bound = [&](int k) { return k >= S ? p.L3 : 16 * ((2 * k * R + 16 * S) / (32 * S)); };
+  const int i0 = bound(s), i1 = bound(s + 1);
   // dZ0 row of this lane as MFMA B operands: element k = 4q + g
   double Zb[NQ];
 #pragma unroll
@@ -574,13 +588,13 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
   };
   auto col_of = [&](int i) { return i + 16 < p.L3 ? i + 16 : i + 16 - p.L3; };
 
-  issue(0, col_of(0));
-  for (int i = 0; i < p.L3; ++i) {
-    const int a = col_of(i), buf = i & 1;
+  if (i0 < i1) issue(0, col_of(i0));
+  for (int i = i0; i < i1; ++i) {
+    const int a = col_of(i), buf = (i - i0) & 1;
     // group i has landed (each wave waits for its own transfers, then the
     // barrier), and no wave still reads the buffer group i + 1 goes to
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (i + 1 < p.L3) issue(buf ^ 1, col_of(i + 1));
+    if (i + 1 < i1) issue(buf ^ 1, col_of(i + 1));
     // D'[b][row] over K: register r of lane (g, c) = dD[row c][a][g + 4r]
     // two independent accumulation chains (the halves of K), operands read
     // from LDS two k-steps ahead
@@ -646,7 +660,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
   }
   // a < 16: first term from the buffer + second term
   wave_lds_sync();
-  if (rowok) {
+  if (rowok && S == 1) {
     double* out = p.dT + (long)my_atom * 4 * p.L3;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -655,7 +669,32 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
         const int b = g + 4 * r;
         out[m * p.L3 + b] = Obw[(c * 4 + m) * 16 + b] + acc2[r][m];
       }
+  } else if (rowok) {
+    double* part = p.ws + ((long)s * p.rows + wrow) * 64;
+    double* first = p.ws + ((long)S * p.rows + wrow) * 64;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int b = g + 4 * r;
+        part[m * 16 + b] = acc2[r][m];
+        if (s == S - 1) first[m * 16 + b] = Obw[(c * 4 + m) * 16 + b];
+      }
   }
+}
+
+// dT[atom][m][b < 16] of a split k_dDdT: the last split's first term plus the
+// splits' second-term partials, summed in split order. One thread per (row,
+// m, b).
+__global__ __launch_bounds__(256) void k_ddt_combine(int rows, int L3, int nsplit, int pos0,
+                                                     const int* items, const double* ws,
+                                                     double* dT) {
+  const long q = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= (long)rows * 64) return;
+  const int row = (int)(q >> 6), e = (int)(q & 63), m = e >> 4, b = e & 15;
+  double sum = ws[q];
+  for (int k = 1; k < nsplit; ++k) sum += ws[(long)k * rows * 64 + q];
+  dT[((long)items[pos0 + row] * 4 + m) * L3 + b] = ws[(long)nsplit * rows * 64 + q] + sum;
 }
 
 template <int WAVES>
@@ -799,7 +838,7 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   if constexpr (sizeof(T) == 8) {
     if (ddt) {
       launch_dDdT(st, rows, F0, L3, b.dZa, ddt->W0T, Tt, ldt, ddt->pos0, ddt->items, ddt->dT, ddt->dD,
-                  ddt->ncu);
+                  ddt->ncu, ddt->nsplit, ddt->ws);
       return;
     }
   }
@@ -815,26 +854,56 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
 
 bool ddt_supported(int K, int L3, int axis) { return K == 240 && axis == 16 && L3 >= 16 && L3 <= 128; }
 
+// Block shape of the fused kernel for a type of `rows` rows: eight waves (128
+// rows) when that gives every compute unit two blocks; four (64 rows) when
+// it gives one; otherwise eight waves with the column groups split over
+// blockIdx.y, enough ways to give every compute unit a block (at most one
+// way per 16 groups a >= 16). Returns the split count; *waves the shape.
+static int ddt_shape(int rows, int L3, int ncu, int* waves) {
+  const int nb8 = (rows + 127) / 128;
+  *waves = 8;
+  if (nb8 >= 2 * ncu) return 1;
+  if (nb8 >= ncu) {
+    *waves = 4;
+    return 1;
+  }
+  const int smax = std::max(1, (L3 - 16) / 16);
+  return std::min(smax, (ncu + nb8 - 1) / nb8);
+}
+
+int ddt_splits(int rows, int L3, int ncu) {
+  int waves = 0;
+  return ddt_shape(rows, L3, ncu, &waves);
+}
+
 void launch_dDdT(hipStream_t st, int rows, int K, int L3, const double* dZ, const double* W0T,
                  const double* Tt, long ldt, int pos0, const int* items, double* dT, double* dD,
-                 int ncu) {
+                 int ncu, int nsplit, double* ws) {
   if (rows <= 0) return;
   if (K != 240) throw HipError{hipErrorInvalidValue, "fused dE/dD kernel needs F0 = 240"};
-  DdtArgs p{rows, K, L3, dZ, W0T, Tt, ldt, pos0, items, dT, dD};
-  // eight waves (128 rows) per block when that still gives every compute
-  // unit two blocks; four (64 rows) otherwise
-  if ((rows + 127) / 128 >= 2 * ncu) {
+  int waves = 0;
+  const int S = ddt_shape(rows, L3, ncu, &waves);
+  if (S != nsplit || (S > 1 && !ws))
+    throw HipError{hipErrorInvalidValue, "fused dE/dD kernel: split workspace does not match"};
+  DdtArgs p{rows, K, L3, dZ, W0T, Tt, ldt, pos0, items, dT, dD, S, ws};
+  if (waves == 8) {
     const size_t bytes = ddt_lds_bytes<8>(K);
     DPAMD_HIP(hipFuncSetAttribute((const void*)k_dDdT<8, 60>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
-    hipLaunchKernelGGL((k_dDdT<8, 60>), dim3((rows + 127) / 128), dim3(512), bytes, st, p);
+    hipLaunchKernelGGL((k_dDdT<8, 60>), dim3((rows + 127) / 128, S), dim3(512), bytes, st, p);
   } else {
     const size_t bytes = ddt_lds_bytes<4>(K);
     DPAMD_HIP(hipFuncSetAttribute((const void*)k_dDdT<4, 60>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
-    hipLaunchKernelGGL((k_dDdT<4, 60>), dim3((rows + 63) / 64), dim3(256), bytes, st, p);
+    hipLaunchKernelGGL((k_dDdT<4, 60>), dim3((rows + 63) / 64, S), dim3(256), bytes, st, p);
   }
   DPAMD_LAUNCH_CHECK();
+  if (S > 1) {
+    const long n = (long)rows * 64;
+    hipLaunchKernelGGL(k_ddt_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, rows, L3,
+                       S, pos0, items, ws, dT);
+    DPAMD_LAUNCH_CHECK();
+  }
 }
 
 template <class T>

@@ -216,11 +216,16 @@ struct FitDdt {
   double* dT;         // [atoms][4][L3]
   double* dD;         // [rows][16 L3] when kept for inspection, else null
   int ncu;
+  // column-group splits (ddt_splits) and their workspace, (nsplit + 1) *
+  // rows * 64 doubles (unused when nsplit == 1)
+  int nsplit;
+  double* ws;
 };
+int ddt_splits(int rows, int L3, int ncu);
 bool ddt_supported(int F0, int L3, int axis);
 void launch_dDdT(hipStream_t, int rows, int K, int L3, const double* dZ, const double* W0T,
                  const double* Tt, long ldt, int pos0, const int* items, double* dT, double* dD,
-                 int ncu);
+                 int ncu, int nsplit, double* ws);
 template <class T>
 void launch_fitting(hipStream_t, const FitNet<T>&, int rows, const T* D, const T* Tt, long ldt,
                     int L3, const FitBufs<T>&, T* dD, double* e_bucket, void* blas,
