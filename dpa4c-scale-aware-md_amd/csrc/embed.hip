@@ -91,6 +91,7 @@ template <class S, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
   static_assert(S::L1 > 2, "layer-1 residual not supported");
   extern __shared__ double lds[];
+  __shared__ int item_next;  // next item of the block (see the item loop)
   constexpr int PS = (S::SIZE + 31) / 32 * 32;
   constexpr int X2LD = S::L2P + 2;
   double* P = lds;
@@ -111,11 +112,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     }
     for (int q = threadIdx.x; q < kTanhTab; q += WAVES * 64) Tab[q] = kExp2Tab128[q];
   }
+  if (threadIdx.x == 0) item_next = 0;
   __syncthreads();
   const int nitems = a.type_off[ti + 1] - a.type_off[ti];
-  for (int it = 0; it < a.ipw; ++it) {
-    const int item = (((int)blockIdx.x - a.block_off[p]) * a.ipw + it) * WAVES + w;
-    if (item >= nitems) break;
+  // the block's WAVES * ipw items are handed out one at a time from an LDS
+  // counter, so a wave whose items have few tiles takes more of them and the
+  // block's waves finish together (the next block can start only when all
+  // of this one's have)
+  const int first_item = ((int)blockIdx.x - a.block_off[p]) * a.ipw * WAVES;
+  for (;;) {
+    int k = 0;
+    if (lane == 0) k = atomicAdd(&item_next, 1);
+    k = __builtin_amdgcn_readfirstlane(k);
+    const int item = first_item + k;
+    if (k >= a.ipw * WAVES || item >= nitems) break;
     const int i = a.items[a.type_off[ti] + item];
     const int nr = a.nreal[(long)i * a.ntypes + tj];
     const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
@@ -318,6 +328,7 @@ template <class S, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
   static_assert(S::L1 > 2, "layer-1 residual not supported");
   extern __shared__ double lds[];
+  __shared__ int item_next;  // next item of the block (see the item loop)
   constexpr int PS = (S::SIZE + 31) / 32 * 32;
   double* P = lds;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
@@ -345,11 +356,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     for (int q = lane; q < 16 * 12; q += 64) own_w[q] = 0.0;
     for (int q = threadIdx.x; q < kTanhTab; q += WAVES * 64) Tab[q] = kExp2Tab128[q];
   }
+  if (threadIdx.x == 0) item_next = 0;
   __syncthreads();
   const int nitems = a.type_off[ti + 1] - a.type_off[ti];
-  for (int it = 0; it < a.ipw; ++it) {
-    const int item = (((int)blockIdx.x - a.block_off[p]) * a.ipw + it) * WAVES + w;
-    if (item >= nitems) break;
+  // the block's WAVES * ipw items are handed out one at a time from an LDS
+  // counter, so a wave whose items have few tiles takes more of them and the
+  // block's waves finish together (the next block can start only when all
+  // of this one's have)
+  const int first_item = ((int)blockIdx.x - a.block_off[p]) * a.ipw * WAVES;
+  for (;;) {
+    int k = 0;
+    if (lane == 0) k = atomicAdd(&item_next, 1);
+    k = __builtin_amdgcn_readfirstlane(k);
+    const int item = first_item + k;
+    if (k >= a.ipw * WAVES || item >= nitems) break;
     const int i = a.items[a.type_off[ti] + item];
     const int nr = a.nreal[(long)i * a.ntypes + tj];
     const long ebase = (long)i * a.nnei + a.sec[tj];

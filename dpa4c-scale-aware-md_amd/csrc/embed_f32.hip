@@ -102,6 +102,7 @@ k_embed_fwd32(EmbArgs a) {
   static_assert(S::L1 > 2, "layer-1 residual not supported");
   static_assert(S::K3P == S::L2P, "fp32 layout expected");
   extern __shared__ __align__(16) float lds32[];
+  __shared__ int item_next;  // next item of the block (see the item loop)
   constexpr int PS = lds_params<S>();
   constexpr int X2LD = x2_ld<S>();
   float* P = lds32;
@@ -120,11 +121,20 @@ k_embed_fwd32(EmbArgs a) {
       EnvS[threadIdx.x] = threadIdx.x < 4 ? v : 1.0 / v;  // avg[4], 1 / dstd[4]
     }
   }
+  if (threadIdx.x == 0) item_next = 0;
   __syncthreads();
   const int nitems = a.type_off[ti + 1] - a.type_off[ti];
-  for (int it = 0; it < a.ipw; ++it) {
-    const int item = (((int)blockIdx.x - a.block_off[p]) * a.ipw + it) * WAVES + w;
-    if (item >= nitems) break;
+  // the block's WAVES * ipw items are handed out one at a time from an LDS
+  // counter, so a wave whose items have few tiles takes more of them and the
+  // block's waves finish together (the next block can start only when all
+  // of this one's have)
+  const int first_item = ((int)blockIdx.x - a.block_off[p]) * a.ipw * WAVES;
+  for (;;) {
+    int k = 0;
+    if (lane == 0) k = atomicAdd(&item_next, 1);
+    k = __builtin_amdgcn_readfirstlane(k);
+    const int item = first_item + k;
+    if (k >= a.ipw * WAVES || item >= nitems) break;
     const int i = a.items[a.type_off[ti] + item];
     const int nr = a.nreal[(long)i * a.ntypes + tj];
     const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
@@ -298,6 +308,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
   static_assert(S::L1 > 2, "layer-1 residual not supported");
   static_assert(S::K3P == S::L2P, "fp32 layout expected");
   extern __shared__ __align__(16) float lds32[];
+  __shared__ int item_next;  // next item of the block (see the item loop)
   constexpr int PS = lds_params<S>();
   float* P = lds32;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
@@ -315,11 +326,20 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       EnvS[threadIdx.x] = threadIdx.x < 4 ? v : 1.0 / v;  // avg[4], 1 / dstd[4]
     }
   }
+  if (threadIdx.x == 0) item_next = 0;
   __syncthreads();
   const int nitems = a.type_off[ti + 1] - a.type_off[ti];
-  for (int it = 0; it < a.ipw; ++it) {
-    const int item = (((int)blockIdx.x - a.block_off[p]) * a.ipw + it) * WAVES + w;
-    if (item >= nitems) break;
+  // the block's WAVES * ipw items are handed out one at a time from an LDS
+  // counter, so a wave whose items have few tiles takes more of them and the
+  // block's waves finish together (the next block can start only when all
+  // of this one's have)
+  const int first_item = ((int)blockIdx.x - a.block_off[p]) * a.ipw * WAVES;
+  for (;;) {
+    int k = 0;
+    if (lane == 0) k = atomicAdd(&item_next, 1);
+    k = __builtin_amdgcn_readfirstlane(k);
+    const int item = first_item + k;
+    if (k >= a.ipw * WAVES || item >= nitems) break;
     const int i = a.items[a.type_off[ti] + item];
     const int nr = a.nreal[(long)i * a.ntypes + tj];
     const long ebase = (long)i * a.nnei + a.sec[tj];
