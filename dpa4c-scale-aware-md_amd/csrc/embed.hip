@@ -48,9 +48,10 @@ namespace dpamd {
 constexpr int kU3 = 2;
 constexpr int kU3B = 1;
 
-// LDS: padded net | env statistics of the pair (8) | exp2 table of the tanh
-// (kTanhTab) | per-wave scratch
-constexpr int kTanhTab = 128;
+// LDS: padded net | env statistics of the pair (8) | table of the tanh
+// (kTanhTab32, padded to kTanhTab) | per-wave scratch
+constexpr int kTanhTab = 648;
+static_assert(kTanhTab >= kTanhTabN && kTanhTab % 8 == 0, "tanh table slot");
 template <class S>
 constexpr int fwd_lds_doubles(int waves) {
   return (S::SIZE + 31) / 32 * 32 + 8 + kTanhTab + waves * 16 * (S::L2P + 2) + waves * 64;
@@ -110,7 +111,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       const double v = a.envp[p * 8 + threadIdx.x];
       EnvS[threadIdx.x] = threadIdx.x < 4 ? v : 1.0 / v;  // avg[4], 1 / dstd[4]
     }
-    for (int q = threadIdx.x; q < kTanhTab; q += WAVES * 64) Tab[q] = kExp2Tab128[q];
+    for (int q = threadIdx.x; q < kTanhTab; q += WAVES * 64)
+      Tab[q] = q < kTanhTabN ? kTanhTab32[q] : 0.0;
   }
   if (threadIdx.x == 0) item_next = 0;
   __syncthreads();
@@ -354,7 +356,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       EnvS[threadIdx.x] = threadIdx.x < 4 ? v : 1.0 / v;  // avg[4], 1 / dstd[4]
     }
     for (int q = lane; q < 16 * 12; q += 64) own_w[q] = 0.0;
-    for (int q = threadIdx.x; q < kTanhTab; q += WAVES * 64) Tab[q] = kExp2Tab128[q];
+    for (int q = threadIdx.x; q < kTanhTab; q += WAVES * 64)
+      Tab[q] = q < kTanhTabN ? kTanhTab32[q] : 0.0;
   }
   if (threadIdx.x == 0) item_next = 0;
   __syncthreads();

@@ -1,67 +1,72 @@
 #!/usr/bin/env python3
 """Derives the constants of the table-driven fp64 tanh in fastmath.h.
 
-2^f for f in [-1/256, 1/256] is p(f) = 1 + f q(f), q a cubic interpolating
-(2^f - 1) / f at the four Chebyshev nodes of the interval (near-minimax);
-the table holds 2^(j/128), j = 0..127, correctly rounded. Everything is
-computed with 60-digit decimal arithmetic and rounded to fp64 once. Prints
-the C++ initialisers and the interpolant's worst relative error on a dense
-grid (evaluated in exact arithmetic from the rounded coefficients).
+tanh(a + b) = (tanh a + tanh b) / (1 + tanh a tanh b) with a = k/32 and
+|b| <= 1/64:
+  * the table holds tanh(k/32), k = 0..640, correctly rounded;
+  * tanh b = b + b^3 (c3 + c5 b^2), the odd quintic that minimises the largest
+    absolute error over |b| <= 1/64 (Remez exchange on three reference points;
+    the error equioscillates at about 3.2e-16).
+Everything is computed with 60-digit decimal arithmetic and rounded to fp64
+once. Prints the C++ initialisers and the quintic's worst absolute error on a
+dense grid (evaluated in exact arithmetic from the rounded coefficients).
 """
 from decimal import Decimal, getcontext
 
 getcontext().prec = 60
-LN2 = Decimal(2).ln()
+H = Decimal(1) / 64  # largest |b|
+NTAB = 641           # a = k/32 up to the clamp at 20
 
 
-def exp2(x):
-    return (x * LN2).exp()
+def tanh_d(x):
+    x = Decimal(x)
+    if x == 0:
+        return Decimal(0)
+    e = (2 * x).exp()
+    return (e - 1) / (e + 1)
 
 
-def q_true(f):
-    if f == 0:
-        return LN2
-    return (exp2(f) - 1) / f
+def solve3(m, r):
+    """Gaussian elimination for a 3x3 system in Decimal."""
+    m = [row[:] + [v] for row, v in zip(m, r)]
+    for i in range(3):
+        p = max(range(i, 3), key=lambda k: abs(m[k][i]))
+        m[i], m[p] = m[p], m[i]
+        for k in range(i + 1, 3):
+            f = m[k][i] / m[i][i]
+            m[k] = [a - f * b for a, b in zip(m[k], m[i])]
+    x = [Decimal(0)] * 3
+    for i in (2, 1, 0):
+        x[i] = (m[i][3] - sum(m[i][j] * x[j] for j in range(i + 1, 3))) / m[i][i]
+    return x
 
 
-def cheb_cubic(h):
-    """Coefficients c1..c4 of q(f) = c1 + c2 f + c3 f^2 + c4 f^3 through the
-    Chebyshev nodes of [-h, h] (Newton divided differences)."""
-    import math
-    nodes = [Decimal(math.cos((2 * k + 1) * math.pi / 8)) * h for k in range(4)]
-    ys = [q_true(x) for x in nodes]
-    n = 4
-    coef = list(ys)
-    for j in range(1, n):
-        for i in range(n - 1, j - 1, -1):
-            coef[i] = (coef[i] - coef[i - 1]) / (nodes[i] - nodes[i - j])
-    # expand the Newton form into monomials
-    poly = [Decimal(0)] * n
-    basis = [Decimal(1)]
-    for k in range(n):
-        for d, b in enumerate(basis):
-            poly[d] += coef[k] * b
-        nb = [Decimal(0)] * (len(basis) + 1)
-        for d, b in enumerate(basis):
-            nb[d + 1] += b
-            nb[d] -= nodes[k] * b
-        basis = nb
-    return poly
+def err(b, c3, c5):
+    return tanh_d(b) - b - c3 * b ** 3 - c5 * b ** 5
+
+
+def remez_quintic(grid=2000, iters=6):
+    """c3, c5 minimising max |tanh b - b - c3 b^3 - c5 b^5| on (0, H]."""
+    ref = [H * Decimal("0.45"), H * Decimal("0.85"), H]
+    pts = [H * k / grid for k in range(1, grid + 1)]
+    for _ in range(iters):
+        c3, c5, _e = solve3([[b ** 3, b ** 5, Decimal((-1) ** i)] for i, b in enumerate(ref)],
+                            [tanh_d(b) - b for b in ref])
+        e = [err(b, c3, c5) for b in pts]
+        ext = [pts[i] for i in range(1, grid - 1)
+               if abs(e[i]) >= abs(e[i - 1]) and abs(e[i]) >= abs(e[i + 1])]
+        ref = (ext + [H])[-3:]
+    return c3, c5
 
 
 def main():
-    h = Decimal(1) / 256
-    c = [float(x) for x in cheb_cubic(h)]
-    table = [float(exp2(Decimal(j) / 128)) for j in range(128)]
-    worst = Decimal(0)
-    for k in range(-4000, 4001):
-        f = h * k / 4000
-        p = 1 + f * (Decimal(c[0]) + f * (Decimal(c[1]) + f * (Decimal(c[2]) + f * Decimal(c[3]))))
-        worst = max(worst, abs(p / exp2(f) - 1))
-    print("// q(f) coefficients c1..c4:", ", ".join(repr(x) for x in c))
-    print("// worst relative error of p:", f"{float(worst):.3e}")
-    print("constexpr double kExp2Tab128[128] = {")
-    for j in range(0, 128, 4):
+    c3, c5 = (float(v) for v in remez_quintic())
+    worst = max(abs(err(H * k / 4000, Decimal(c3), Decimal(c5))) for k in range(1, 4001))
+    table = [float(tanh_d(Decimal(k) / 32)) for k in range(NTAB)]
+    print(f"constexpr double kTanhC3 = {c3!r}, kTanhC5 = {c5!r};")
+    print(f"// worst absolute error of the quintic on |b| <= 1/64: {float(worst):.3e}")
+    print(f"constexpr double kTanhTab32[{NTAB}] = {{")
+    for j in range(0, NTAB, 4):
         print("    " + ", ".join(repr(t) for t in table[j:j + 4]) + ",")
     print("};")
 

@@ -52,7 +52,7 @@ int main() {
   double max_tab = 0;
   auto tab4 = [&](const double* x) {
     double y[4];
-    dpamd::tanh_tab4(x, y, dpamd::kExp2Tab128);
+    dpamd::tanh_tab4(x, y, dpamd::kTanhTab32);
     for (int k = 0; k < 4; ++k) max_tab = std::fmax(max_tab, std::fabs(y[k] - std::tanh(x[k])));
   };
   for (int i = -2000000; i <= 2000000; i += 4) {
@@ -67,8 +67,8 @@ int main() {
     tab4(x);
   }
   double t4[4], tx[4] = {0.0, -0.0, 1e-300, -3.0}, tn[4], txn[4] = {0.0, 0.0, -1e-300, 3.0};
-  dpamd::tanh_tab4(tx, t4, dpamd::kExp2Tab128);
-  dpamd::tanh_tab4(txn, tn, dpamd::kExp2Tab128);
+  dpamd::tanh_tab4(tx, t4, dpamd::kTanhTab32);
+  dpamd::tanh_tab4(txn, tn, dpamd::kTanhTab32);
   const bool tzero = t4[0] == 0.0 && t4[1] == 0.0 && std::signbit(t4[1]) && t4[3] == -tn[3];
   std::printf("tanh_tab4 max_abs %.3e, zeros / odd symmetry %d\n", max_tab, (int)tzero);
   return (max_abs <= 4e-15 && max_abs4 <= 4e-15 && zeros && max_tab <= 4e-15 && tzero) ? 0 : 1;
