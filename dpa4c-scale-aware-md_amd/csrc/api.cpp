@@ -439,14 +439,17 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   // Blocks of WAVES * ipw items: each block stages its pair's net in LDS once
   // and its waves then walk ipw items each, which amortises the staging and
   // the start-up latency of a block. ipw aims at about 32 tiles of 16 slots
-  // per wave, as long as the grid still gives every compute unit three blocks
-  // or more (fewer leave a tail where some units idle).
+  // per wave, as long as the grid still gives every compute unit six blocks
+  // or more: the blocks of different pairs differ in length, and with few
+  // blocks per unit the last ones leave a tail where some units idle
+  // (12,288-atom water, per-block timestamps: 12 % of the units' time idle
+  // with three blocks per unit; six: embedding kernels -9 %).
   auto block_table = [&](int waves) {
     long items = 0;
     for (int p = 0; p < nt * nt; ++p) items += M->type_off[p / nt + 1] - M->type_off[p / nt];
     const long tiles = std::max(1, (ea.tiles_per_atom + nt - 1) / nt);  // per item
     const long by_tiles = (32 + tiles - 1) / tiles;
-    const long by_grid = items / ((long)waves * 3 * M->ncu);
+    const long by_grid = items / ((long)waves * 6 * M->ncu);
     ea.ipw = (int)std::clamp(std::min(by_tiles, by_grid), 1L, 16L);
     const int per = waves * ea.ipw;
     int acc = 0;
