@@ -379,7 +379,9 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
                                             : nullptr;
   E* dT = need<E>(M, M->dT, (size_t)nloc * 4 * L3);
   const int Fmax = std::max(m.fit[0], std::max(m.fit[1], m.fit[2]));
-  E* fitb = need<E>(M, M->fitb, (size_t)8 * std::max(nb, 1) * Fmax);
+  // six activation slabs [nb][Fmax] and the head's partial energies
+  // [nb][F2 / 16] fp64 (no larger than one slab of E)
+  E* fitb = need<E>(M, M->fitb, (size_t)7 * std::max(nb, 1) * Fmax);
   double* e_bucket = need<double>(M, M->e_bucket, (size_t)std::max(nb, 1));
   // fp64: the backward scatters each edge's forces itself (fixed point) and
   // stores g only when kept; fp32 (mixed): the backward stores g and the
@@ -531,9 +533,11 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
     if (fb.split > 1) fb.ws = split_ws + ws_off;
     ws_off += (size_t)fb.split * rows * m.fit[0];
     E* base = fitb;
-    E** slots[8] = {&fb.H0, &fb.T1, &fb.H1, &fb.T2, &fb.H2, &fb.dZa, &fb.dZb, &fb.dH};
-    // slab q holds [rows][F] of every type back to back; F <= Fmax
-    for (int q = 0; q < 8; ++q) *slots[q] = base + q * slab + r0 * (size_t)Fmax;
+    E** slots[6] = {&fb.H0, &fb.T1, &fb.H1, &fb.dZa, &fb.dZb, &fb.dH};
+    // slab q holds [rows][F] of every type back to back; F <= Fmax. Slab 6
+    // holds the head's partial energies (at most F2 / 16 doubles per row).
+    for (int q = 0; q < 6; ++q) *slots[q] = base + q * slab + r0 * (size_t)Fmax;
+    fb.epart = reinterpret_cast<double*>(base + 6 * slab) + r0 * (size_t)(m.fit[2] / 16);
     FitDdt ddt{};
     if (fused_ddt) {
       ddt.W0T = M->d_w0t + (size_t)t * m.fit[0] * Dn;

@@ -28,7 +28,7 @@ struct GemmArgs {
   int lda;
   const T* B;
   int ldb;
-  int epi;  // 0 plain store, 1 forward layer, 2 backward layer
+  int epi;  // 0 plain store, 1 forward layer, 2 backward layer, 3 last layer + head
   const T* bias;
   const T* idt;
   T* C;
@@ -50,14 +50,61 @@ struct GemmArgs {
   // fp32 only: B pre-split into bf16 fragments (pack_gemm_bf16 layout), which
   // selects the bf16 three-piece kernel k_gemm3; null for the fp32 / fp64 MFMA
   const void* Bf;
+  // epi 3 (the last layer with the energy head fused): the head's weights Wo
+  // [N] and the per-row partial energies epart[M][N / BN] (one per column
+  // block, fp64), summed in column-block order by k_head_sum
+  const T* Wo;
+  double* epart;
 };
 
 // Block tile output: the split-K slice store, or the layer epilogue (plain,
-// forward: bias + tanh + residual, backward: (dH_in + acc) idt (1 - t^2)).
+// forward: bias + tanh + residual, backward: (dH_in + acc) idt (1 - t^2),
+// last layer + head: see below).
 // acc[n] register r of wave w holds C[row0 + 16w + Frag::row(g, r)][col0 + 16n + c].
 template <class T, int NT>
 __device__ __forceinline__ void gemm_store(const GemmArgs<T>& a, const typename Frag<T>::V (&acc)[NT],
                                            int row0, int col0, int zs, int w, int g, int c) {
+  if (a.epi == 3) {
+    // last layer h = x + idt t (t = tanh(z)) with the energy head fused: h is
+    // consumed here and never stored. C receives the backward's seed
+    // dZ = Wo idt (1 - t^2) (the head's dE/dh is Wo), and each row's partial
+    // energy sum_col h Wo over this block's columns (fp64, summed over the 16
+    // column lanes of the row by a fixed xor tree) goes to epart.
+    double es[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int col = col0 + 16 * n + c;
+      T z[4], th[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
+      if constexpr (sizeof(T) == 8) {
+        tanh_fast4(z, th);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) th[r] = tanh_act(z[r]);
+      }
+      const T wo = a.Wo[col], id = a.idt ? a.idt[col] : T(1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = row0 + 16 * w + Frag<T>::row(g, r);
+        if (row >= a.M) continue;
+        const long o = (long)row * a.ldc + col;
+        const T t = th[r];
+        const T h = a.idt ? a.A[(long)row * a.lda + col] + id * t : t;
+        es[r] += (double)h * (double)wo;
+        a.C[o] = wo * id * (T(1) - t * t);
+      }
+    }
+    const int ncb = a.N / (16 * NT);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) es[r] += shfl_xor_d(es[r], off);
+      const int row = row0 + 16 * w + Frag<T>::row(g, r);
+      if (c == 0 && row < a.M) a.epart[(long)row * ncb + col0 / (16 * NT)] = es[r];
+    }
+    return;
+  }
   if (a.split > 1) {
     T* out = a.ws + (long)zs * a.M * a.ldc;
 #pragma unroll
@@ -375,26 +422,16 @@ int fit_splits(int rows, int N, int K, int ncu) {
   return split;
 }
 
-// Energy head and the seed of the backward: e = h2.Wo + bo + bias,
-// dZ2 = Wo * idt2 * (1 - t2^2). One wave per atom row.
-// The dot product is accumulated in fp64 for both element types.
-template <class T>
-__global__ __launch_bounds__(256) void k_head(int rows, int F2, const T* __restrict__ H2,
-                                              const T* __restrict__ T2, const T* __restrict__ Wo,
-                                              const T* __restrict__ idt2, double bo, double bias,
-                                              double* __restrict__ e, T* __restrict__ dZ2) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+// Energy head, second half: e = sum of the row's column-block partials of
+// h2.Wo (in column-block order) + bo + bias; the partials and the backward's
+// seed come from the last layer's epilogue (gemm_store, epi 3).
+__global__ __launch_bounds__(256) void k_head_sum(int rows, int ncb, const double* __restrict__ epart,
+                                                  double bo, double bias, double* __restrict__ e) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
   if (row >= rows) return;
-  double acc = 0.0;
-  for (int f = lane; f < F2; f += 64) {
-    const long o = (long)row * F2 + f;
-    acc += (double)H2[o] * (double)Wo[f];
-    const T t = T2[o];
-    dZ2[o] = Wo[f] * (idt2 ? idt2[f] : T(1)) * (T(1) - t * t);
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) acc += shfl_xor_d(acc, off);
-  if (lane == 0) e[row] = acc + bo + bias;
+  double acc = epart[(long)row * ncb];
+  for (int k = 1; k < ncb; ++k) acc += epart[(long)row * ncb + k];
+  e[row] = acc + bo + bias;
 }
 
 // dT[m][a] = sum_b dD[a][b] T[m][b] + (a < axis) sum_a' dD[a'][a] T[m][a'].
@@ -720,14 +757,19 @@ static void gemm_nt(hipStream_t st, const GemmArgs<T>& a) {
 // the register footprint low enough for two or more waves per SIMD (the
 // barrier per K chunk is then covered by the other waves); N is a multiple of
 // 16 (checked at model load).
+static int col_tiles(int N) {
+  const int tiles = N / 16;
+  return tiles % 8 == 0 ? 8 : tiles % 5 == 0 ? 5 : tiles % 4 == 0 ? 4 : 1;
+}
 template <bool TRANSB, class T>
 static void gemm(hipStream_t st, const GemmArgs<T>& a) {
   if (a.M <= 0) return;
-  const int tiles = a.N / 16;
-  if (tiles % 8 == 0) gemm_nt<T, 8, TRANSB>(st, a);
-  else if (tiles % 5 == 0) gemm_nt<T, 5, TRANSB>(st, a);
-  else if (tiles % 4 == 0) gemm_nt<T, 4, TRANSB>(st, a);
-  else gemm_nt<T, 1, TRANSB>(st, a);
+  switch (col_tiles(a.N)) {
+    case 8: gemm_nt<T, 8, TRANSB>(st, a); break;
+    case 5: gemm_nt<T, 5, TRANSB>(st, a); break;
+    case 4: gemm_nt<T, 4, TRANSB>(st, a); break;
+    default: gemm_nt<T, 1, TRANSB>(st, a);
+  }
 }
 
 // First layer with A formed from T: the column tile is the widest of 8, 5, 4
@@ -812,13 +854,16 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   g.epi = 1; g.bias = net.L[1].b; g.idt = net.L[1].idt; g.C = b.H1; g.ldc = F1; g.T_out = b.T1;
   g.Bf = net.L[1].Wf;
   gemm<false>(st, g);
+  // last layer with the energy head: dZ2 = Wo idt2 (1 - T2^2) and the
+  // partial energies; h2 and T2 are not stored
   g = G{};
   g.M = rows; g.N = F2; g.K = F1; g.A = b.H1; g.lda = F1; g.B = net.L[2].W; g.ldb = F2;
-  g.epi = 1; g.bias = net.L[2].b; g.idt = net.L[2].idt; g.C = b.H2; g.ldc = F2; g.T_out = b.T2;
-  g.Bf = net.L[2].Wf;
+  g.epi = 3; g.bias = net.L[2].b; g.idt = net.L[2].idt; g.C = b.dZa; g.ldc = F2;
+  g.Bf = net.L[2].Wf; g.Wo = net.Wo; g.epart = b.epart;
   gemm<false>(st, g);
-  hipLaunchKernelGGL(k_head<T>, dim3((rows + 3) / 4), dim3(256), 0, st, rows, F2, b.H2, b.T2, net.Wo,
-                     net.L[2].idt, net.bo, net.bias, e_bucket, b.dZa);
+  const int ncb = F2 / (16 * col_tiles(F2));
+  hipLaunchKernelGGL(k_head_sum, dim3((rows + 255) / 256), dim3(256), 0, st, rows, ncb, b.epart,
+                     net.bo, net.bias, e_bucket);
   DPAMD_LAUNCH_CHECK();
   // backward: dH1 = [res2] Wo + dZ2 W2^T, dZ1 = dH1 idt1 (1 - T1^2)
   g = G{};

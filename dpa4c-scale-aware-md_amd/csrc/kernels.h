@@ -192,7 +192,8 @@ struct FitNet {
 };
 template <class T>
 struct FitBufs {
-  T *H0, *T1, *H1, *T2, *H2, *dZa, *dZb, *dH;  // [rows][F] each
+  T *H0, *T1, *H1, *dZa, *dZb, *dH;  // [rows][F] each
+  double* epart;  // [rows][F2 / column tile] partial energies of the head
   // first layer split over K into `split` slices (fit_splits) summed through
   // ws [split][rows][F0] when split > 1
   int split;
