@@ -566,18 +566,22 @@ struct DdtArgs {
   double* ws;
 };
 
+constexpr int kObRow = 66;  // row stride of k_dDdT's first-term buffer (64 + 2)
+
 template <int WAVES, int NQ>
 __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
   constexpr int BM = 16 * WAVES, K = 4 * NQ;
   extern __shared__ double lds[];
   double* Bs = lds;                   // [2][K][16]
   double* Ts = Bs + 2 * K * 16;       // [2][BM][4]
-  double* Ob = Ts + 2 * BM * 4;       // [WAVES][16 rows][4 m][16 columns]
+  // [WAVES][16 rows][4 m][16 columns], rows padded to kObRow doubles so that
+  // the per-group writes (lane (g, c): row c, m = g) fall in distinct banks
+  double* Ob = Ts + 2 * BM * 4;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int row0 = blockIdx.x * BM, wrow = row0 + 16 * w + c;  // this lane's row
   const bool rowok = wrow < p.rows;
   const int Dn = 16 * p.L3;
-  double* Obw = Ob + w * 16 * 4 * 16;
+  double* Obw = Ob + w * 16 * kObRow;
   // this block's column groups: split s takes i in [i0, i1), the boundaries
   // 16-aligned within the a >= 16 groups (so every flush stays whole), the
   // last split also the 16 groups a < 16
@@ -667,7 +671,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
       v = add_xor32(add_xor16(v));
       s[m] = v;
     }
-    Obw[(c * 4 + g) * 16 + (a & 15)] = g == 0 ? s[0] : g == 1 ? s[1] : g == 2 ? s[2] : s[3];
+    Obw[c * kObRow + g * 16 + (a & 15)] = g == 0 ? s[0] : g == 1 ? s[1] : g == 2 ? s[2] : s[3];
     // second term: T[row][m][a]
     const double* tr = Ts + buf * BM * 4 + (16 * w + c) * 4;
 #pragma unroll
@@ -690,7 +694,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
         const int atom = __shfl(my_atom, rl, 64);
         const int m = lane >> 4, al = lane & 15;
         if (al < na && row0 + 16 * w + rl < p.rows)
-          p.dT[((long)atom * 4 + m) * p.L3 + abase + al] = Obw[64 * rl + lane];
+          p.dT[((long)atom * 4 + m) * p.L3 + abase + al] = Obw[kObRow * rl + lane];
       }
       wave_lds_sync();
     }
@@ -704,7 +708,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int b = g + 4 * r;
-        out[m * p.L3 + b] = Obw[(c * 4 + m) * 16 + b] + acc2[r][m];
+        out[m * p.L3 + b] = Obw[c * kObRow + m * 16 + b] + acc2[r][m];
       }
   } else if (rowok) {
     double* part = p.ws + ((long)s * p.rows + wrow) * 64;
@@ -715,7 +719,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
       for (int m = 0; m < 4; ++m) {
         const int b = g + 4 * r;
         part[m * 16 + b] = acc2[r][m];
-        if (s == S - 1) first[m * 16 + b] = Obw[(c * 4 + m) * 16 + b];
+        if (s == S - 1) first[m * 16 + b] = Obw[c * kObRow + m * 16 + b];
       }
   }
 }
@@ -736,7 +740,7 @@ __global__ __launch_bounds__(256) void k_ddt_combine(int rows, int L3, int nspli
 
 template <int WAVES>
 static size_t ddt_lds_bytes(int K) {
-  return sizeof(double) * (2 * K * 16 + 2 * 16 * WAVES * 4 + WAVES * 16 * 4 * 16);
+  return sizeof(double) * (2 * K * 16 + 2 * 16 * WAVES * 4 + WAVES * 16 * kObRow);
 }
 
 template <class T, int NT, bool TRANSB, bool AT = false>
