@@ -151,7 +151,8 @@ void launch_edges_fill(hipStream_t, int nloc, int nedge, int nnode, const int* e
 size_t noalloc_scratch_bytes();
 void* noalloc_scratch_init(int device);
 
-// Scans (hipCUB)
+// Device-wide exclusive int prefix sums (scan.hip): scan_temp_bytes(n) of
+// temporary device memory
 size_t scan_temp_bytes(int n);
 void exclusive_scan_int(hipStream_t, const int* in, int* out, int n, void* temp, size_t temp_bytes);
 
