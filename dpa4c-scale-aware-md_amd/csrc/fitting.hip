@@ -61,98 +61,143 @@ struct GemmArgs {
 // forward: bias + tanh + residual, backward: (dH_in + acc) idt (1 - t^2),
 // last layer + head: see below).
 // acc[n] register r of wave w holds C[row0 + 16w + Frag::row(g, r)][col0 + 16n + c].
-template <class T, int NT>
-__device__ __forceinline__ void gemm_store(const GemmArgs<T>& a, const typename Frag<T>::V (&acc)[NT],
-                                           int row0, int col0, int zs, int w, int g, int c) {
-  if (a.epi == 3) {
-    // last layer h = x + idt t (t = tanh(z)) with the energy head fused: h is
-    // consumed here and never stored. C receives the backward's seed
-    // dZ = Wo idt (1 - t^2) (the head's dE/dh is Wo), and each row's partial
-    // energy sum_col h Wo over this block's columns (fp64, summed over the 16
-    // column lanes of the row by a fixed xor tree) goes to epart.
-    double es[4] = {0.0, 0.0, 0.0, 0.0};
+// The global inputs of an epilogue are loaded two column tiles ahead of their
+// use, so several loads are in flight at once without holding every tile's
+// inputs in registers; the per-element row check is compiled only for the
+// last row block (FULL = false).
+template <class T, int NT, int EPI, bool FULL>
+__device__ __forceinline__ void gemm_store_rows(const GemmArgs<T>& a,
+                                                const typename Frag<T>::V (&acc)[NT], int row0,
+                                                int col0, int zs, int w, int g, int c) {
+  long ro[4];  // row offsets (in elements of a row of ldc / lda) of the lane's rows
+  bool ok[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = row0 + 16 * w + Frag<T>::row(g, r);
+    ok[r] = FULL || row < a.M;
+    ro[r] = row;
+  }
+  if (a.split > 1 || EPI == 0) {
+    T* out = a.split > 1 ? a.ws + (long)zs * a.M * a.ldc : a.C;
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (ok[r]) out[ro[r] * a.ldc + col0 + 16 * n + c] = acc[n][r];
+    return;
+  }
+  if constexpr (EPI == 2) {
+    // backward layer: dh = acc + dH_in, C = dh idt (1 - tk^2). The inputs of
+    // column tile n + 2 are loaded while tile n is finished (two tiles'
+    // loads in flight at a time, few registers).
+    T tk[NT][4], dh[NT][4];
+    auto load = [&](int n) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tk[n][r] = ok[r] ? a.Tk[ro[r] * a.ldc + col0 + 16 * n + c] : T(0);
+      if (a.dHin && a.ld_dhin > 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          dh[n][r] = ok[r] ? a.dHin[ro[r] * a.ld_dhin + col0 + 16 * n + c] : T(0);
+      } else {
+        const T d = a.dHin ? a.dHin[col0 + 16 * n + c] : T(0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dh[n][r] = d;
+      }
+    };
+    load(0);
+    if (NT > 1) load(1);
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (n + 2 < NT) load(n + 2);
       const int col = col0 + 16 * n + c;
-      T z[4], th[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
-      if constexpr (sizeof(T) == 8) {
-        tanh_fast4(z, th);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) th[r] = tanh_act(z[r]);
-      }
-      const T wo = a.Wo[col], id = a.idt ? a.idt[col] : T(1);
+      const T id = a.idt ? a.idt[col] : T(1);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = row0 + 16 * w + Frag<T>::row(g, r);
-        if (row >= a.M) continue;
-        const long o = (long)row * a.ldc + col;
-        const T t = th[r];
-        const T h = a.idt ? a.A[(long)row * a.lda + col] + id * t : t;
-        es[r] += (double)h * (double)wo;
-        a.C[o] = wo * id * (T(1) - t * t);
+        if (!ok[r]) continue;
+        const long o = ro[r] * a.ldc + col;
+        const T d = acc[n][r] + dh[n][r];
+        if (a.dH_out) a.dH_out[o] = d;
+        a.C[o] = d * id * (T(1) - tk[n][r] * tk[n][r]);
       }
     }
+    return;
+  } else {
+  // forward layers (epi 1, and epi 3 with the head): residual x first
+  // (column tile n + 2's residual loaded while tile n is finished)
+  __builtin_amdgcn_sched_barrier(0);
+  T res[NT][4];
+  auto load = [&](int n) {
+    if (EPI == 1 && a.idt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) res[n][r] = ok[r] ? a.A[ro[r] * a.lda + col0 + 16 * n + c] : T(0);
+    }
+  };
+  load(0);
+  if (NT > 1) load(1);
+  // epi 3: the last layer h = x + idt t (t = tanh(z)) with the energy head
+  // fused: h is consumed here and never stored. C receives the backward's
+  // seed dZ = Wo idt (1 - t^2) (the head's dE/dh is Wo), and each row's
+  // partial energy sum_col h Wo over this block's columns (fp64, summed over
+  // the 16 column lanes of the row by a fixed xor tree) goes to epart.
+  double es[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    // keep each tile's work (and the loads two tiles ahead) in its own
+    // scheduling region: hoisting every tile's loads to the top raised the
+    // register count past four waves per SIMD
+    __builtin_amdgcn_sched_barrier(0);
+    if (n + 2 < NT) load(n + 2);
+    const int col = col0 + 16 * n + c;
+    // the four tanh of this column at once (fp64: shared reciprocal; rows
+    // past M hold zeros and are not stored)
+    T z[4], th[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
+    if constexpr (sizeof(T) == 8) {
+      tanh_fast4(z, th);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) th[r] = tanh_act(z[r]);
+    }
+    const T id = a.idt ? a.idt[col] : T(1);
+    if constexpr (EPI == 3) {
+      const T wo = a.Wo[col];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (!ok[r]) continue;
+        const T t = th[r];
+        const T h = a.idt ? a.A[ro[r] * a.lda + col] + id * t : t;
+        es[r] += (double)h * (double)wo;
+        a.C[ro[r] * a.ldc + col] = wo * id * (T(1) - t * t);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (!ok[r]) continue;
+        const long o = ro[r] * a.ldc + col;
+        if (a.T_out) a.T_out[o] = th[r];
+        a.C[o] = a.idt ? res[n][r] + id * th[r] : th[r];
+      }
+    }
+  }
+  if constexpr (EPI == 3) {
     const int ncb = a.N / (16 * NT);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
 #pragma unroll
       for (int off = 8; off > 0; off >>= 1) es[r] += shfl_xor_d(es[r], off);
-      const int row = row0 + 16 * w + Frag<T>::row(g, r);
-      if (c == 0 && row < a.M) a.epart[(long)row * ncb + col0 / (16 * NT)] = es[r];
-    }
-    return;
-  }
-  if (a.split > 1) {
-    T* out = a.ws + (long)zs * a.M * a.ldc;
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = row0 + 16 * w + Frag<T>::row(g, r);
-        if (row < a.M) out[(long)row * a.ldc + col0 + 16 * n + c] = acc[n][r];
-      }
-    return;
-  }
-#pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    const int col = col0 + 16 * n + c;
-    // forward epilogue: the four tanh of this column at once (fp64: shared
-    // reciprocal; rows past M hold zeros and are not stored)
-    T th[4];
-    if (a.epi == 1) {
-      T z[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
-      if constexpr (sizeof(T) == 8) {
-        tanh_fast4(z, th);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) th[r] = tanh_act(z[r]);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = row0 + 16 * w + Frag<T>::row(g, r);
-      if (row >= a.M) continue;
-      const long o = (long)row * a.ldc + col;
-      const T v = acc[n][r];
-      if (a.epi == 0) {
-        a.C[o] = v;
-      } else if (a.epi == 1) {
-        const T t = th[r];
-        if (a.T_out) a.T_out[o] = t;
-        a.C[o] = a.idt ? a.A[(long)row * a.lda + col] + a.idt[col] * t : t;
-      } else {
-        const T dh = v + (a.dHin ? a.dHin[(long)row * a.ld_dhin + col] : T(0));
-        if (a.dH_out) a.dH_out[o] = dh;
-        const T tk = a.Tk[o];
-        a.C[o] = dh * (a.idt ? a.idt[col] : T(1)) * (T(1) - tk * tk);
-      }
+      if (c == 0 && ok[r]) a.epart[ro[r] * ncb + col0 / (16 * NT)] = es[r];
     }
   }
+  }
+}
+
+template <class T, int NT, int EPI>
+__device__ __forceinline__ void gemm_store(const GemmArgs<T>& a, const typename Frag<T>::V (&acc)[NT],
+                                           int row0, int col0, int zs, int w, int g, int c) {
+  if (row0 + 64 <= a.M) gemm_store_rows<T, NT, EPI, true>(a, acc, row0, col0, zs, w, g, c);
+  else gemm_store_rows<T, NT, EPI, false>(a, acc, row0, col0, zs, w, g, c);
 }
 
 // C = epi(A[MxK] B[KxN]); B(k,n) = TRANSB ? B[n*ldb + k] : B[k*ldb + n].
@@ -165,7 +210,7 @@ __device__ __forceinline__ void gemm_store(const GemmArgs<T>& a, const typename 
 // keeps T[m][4 part .. 4 part + 3] of row r in registers and fetches the 4
 // values T[0..3][a] per chunk (contiguous in the column-major copy of T, so a
 // wave reads 16 rows as one run) instead of 16 values of D.
-template <class T, int NT, bool TRANSB, bool AT = false>
+template <class T, int NT, bool TRANSB, bool AT, int EPI>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
   constexpr int BM = 64, BK = 16, BN = 16 * NT;
   constexpr int ALD = BK + 1, BLD = BN + 1;
@@ -272,7 +317,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
     if (kc + 1 < nk) stash(buf ^ 1);
     __syncthreads();
   }
-  gemm_store<T, NT>(a, acc, row0, col0, bid.z, w, g, c);
+  gemm_store<T, NT, EPI>(a, acc, row0, col0, bid.z, w, g, c);
 }
 
 // fp32 GEMM on the bf16 matrix cores at fp32 accuracy (mixed precision):
@@ -288,7 +333,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs<T> a) {
 // per unit time. AT: A is D = T^T T[:, :16] formed while staging; chunk kc
 // holds D columns 32kc.. 32kc + 31 (a = 2kc, 2kc + 1), thread (row, part)
 // stages columns 8 part .. 8 part + 7 and keeps T[m][8 (part % 2) + e].
-template <int NT, bool AT>
+template <int NT, bool AT, int EPI>
 __global__ __launch_bounds__(256) void k_gemm3(GemmArgs<float> a) {
   constexpr int BM = 64, BK = 32, BN = 16 * NT, ALD = BK + 4;
   __shared__ __align__(16) float As[2][BM * ALD];
@@ -374,7 +419,7 @@ __global__ __launch_bounds__(256) void k_gemm3(GemmArgs<float> a) {
     if (kc + 1 < nk) stash(buf ^ 1);
     __syncthreads();
   }
-  gemm_store<float, NT>(a, acc, row0, col0, bid.z, w, g, c);
+  gemm_store<float, NT, EPI>(a, acc, row0, col0, bid.z, w, g, c);
 }
 
 // Split-K forward epilogue of a layer without residual: C = tanh(sum over
@@ -743,24 +788,38 @@ static size_t ddt_lds_bytes(int K) {
   return sizeof(double) * (2 * K * 16 + 2 * 16 * WAVES * 4 + WAVES * 16 * kObRow);
 }
 
-template <class T, int NT, bool TRANSB, bool AT = false>
-static void gemm_nt(hipStream_t st, const GemmArgs<T>& a) {
-  dim3 grid(a.N / (16 * NT), (a.M + 63) / 64, a.split > 1 ? a.split : 1);
+// Launch with the epilogue as a template parameter, instantiated only for the
+// epilogues each operand form is used with: the first layer (A from T) plain
+// or forward, the other forward layers forward or last-layer-with-head, the
+// transposed-B products plain or backward.
+template <class T, int NT, bool TRANSB, bool AT, int EPI>
+static void gemm_launch(hipStream_t st, const GemmArgs<T>& a, dim3 grid) {
   if constexpr (sizeof(T) == 4) {
     if (a.Bf) {  // B pre-split: the bf16 three-piece kernel (B's orientation is in the fragments)
-      hipLaunchKernelGGL((k_gemm3<NT, AT>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((k_gemm3<NT, AT, EPI>), grid, dim3(256), 0, st, a);
       DPAMD_LAUNCH_CHECK();
       return;
     }
   }
-  hipLaunchKernelGGL((k_gemm<T, NT, TRANSB, AT>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((k_gemm<T, NT, TRANSB, AT, EPI>), grid, dim3(256), 0, st, a);
   DPAMD_LAUNCH_CHECK();
 }
 
-// Column tile: the widest of 8, 5, 4 or 1 MFMA tiles dividing N, which keeps
-// the register footprint low enough for two or more waves per SIMD (the
-// barrier per K chunk is then covered by the other waves); N is a multiple of
-// 16 (checked at model load).
+template <class T, int NT, bool TRANSB, bool AT = false>
+static void gemm_nt(hipStream_t st, const GemmArgs<T>& a) {
+  dim3 grid(a.N / (16 * NT), (a.M + 63) / 64, a.split > 1 ? a.split : 1);
+  if constexpr (TRANSB) {
+    if (a.epi == 0) return gemm_launch<T, NT, TRANSB, AT, 0>(st, a, grid);
+    if (a.epi == 2) return gemm_launch<T, NT, TRANSB, AT, 2>(st, a, grid);
+  } else if constexpr (AT) {
+    if (a.epi == 1) return gemm_launch<T, NT, TRANSB, AT, 1>(st, a, grid);
+  } else {
+    if (a.epi == 1) return gemm_launch<T, NT, TRANSB, AT, 1>(st, a, grid);
+    if (a.epi == 3) return gemm_launch<T, NT, TRANSB, AT, 3>(st, a, grid);
+  }
+  throw HipError{hipErrorInvalidValue, "fitting GEMM: epilogue not available for this operand form"};
+}
+
 static int col_tiles(int N) {
   const int tiles = N / 16;
   return tiles % 8 == 0 ? 8 : tiles % 5 == 0 ? 5 : tiles % 4 == 0 ? 4 : 1;
