@@ -242,3 +242,23 @@ def test_fixed_point_range_guard(dp):
     # two atoms farther apart than rcut: no edges, nothing to overflow
     e, f, v = pot.compute(np.array([[0.0, 0.0, 0.0], [9.0, 0.0, 0.0]]), np.array([0, 1]), None)
     assert np.all(f == 0.0) and np.isfinite(e)
+
+
+@pytest.mark.parametrize("fit", [(240, 240, 160), (240, 160, 160), (240, 240, 80)])
+def test_fitting_shapes(dp, orc, fit):
+    """Fitting nets whose hidden layers are not all square: a non-square layer
+    has no residual and no timestep (h = tanh(xW + b)), in the layer before
+    the head (the last layer's epilogue with the energy head fused) and in a
+    middle layer; widths that are not multiples of the GEMM's 80-column tile
+    (160, 80) give other column-block counts for the head's partial energies."""
+    coord, atype, box = dp.systems.build(0)
+    m = dp.model.random_model("water", seed=1010, fit=list(fit))
+    mb = model_bytes(m)
+    ref = orc.Oracle(mb).compute(coord, atype, box)
+    e, f, v, ae, av = dp.DeepPot(file_content=mb).compute(coord, atype, box, atomic=True)
+    n = len(atype)
+    assert abs(e - ref["energy"]) / n <= E_TOL
+    assert np.abs(ae - ref["atom_energy"]).max() <= E_TOL
+    assert np.abs(f - ref["force"]).max() <= F_TOL
+    assert np.abs(v - ref["virial"]).max() <= V_TOL
+    assert np.abs(av - ref["atom_virial"]).max() <= V_TOL
