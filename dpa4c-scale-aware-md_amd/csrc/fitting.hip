@@ -59,17 +59,134 @@ struct GemmArgs {
 
 // Block tile output: the split-K slice store, or the layer epilogue (plain,
 // forward: bias + tanh + residual, backward: (dH_in + acc) idt (1 - t^2),
-// last layer + head: see below).
-// acc[n] register r of wave w holds C[row0 + 16w + Frag::row(g, r)][col0 + 16n + c].
+// last layer + head: see store_last).
+// acc[n] register r of wave w holds C[row0 + 16w + Frag::row(g, r)][col0 + 16n + c];
+// ro[r] is that row and ok[r] whether it exists (row < M).
 // The global inputs of an epilogue are loaded two column tiles ahead of their
 // use, so several loads are in flight at once without holding every tile's
-// inputs in registers; the per-element row check is compiled only for the
-// last row block (FULL = false).
+// inputs in registers; each tile's work is kept in its own scheduling region
+// (hoisting every tile's loads to the top raised the register count past
+// four waves per SIMD). The per-element row check is compiled only for the
+// last row block (FULL = false in gemm_store_rows).
+template <class T, int NT>
+using Acc = typename Frag<T>::V[NT];
+
+// forward layer: C = x + idt t (or t without a timestep), T_out = t
+template <class T, int NT>
+__device__ __forceinline__ void store_forward(const GemmArgs<T>& a, const Acc<T, NT>& acc,
+                                              const bool (&ok)[4], const long (&ro)[4], int col0,
+                                              int c) {
+  T res[NT][4];
+  auto load = [&](int n) {
+    if (a.idt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) res[n][r] = ok[r] ? a.A[ro[r] * a.lda + col0 + 16 * n + c] : T(0);
+    }
+  };
+  load(0);
+  if (NT > 1) load(1);
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (n + 2 < NT) load(n + 2);
+    const int col = col0 + 16 * n + c;
+    // the four tanh of this column at once (fp64: shared reciprocal; rows
+    // past M hold zeros and are not stored)
+    T z[4], th[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
+    tanh_act4(z, th);
+    const T id = a.idt ? a.idt[col] : T(1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (!ok[r]) continue;
+      const long o = ro[r] * a.ldc + col;
+      if (a.T_out) a.T_out[o] = th[r];
+      a.C[o] = a.idt ? res[n][r] + id * th[r] : th[r];
+    }
+  }
+}
+
+// The last layer h = x + idt t (t = tanh(z)) with the energy head fused: h is
+// consumed here and never stored. C receives the backward's seed
+// dZ = Wo idt (1 - t^2) (the head's dE/dh is Wo), and each row's partial
+// energy sum_col h Wo over this block's columns (fp64, summed over the 16
+// column lanes of the row by a fixed xor tree) goes to epart. (The residual
+// is read where it is used: a prefetched copy here kept twenty values live.)
+template <class T, int NT>
+__device__ __forceinline__ void store_last(const GemmArgs<T>& a, const Acc<T, NT>& acc,
+                                           const bool (&ok)[4], const long (&ro)[4], int col0,
+                                           int c) {
+  double es[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int col = col0 + 16 * n + c;
+    T z[4], th[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
+    tanh_act4(z, th);
+    const T id = a.idt ? a.idt[col] : T(1), wo = a.Wo[col];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (!ok[r]) continue;
+      const T t = th[r];
+      const T h = a.idt ? a.A[ro[r] * a.lda + col] + id * t : t;
+      es[r] += (double)h * (double)wo;
+      a.C[ro[r] * a.ldc + col] = wo * id * (T(1) - t * t);
+    }
+  }
+  const int ncb = a.N / (16 * NT);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) es[r] += shfl_xor_d(es[r], off);
+    if (c == 0 && ok[r]) a.epart[ro[r] * ncb + col0 / (16 * NT)] = es[r];
+  }
+}
+
+// backward layer: dh = acc + dH_in, C = dh idt (1 - tk^2), dH_out = dh
+template <class T, int NT>
+__device__ __forceinline__ void store_backward(const GemmArgs<T>& a, const Acc<T, NT>& acc,
+                                               const bool (&ok)[4], const long (&ro)[4],
+                                               int col0, int c) {
+  T tk[NT][4], dh[NT][4];
+  auto load = [&](int n) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tk[n][r] = ok[r] ? a.Tk[ro[r] * a.ldc + col0 + 16 * n + c] : T(0);
+    if (a.dHin && a.ld_dhin > 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        dh[n][r] = ok[r] ? a.dHin[ro[r] * a.ld_dhin + col0 + 16 * n + c] : T(0);
+    } else {
+      const T d = a.dHin ? a.dHin[col0 + 16 * n + c] : T(0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dh[n][r] = d;
+    }
+  };
+  load(0);
+  if (NT > 1) load(1);
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (n + 2 < NT) load(n + 2);
+    const int col = col0 + 16 * n + c;
+    const T id = a.idt ? a.idt[col] : T(1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (!ok[r]) continue;
+      const long o = ro[r] * a.ldc + col;
+      const T d = acc[n][r] + dh[n][r];
+      if (a.dH_out) a.dH_out[o] = d;
+      a.C[o] = d * id * (T(1) - tk[n][r] * tk[n][r]);
+    }
+  }
+}
+
 template <class T, int NT, int EPI, bool FULL>
-__device__ __forceinline__ void gemm_store_rows(const GemmArgs<T>& a,
-                                                const typename Frag<T>::V (&acc)[NT], int row0,
-                                                int col0, int zs, int w, int g, int c) {
-  long ro[4];  // row offsets (in elements of a row of ldc / lda) of the lane's rows
+__device__ __forceinline__ void gemm_store_rows(const GemmArgs<T>& a, const Acc<T, NT>& acc,
+                                                int row0, int col0, int zs, int w, int g, int c) {
+  long ro[4];
   bool ok[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -86,111 +203,10 @@ __device__ __forceinline__ void gemm_store_rows(const GemmArgs<T>& a,
         if (ok[r]) out[ro[r] * a.ldc + col0 + 16 * n + c] = acc[n][r];
     return;
   }
-  if constexpr (EPI == 2) {
-    // backward layer: dh = acc + dH_in, C = dh idt (1 - tk^2). The inputs of
-    // column tile n + 2 are loaded while tile n is finished (two tiles'
-    // loads in flight at a time, few registers).
-    T tk[NT][4], dh[NT][4];
-    auto load = [&](int n) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) tk[n][r] = ok[r] ? a.Tk[ro[r] * a.ldc + col0 + 16 * n + c] : T(0);
-      if (a.dHin && a.ld_dhin > 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          dh[n][r] = ok[r] ? a.dHin[ro[r] * a.ld_dhin + col0 + 16 * n + c] : T(0);
-      } else {
-        const T d = a.dHin ? a.dHin[col0 + 16 * n + c] : T(0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dh[n][r] = d;
-      }
-    };
-    load(0);
-    if (NT > 1) load(1);
-#pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (n + 2 < NT) load(n + 2);
-      const int col = col0 + 16 * n + c;
-      const T id = a.idt ? a.idt[col] : T(1);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (!ok[r]) continue;
-        const long o = ro[r] * a.ldc + col;
-        const T d = acc[n][r] + dh[n][r];
-        if (a.dH_out) a.dH_out[o] = d;
-        a.C[o] = d * id * (T(1) - tk[n][r] * tk[n][r]);
-      }
-    }
-    return;
-  } else {
-  // forward layers (epi 1, and epi 3 with the head): residual x first
-  // (column tile n + 2's residual loaded while tile n is finished)
   __builtin_amdgcn_sched_barrier(0);
-  T res[NT][4];
-  auto load = [&](int n) {
-    if (EPI == 1 && a.idt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) res[n][r] = ok[r] ? a.A[ro[r] * a.lda + col0 + 16 * n + c] : T(0);
-    }
-  };
-  load(0);
-  if (NT > 1) load(1);
-  // epi 3: the last layer h = x + idt t (t = tanh(z)) with the energy head
-  // fused: h is consumed here and never stored. C receives the backward's
-  // seed dZ = Wo idt (1 - t^2) (the head's dE/dh is Wo), and each row's
-  // partial energy sum_col h Wo over this block's columns (fp64, summed over
-  // the 16 column lanes of the row by a fixed xor tree) goes to epart.
-  double es[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    // keep each tile's work (and the loads two tiles ahead) in its own
-    // scheduling region: hoisting every tile's loads to the top raised the
-    // register count past four waves per SIMD
-    __builtin_amdgcn_sched_barrier(0);
-    if (n + 2 < NT) load(n + 2);
-    const int col = col0 + 16 * n + c;
-    // the four tanh of this column at once (fp64: shared reciprocal; rows
-    // past M hold zeros and are not stored)
-    T z[4], th[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) z[r] = acc[n][r] + a.bias[col];
-    if constexpr (sizeof(T) == 8) {
-      tanh_fast4(z, th);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) th[r] = tanh_act(z[r]);
-    }
-    const T id = a.idt ? a.idt[col] : T(1);
-    if constexpr (EPI == 3) {
-      const T wo = a.Wo[col];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (!ok[r]) continue;
-        const T t = th[r];
-        const T h = a.idt ? a.A[ro[r] * a.lda + col] + id * t : t;
-        es[r] += (double)h * (double)wo;
-        a.C[ro[r] * a.ldc + col] = wo * id * (T(1) - t * t);
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (!ok[r]) continue;
-        const long o = ro[r] * a.ldc + col;
-        if (a.T_out) a.T_out[o] = th[r];
-        a.C[o] = a.idt ? res[n][r] + id * th[r] : th[r];
-      }
-    }
-  }
-  if constexpr (EPI == 3) {
-    const int ncb = a.N / (16 * NT);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) es[r] += shfl_xor_d(es[r], off);
-      if (c == 0 && ok[r]) a.epart[ro[r] * ncb + col0 / (16 * NT)] = es[r];
-    }
-  }
-  }
+  if constexpr (EPI == 1) store_forward<T, NT>(a, acc, ok, ro, col0, c);
+  if constexpr (EPI == 2) store_backward<T, NT>(a, acc, ok, ro, col0, c);
+  if constexpr (EPI == 3) store_last<T, NT>(a, acc, ok, ro, col0, c);
 }
 
 template <class T, int NT, int EPI>
