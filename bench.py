@@ -10,8 +10,8 @@ input gradient, embedding backward, force / virial gather and reductions.
 Prints ONE JSON line. `value` is microseconds per step per atom on the
 131,072-atom FCC Cu system (config 2, fp64) unless --config says otherwise;
 the 12,288-atom water system (config 1, fp64), the 128,000-atom HEA (config
-3, mixed precision: fp32 nets on FP32 MFMA, fp64 env matrix, forces and
-virial) and the 393,216-atom water system (config 4, fp64, with its device
+3, mixed precision: fp32 nets, their products on the bf16 matrix cores at
+fp32 accuracy, fp64 env matrix, forces and virial) and the 393,216-atom water system (config 4, fp64, with its device
 memory high-water mark) are measured in the same run and reported under
 "secondary". The timed steps are queued back to back on the device
 (dp_compute_device_async, the form an MD loop with device-resident data
@@ -53,7 +53,7 @@ WORKLOAD = {2: "cu131k FCC Cu 131,072 atoms, rcut 8, sel 138, 32-64-128/240x3",
             4: "water393k 393,216 atoms, rcut 6, sel [46,92], 25-50-100/240x3"}
 
 
-def flops_bytes(pot, n_real, nloc, nb_edges, mixed=False):
+def flops_bytes(pot, n_real, nloc, mixed=False):
     """Algorithmic FLOPs / bytes of each stage for one step (real slots only;
     padded slots are a per-(type, type) constant and not evaluated). The
     descriptor arrays (section sums, T, dE/dD, dE/dT) are fp32 in mixed mode.
@@ -75,14 +75,11 @@ def flops_bytes(pot, n_real, nloc, nb_edges, mixed=False):
         # mixed precision: a pass reading dE/dD and T, writing dE/dT (fp64:
         # fused into the fitting's input-gradient kernel, no pass of its own)
         "dE_dT": ("byte", es * nloc * (Dn + 4 * L3 + 4 * L3)),
-        # fp64: the edges are scattered inside the embedding backward (fixed
-        # point); this stage folds ghost sums onto owners and assembles per
-        # atom the section sums (96 B per section), the fixed-point force
-        # (24 B), the force (24 B) and the centre partials (96 B). Mixed: the
-        # reverse-list gather reads each edge gradient (24 B) and its index
-        # (4 B) and writes the force (24 B per atom)
-        "force": ("byte", 28.0 * nb_edges + 24.0 * nloc) if mixed else
-                 ("byte", (96.0 * nt + 24.0 + 24.0 + 96.0) * nloc),
+        # the edges are scattered inside the embedding backward (fixed point);
+        # this stage folds ghost sums onto owners and assembles per atom the
+        # section sums (96 B per section), the fixed-point force (24 B), the
+        # force (24 B) and the centre partials (96 B)
+        "force": ("byte", (96.0 * nt + 24.0 + 24.0 + 96.0) * nloc),
         "nlist": ("byte", 4.0 * nloc * pot.nnei + 24.0 * nloc),
     }
     if nt > 1:
@@ -196,7 +193,7 @@ def run_config(dp, hip, config, steps, warmup):
     ms_host = (time.perf_counter() - t3) * 1e3 / host_steps
     energy = d_e.to_host(np.float64, (1,))[0]
     force = d_f.to_host(np.float64, (n, 3))
-    work = flops_bytes(pot, n_real, n, n_real, mixed)
+    work = flops_bytes(pot, n_real, n, mixed)
     stages = {}
     for k, t in stage_ms.items():
         entry = {"ms": round(t, 4)}

@@ -383,18 +383,15 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   // [nb][F2 / 16] fp64 (no larger than one slab of E)
   E* fitb = need<E>(M, M->fitb, (size_t)7 * std::max(nb, 1) * Fmax);
   double* e_bucket = need<double>(M, M->e_bucket, (size_t)std::max(nb, 1));
-  // fp64: the backward scatters each edge's forces itself (fixed point) and
-  // stores g only when kept; fp32 (mixed): the backward stores g and the
-  // reverse-list gather assembles the forces (a separate atomic pass was
-  // slower there: global atomics run at ~30 G/s on this device, and inside
-  // the fp32 backward they hold up its just-in-time activation loads)
-  double* edge_grad = (f32 || M->keep_edge_grad)
+  // the backward scatters each edge's forces itself (fixed point) and stores
+  // g only when kept
+  double* edge_grad = M->keep_edge_grad
                           ? need<double>(M, M->edge_grad, (size_t)std::max(nloc, 1) * nnei * 3)
                           : nullptr;
   const size_t nfix = (size_t)std::max(std::max(nall, ntarget), 1);
-  auto* facc = f32 ? nullptr : need<unsigned long long>(M, M->facc, nfix * 3);
-  auto* vacc = (!f32 && out.atom_virial) ? need<unsigned long long>(M, M->vacc, nfix * 9) : nullptr;
-  double* cpsec = f32 ? nullptr : need<double>(M, M->cpsec, (size_t)std::max(nloc, 1) * nt * 12);
+  auto* facc = need<unsigned long long>(M, M->facc, nfix * 3);
+  auto* vacc = out.atom_virial ? need<unsigned long long>(M, M->vacc, nfix * 9) : nullptr;
+  double* cpsec = need<double>(M, M->cpsec, (size_t)std::max(nloc, 1) * nt * 12);
 
   EmbArgs ea{};
   ea.ntypes = nt;
@@ -435,8 +432,10 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
     }
     ea.tile_off[nt] = acc;
     ea.tiles_per_atom = acc;
+    // fp64: the forward saves the layer-2/3 activations for the backward;
+    // mixed precision recomputes them there (no buffer)
     const size_t blk = 16 * (size_t)(M->el.L2P + M->el.L3P);
-    ea.act = need<E>(M, M->act, (size_t)std::max(nloc, 1) * acc * blk);
+    ea.act = f32 ? nullptr : need<E>(M, M->act, (size_t)std::max(nloc, 1) * acc * blk);
   }
   // Blocks of WAVES * ipw items: each block stages its pair's net in LDS once
   // and its waves then walk ipw items each, which amortises the staging and
@@ -564,15 +563,6 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   M->dd_valid = dD != nullptr;
   record(M, st, kStDT + 1);
 
-  if (f32) {
-    nblk = block_table(embed_waves_bwd(M->el, f32));
-    launch_embed_bwd(st, M->el, ea, nblk, f32);
-    M->eg_valid = true;
-    record(M, st, kStEmbBwd + 1);
-    gather_and_reduce(M, st, nloc, ntarget, d_mapping, e_bucket, nb, items, out);
-    (void)nall;
-    return;
-  }
   // the fixed-point sums start at zero (a kernel, so that the step can be
   // captured in a graph); on the standalone path over the ghosts counted on
   // the device

@@ -51,4 +51,16 @@ __device__ __forceinline__ f4 mfma3(const Split3& a, const Split3& b, f4 c) {
   return mfma_bf16(a.h, b.h, c);
 }
 
+// The transposed product of mfma3(b, a): the same six piece products
+// accumulated in the same order, so D = mfma3_t(a, b, .) is the transpose of
+// mfma3(b, a, .) term for term (each bf16 x bf16 product is exact in fp32).
+__device__ __forceinline__ f4 mfma3_t(const Split3& a, const Split3& b, f4 c) {
+  c = mfma_bf16(a.m, b.m, c);
+  c = mfma_bf16(a.h, b.l, c);
+  c = mfma_bf16(a.l, b.h, c);
+  c = mfma_bf16(a.h, b.m, c);
+  c = mfma_bf16(a.m, b.h, c);
+  return mfma_bf16(a.h, b.h, c);
+}
+
 }  // namespace dpamd

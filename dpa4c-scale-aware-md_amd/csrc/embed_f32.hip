@@ -1,9 +1,9 @@
 // Mixed-precision embedding kernels: the fp32 counterparts of the fp64
 // forward and backward in embed.hip. The env row of each slot, its gradient
 // and the edge gradient written for the force stage stay fp64; the nets, the
-// T contraction, the saved activations and the u/v dot products are fp32
-// (reference precision rule for the mixed mode: fp32 embedding/fitting, fp64
-// env matrix, force and virial).
+// T contraction and the u/v dot products are fp32 (reference precision rule
+// for the mixed mode: fp32 embedding/fitting, fp64 env matrix, force and
+// virial).
 //
 // The layer-2 and layer-3 products run on v_mfma_f32_16x16x32_bf16 at fp32
 // accuracy: each fp32 operand is split exactly into three bf16 pieces and the
@@ -12,8 +12,14 @@
 // tangents in registers. On gfx950 the bf16 form does 8x the work of
 // v_mfma_f32_16x16x4f32 in 0.65x its time.
 //
-// Work decomposition, tiles and the saved-activation scheme are those of the
-// fp64 kernels. What differs is the MFMA output layout: register r of lane
+// Work decomposition and tiles are those of the fp64 kernels. Unlike them,
+// the forward saves no activations: the backward recomputes layers 2 and 3
+// next to their tangents. On the bf16 matrix cores the products cost less
+// than moving the 12 KB of fp32 activations per tile through HBM twice
+// (measured on the 128,000-atom HEA: forward 2.50 -> 1.78 ms, backward
+// 2.56 -> 3.18 ms, and the kernels after the forward no longer wait behind
+// its write-back: step 9.75 -> 9.51 ms; saving layer 3 only was in between,
+// 9.66 ms). What differs as well is the MFMA output layout: register r of lane
 // (g, c) holds row 4g + r (fp64: g + 4r). Every layer therefore takes its
 // k elements in the order that layout leaves the previous layer in
 // registers: element e of 32-wide k chunk h of lane group g is feature
@@ -22,13 +28,10 @@
 // L1 is a multiple of 16, which keeps the layer-2 [x, x] residual in the
 // lane's own registers.
 //
-// Saved activations, per tile of 16 slots, float:
-//   layer 2: element (t, r) of lane L at [256t + 4L + r] (same layout in
-//            both kernels, so one 16-byte store / load per t);
-//   layer 3: written by the forward as (slot 4g + r, feature 16u + c) at
-//            [16 L2P + 256u + 4L + r] (one 16-byte store per u), read by the
-//            backward lane (g', c') as (feature 16u + 4g' + r, slot c') at
-//            [16 L2P + 256u + 64(c' >> 2) + 16g' + 4r + (c' & 3)].
+// The forward's layer 3 is X2 W3 (register r of tile u: slot 4g + r, feature
+// 16u + c); the backward recomputes it transposed, W3^T X2^T (feature 16u +
+// 4g + r, slot c), with the six piece products in the forward's order
+// (mfma3_t), so both kernels see the same activations bit for bit.
 #include "bf16x3.h"
 #include "env.h"
 #include "fastmath.h"
@@ -68,12 +71,13 @@ __device__ __forceinline__ Split3 x2_pieces(const float (&x2)[S::NT2][4], int h)
   return split3(v);
 }
 
-// Layer-3 output tiles per group (MFMA accumulators in flight). Both kernels
-// are latency-bound on short neighbour sections (one or two tiles per item),
-// so registers go to occupancy rather than to accumulators: the forward is
-// held to 128 VGPRs (4 waves per SIMD), the backward fits 168 (3 waves). An
-// accumulation chain into one register issues back to back, so one or two
-// tiles keep the matrix pipe fed.
+// Layer-3 output tiles per group (MFMA accumulators in flight). The forward
+// is latency-bound on short neighbour sections (one or two tiles per item),
+// so its registers go to occupancy: 128 VGPRs (4 waves per SIMD). The
+// backward carries the recomputed primal next to the tangent and runs two
+// waves per SIMD (up to 256 VGPRs; three waves spilled). An accumulation
+// chain into one register issues back to back, so one or two tiles keep the
+// matrix pipe fed.
 constexpr int kU3F = 1;  // forward
 constexpr int kU3B = 2;  // backward
 
@@ -91,9 +95,11 @@ template <class S>
 constexpr int fwd_lds_floats(int waves) {
   return lds_params<S>() + 16 + waves * 16 * x2_ld<S>() + waves * 64;
 }
+// ... | per wave: dT and its folded copy (float) | the section-sum cells
+// [16 slot lanes][12] (double, edge_out)
 template <class S>
 constexpr int bwd_lds_floats(int waves) {
-  return lds_params<S>() + 16 + waves * 4 * (S::L3P + S::L2P);
+  return lds_params<S>() + 16 + waves * 4 * (S::L3P + S::L2P) + waves * 2 * 16 * 12;
 }
 
 template <class S, int WAVES>
@@ -138,9 +144,7 @@ k_embed_fwd32(EmbArgs a) {
     const int i = a.items[a.type_off[ti] + item];
     const int nr = a.nreal[(long)i * a.ntypes + tj];
     const int* row = a.nlist + (long)i * a.nnei + a.sec[tj];
-    // env statistics from LDS: a global load inside the tile loop would be
-    // ordered behind the activation traffic by the in-order vector memory
-    // counter
+    // env statistics from LDS (staged once per block)
     const double* avg = EnvS;
     const double* sd = EnvS + 4;  // 1 / dstd
     const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
@@ -148,11 +152,6 @@ k_embed_fwd32(EmbArgs a) {
     float Tacc[S::NU3 * 4];
 #pragma unroll
     for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0f;
-    constexpr int BLK = 16 * (S::L2P + S::L3P);
-    float* act = static_cast<float*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
-    f4* act2 = reinterpret_cast<f4*>(act) + lane;                // (t) at act2[64t]
-    f4* act3 = reinterpret_cast<f4*>(act + 16 * S::L2P) + lane;  // (u) at act3[64u]
-
     // neighbour coordinates one tile ahead, their index two tiles ahead
     double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
     if (c < nr) {
@@ -162,7 +161,7 @@ k_embed_fwd32(EmbArgs a) {
       nx2 = a.ext[3 * j + 2];
     }
     int jn = 16 + c < nr ? row[16 + c] : 0;
-    for (int tile = 0; tile < nr; tile += 16, act2 += BLK / 4, act3 += BLK / 4) {
+    for (int tile = 0; tile < nr; tile += 16) {
       const int slot = tile + c;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
       if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, a.inv_sw, avg, sd, Rn);
@@ -203,12 +202,10 @@ k_embed_fwd32(EmbArgs a) {
       float x2[S::NT2][4];
 #pragma unroll
       for (int t = 0; t < S::NT2; ++t) {
-        f4 th4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int f = 16 * t + 4 * g + r;
           const float th = tanh_f32(acc2[t][r] + P[S::OFF_B2 + f]);
-          th4[r] = th;
           float res = 0.0f;
           if constexpr (S::RES2 != 0) {
             if constexpr (S::X1_ALIGNED) {
@@ -220,7 +217,6 @@ k_embed_fwd32(EmbArgs a) {
           }
           x2[t][r] = (f < S::L2) ? res + th : 0.0f;
         }
-        __builtin_nontemporal_store(th4, &act2[64 * t]);
       }
       if constexpr (S::RES3 != 0) {
 #pragma unroll
@@ -250,19 +246,16 @@ k_embed_fwd32(EmbArgs a) {
           const int u = u0 + uu;
           if (u < S::NU3) {
             const int f = 16 * u + c;
-            f4 th4;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int sl = 4 * g + r;
               const float th = tanh_f32(acc3[uu][r] + P[S::OFF_B3 + f]);
-              th4[r] = th;
               float G = th;
               if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
               if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
 #pragma unroll
               for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
             }
-            __builtin_nontemporal_store(th4, &act3[64 * u]);
           }
         }
       }
@@ -315,6 +308,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
   double* EnvS = reinterpret_cast<double*>(lds32 + PS);  // PS is a multiple of 64
   float* dTs = lds32 + PS + 16 + w * 4 * (S::L3P + S::L2P);
   float* dTf = dTs + 4 * S::L3P;
+  // 8-byte aligned: every region before it is a multiple of two floats
+  double* own_w = reinterpret_cast<double*>(lds32 + PS + 16 + WAVES * 4 * (S::L3P + S::L2P)) + w * 16 * 12;
 
   const int p = find_pair(a);
   const int ti = p / a.ntypes, tj = p % a.ntypes;
@@ -325,6 +320,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
       const double v = a.envp[p * 8 + threadIdx.x];
       EnvS[threadIdx.x] = threadIdx.x < 4 ? v : 1.0 / v;  // avg[4], 1 / dstd[4]
     }
+    for (int q = lane; q < 16 * 12; q += 64) own_w[q] = 0.0;
   }
   if (threadIdx.x == 0) item_next = 0;
   __syncthreads();
@@ -344,16 +340,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
     const int nr = a.nreal[(long)i * a.ntypes + tj];
     const long ebase = (long)i * a.nnei + a.sec[tj];
     const int* row = a.nlist + ebase;
-    // env statistics from LDS: a global load inside the tile loop would be
-    // ordered behind the activation traffic by the in-order vector memory
-    // counter
+    // env statistics from LDS (staged once per block)
     const double* avg = EnvS;
     const double* sd = EnvS + 4;  // 1 / dstd
     const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
-    constexpr int BLK = 16 * (S::L2P + S::L3P);
-    const float* act =
-        static_cast<const float*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
-
     {
       const float* dTi = static_cast<const float*>(a.dT) + (long)i * 4 * S::L3;
       for (int q = lane; q < 4 * S::L3P; q += 64) {
@@ -372,34 +362,26 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
     }
     wave_lds_sync();
 
-    const f4* act2 = reinterpret_cast<const f4*>(act) + lane;  // (t) at act2[64t]
-    // (u, r) at act3[256u + 4r]
-    const float* act3 = act + 16 * S::L2P + 64 * (c >> 2) + 16 * g + (c & 3);
     // neighbour coordinates of tile k+1 fetched during tile k, the neighbour
-    // index one tile earlier; the saved activations are loaded where they are
-    // used, layer 3's per output tile (holding them, or the next tile's, in
-    // registers costs occupancy or spills, worth more than the hidden latency)
+    // index one tile earlier
+    // (jx: the neighbour whose coordinates are in nx, for the slot's output)
     double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
-    int jn = 0;
+    int jn = 0, jx = 0;
     auto prefetch = [&](int tile) {
       if (tile + c < nr) {
         nx0 = a.ext[3 * (long)jn];
         nx1 = a.ext[3 * (long)jn + 1];
         nx2 = a.ext[3 * (long)jn + 2];
       }
+      jx = jn;
       jn = tile + 16 + c < nr ? row[tile + 16 + c] : 0;
     };
     jn = c < nr ? row[c] : 0;
     if (nr > 0) prefetch(0);
 
-    for (int tile = 0; tile < nr; tile += 16, act2 += BLK / 4, act3 += BLK) {
+    for (int tile = 0; tile < nr; tile += 16) {
       const int slot = tile + c;
       const bool valid = slot < nr;
-      f4 th2[S::NT2];
-
-#pragma unroll
-      for (int t = 0; t < S::NT2; ++t) th2[t] = act2[64 * t];
-
       double d0 = 0.0, d1 = 0.0, d2 = 0.0;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
       if (valid) {
@@ -408,6 +390,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
         d2 = nx2 - zi;
         env_value(d0, d1, d2, a.rcut_smth, a.rcut, a.inv_sw, avg, sd, Rn);
       }
+      const int jslot = jx;
       if (tile + 16 < nr) prefetch(tile + 16);
       const float s = (float)Rn[0];
 
@@ -426,18 +409,26 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
           x1t[q] = 0.0f;
         }
       }
-      // layer 2 tangent (transposed); tanh of the primal from the forward
-      f4 acc2t[S::NT2];
+      // layer 2 (transposed), the primal recomputed exactly as the forward
+      // computed it, and its tangent
+      f4 acc2[S::NT2], acc2t[S::NT2];
       {
-        Split3 xb[S::KC2];
+        Split3 xb[S::KC2], xbt[S::KC2];
 #pragma unroll
-        for (int h = 0; h < S::KC2; ++h) xb[h] = split3(x1t + 8 * h);
+        for (int h = 0; h < S::KC2; ++h) {
+          xb[h] = split3(x1 + 8 * h);
+          xbt[h] = split3(x1t + 8 * h);
+        }
 #pragma unroll
         for (int t = 0; t < S::NT2; ++t) {
+          acc2[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
           acc2t[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-          for (int h = 0; h < S::KC2; ++h)
-            acc2t[t] = mfma3(wpieces(P + S::OFF_W2, t * S::KC2 + h, lane), xb[h], acc2t[t]);
+          for (int h = 0; h < S::KC2; ++h) {
+            const Split3 wp = wpieces(P + S::OFF_W2, t * S::KC2 + h, lane);
+            acc2[t] = mfma3(wp, xb[h], acc2[t]);
+            acc2t[t] = mfma3(wp, xbt[h], acc2t[t]);
+          }
         }
       }
       float x2[S::NT2][4], x2t[S::NT2][4];
@@ -446,7 +437,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int f = 16 * t + 4 * g + r;
-          const float th = th2[t][r];
+          const float th = tanh_f32(acc2[t][r] + P[S::OFF_B2 + f]);
           float res = 0.0f, rest = 0.0f;
           if constexpr (S::RES2 != 0) {
             if constexpr (S::X1_ALIGNED) {
@@ -484,32 +475,33 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
             }
           }
       }
-      // layer 3 tangent, transposed: register r of tile u is feature 16u + 4g + r
-      Split3 xt[S::KC3];
+      // layer 3, transposed: register r of tile u is feature 16u + 4g + r.
+      // The primal is recomputed with the forward's products in the forward's
+      // order (mfma3_t: the transpose of the forward's X2 W3, bit for bit).
+      Split3 xp[S::KC3], xt[S::KC3];
 #pragma unroll
-      for (int h = 0; h < S::KC3; ++h) xt[h] = x2_pieces<S>(x2t, h);
+      for (int h = 0; h < S::KC3; ++h) {
+        xp[h] = x2_pieces<S>(x2, h);
+        xt[h] = x2_pieces<S>(x2t, h);
+      }
 #pragma unroll
       for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
         __builtin_amdgcn_sched_barrier(0);
-        // this output tile's saved activations, issued ahead of its products
-        // (which cover their latency) and pinned there: left to itself the
-        // scheduler may sink each load to its use and wait on it alone
-        float th3v[kU3B][4];
+        f4 acc3[kU3B], acc3t[kU3B];
 #pragma unroll
-        for (int uu = 0; uu < kU3B; ++uu)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            th3v[uu][r] = u0 + uu < S::NU3 ? act3[256 * (u0 + uu) + 4 * r] : 0.0f;
-        __builtin_amdgcn_sched_barrier(0);
-        f4 acc3t[kU3B];
-#pragma unroll
-        for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int uu = 0; uu < kU3B; ++uu) {
+          acc3[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+          acc3t[uu] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
 #pragma unroll
         for (int h = 0; h < S::KC3; ++h)
 #pragma unroll
           for (int uu = 0; uu < kU3B; ++uu)
-            if (u0 + uu < S::NU3)
-              acc3t[uu] = mfma3(wpieces(P + S::OFF_W3, (u0 + uu) * S::KC3 + h, lane), xt[h], acc3t[uu]);
+            if (u0 + uu < S::NU3) {
+              const Split3 wp = wpieces(P + S::OFF_W3, (u0 + uu) * S::KC3 + h, lane);
+              acc3[uu] = mfma3_t(wp, xp[h], acc3[uu]);
+              acc3t[uu] = mfma3(wp, xt[h], acc3t[uu]);
+            }
 #pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) {
           const int u = u0 + uu;
@@ -517,7 +509,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int f = 16 * u + 4 * g + r;
-              const float th = th3v[uu][r];
+              const float th = tanh_f32(acc3[uu][r] + P[S::OFF_B3 + f]);
               const float tt = (1.0f - th * th) * acc3t[uu][r];
 #pragma unroll
               for (int m = 0; m < 4; ++m) {
@@ -541,35 +533,25 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
         nd[0] += (Rn[0] * (double)vp[0] + Rn[1] * (double)vp[1] + Rn[2] * (double)vp[2] +
                   Rn[3] * (double)vp[3]) *
                  a.inv_nnei;
-        // stored (coalesced); the forces are scattered from them by a
-        // streaming pass afterwards (launch_edge_scatter): atomics here would
-        // hold up the just-in-time activation loads behind them in the
-        // in-order memory counter
+        // forces and virials as in the fp64 backward: the neighbour side in
+        // fixed point onto slot jslot, the centre side into the lane's cells
         double gv[3];
         env_grad(d0, d1, d2, a.rcut_smth, a.rcut, a.inv_sw, sd, nd, gv);
-        double* eg = a.edge_grad + (ebase + slot) * 3;
-        eg[0] = gv[0];
-        eg[1] = gv[1];
-        eg[2] = gv[2];
+        const double dv[3] = {d0, d1, d2};
+        edge_out(a, ebase + slot, jslot, dv, gv, own_w + 12 * c);
       }
     }
-    // padded slots carry no gradient
-    for (int sl = nr + lane; sl < a.sel[tj]; sl += 64) {
-      double* eg = a.edge_grad + (ebase + sl) * 3;
-      eg[0] = 0.0;
-      eg[1] = 0.0;
-      eg[2] = 0.0;
-    }
+    own_flush(a, i, tj, nr, ebase, own_w, lane);
   }
 }
 
 using ShapeWater32 = EmbShape<25, 50, 100, true>;
 using ShapeMetal32 = EmbShape<32, 64, 128, true>;
 // One block per CU holds the pre-split nets (about 61 KB) once: 16 waves
-// (4 per SIMD) for the forward, 12 (3 per SIMD, its register budget) for the
+// (4 per SIMD) for the forward, 8 (2 per SIMD, its register budget) for the
 // backward.
 constexpr int kFwdWaves32 = 16;
-constexpr int kBwdWaves32 = 12;
+constexpr int kBwdWaves32 = 8;
 
 template <class S>
 void fwd32_impl(hipStream_t st, const EmbArgs& a, int nblocks) {

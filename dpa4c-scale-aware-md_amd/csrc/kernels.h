@@ -51,7 +51,7 @@ struct EmbArgs {
   double rcut, rcut_smth, inv_nnei;
   double inv_sw;                 // 1 / (rcut - rcut_smth)
   // Precision-dependent arrays (double in fp64 mode, float in mixed mode):
-  // emb, Tsec, dT and act; everything else is fp64 in both modes.
+  // emb, Tsec and dT; everything else is fp64 in both modes.
   const void* emb;     // [npair][stride] padded nets
   const double* envp;  // [npair][8] davg[4], dstd[4]
   const double* ext;   // [nall][3]
@@ -75,10 +75,10 @@ struct EmbArgs {
   // point accepts (raising kStatusFixedRange above it or on NaN)
   int* status;
   double fix_gmax;
-  // Saved activations: per (centre, tile of 16 slots) a block of
-  // 16*(L2P + L3P) doubles holding tanh of layers 2 and 3 in the backward's
-  // register order; tiles of section tj start at tile_off[tj], tiles_per_atom
-  // in total per centre.
+  // Saved activations (fp64 kernels; the mixed backward recomputes them):
+  // per (centre, tile of 16 slots) a block of 16*(L2P + L3P) doubles holding
+  // tanh of layers 2 and 3 in the backward's register order; tiles of
+  // section tj start at tile_off[tj], tiles_per_atom in total per centre.
   void* act;
   int tile_off[kMaxTypes + 1];
   int tiles_per_atom;
