@@ -72,8 +72,9 @@ def flops_bytes(pot, n_real, nloc, mixed=False):
         "embed_fwd": ("flop", emb_fwd * n_real),
         "embed_bwd": ("flop", emb_vjp * n_real),
         "fitting": ("flop", fit * nloc),
-        # mixed precision: a pass reading dE/dD and T, writing dE/dT (fp64:
-        # fused into the fitting's input-gradient kernel, no pass of its own)
+        # a pass reading dE/dD and T, writing dE/dT, only where the fitting's
+        # fused input-gradient kernel does not apply (axis 16 and F0 240 it
+        # does, in both precisions)
         "dE_dT": ("byte", es * nloc * (Dn + 4 * L3 + 4 * L3)),
         # the edges are scattered inside the embedding backward (fixed point);
         # this stage folds ghost sums onto owners and assembles per atom the
@@ -85,7 +86,7 @@ def flops_bytes(pot, n_real, nloc, mixed=False):
     if nt > 1:
         # reads the section sums, writes T (the first fitting GEMM forms D from T)
         work["descriptor"] = ("byte", es * nloc * (nt * 4 * L3 + 4 * L3))
-    if not mixed and M2 == 16:
+    if M2 == 16 and F0 == 240:
         del work["dE_dT"]
     return work
 
@@ -199,7 +200,7 @@ def run_config(dp, hip, config, steps, warmup):
         entry = {"ms": round(t, 4)}
         if k in work and t > 0:
             priced(entry, *work[k], t, peak_mfma)
-        elif k == "dE_dT" and not mixed:
+        elif k == "dE_dT" and k not in work:
             entry["note"] = "fused into the fitting stage's input-gradient kernel"
         stages[k] = entry
     return dict(n=n, ms=ms, ms_sync=ms_sync, ms_host=ms_host, stage_ms=stage_ms, stages=stages,

@@ -374,7 +374,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   E* D = d_from_t ? nullptr : need<E>(M, M->D, (size_t)std::max(nb, 1) * Dn);
   // fp64 with the fused input-gradient kernel: dE/dD is not stored (only
   // when kept for inspection)
-  const bool fused_ddt = !f32 && M->d_w0t && d_from_t;
+  const bool fused_ddt = d_from_t && (f32 ? M->fitf_off[0][0][1] >= 0 : M->d_w0t != nullptr);
   E* dD = (!fused_ddt || M->keep_edge_grad) ? need<E>(M, M->dD, (size_t)std::max(nb, 1) * Dn)
                                             : nullptr;
   E* dT = need<E>(M, M->dT, (size_t)nloc * 4 * L3);
@@ -539,11 +539,14 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
     fb.epart = reinterpret_cast<double*>(base + 6 * slab) + r0 * (size_t)(m.fit[2] / 16);
     FitDdt ddt{};
     if (fused_ddt) {
-      ddt.W0T = M->d_w0t + (size_t)t * m.fit[0] * Dn;
+      if constexpr (f32)
+        ddt.W0T = static_cast<const char*>(M->d_fitf) + M->fitf_off[t][0][1];
+      else
+        ddt.W0T = M->d_w0t + (size_t)t * m.fit[0] * Dn;
       ddt.items = items;
       ddt.pos0 = (int)r0;
-      ddt.dT = reinterpret_cast<double*>(dT);
-      ddt.dD = dD ? reinterpret_cast<double*>(dD) + r0 * Dn : nullptr;
+      ddt.dT = dT;
+      ddt.dD = dD ? dD + r0 * Dn : nullptr;
       ddt.ncu = M->ncu;
       ddt.nsplit = ddt_splits(rows, L3, M->ncu);
       ddt.ws = ddt.nsplit > 1 ? ddt_ws + ddt_off : nullptr;
@@ -1255,20 +1258,23 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
       const std::vector<float> fit32(m.fit_params.begin(), m.fit_params.end());
       upload(M->d_emb, emb32);
       upload(M->d_fit, fit32);
-      // fitting GEMM operands pre-split for the bf16 matrix cores: W0 forward
-      // (its backward dE/dD is rocBLAS sgemm), W1 / W2 forward and transposed
+      // fitting GEMM operands pre-split for the bf16 matrix cores: W0, W1,
+      // W2 forward, W1 / W2 transposed, and W0 transposed tile-major for the
+      // fused dE/dD -> dE/dT kernel (when it applies; otherwise dE/dD is
+      // rocBLAS sgemm)
       const FitOffsets fo = fit_offsets(m);
       const int ins[3] = {m.emb[2] * m.axis, m.fit[0], m.fit[1]};
+      const bool w0t = ddt_supported(m.fit[0], m.emb[2], m.axis);
       std::vector<uint16_t> frag;
       for (int t = 0; t < m.ntypes; ++t)
         for (int k = 0; k < 3; ++k)
           for (int tr = 0; tr < 2; ++tr) {
             M->fitf_off[t][k][tr] = -1;
-            if (k == 0 && tr == 1) continue;  // dE/dD: rocBLAS sgemm (faster there)
+            if (k == 0 && tr == 1 && !w0t) continue;
             frag.resize((frag.size() + 127) / 128 * 128);  // 256-byte aligned blocks
             M->fitf_off[t][k][tr] = (long)(frag.size() * sizeof(uint16_t));
             pack_gemm_bf16(m.fit_params.data() + (size_t)t * m.fit_block + fo.W[k], ins[k],
-                           m.fit[k], tr == 1, frag);
+                           m.fit[k], tr == 1, frag, k == 0 && tr == 1);
           }
       upload(M->d_fitf, frag);
     } else {

@@ -788,15 +788,179 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT(DdtArgs p) {
 // dT[atom][m][b < 16] of a split k_dDdT: the last split's first term plus the
 // splits' second-term partials, summed in split order. One thread per (row,
 // m, b).
+template <class T>
 __global__ __launch_bounds__(256) void k_ddt_combine(int rows, int L3, int nsplit, int pos0,
-                                                     const int* items, const double* ws,
-                                                     double* dT) {
+                                                     const int* items, const double* ws, T* dT) {
   const long q = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (q >= (long)rows * 64) return;
   const int row = (int)(q >> 6), e = (int)(q & 63), m = e >> 4, b = e & 15;
   double sum = ws[q];
   for (int k = 1; k < nsplit; ++k) sum += ws[(long)k * rows * 64 + q];
-  dT[((long)items[pos0 + row] * 4 + m) * L3 + b] = ws[(long)nsplit * rows * 64 + q] + sum;
+  dT[((long)items[pos0 + row] * 4 + m) * L3 + b] = (T)(ws[(long)nsplit * rows * 64 + q] + sum);
+}
+
+// Mixed-precision form of k_dDdT: the same decomposition with the products on
+// the bf16 matrix cores at fp32 accuracy (three-piece split, mfma3), fp32
+// T / dT and fp32 sums. Lane (g, c) keeps the pieces of its row's dZ0 (row c
+// of the wave; elements 32h + 8g + e of k chunk h, zero past K) as B
+// operands; the block walks the column groups a with group a's pre-split W0
+// fragments (tile-major pack_gemm_bf16 of W0^T: [L3][NC][3][64 lanes] x 16
+// bytes, lane 16g + c holding W0[16a + c][32h + 8g + e]) and T column a of
+// its rows staged through the LDS DMA. Register r of lane (g, c) of the
+// product D'[b][row] is dD[row c][a][b = 4g + r] (the bf16 MFMA's result
+// layout); first and second terms, flushes and splits as in k_dDdT.
+constexpr int kObRow3 = 65;  // row stride (floats) of the first-term buffer: 64 + 1
+
+struct DdtArgs3 {
+  int rows, K, L3;
+  const float* dZ;  // [rows][K]
+  const bf8* W0f;   // tile-major fragments, NC * 192 per column group
+  const float* Tt;
+  long ldt;
+  int pos0;
+  const int* items;
+  float* dT;  // [atoms][4][L3]
+  float* dD;  // [rows][16 L3] or null
+  int nsplit;
+  double* ws;  // as k_dDdT's
+};
+
+template <int WAVES, int NC>
+__global__ __launch_bounds__(WAVES * 64) void k_dDdT3(DdtArgs3 p) {
+  constexpr int BM = 16 * WAVES, NGB = NC * 192;
+  static_assert(BM % 64 == 0 && NC % 2 == 0, "block rows in whole granule passes; K halves");
+  extern __shared__ __align__(16) float lds3[];
+  bf8* Ws = reinterpret_cast<bf8*>(lds3);        // [2][NGB]
+  float* Ts = lds3 + 2 * NGB * 4;               // [2][BM][4]
+  float* Ob = Ts + 2 * BM * 4;                  // [WAVES][16 rows][kObRow3]
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  const int row0 = blockIdx.x * BM, wrow = row0 + 16 * w + c;
+  const bool rowok = wrow < p.rows;
+  const int Dn = 16 * p.L3;
+  float* Obw = Ob + w * 16 * kObRow3;
+  const int S = p.nsplit, s = blockIdx.y, R = p.L3 - 16;
+  auto bound = [&](int k) { return k >= S ? p.L3 : 16 * ((2 * k * R + 16 * S) / (32 * S)); };
+  const int i0 = bound(s), i1 = bound(s + 1);
+  Split3 Zb[NC];
+#pragma unroll
+  for (int h = 0; h < NC; ++h) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int k = 32 * h + 8 * g + e;
+      v[e] = (rowok && k < p.K) ? p.dZ[(long)wrow * p.K + k] : 0.0f;
+    }
+    Zb[h] = split3(v);
+  }
+  const long tpos = 4L * wrow;
+  const int my_atom = rowok ? p.items[p.pos0 + wrow] : 0;
+  // T[row c][m][b = 4g + r]
+  float Tc[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) Tc[r][m] = rowok ? p.Tt[(long)(4 * g + r) * p.ldt + tpos + m] : 0.0f;
+  float acc2[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc2[r][m] = 0.0f;
+
+  // group a through the LDS DMA (16 bytes per lane, lane L's granule at
+  // base + 16 L): its NGB weight granules, contiguous in the tile-major pack,
+  // and T column a of the block's rows (one granule per row; rows past the
+  // type's end read its last row and are not used)
+  auto issue = [&](int buf, int a) {
+    for (int i = w; 64 * i < NGB; i += WAVES) {
+      const int q = 64 * i + lane;
+      if (q < NGB)
+        __builtin_amdgcn_global_load_lds(p.W0f + (long)a * NGB + q, LDS_PTR(Ws + buf * NGB + 64 * i),
+                                         16, 0, 0);
+    }
+    for (int i = w; 64 * i < BM; i += WAVES) {
+      const int r = min(row0 + 64 * i + lane, p.rows - 1);
+      __builtin_amdgcn_global_load_lds(p.Tt + (long)a * p.ldt + 4L * r,
+                                       LDS_PTR(Ts + buf * BM * 4 + 256 * i), 16, 0, 0);
+    }
+  };
+  auto col_of = [&](int i) { return i + 16 < p.L3 ? i + 16 : i + 16 - p.L3; };
+
+  if (i0 < i1) issue(0, col_of(i0));
+  for (int i = i0; i < i1; ++i) {
+    const int a = col_of(i), buf = (i - i0) & 1;
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (i + 1 < i1) issue(buf ^ 1, col_of(i + 1));
+    // D'[b][row] over K in two accumulation chains (the halves of the chunks)
+    const bf8* A = Ws + buf * NGB + lane;
+    f4 acc0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int h = 0; h < NC / 2; ++h) {
+      const bf8* a0 = A + 192 * h;
+      const bf8* a1 = A + 192 * (h + NC / 2);
+      acc0 = mfma3(Split3{a0[0], a0[64], a0[128]}, Zb[h], acc0);
+      acc1 = mfma3(Split3{a1[0], a1[64], a1[128]}, Zb[h + NC / 2], acc1);
+    }
+    f4 acc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = acc0[r] + acc1[r];
+    // first term: sum over b = 4g + r (lane-local over r, then the groups)
+    float sm[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      float v = acc[0] * Tc[0][m];
+      v += acc[1] * Tc[1][m];
+      v += acc[2] * Tc[2][m];
+      v += acc[3] * Tc[3][m];
+      sm[m] = add_xor32(add_xor16(v));
+    }
+    Obw[c * kObRow3 + g * 16 + (a & 15)] = g == 0 ? sm[0] : g == 1 ? sm[1] : g == 2 ? sm[2] : sm[3];
+    // second term: T[row][m][a]
+    const float* tr = Ts + buf * BM * 4 + (16 * w + c) * 4;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const float t = tr[m];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc2[r][m] += acc[r] * t;
+    }
+    if (p.dD && rowok) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p.dD[(long)wrow * Dn + 16 * a + 4 * g + r] = acc[r];
+    }
+    if (a >= 16 && ((a & 15) == 15 || a == p.L3 - 1)) {
+      wave_lds_sync();
+      const int abase = a & ~15, na = a - abase + 1;
+#pragma unroll
+      for (int rl = 0; rl < 16; ++rl) {
+        const int atom = __shfl(my_atom, rl, 64);
+        const int m = lane >> 4, al = lane & 15;
+        if (al < na && row0 + 16 * w + rl < p.rows)
+          p.dT[((long)atom * 4 + m) * p.L3 + abase + al] = Obw[kObRow3 * rl + lane];
+      }
+      wave_lds_sync();
+    }
+  }
+  wave_lds_sync();
+  if (rowok && S == 1) {
+    float* out = p.dT + (long)my_atom * 4 * p.L3;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int b = 4 * g + r;
+        out[m * p.L3 + b] = Obw[c * kObRow3 + m * 16 + b] + acc2[r][m];
+      }
+  } else if (rowok) {
+    double* part = p.ws + ((long)s * p.rows + wrow) * 64;
+    double* first = p.ws + ((long)S * p.rows + wrow) * 64;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int b = 4 * g + r;
+        part[m * 16 + b] = acc2[r][m];
+        if (s == S - 1) first[m * 16 + b] = Obw[c * kObRow3 + m * 16 + b];
+      }
+  }
 }
 
 template <int WAVES>
@@ -958,13 +1122,17 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   g.dHin = net.L[1].idt ? b.dH : nullptr; g.ld_dhin = F1; g.dH_out = nullptr; g.Tk = b.H0;
   g.Bf = net.L[1].WfT;
   gemm<true>(st, g);
-  // dD = dZ0 W0^T, or (fp64) straight on to dE/dT
-  if constexpr (sizeof(T) == 8) {
-    if (ddt) {
-      launch_dDdT(st, rows, F0, L3, b.dZa, ddt->W0T, Tt, ldt, ddt->pos0, ddt->items, ddt->dT, ddt->dD,
-                  ddt->ncu, ddt->nsplit, ddt->ws);
-      return;
-    }
+  // dD = dZ0 W0^T, or straight on to dE/dT
+  if (ddt) {
+    if constexpr (sizeof(T) == 8)
+      launch_dDdT(st, rows, F0, L3, b.dZa, static_cast<const double*>(ddt->W0T), Tt, ldt, ddt->pos0,
+                  ddt->items, static_cast<double*>(ddt->dT), static_cast<double*>(ddt->dD), ddt->ncu,
+                  ddt->nsplit, ddt->ws);
+    else
+      launch_dDdT3(st, rows, F0, L3, b.dZa, ddt->W0T, Tt, ldt, ddt->pos0, ddt->items,
+                   static_cast<float*>(ddt->dT), static_cast<float*>(ddt->dD), ddt->ncu, ddt->nsplit,
+                   ddt->ws);
+    return;
   }
   if (blas) {
     blas_gemm_nt(blas, st, rows, Dn, F0, b.dZa, net.L[0].W, dD);
@@ -1024,8 +1192,44 @@ void launch_dDdT(hipStream_t st, int rows, int K, int L3, const double* dZ, cons
   DPAMD_LAUNCH_CHECK();
   if (S > 1) {
     const long n = (long)rows * 64;
-    hipLaunchKernelGGL(k_ddt_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, rows, L3,
-                       S, pos0, items, ws, dT);
+    hipLaunchKernelGGL(k_ddt_combine<double>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       rows, L3, S, pos0, items, ws, dT);
+    DPAMD_LAUNCH_CHECK();
+  }
+}
+
+template <int WAVES>
+static size_t ddt3_lds_bytes(int NC) {
+  return (size_t)2 * NC * 192 * 16 + sizeof(float) * (2 * 16 * WAVES * 4 + WAVES * 16 * kObRow3);
+}
+
+void launch_dDdT3(hipStream_t st, int rows, int K, int L3, const float* dZ, const void* W0f,
+                  const float* Tt, long ldt, int pos0, const int* items, float* dT, float* dD,
+                  int ncu, int nsplit, double* ws) {
+  if (rows <= 0) return;
+  if (K != 240) throw HipError{hipErrorInvalidValue, "fused dE/dD kernel needs F0 = 240"};
+  constexpr int NC = 8;  // 32-wide k chunks of K = 240 (zero-padded to 256)
+  int waves = 0;
+  const int S = ddt_shape(rows, L3, ncu, &waves);
+  if (S != nsplit || (S > 1 && !ws))
+    throw HipError{hipErrorInvalidValue, "fused dE/dD kernel: split workspace does not match"};
+  DdtArgs3 p{rows, K, L3, dZ, static_cast<const bf8*>(W0f), Tt, ldt, pos0, items, dT, dD, S, ws};
+  if (waves == 8) {
+    const size_t bytes = ddt3_lds_bytes<8>(NC);
+    DPAMD_HIP(hipFuncSetAttribute((const void*)k_dDdT3<8, NC>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    hipLaunchKernelGGL((k_dDdT3<8, NC>), dim3((rows + 127) / 128, S), dim3(512), bytes, st, p);
+  } else {
+    const size_t bytes = ddt3_lds_bytes<4>(NC);
+    DPAMD_HIP(hipFuncSetAttribute((const void*)k_dDdT3<4, NC>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    hipLaunchKernelGGL((k_dDdT3<4, NC>), dim3((rows + 63) / 64, S), dim3(256), bytes, st, p);
+  }
+  DPAMD_LAUNCH_CHECK();
+  if (S > 1) {
+    const long n = (long)rows * 64;
+    hipLaunchKernelGGL(k_ddt_combine<float>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, rows,
+                       L3, S, pos0, items, ws, dT);
     DPAMD_LAUNCH_CHECK();
   }
 }

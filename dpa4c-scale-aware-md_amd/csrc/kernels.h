@@ -212,11 +212,13 @@ int fit_splits(int rows, int N, int K, int ncu);
 // (launch_dDdT); when given, launch_fitting computes dE/dT of its rows
 // instead of dE/dD.
 struct FitDdt {
-  const double* W0T;  // [F0][16 L3] first-layer weights, transposed
+  // first-layer weights: fp64 W0^T [F0][16 L3]; mixed precision the
+  // tile-major bf16 pieces of W0^T (pack_gemm_bf16)
+  const void* W0T;
   const int* items;   // bucket position -> atom
   int pos0;           // bucket position of the type's first row
-  double* dT;         // [atoms][4][L3]
-  double* dD;         // [rows][16 L3] when kept for inspection, else null
+  void* dT;           // [atoms][4][L3] (the net's precision)
+  void* dD;           // [rows][16 L3] when kept for inspection, else null
   int ncu;
   // column-group splits (ddt_splits) and their workspace, (nsplit + 1) *
   // rows * 64 doubles (unused when nsplit == 1)
@@ -228,6 +230,9 @@ bool ddt_supported(int F0, int L3, int axis);
 void launch_dDdT(hipStream_t, int rows, int K, int L3, const double* dZ, const double* W0T,
                  const double* Tt, long ldt, int pos0, const int* items, double* dT, double* dD,
                  int ncu, int nsplit, double* ws);
+void launch_dDdT3(hipStream_t, int rows, int K, int L3, const float* dZ, const void* W0f,
+                  const float* Tt, long ldt, int pos0, const int* items, float* dT, float* dD,
+                  int ncu, int nsplit, double* ws);
 template <class T>
 void launch_fitting(hipStream_t, const FitNet<T>&, int rows, const T* D, const T* Tt, long ldt,
                     int L3, const FitBufs<T>&, T* dD, double* e_bucket, void* blas,

@@ -245,7 +245,8 @@ void pack_pieces(const double* W, int K, int N, int tiles, int chunks, bool row_
 }
 }  // namespace
 
-void pack_gemm_bf16(const double* W, int rows, int cols, bool trans, std::vector<uint16_t>& out) {
+void pack_gemm_bf16(const double* W, int rows, int cols, bool trans, std::vector<uint16_t>& out,
+                    bool tile_major) {
   const int K = trans ? cols : rows, N = trans ? rows : cols;
   const int chunks = (K + 31) / 32, tiles = N / 16;
   const size_t base = out.size();
@@ -261,7 +262,8 @@ void pack_gemm_bf16(const double* W, int rows, int cols, bool trans, std::vector
           uint16_t pc[3];
           split3((float)v, pc);
           for (int q = 0; q < 3; ++q)
-            dst[((((size_t)h * tiles + t) * 3 + q) * 64 + lane) * 8 + e] = pc[q];
+            dst[(((tile_major ? (size_t)t * chunks + h : (size_t)h * tiles + t) * 3 + q) * 64 +
+                 lane) * 8 + e] = pc[q];
         }
       }
 }

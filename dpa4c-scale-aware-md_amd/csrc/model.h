@@ -44,7 +44,10 @@ void pack_embedding_bf16(const ModelHost& m, const EmbLayout& e, std::vector<flo
 // split exactly into three bf16 pieces) in the layout the bf16 GEMM reads:
 // [ceil(K/32)][N/16][3][64 lanes][8], lane 16g + c of (chunk h, tile n)
 // holding B(32h + 8g + e, 16n + c), e = 0..7, zero past K. N % 16 == 0.
-void pack_gemm_bf16(const double* W, int rows, int cols, bool trans, std::vector<uint16_t>& out);
+// tile_major: [N/16][ceil(K/32)][3][64][8] instead (all chunks of a column
+// tile contiguous, the order the fused input-gradient kernel stages them).
+void pack_gemm_bf16(const double* W, int rows, int cols, bool trans, std::vector<uint16_t>& out,
+                    bool tile_major = false);
 
 // Offsets (in doubles) of each fitting layer inside a type's block.
 struct FitOffsets {
