@@ -73,6 +73,30 @@ __device__ __forceinline__ void tanh_n(const double* z, double* y, const double*
   }
 }
 
+// A last output tile with at most four real features (water's 50 and 100:
+// 2 and 4 of 16) costs a tile's MFMAs and tanh for a few values; the kernels
+// form it on the VALU instead: lane (g, c) sums its slot's k elements against
+// the tail columns, the four lane groups are added, and lane group g keeps
+// tail feature g.
+template <int L>
+constexpr bool vtail() {
+  return L % 16 != 0 && L % 16 <= 4;
+}
+// element g of v[0 .. N) (0 past N)
+template <int N>
+__device__ __forceinline__ double pick(const double (&v)[N], int g) {
+  double r = 0.0;
+#pragma unroll
+  for (int j = 0; j < N; ++j) r = g == j ? v[j] : r;
+  return r;
+}
+// sum over the 16 slot lanes (c) of a lane group
+__device__ __forceinline__ double add_c16(double v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
 // layer-1 stash [16 slots][K2P + 1] per wave, for a layer-2 [x, x] residual
 // whose features do not fall in the lane that computed them (L1 % 16 != 0)
 template <class S>
@@ -138,11 +162,17 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     const double* sd = EnvS + 4;  // 1 / dstd
     const double xi = a.ext[3 * (long)i], yi = a.ext[3 * (long)i + 1], zi = a.ext[3 * (long)i + 2];
 
+    // layer-2 / layer-3 tails on the VALU (vtail); U3 MFMA tiles of layer 3
+    constexpr bool T2V = vtail<S::L2>(), T3V = vtail<S::L3>();
+    constexpr int NT2M = S::NT2 - (T2V ? 1 : 0), U3 = S::NU3 - (T3V ? 1 : 0);
     double Tacc[S::NU3 * 4];
 #pragma unroll
     for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0;
     constexpr int BLK = 16 * (S::L2P + S::L3P);
     double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
+    // the layer-3 tail's activation (slot c, feature 16 U3 + g), where the
+    // backward reads tile U3's register 0
+    double* act3t = act + 16 * S::L2P + 256 * U3 + 4 * c + g;
 
     // per-lane bases: layer 2 element (t, r) at act2[(4t + r) * 64], layer 3
     // element (u, r) of slot g + 4r at act3[256u + 16r]. The activations are
@@ -162,7 +192,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       nx2 = a.ext[3 * j + 2];
     }
     int jn = 16 + c < nr ? row[16 + c] : 0;
-    for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
+    for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK, act3t += BLK) {
       const int slot = tile + c;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
       if (slot < nr) env_value(nx0 - xi, nx1 - yi, nx2 - zi, a.rcut_smth, a.rcut, a.inv_sw, avg, sd, Rn);
@@ -205,12 +235,41 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
 #pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
 #pragma unroll
-        for (int t = 0; t < S::NT2; ++t)
+        for (int t = 0; t < NT2M; ++t)
           acc2[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1[q], acc2[t]);
       }
       double x2[S::NT2][4];
+      if constexpr (T2V) {
+        // tail features 16 NT2M + j: register 0 of tile NT2M (lane group g: j = g)
+        constexpr int TL = S::L2 % 16;
+        double pj[TL];
 #pragma unroll
-      for (int t = 0; t < S::NT2; ++t) {
+        for (int j = 0; j < TL; ++j) pj[j] = 0.0;
+#pragma unroll
+        for (int q = 0; q < S::NQ2; ++q) {
+          const double* wr = P + S::OFF_W2 + (4 * q + g) * S::L2P + 16 * NT2M;
+#pragma unroll
+          for (int j = 0; j < TL; ++j) pj[j] = fma(x1[q], wr[j], pj[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < TL; ++j) pj[j] = add_xor32(add_xor16(pj[j]));
+        const int f = 16 * NT2M + g;
+        const double th = tanh_tab1(pick(pj, g) + P[S::OFF_B2 + f], Tab);
+        __builtin_nontemporal_store(th, &act2[(4 * NT2M) * 64]);
+        double res = 0.0;
+        if constexpr (S::RES2 != 0) {
+          if constexpr (S::X1_ALIGNED) {
+            res = x1[(S::RES2 == 2 ? 4 * (NT2M % (S::L1 / 16)) : 4 * NT2M)];
+          } else {
+            const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
+            res = (f1 < S::L1) ? X2s[c * X1LD + f1] : 0.0;
+          }
+        }
+        x2[NT2M][0] = (f < S::L2) ? res + th : 0.0;
+        x2[NT2M][1] = x2[NT2M][2] = x2[NT2M][3] = 0.0;
+      }
+#pragma unroll
+      for (int t = 0; t < NT2M; ++t) {
         double z2[4], th2v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) z2[r] = acc2[t][r] + P[S::OFF_B2 + 16 * t + 4 * r + g];
@@ -241,7 +300,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       wave_lds_sync();
       // layer 3, non-transposed, two output tiles at a time
 #pragma unroll
-      for (int u0 = 0; u0 < S::NU3; u0 += kU3) {
+      for (int u0 = 0; u0 < U3; u0 += kU3) {
         __builtin_amdgcn_sched_barrier(0);
         d4 acc3[kU3];
 #pragma unroll
@@ -249,25 +308,25 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
         double wcur[kU3], wnxt[kU3];
         const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
 #pragma unroll
-        for (int uu = 0; uu < kU3; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
+        for (int uu = 0; uu < kU3; ++uu) wcur[uu] = u0 + uu < U3 ? W3[16 * uu] : 0.0;
 #pragma unroll
         for (int q = 0; q < S::NQ3; ++q) {
           if (q + 1 < S::NQ3) {
 #pragma unroll
             for (int uu = 0; uu < kU3; ++uu)
-              wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
+              wnxt[uu] = u0 + uu < U3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
           }
           const double av = x2[q / 4][q % 4];
 #pragma unroll
           for (int uu = 0; uu < kU3; ++uu)
-            if (u0 + uu < S::NU3) acc3[uu] = mfma_f64(av, wcur[uu], acc3[uu]);
+            if (u0 + uu < U3) acc3[uu] = mfma_f64(av, wcur[uu], acc3[uu]);
 #pragma unroll
           for (int uu = 0; uu < kU3; ++uu) wcur[uu] = wnxt[uu];
         }
 #pragma unroll
         for (int uu = 0; uu < kU3; ++uu) {
           const int u = u0 + uu;
-          if (u < S::NU3) {
+          if (u < U3) {
             const int f = 16 * u + c;
             double z3[4], th3v[4];
             const double b3 = P[S::OFF_B3 + f];
@@ -289,13 +348,63 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
           }
         }
       }
+      if constexpr (T3V) {
+        // tail features 16 U3 + j of this lane's slot c (lane group g: j = g);
+        // T of the tail accumulates per slot lane (Tacc[4 U3 + m], summed over
+        // the slot lanes at the end of the item)
+        constexpr int TL = S::L3 % 16;
+        double pj[TL];
+#pragma unroll
+        for (int j = 0; j < TL; ++j) pj[j] = 0.0;
+#pragma unroll
+        for (int t = 0; t < S::NT2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (16 * t + 4 * r >= 4 * S::NQ3) continue;  // past W3's rows (x2 is 0 there)
+            const double* wr = P + S::OFF_W3 + (16 * t + 4 * r + g) * S::L3P + 16 * U3;
+#pragma unroll
+            for (int j = 0; j < TL; ++j) pj[j] = fma(x2[t][r], wr[j], pj[j]);
+          }
+#pragma unroll
+        for (int j = 0; j < TL; ++j) pj[j] = add_xor32(add_xor16(pj[j]));
+        const int f = 16 * U3 + g;
+        const double th = tanh_tab1(pick(pj, g) + P[S::OFF_B3 + f], Tab);
+        __builtin_nontemporal_store(th, act3t);
+        double G = th;
+        if constexpr (S::RES3 == 2) G += X2s[c * X2LD + f % S::L2];
+        if constexpr (S::RES3 == 1) G += X2s[c * X2LD + f];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) Tacc[4 * U3 + m] += Rn[m] * G;
+      }
       wave_lds_sync();
     }
 #pragma unroll
-    for (int q = 0; q < S::NU3 * 4; ++q) {
+    for (int q = 0; q < U3 * 4; ++q) {
       double v = Tacc[q];
       v = add_xor32(add_xor16(v));
       Tacc[q] = v;
+    }
+    if constexpr (T3V) {
+      // the tail's T: summed over the slot lanes, held by lane (g, 0) for
+      // feature 16 U3 + g
+#pragma unroll
+      for (int m = 0; m < 4; ++m) Tacc[4 * U3 + m] = add_c16(Tacc[4 * U3 + m]);
+      constexpr int TL = S::L3 % 16;
+      if (c == 0 && g < TL) {
+        const int f = 16 * U3 + g;
+        if (a.Tt) {
+          const double npad = (double)(a.sel[tj] - nr);
+          const double* tp = a.tpad + (long)p * 4 * S::L3;
+          double* Tt = static_cast<double*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+            Tt[f * a.ldt + m] = (double)((Tacc[4 * U3 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
+        } else {
+          double* out = static_cast<double*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
+#pragma unroll
+          for (int m = 0; m < 4; ++m) out[m * S::L3 + f] = Tacc[4 * U3 + m];
+        }
+      }
     }
     if (g == 0 && a.Tt) {
       // single neighbour type: this section is all of T
@@ -303,7 +412,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       const double* tp = a.tpad + (long)p * 4 * S::L3;
       double* Tt = static_cast<double*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
 #pragma unroll
-      for (int u = 0; u < S::NU3; ++u) {
+      for (int u = 0; u < U3; ++u) {
         const int f = 16 * u + c;
         if (f < S::L3) {
 #pragma unroll
@@ -315,7 +424,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     } else if (g == 0) {
       double* out = static_cast<double*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
 #pragma unroll
-      for (int u = 0; u < S::NU3; ++u) {
+      for (int u = 0; u < U3; ++u) {
         const int f = 16 * u + c;
         if (f < S::L3) {
 #pragma unroll
@@ -428,15 +537,18 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       const int par = (tile >> 4) & 1;
       const int slot = tile + c;
       const bool valid = slot < nr;
+      // (registers whose features are all past L2 / L3 are neither loaded nor used)
+      constexpr bool T2V = vtail<S::L2>(), T3V = vtail<S::L3>();
+      constexpr int NT2M = S::NT2 - (T2V ? 1 : 0), U3 = S::NU3 - (T3V ? 1 : 0);
       double th2[S::NT2][4], th3[S::NU3][4];
 #pragma unroll
       for (int t = 0; t < S::NT2; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) th2[t][r] = act2[(4 * t + r) * 64];
+        for (int r = 0; r < 4; ++r) th2[t][r] = 16 * t + 4 * r < S::L2 ? act2[(4 * t + r) * 64] : 0.0;
 #pragma unroll
       for (int u = 0; u < S::NU3; ++u)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) th3[u][r] = act3[256 * u + 64 * r];
+        for (int r = 0; r < 4; ++r) th3[u][r] = 16 * u + 4 * r < S::L3 ? act3[256 * u + 64 * r] : 0.0;
       double d0 = 0.0, d1 = 0.0, d2 = 0.0;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
       if (valid) {
@@ -480,8 +592,24 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 #pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
 #pragma unroll
-        for (int t = 0; t < S::NT2; ++t)
+        for (int t = 0; t < NT2M; ++t)
           acc2t[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1t[q], acc2t[t]);
+      }
+      if constexpr (T2V) {
+        // tangent of the tail features 16 NT2M + j (lane group g: j = g, register 0)
+        constexpr int TL = S::L2 % 16;
+        double pj[TL];
+#pragma unroll
+        for (int j = 0; j < TL; ++j) pj[j] = 0.0;
+#pragma unroll
+        for (int q = 0; q < S::NQ2; ++q) {
+          const double* wr = P + S::OFF_W2 + (4 * q + g) * S::L2P + 16 * NT2M;
+#pragma unroll
+          for (int j = 0; j < TL; ++j) pj[j] = fma(x1t[q], wr[j], pj[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < TL; ++j) pj[j] = add_xor32(add_xor16(pj[j]));
+        acc2t[NT2M][0] = pick(pj, g);
       }
       double x2[S::NT2][4], x2t[S::NT2][4];
 #pragma unroll
@@ -528,7 +656,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
       }
       // layer 3 tangent, transposed; tanh part of G from the forward
 #pragma unroll
-      for (int u0 = 0; u0 < S::NU3; u0 += kU3B) {
+      for (int u0 = 0; u0 < U3; u0 += kU3B) {
         // keep the scheduler from hoisting later tile groups' weight loads
         __builtin_amdgcn_sched_barrier(0);
         d4 acc3t[kU3B];
@@ -538,26 +666,27 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         double wcur[kU3B], wnxt[kU3B];
         const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
 #pragma unroll
-        for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = u0 + uu < S::NU3 ? W3[16 * uu] : 0.0;
+        for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = u0 + uu < U3 ? W3[16 * uu] : 0.0;
 #pragma unroll
         for (int q = 0; q < S::NQ3; ++q) {
           if (q + 1 < S::NQ3) {
 #pragma unroll
             for (int uu = 0; uu < kU3B; ++uu)
-              wnxt[uu] = u0 + uu < S::NU3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
+              wnxt[uu] = u0 + uu < U3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
           }
 #pragma unroll
           for (int uu = 0; uu < kU3B; ++uu)
-            if (u0 + uu < S::NU3) acc3t[uu] = mfma_f64(wcur[uu], x2t[q / 4][q % 4], acc3t[uu]);
+            if (u0 + uu < U3) acc3t[uu] = mfma_f64(wcur[uu], x2t[q / 4][q % 4], acc3t[uu]);
 #pragma unroll
           for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = wnxt[uu];
         }
 #pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) {
           const int u = u0 + uu;
-          if (u < S::NU3) {
+          if (u < U3) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
+              if (16 * u + 4 * r >= S::L3) continue;
               const int f = 16 * u + 4 * r + g;
               const double th = th3[u][r];
               const double tt = (1.0 - th * th) * acc3t[uu][r];
@@ -569,6 +698,33 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
               }
             }
           }
+        }
+      }
+      if constexpr (T3V) {
+        // tangent of the tail features 16 U3 + j (lane group g: j = g, register 0)
+        constexpr int TL = S::L3 % 16;
+        double pj[TL];
+#pragma unroll
+        for (int j = 0; j < TL; ++j) pj[j] = 0.0;
+#pragma unroll
+        for (int t = 0; t < S::NT2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (16 * t + 4 * r >= 4 * S::NQ3) continue;  // past W3's rows (x2t is 0 there)
+            const double* wr = P + S::OFF_W3 + (16 * t + 4 * r + g) * S::L3P + 16 * U3;
+#pragma unroll
+            for (int j = 0; j < TL; ++j) pj[j] = fma(x2t[t][r], wr[j], pj[j]);
+          }
+#pragma unroll
+        for (int j = 0; j < TL; ++j) pj[j] = add_xor32(add_xor16(pj[j]));
+        const int f = 16 * U3 + g;
+        const double th = th3[U3][0];
+        const double tt = (1.0 - th * th) * pick(pj, g);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const double wv = dTs[m * S::L3P + f];
+          up[m] += wv * th;
+          vp[m] += wv * tt;
         }
       }
 #pragma unroll

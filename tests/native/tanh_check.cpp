@@ -71,5 +71,21 @@ int main() {
   dpamd::tanh_tab4(txn, tn, dpamd::kTanhTab32);
   const bool tzero = t4[0] == 0.0 && t4[1] == 0.0 && std::signbit(t4[1]) && t4[3] == -tn[3];
   std::printf("tanh_tab4 max_abs %.3e, zeros / odd symmetry %d\n", max_tab, (int)tzero);
-  return (max_abs <= 4e-15 && max_abs4 <= 4e-15 && zeros && max_tab <= 4e-15 && tzero) ? 0 : 1;
+  // one value at a time (the embedding kernels' lone tail features)
+  double max_tab1 = 0;
+  auto tab1 = [&](double x) {
+    max_tab1 = std::fmax(max_tab1, std::fabs(dpamd::tanh_tab1(x, dpamd::kTanhTab32) - std::tanh(x)));
+  };
+  for (int i = -2000000; i <= 2000000; ++i) tab1(i * 1e-5);
+  for (int i = 0; i < 2000000; ++i) tab1((i % 3 == 0) ? U(g) : W(g) * std::pow(10.0, (i % 7) - 4));
+  tab1(25.0);
+  tab1(-30.0);
+  const double o0 = dpamd::tanh_tab1(0.0, dpamd::kTanhTab32), o1 = dpamd::tanh_tab1(-0.0, dpamd::kTanhTab32);
+  const bool t1zero = o0 == 0.0 && o1 == 0.0 && std::signbit(o1) &&
+                      dpamd::tanh_tab1(-3.0, dpamd::kTanhTab32) == -dpamd::tanh_tab1(3.0, dpamd::kTanhTab32);
+  std::printf("tanh_tab1 max_abs %.3e, zeros / odd symmetry %d\n", max_tab1, (int)t1zero);
+  return (max_abs <= 4e-15 && max_abs4 <= 4e-15 && zeros && max_tab <= 4e-15 && tzero &&
+          max_tab1 <= 4e-15 && t1zero)
+             ? 0
+             : 1;
 }
