@@ -810,6 +810,11 @@ __global__ __launch_bounds__(256) void k_ddt_combine(int rows, int L3, int nspli
 // product D'[b][row] is dD[row c][a][b = 4g + r] (the bf16 MFMA's result
 // layout); first and second terms, flushes and splits as in k_dDdT.
 constexpr int kObRow3 = 65;  // row stride (floats) of the first-term buffer: 64 + 1
+// Column groups whose staging is in flight ahead of the one being multiplied
+// (LDS holds kDdt3Ahead + 1). Measured on HEA-128k: two or three ahead gained
+// nothing over one (fitting 2.50-2.52 ms either way), reading each chunk's
+// weight pieces one chunk ahead of its products did (2.61 -> 2.50 ms).
+constexpr int kDdt3Ahead = 1;
 
 struct DdtArgs3 {
   int rows, K, L3;
@@ -830,9 +835,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT3(DdtArgs3 p) {
   constexpr int BM = 16 * WAVES, NGB = NC * 192;
   static_assert(BM % 64 == 0 && NC % 2 == 0, "block rows in whole granule passes; K halves");
   extern __shared__ __align__(16) float lds3[];
-  bf8* Ws = reinterpret_cast<bf8*>(lds3);        // [2][NGB]
-  float* Ts = lds3 + 2 * NGB * 4;               // [2][BM][4]
-  float* Ob = Ts + 2 * BM * 4;                  // [WAVES][16 rows][kObRow3]
+  constexpr int NBUF = kDdt3Ahead + 1;
+  bf8* Ws = reinterpret_cast<bf8*>(lds3);       // [NBUF][NGB]
+  float* Ts = lds3 + NBUF * NGB * 4;            // [NBUF][BM][4]
+  float* Ob = Ts + NBUF * BM * 4;               // [WAVES][16 rows][kObRow3]
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
   const int row0 = blockIdx.x * BM, wrow = row0 + 16 * w + c;
   const bool rowok = wrow < p.rows;
@@ -869,36 +875,63 @@ __global__ __launch_bounds__(WAVES * 64) void k_dDdT3(DdtArgs3 p) {
   // group a through the LDS DMA (16 bytes per lane, lane L's granule at
   // base + 16 L): its NGB weight granules, contiguous in the tile-major pack,
   // and T column a of the block's rows (one granule per row; rows past the
-  // type's end read its last row and are not used)
+  // type's end read its last row and are not used). Every wave issues the
+  // same number of transfers per group, NOPS (the weights in whole passes of
+  // 64 granules, T as one pass of 16 lanes for the wave's own rows), so that
+  // a fixed vmcnt finds a group landed with later groups still in flight.
+  static_assert(NGB % (64 * WAVES) == 0, "weight passes per wave");
+  constexpr int NOPS = NGB / (64 * WAVES) + 1;
   auto issue = [&](int buf, int a) {
-    for (int i = w; 64 * i < NGB; i += WAVES) {
-      const int q = 64 * i + lane;
-      if (q < NGB)
-        __builtin_amdgcn_global_load_lds(p.W0f + (long)a * NGB + q, LDS_PTR(Ws + buf * NGB + 64 * i),
-                                         16, 0, 0);
+#pragma unroll
+    for (int k = 0; k < NGB / (64 * WAVES); ++k) {
+      const int i = w + WAVES * k, q = 64 * i + lane;
+      __builtin_amdgcn_global_load_lds(p.W0f + (long)a * NGB + q, LDS_PTR(Ws + buf * NGB + 64 * i),
+                                       16, 0, 0);
     }
-    for (int i = w; 64 * i < BM; i += WAVES) {
-      const int r = min(row0 + 64 * i + lane, p.rows - 1);
+    if (lane < 16) {
+      const int r = min(row0 + 16 * w + lane, p.rows - 1);
       __builtin_amdgcn_global_load_lds(p.Tt + (long)a * p.ldt + 4L * r,
-                                       LDS_PTR(Ts + buf * BM * 4 + 256 * i), 16, 0, 0);
+                                       LDS_PTR(Ts + buf * BM * 4 + 64 * w), 16, 0, 0);
     }
   };
   auto col_of = [&](int i) { return i + 16 < p.L3 ? i + 16 : i + 16 - p.L3; };
 
-  if (i0 < i1) issue(0, col_of(i0));
+#pragma unroll
+  for (int k = 0; k < kDdt3Ahead; ++k)
+    if (i0 + k < i1) issue(k, col_of(i0 + k));
   for (int i = i0; i < i1; ++i) {
-    const int a = col_of(i), buf = (i - i0) & 1;
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (i + 1 < i1) issue(buf ^ 1, col_of(i + 1));
-    // D'[b][row] over K in two accumulation chains (the halves of the chunks)
+    const int a = col_of(i), buf = (i - i0) % NBUF;
+    // group i has landed: each wave's transfers of the kDdt3Ahead - 1 groups
+    // after it may still be in flight (waiting for everything when fewer were
+    // issued, and at the output flushes, whose stores come later in the
+    // in-order count, is merely conservative); then the barrier, after which
+    // no wave still reads the buffer group i + kDdt3Ahead goes to
+    if (i + kDdt3Ahead - 1 < i1)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NOPS * (kDdt3Ahead - 1)) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (i + kDdt3Ahead < i1) issue((i - i0 + kDdt3Ahead) % NBUF, col_of(i + kDdt3Ahead));
+    // D'[b][row] over K in two accumulation chains (the halves of the
+    // chunks), each chunk's weight pieces read from LDS one chunk ahead
     const bf8* A = Ws + buf * NGB + lane;
+    auto wp = [&](int h) { return Split3{A[192 * h], A[192 * h + 64], A[192 * h + 128]}; };
     f4 acc0 = f4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    Split3 w0 = wp(0), w1 = wp(NC / 2);
 #pragma unroll
     for (int h = 0; h < NC / 2; ++h) {
-      const bf8* a0 = A + 192 * h;
-      const bf8* a1 = A + 192 * (h + NC / 2);
-      acc0 = mfma3(Split3{a0[0], a0[64], a0[128]}, Zb[h], acc0);
-      acc1 = mfma3(Split3{a1[0], a1[64], a1[128]}, Zb[h + NC / 2], acc1);
+      // (scheduling barriers keep the reads ahead of this chunk's products;
+      // left alone the compiler sinks each read to its use)
+      Split3 n0 = w0, n1 = w1;
+      if (h + 1 < NC / 2) {
+        n0 = wp(h + 1);
+        n1 = wp(h + 1 + NC / 2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      acc0 = mfma3(w0, Zb[h], acc0);
+      acc1 = mfma3(w1, Zb[h + NC / 2], acc1);
+      __builtin_amdgcn_sched_barrier(0);
+      w0 = n0;
+      w1 = n1;
     }
     f4 acc;
 #pragma unroll
@@ -1200,7 +1233,9 @@ void launch_dDdT(hipStream_t st, int rows, int K, int L3, const double* dZ, cons
 
 template <int WAVES>
 static size_t ddt3_lds_bytes(int NC) {
-  return (size_t)2 * NC * 192 * 16 + sizeof(float) * (2 * 16 * WAVES * 4 + WAVES * 16 * kObRow3);
+  constexpr int NBUF = kDdt3Ahead + 1;
+  return (size_t)NBUF * NC * 192 * 16 +
+         sizeof(float) * (NBUF * 16 * WAVES * 4 + WAVES * 16 * kObRow3);
 }
 
 void launch_dDdT3(hipStream_t st, int rows, int K, int L3, const float* dZ, const void* W0f,
