@@ -427,10 +427,22 @@ __global__ __launch_bounds__(256) void k_gemm3(GemmArgs<float> a) {
     const int buf = kc & 1;
     if (kc + 1 < nk) fetch(kc + 1);
     const Split3 xa = split3(As[buf] + (16 * w + c) * ALD + 8 * g);
+    // each column tile's B pieces are read from LDS one tile ahead of its
+    // products (scheduling barriers keep the compiler from sinking the reads
+    // to their use)
+    auto bp = [&](int n) {
+      const bf8* b = Bs[buf] + n * 192 + lane;
+      return Split3{b[0], b[64], b[128]};
+    };
+    Split3 bc = bp(0);
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-      const bf8* b = Bs[buf] + n * 192 + lane;
-      acc[n] = mfma3(xa, Split3{b[0], b[64], b[128]}, acc[n]);
+      Split3 bn = bc;
+      if (n + 1 < NT) bn = bp(n + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[n] = mfma3(xa, bc, acc[n]);
+      __builtin_amdgcn_sched_barrier(0);
+      bc = bn;
     }
     if (kc + 1 < nk) stash(buf ^ 1);
     __syncthreads();
