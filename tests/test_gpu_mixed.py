@@ -1,5 +1,6 @@
-"""GPU parity of the mixed-precision mode (fp32 embedding and fitting nets on
-FP32 MFMA; fp64 env matrix, edge gradients, forces, virial and energy sums)
+"""GPU parity of the mixed-precision mode (fp32 embedding and fitting nets,
+their products on the bf16 matrix cores at fp32 accuracy; fp64 env matrix,
+edge gradients, forces, virial and energy sums)
 against the fp64 oracle, to the reference's acceptance limits for mixed
 precision (data/numeric-tolerances.json:3-9, docs/VALIDATION.md:56-60 of the
 reference):
@@ -153,3 +154,29 @@ def test_mixed_device_entry_point_and_reproducible(dp):
         assert de.to_host(np.float64, (1,))[0] == e
         assert df.to_host(np.float64, (n, 3)).tobytes() == f.tobytes()
         assert dv.to_host(np.float64, (9,)).tobytes() == v.tobytes()
+
+
+def test_fused_input_gradient_four_wave_blocks(dp, orc):
+    """A type of 32,768-65,535 rows runs the fused dE/dD -> dE/dT kernels in
+    their 64-row (four-wave) form, which none of the benchmark systems
+    reaches: FCC Cu of 55,296 atoms (24^3 cells) in fp64 against the oracle
+    on the first and last 256 centres (atom energies, edge gradients), and in
+    mixed precision against that fp64 result."""
+    from test_gpu_fullsize import _sample, sample_centres
+    coord, atype, box = dp.systems.fcc(24, 3.615, seed=77)
+    n = len(atype)
+    assert 32768 <= n < 65536
+    mb = dp.model.to_bytes(dp.model.random_model("cu", seed=1077))
+    pot = dp.DeepPot(file_content=mb)
+    pot.keep_stages(True)
+    e, f, v, ae, av = pot.compute(coord, atype, box, atomic=True)
+    O = orc.Oracle(mb)
+    ext, et, mp, nl = O.neighbor_list(coord, atype, box)
+    idx = sample_centres(n, 256)
+    r = _sample(O, ext, et, nl, idx)
+    assert np.abs(ae[idx] - r["atom_energy"]).max() <= 1e-10
+    eg = pot.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))[idx]
+    assert np.abs(eg - r["edge_grad"]).max() <= 1e-11
+    mix = dp.DeepPot(file_content=mb, precision=dp.PREC_MIXED)
+    got = mix.compute(coord, atype, box, atomic=True)
+    _check(n, _volume(box), got, {"energy": e, "force": f, "virial": v, "atom_energy": ae}, "cu55k")
