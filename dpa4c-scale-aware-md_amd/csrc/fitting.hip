@@ -1073,10 +1073,12 @@ static void gemm_at(hipStream_t st, const GemmArgs<T>& a) {
 }
 
 // dD = dZ0 W0^T (row-major [rows][Dn]; W0 row-major [Dn][F0]) through the
-// vendor BLAS: it is a plain GEMM with no epilogue, where rocBLAS' tuned
-// kernels beat this file's (measured on MI355X for rows 131072, Dn 2048, F0
-// 240: 2.03 vs 2.49 ms in fp64). In column-major terms C' = W0'^T A' with
-// C' = dD^T [Dn x rows], W0' [F0 x Dn], A' = dZ0^T [F0 x rows].
+// vendor BLAS, for fitting shapes the fused dE/dD -> dE/dT kernels do not
+// cover (F0 != 240 or axis != 16): a plain GEMM with no epilogue, where
+// rocBLAS' tuned kernels beat this file's (measured on MI355X for rows
+// 131072, Dn 2048, F0 240: 2.03 vs 2.49 ms in fp64). In column-major terms
+// C' = W0'^T A' with C' = dD^T [Dn x rows], W0' [F0 x Dn], A' = dZ0^T
+// [F0 x rows].
 static void blas_gemm_nt(void* handle, hipStream_t st, int rows, int Dn, int F0, const double* dZ,
                          const double* W, double* dD) {
   auto h = static_cast<rocblas_handle>(handle);
