@@ -225,18 +225,20 @@ def test_bitwise_reproducible(dp):
         assert a.tobytes() == b.tobytes()
 
 
-def test_fixed_point_range_guard(dp):
-    """The fp64 force stage sums edge forces in 64-bit fixed point; an edge
-    gradient large enough to wrap those sums (here: the energy head scaled by
-    1e9) is reported as a capacity error instead of giving wrong forces, and
-    the flag does not outlive the evaluation that raised it."""
+@pytest.mark.parametrize("mixed", [False, True])
+def test_fixed_point_range_guard(dp, mixed):
+    """The force stage (both precisions) sums edge forces in 64-bit fixed
+    point; an edge gradient large enough to wrap those sums (here: the energy
+    head scaled by 1e9) is reported as a capacity error instead of giving
+    wrong forces, and the flag does not outlive the evaluation that raised
+    it."""
     (coord, atype, box), m = CASES["water192"]()
     m = dict(m)
     fp = m["fit_params"].copy()
     F2 = int(m["fit"][2])
     fp[:, -(F2 + 1):-1] *= 1e9
     m["fit_params"] = fp
-    pot = dp.DeepPot(file_content=model_bytes(m))
+    pot = dp.DeepPot(file_content=model_bytes(m), precision=dp.PREC_MIXED if mixed else dp.PREC_FP64)
     with pytest.raises(dp.DeepmdException, match="fixed-point"):
         pot.compute(coord, atype, box)
     # two atoms farther apart than rcut: no edges, nothing to overflow
