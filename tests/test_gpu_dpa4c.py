@@ -188,6 +188,12 @@ def test_lammps_path(dp, orc):
                             atomic=True)
     e, f, v, ae, av = got
     _check(ref, (e, f, v, ae[:nloc], av), nloc, _volume(box))
+    # the reverse-list gather sums in a fixed order: a second evaluation
+    # gives the same bits
+    got2 = pot.compute_nlist(ext, et, box, nall - nloc, ilist, numneigh, firstneigh, ago=0,
+                             atomic=True)
+    for a, b in zip(got, got2):
+        assert np.asarray(a).tobytes() == np.asarray(b).tobytes()
 
 
 def _canonical(ref_ext, ref_et, src, dst, dv, nloc, extra=5):

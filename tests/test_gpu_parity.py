@@ -215,9 +215,12 @@ def test_virtual_atoms(dp, orc):
     assert np.all(f[[3, 70, 150]] == 0.0) and np.all(ae[[3, 70, 150]] == 0.0)
 
 
-def test_bitwise_reproducible(dp):
-    (coord, atype, box), m = CASES["cu864"]()
-    pot = dp.DeepPot(file_content=model_bytes(m))
+@pytest.mark.parametrize("case,mixed", [("cu864", False), ("hea1024", True)])
+def test_bitwise_reproducible(dp, case, mixed):
+    """Two evaluations give the same bits (fixed-point force sums, fixed
+    reduction trees; mixed: four type chains on their own streams)."""
+    (coord, atype, box), m = CASES[case]()
+    pot = dp.DeepPot(file_content=model_bytes(m), precision=dp.PREC_MIXED if mixed else dp.PREC_FP64)
     r1 = pot.compute(coord, atype, box, atomic=True)
     r2 = pot.compute(coord, atype, box, atomic=True)
     assert r1[0] == r2[0]
