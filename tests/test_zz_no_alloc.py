@@ -66,13 +66,14 @@ def _check(got, ref, n):
     assert np.abs(av - av0).max() <= V_TOL
 
 
-@pytest.mark.parametrize("case", ["water192", "hea250"])
+@pytest.mark.parametrize("case", ["water192", "hea250", "hea250_mixed"])
 def test_noalloc_matches_device_entry_point_twice(dp, case):
     """Two calls in a row on one handle, the second with a smaller system
     (192 water atoms -> 24 in a small box; 250 HEA atoms of four types ->
-    128), then the first again: each agrees with dp_compute_device. The
-    saved embedding activations (16 (L2P + L3P) doubles per 16-slot tile:
-    295 KB per HEA atom, 221 KB per Cu atom) bound what fits in 128 MiB."""
+    128, in fp64 and in mixed precision), then the first again: each agrees
+    with dp_compute_device. The saved fp64 embedding activations (16 (L2P +
+    L3P) doubles per 16-slot tile: 295 KB per HEA atom, 221 KB per Cu atom)
+    bound what fits in 128 MiB; the mixed path saves none."""
     hip = importlib.import_module("dpamd.hip")
     if case == "water192":
         (coord, atype, box), m = CASES[case]()
@@ -81,14 +82,15 @@ def test_noalloc_matches_device_entry_point_twice(dp, case):
         m = CASES["hea1024"]()[1]
         coord, atype, box = dp.systems.bcc_hea(5, 3.2, seed=35)
         small = dp.systems.bcc_hea(4, 3.2, seed=36)
-    pot = dp.DeepPot(file_content=model_bytes(m))
+    prec = dp.PREC_MIXED if case.endswith("_mixed") else dp.PREC_FP64
+    pot = dp.DeepPot(file_content=model_bytes(m), precision=prec)
     bytes0 = pot.device_bytes()
     big = (coord, atype, box)
     for system in (big, small, big):
         got, ref = _both(hip, pot, system)
         _check(got, ref, len(system[1]))
     # the handle's own buffers were only sized by dp_compute_device
-    pot2 = dp.DeepPot(file_content=model_bytes(m))
+    pot2 = dp.DeepPot(file_content=model_bytes(m), precision=prec)
     n = len(atype)
     dc = hip.DeviceArray(np.ascontiguousarray(coord, np.float64))
     da = hip.DeviceArray(np.ascontiguousarray(atype, np.int32))
