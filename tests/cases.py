@@ -26,8 +26,39 @@ def water_small_box():
     return dp.systems.water(2, 6.21, seed=44), dp.model.random_model("water", seed=1004)
 
 
+def tilted(system, tilt):
+    """The same fractional positions in a triclinic cell whose lattice vectors
+    (rows of h) are a = (L, 0, 0), b = (xy, L, 0), c = (xz, yz, L), with
+    (xy, xz, yz) = tilt * L: LAMMPS' [xx,0,0, xy,yy,0, xz,yz,zz] box."""
+    coord, atype, box = system
+    H0 = box.reshape(3, 3)
+    frac = coord @ np.linalg.inv(H0)
+    H = H0.copy()
+    H[1, 0], H[2, 0], H[2, 1] = np.asarray(tilt, np.float64) * H0[0, 0]
+    return frac @ H, atype, H.reshape(9).copy()
+
+
+def water192_tric():
+    return tilted(dp.systems.build(0), (0.2, -0.15, 0.1)), dp.model.random_model("water", seed=1005)
+
+
+def cu_tric():
+    # 864 atoms with tilts up to a quarter of the edge: the perpendicular
+    # heights shrink, still above 2 rcut
+    return tilted(dp.systems.fcc(6, 3.615, seed=23), (-0.1, 0.2, 0.25)), \
+        dp.model.random_model("cu", seed=1006)
+
+
+def water_small_tric():
+    # 24 atoms in a tilted 6.21 A cell: several images of each atom per
+    # direction, along tilted lattice vectors
+    return tilted(dp.systems.water(2, 6.21, seed=45), (0.3, 0.25, -0.2)), \
+        dp.model.random_model("water", seed=1007)
+
+
 CASES = {"water192": water192, "cu864": cu_small, "hea1024": hea_small,
-         "water24_smallbox": water_small_box}
+         "water24_smallbox": water_small_box, "water192_tric": water192_tric,
+         "cu864_tric": cu_tric, "water24_tric": water_small_tric}
 
 
 def model_bytes(m):

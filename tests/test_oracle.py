@@ -108,6 +108,38 @@ def test_ghosts_cover_every_image_within_rcut(orc, dp):
     assert np.abs(shift - np.rint(shift)).max() < 1e-12
 
 
+def test_ghosts_cover_every_image_triclinic(orc, dp):
+    """Triclinic cell smaller than 2 rcut: every image x_k + n_a a + n_b b +
+    n_c c within rcut of a local atom is present exactly once, and each
+    ghost is its owner shifted by an integer combination of the lattice
+    vectors (rows of h)."""
+    (coord, atype, box), m = CASES["water24_tric"]()
+    O = orc.Oracle(model_bytes(m))
+    rc = O.m["rcut"]
+    H = box.reshape(3, 3)
+    ext, et, mp = O.ghosts(coord, atype, box, rc)
+    nloc = len(atype)
+    assert np.array_equal(mp[:nloc], np.arange(nloc))
+    wrapped = ext[:nloc]
+    shifts = np.stack(np.meshgrid(*[np.arange(-4, 5)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    lat = shifts @ H
+    for i in range(nloc):
+        cnt = 0
+        for k in range(nloc):
+            d2 = np.sum((wrapped[k] + lat - wrapped[i]) ** 2, axis=1)
+            if k == i:
+                d2[np.all(shifts == 0, axis=1)] = np.inf
+            cnt += int((d2 <= rc * rc).sum())
+        d2 = np.sum((ext - ext[i]) ** 2, axis=1)
+        d2[i] = np.inf
+        assert (d2 <= rc * rc).sum() == cnt
+    # the image shifts reach past the searched range only if the brute force
+    # above could have missed images: the largest shift used must be inside it
+    n = (ext - ext[mp]) @ np.linalg.inv(H)
+    assert np.abs(n - np.rint(n)).max() < 1e-9
+    assert np.abs(np.rint(n)).max() < 4
+
+
 def _nlist_of(O, ext, et):
     nloc = 1
     off = np.array([0, len(et) - 1], np.int64)
@@ -162,7 +194,7 @@ def test_nlist_sorted_and_within_cutoff(water, orc):
 
 
 # ---- energy, force, virial -------------------------------------------------
-@pytest.mark.parametrize("case", ["water192", "hea1024"])
+@pytest.mark.parametrize("case", ["water192", "hea1024", "water24_tric"])
 def test_force_is_minus_gradient(orc, case):
     (coord, atype, box), m = CASES[case]()
     O = orc.Oracle(model_bytes(m))
@@ -177,7 +209,7 @@ def test_force_is_minus_gradient(orc, case):
             assert out["force"][a, c] == pytest.approx(fd, abs=2e-7)
 
 
-@pytest.mark.parametrize("case", ["water192", "cu864"])
+@pytest.mark.parametrize("case", ["water192", "cu864", "water24_tric"])
 def test_virial_is_minus_strain_derivative(orc, case):
     (coord, atype, box), m = CASES[case]()
     O = orc.Oracle(model_bytes(m))
