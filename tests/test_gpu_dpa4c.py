@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from _pkg import load_dpa4c_oracle
-from cases import lammps_inputs
+from cases import lammps_inputs, tilted
 
 pytestmark = pytest.mark.gpu
 
@@ -33,6 +33,8 @@ def _systems(dp):
         "hea250": (dp.systems.bcc_hea(5, 3.2, seed=8), "hea"),
         "water192": (dp.systems.build(0), "water"),
         "water24_smallbox": (dp.systems.water(2, 6.21, seed=44), "water"),
+        "cu256_tric": (tilted(dp.systems.fcc(4, 3.615, seed=9), (0.15, -0.2, 0.1)), "cu"),
+        "water24_tric": (tilted(dp.systems.water(2, 6.21, seed=46), (-0.3, 0.2, 0.25)), "water"),
     }
 
 
@@ -63,7 +65,8 @@ def _model(dp, kind, seed):
     return m, mb, C4.Dpa4cOracle(mb)
 
 
-@pytest.mark.parametrize("case", ["cu256", "hea250", "water192", "water24_smallbox"])
+@pytest.mark.parametrize("case", ["cu256", "hea250", "water192", "water24_smallbox",
+                                  "cu256_tric", "water24_tric"])
 def test_standalone_parity(dp, case):
     (coord, atype, box), kind = _systems(dp)[case]
     m, mb, O = _model(dp, kind, 300)

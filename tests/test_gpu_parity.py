@@ -72,7 +72,7 @@ def test_stage_parity(dp, orc, case):
         pot2.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))
 
 
-@pytest.mark.parametrize("case", ["water192", "hea1024"])
+@pytest.mark.parametrize("case", ["water192", "hea1024", "water192_tric"])
 def test_lammps_path(dp, orc, case):
     (coord, atype, box), m = CASES[case]()
     mb = model_bytes(m)
