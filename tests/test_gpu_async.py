@@ -49,6 +49,47 @@ def test_async_steps_match_sync(dp, case):
             assert np.array_equal(got, want)
 
 
+def test_async_steps_with_changing_box(dp, orc):
+    """NPT-shaped queue: every queued step brings its own cell (isotropic
+    scaling, then a tilt), passed by value while earlier steps are still in
+    flight. Each step equals the synchronous evaluation on its own cell bit
+    for bit, and the last one the oracle at the fp64 bars."""
+    hip = importlib.import_module("dpamd.hip")
+    (coord, atype, box), m = CASES["hea1024"]()
+    n = len(atype)
+    mb = model_bytes(m)
+    pot_a = dp.DeepPot(file_content=mb)
+    pot_s = dp.DeepPot(file_content=mb)
+    H0 = box.reshape(3, 3)
+    frac = coord @ np.linalg.inv(H0)
+    steps = 5
+    boxes, coords = [], []
+    for k in range(steps):
+        H = H0 * (1.0 + 0.003 * k)
+        if k >= 3:
+            H[1, 0], H[2, 0], H[2, 1] = 0.02 * k * H0[0, 0], -0.01 * k * H0[0, 0], 0.015 * k * H0[0, 0]
+        boxes.append(H.reshape(9).copy())
+        coords.append(np.ascontiguousarray(frac @ H, np.float64))
+    da = hip.DeviceArray(atype.astype(np.int32))
+    dcs = [hip.DeviceArray(c) for c in coords]
+    outs = [_outputs(hip, n) for _ in range(steps)]
+    hbox = np.zeros(9)
+    for k in range(steps):
+        hbox[:] = boxes[k]  # one host buffer, rewritten before the queue drains
+        pot_a.compute_device_async(dcs[k].ptr, da.ptr, n, hbox, *[b.ptr for b in outs[k]], ago=0)
+    pot_a.sync()
+    for k in range(steps):
+        ref = _outputs(hip, n)
+        pot_s.compute_device(dcs[k].ptr, da.ptr, n, boxes[k], *[b.ptr for b in ref], ago=0)
+        for got, want in zip(_host(outs[k], n), _host(ref, n)):
+            assert np.array_equal(got, want)
+    e, f, v, ae, av = _host(outs[-1], n)
+    r = orc.Oracle(mb).compute(coords[-1], atype, boxes[-1])
+    assert abs(e[0] - r["energy"]) / n <= 1e-10
+    assert np.abs(f - r["force"]).max() <= 1e-8
+    assert np.abs(v - r["virial"]).max() <= 1e-8
+
+
 def test_async_capacity_error_reported_by_sync(dp):
     """A perfect FCC lattice at a = 2.2 A puts ~800 atoms within the Cu
     model's 8 A cutoff, above the 512 candidates a centre can hold: the
