@@ -56,6 +56,7 @@ def lib():
         L.orc_embed.argtypes = [P, C.c_int, C.c_int, C.c_double, P]
         L.orc_eval.argtypes = [P, C.c_int, C.c_int, P, P, P, C.c_int, P, P, P, P, P, P, P, P]
         L.orc_fold.argtypes = [C.c_int, C.c_int, P, P, P, P, P]
+        L.orc_prod_force.argtypes = [C.c_int, C.c_int, C.c_int, P, P, P, P, P, P]
         _LIB = L
     return _LIB
 
@@ -206,6 +207,29 @@ class Oracle:
         if want_internals:
             out.update(descrpt=d, dE_dD=dd, net_deriv=nd)
         return out
+
+    def prod_force(self, nloc, ext, nlist, edge_grad, mapping=None):
+        """ProdForce / ProdVirial of given per-slot edge gradients (the
+        oracle's own assembly, orc_prod_force). Over the extended atoms, or,
+        with `mapping`, folded onto the nloc owners (orc_fold)."""
+        ext = np.ascontiguousarray(ext, np.float64)
+        nlist = np.ascontiguousarray(nlist, np.int32)
+        eg = np.ascontiguousarray(edge_grad, np.float64)
+        nall = len(ext)
+        assert nlist.shape == (nloc, self.nnei) and eg.shape == (nloc, self.nnei, 3)
+        assert nlist.max(initial=-1) < nall
+        f = np.zeros((nall, 3))
+        v = np.zeros(9)
+        av = np.zeros((nall, 9))
+        lib().orc_prod_force(nloc, nall, self.nnei, _p(ext), _p(nlist), _p(eg), _p(f), _p(v), _p(av))
+        if mapping is None:
+            return f, v, av
+        mp = np.ascontiguousarray(mapping, np.int32)
+        assert len(mp) == nall
+        f2 = np.zeros((nloc, 3))
+        av2 = np.zeros((nloc, 9))
+        lib().orc_fold(nloc, nall, _p(mp), _p(f), _p(av), _p(f2), _p(av2))
+        return f2, v, av2
 
     def neighbor_list(self, coord, atype, box):
         """Ghosts + cell-list candidates + sel formatting for a periodic box."""

@@ -405,7 +405,22 @@ int orc_eval(const orc_model* m, int nloc, int nall, const double* ext, const in
     scratch_free(&s);
   }
   (void)nthreads;
-  /* ProdForce / ProdVirial in (centre, slot) order */
+  orc_prod_force(nloc, nall, nnei, ext, nlist, eg, force, virial, atom_virial);
+  if (!edge_grad) free(eg);
+  return 0;
+}
+
+/*
+ * ProdForce / ProdVirial from per-slot edge gradients g = dE/d(x_j - x_i),
+ * summed in (centre, slot) order: F_i += g, F_j -= g, W[3c+d] -= g_c d_d with
+ * d = x_j - x_i, the per-atom share charged to the neighbour j
+ * (edge_force_virial.cu:1-14, :138-146 of the reference). Over the nall
+ * extended atoms; ghost contributions stay in ghost slots (orc_fold moves
+ * them onto owners). Slots with nlist < 0 are skipped.
+ */
+void orc_prod_force(int nloc, int nall, int nnei, const double* ext, const int* nlist,
+                    const double* edge_grad, double* force, double* virial,
+                    double* atom_virial) {
   memset(force, 0, sizeof(double) * 3 * (size_t)nall);
   memset(virial, 0, sizeof(double) * 9);
   if (atom_virial) memset(atom_virial, 0, sizeof(double) * 9 * (size_t)nall);
@@ -413,7 +428,7 @@ int orc_eval(const orc_model* m, int nloc, int nall, const double* ext, const in
     for (int sl = 0; sl < nnei; ++sl) {
       const int j = nlist[(long)i * nnei + sl];
       if (j < 0) continue;
-      const double* g = eg + ((long)i * nnei + sl) * 3;
+      const double* g = edge_grad + ((long)i * nnei + sl) * 3;
       double d[3];
       for (int c = 0; c < 3; ++c) d[c] = ext[3L * j + c] - ext[3L * i + c];
       for (int c = 0; c < 3; ++c) {
@@ -427,8 +442,6 @@ int orc_eval(const orc_model* m, int nloc, int nall, const double* ext, const in
           if (atom_virial) atom_virial[9L * j + 3 * c + dd] += v;
         }
     }
-  if (!edge_grad) free(eg);
-  return 0;
 }
 
 /* Fold ghost-image force / atom virial onto their owners (standalone path). */

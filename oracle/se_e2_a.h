@@ -65,6 +65,9 @@ int orc_eval(const orc_model* m, int nloc, int nall, const double* ext_coord, co
              const int* nlist, int nthreads, double* atom_energy, double* descrpt, double* dE_dD,
              double* net_deriv, double* edge_grad, double* force, double* virial, double* atom_virial);
 
+void orc_prod_force(int nloc, int nall, int nnei, const double* ext_coord, const int* nlist,
+                    const double* edge_grad, double* force, double* virial, double* atom_virial);
+
 void orc_fold(int nloc, int nall, const int* mapping, const double* force_ext,
               const double* atom_virial_ext, double* force, double* atom_virial);
 

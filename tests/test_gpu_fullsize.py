@@ -3,8 +3,11 @@
 Full-size parity: neighbour lists bit-exact against the oracle's cell list,
 full E/F/V against the oracle on the 12,288-atom water box, and on the large
 systems the atom energies and edge gradients of the first and last 512
-centres plus size-independent properties (sum of forces, virial symmetry,
-sum of atom virials). Tolerances as in
+centres against the oracle, every atom's force and atom virial against the
+oracle's own ProdForce / ProdVirial and ghost fold applied to all of the
+GPU's edge gradients (so a mis-routed scatter target, a wrong fold or an
+index overflow fails at full size), plus size-independent properties (sum of
+forces, virial symmetry, sum of atom virials). Tolerances as in
 test_gpu_parity.py (fp64: 1e-10 eV/atom, 1e-8 eV/A, 1e-8 eV)."""
 import hashlib
 import importlib
@@ -160,16 +163,36 @@ def sample_centres(n, K=512):
     return np.concatenate([np.arange(K), np.arange(n - K, n)])
 
 
+def check_assembly(dp, O, pot, ext, nl, mp, f, v, av, label):
+    """Every atom's force, atom virial and the virial of one evaluation
+    against the oracle's ProdForce / ProdVirial (orc_prod_force) and ghost
+    fold (orc_fold) applied to all of the GPU's per-slot edge gradients, and
+    the GPU's mapping against the oracle's. The edge gradients themselves are
+    pinned against the oracle on the sampled centres."""
+    n = len(nl)
+    gmp = pot.stage(dp.STAGE_MAPPING, np.int32, mp.shape)
+    assert np.array_equal(gmp, mp), "ghost mapping differs"
+    eg = pot.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))
+    fr, vr, avr = O.prod_force(n, ext, nl, eg, mapping=mp)
+    df, dv, dav = (float(np.abs(a - b).max()) for a, b in ((f, fr), (v, vr), (av, avr)))
+    print(f"{label}: assembly from edge gradients: max |dF| {df:.2e}, |dW| {dv:.2e}, "
+          f"|d atom_W| {dav:.2e}", flush=True)
+    assert df <= F_TOL and dv <= V_TOL and dav <= V_TOL
+    return eg
+
+
 @pytest.mark.parametrize("cfg", [2, 3, 4])
 def test_full_size_sample_and_invariants(dp, orc, cfg):
     """Atom energies and edge gradients (the backward's output, per slot) of
-    1,024 centres against the oracle, plus the size-independent properties."""
+    1,024 centres against the oracle; every atom's force and atom virial
+    against the oracle's assembly of all edge gradients; the size-independent
+    properties."""
     O, pot, (coord, atype, box), (e, f, v, ae, av), (ext, et, mp, nl) = _full(dp, orc, cfg)
     n = len(atype)
     idx = sample_centres(n)
     ref = _sample(O, ext, et, nl, idx)
     assert np.abs(ae[idx] - ref["atom_energy"]).max() <= E_TOL
-    eg = pot.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))[idx]
+    eg = check_assembly(dp, O, pot, ext, nl, mp, f, v, av, f"config {cfg}")[idx]
     assert np.abs(eg - ref["edge_grad"]).max() <= 1e-11
     assert np.abs(f.sum(0)).max() <= 1e-12 * n
     W = v.reshape(3, 3)

@@ -111,10 +111,14 @@ def test_mixed_lammps_path(dp, orc):
 def test_mixed_full_size_hea128k(dp, orc):
     """Config 3 at its full size (128,000-atom HEA, the configuration the
     mixed mode is specified for): mixed against this library's fp64 result,
-    which the fp64 tests hold to the oracle, to the same limits; and the atom
+    which the fp64 tests hold to the oracle, to the same limits; the atom
     energies and edge gradients of the first and last 512 centres against
-    the fp64 oracle itself (edge gradients to the force limits)."""
-    from test_gpu_fullsize import _sample, sample_centres
+    the fp64 oracle itself (edge gradients to the force limits); and every
+    atom's force and atom virial against the oracle's ProdForce / ProdVirial
+    and fold of all the mixed run's own edge gradients (fp64 in both modes,
+    so to the fp64 bar: the scatter and fold are exact up to fixed-point
+    rounding)."""
+    from test_gpu_fullsize import _sample, check_assembly, sample_centres
     coord, atype, box = dp.systems.build(3)
     mb = dp.model.to_bytes(dp.model.random_model("hea", seed=1003))
     ref64 = dp.DeepPot(file_content=mb).compute(coord, atype, box, atomic=True)
@@ -131,7 +135,8 @@ def test_mixed_full_size_hea128k(dp, orc):
     idx = sample_centres(n)
     r = _sample(O, ext, et, nl, idx)
     dae = float(np.abs(got[3][idx] - r["atom_energy"]).max())
-    deg = pot.stage(dp.STAGE_EDGE_GRAD, np.float64, (n, O.nnei, 3))[idx] - r["edge_grad"]
+    eg = check_assembly(dp, O, pot, ext, nl, mp, got[1], got[2], got[4], "hea128k mixed")
+    deg = eg[idx] - r["edge_grad"]
     print(f"hea128k sample vs oracle: atom energy max {dae:.2e} eV, edge grad rmse "
           f"{np.sqrt((deg ** 2).mean()):.2e} max {np.abs(deg).max():.2e} eV/A", flush=True)
     assert dae <= E_ATOM

@@ -280,6 +280,29 @@ def test_atom_virial_split_and_orientation(dp, orc):
     np.testing.assert_allclose(av.sum(0).reshape(9), out["virial"], rtol=0, atol=1e-12)
 
 
+def test_prod_force_reassembles_eval(orc):
+    """orc_prod_force + orc_fold applied to the oracle's own edge gradients
+    give the forces / virials / atom virials of compute() bit for bit (the
+    GPU full-size tests use this assembly as the per-atom check), and a
+    planted routing mistake (two neighbour indices swapped in one row, or the
+    ghost mapping shifted by one) changes the result far beyond 1e-8."""
+    (coord, atype, box), m = CASES["water192"]()
+    O = orc.Oracle(model_bytes(m))
+    out = O.compute(coord, atype, box)
+    ext, mp, nl, eg = out["ext_coord"], out["mapping"], out["nlist"], out["edge_grad"]
+    n = len(atype)
+    f, v, av = O.prod_force(n, ext, nl, eg, mapping=mp)
+    assert np.array_equal(f, out["force"]) and np.array_equal(v, out["virial"])
+    assert np.array_equal(av, out["atom_virial"])
+    nl2 = nl.copy()
+    nl2[5, [0, 1]] = nl2[5, [1, 0]]
+    assert np.abs(O.prod_force(n, ext, nl2, eg, mapping=mp)[0] - f).max() > 1e-4
+    mp2 = mp.copy()
+    mp2[n:] = (mp2[n:] + 1) % n
+    f2, _, av2 = O.prod_force(n, ext, nl, eg, mapping=mp2)
+    assert np.abs(f2 - f).max() > 1e-4 and np.abs(av2 - av).max() > 1e-4
+
+
 def test_invariances(dp, orc, water):
     O, coord, atype, box = water
     e0 = O.compute(coord, atype, box)
