@@ -90,12 +90,10 @@ struct dp_model {
   void* d_fitf = nullptr;
   long fitf_off[kMaxTypes][3][2];
   FitOffsets fo{};
-  void* blas = nullptr;  // rocBLAS handle for the plain input-gradient GEMM
   // With several centre types the per-type fitting chains run concurrently,
-  // each on a stream of its own (default priority) with its own rocBLAS
-  // handle, forked from and joined back into the evaluation stream.
+  // each on a stream of its own (default priority), forked from and joined
+  // back into the evaluation stream.
   hipStream_t fit_st[kMaxTypes] = {};
-  void* fit_blas[kMaxTypes] = {};
   hipEvent_t fork_ev = nullptr;
   hipEvent_t join_ev[kMaxTypes] = {};
   // workspace
@@ -495,16 +493,12 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
     const int rows = M->type_off[t + 1] - M->type_off[t];
     if (rows <= 0) continue;
     hipStream_t fst = st;
-    void* blas = M->arena_on ? nullptr : M->blas;
     if (fork) {
       if (!M->fit_st[t]) {
         DPAMD_HIP(hipStreamCreateWithFlags(&M->fit_st[t], hipStreamNonBlocking));
         DPAMD_HIP(hipEventCreateWithFlags(&M->join_ev[t], hipEventDisableTiming));
-        M->fit_blas[t] = blas_create();
-        if (!M->fit_blas[t]) throw ApiError{DP_ERR_NO_GPU, "rocblas_create_handle failed"};
       }
       fst = M->fit_st[t];
-      blas = M->fit_blas[t];
       DPAMD_HIP(hipStreamWaitEvent(fst, M->fork_ev, 0));
     }
     const E* P = static_cast<const E*>(M->d_fit) + (size_t)t * m.fit_block;
@@ -554,7 +548,7 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
     }
     launch_fitting(fst, net, rows, d_from_t ? nullptr : D + r0 * Dn,
                    d_from_t ? Tt + r0 * 4 : nullptr, 4L * nb, L3, fb, dD ? dD + r0 * Dn : nullptr,
-                   e_bucket + r0, blas, fused_ddt ? &ddt : nullptr);
+                   e_bucket + r0, fused_ddt ? &ddt : nullptr);
     if (fork) {
       DPAMD_HIP(hipEventRecord(M->join_ev[t], fst));
       DPAMD_HIP(hipStreamWaitEvent(st, M->join_ev[t], 0));
@@ -601,8 +595,8 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
 }
 
 // Reverse list + force / atom-virial gather from stored edge gradients (the
-// mixed-precision se_e2_a path and the DPA4C edge-gradient paths), then the
-// energy / virial reduction. Atom
+// DPA4C edge-gradient paths: the LAMMPS list and the edge-graph entries),
+// then the energy / virial reduction. Atom
 // energies e_vals[0..ne) are in bucket order (items maps a position to its
 // atom) or, with items null, in atom order.
 void gather_and_reduce(dp_model* M, hipStream_t st, int nloc, int ntarget, const int* d_mapping,
@@ -824,7 +818,8 @@ void throw_status(int s) {
   if (s & kStatusFixedRange)
     throw ApiError{DP_ERR_CAPACITY,
                    "an edge's force is outside the fixed-point force accumulators' range "
-                   "(|dE/dd| > 8192 eV/A / max(1, rcut), or not finite)"};
+                   "(|dE/dd| > " + std::to_string((int)kFixTermMax) +
+                       " eV/A / max(1, rcut), or not finite)"};
 }
 
 void check_status(dp_model* M, hipStream_t st) {
@@ -1261,7 +1256,7 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
       // fitting GEMM operands pre-split for the bf16 matrix cores: W0, W1,
       // W2 forward, W1 / W2 transposed, and W0 transposed tile-major for the
       // fused dE/dD -> dE/dT kernel (when it applies; otherwise dE/dD is
-      // rocBLAS sgemm)
+      // the plain fp32 product of the library's GEMM, then the dE/dT pass)
       const FitOffsets fo = fit_offsets(m);
       const int ins[3] = {m.emb[2] * m.axis, m.fit[0], m.fit[1]};
       const bool w0t = ddt_supported(m.fit[0], m.emb[2], m.axis);
@@ -1295,8 +1290,6 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
     M->bytes_peak = M->bytes_now;
     M->fo = fit_offsets(m);
     if (const char* g = std::getenv("DPAMD_GRAPH")) M->graph_on = std::atoi(g) != 0;
-    M->blas = blas_create();
-    if (!M->blas) throw ApiError{DP_ERR_NO_GPU, "rocblas_create_handle failed"};
   });
   if (rc != DP_OK) {
     // keep the handle so the caller can read dp_last_error, unless nothing usable
@@ -1321,9 +1314,7 @@ void dp_destroy(dp_model* M) {
     for (hipEvent_t e : set)
       if (e) (void)hipEventDestroy(e);
   if (M->status_host) (void)hipHostFree(M->status_host);
-  blas_destroy(M->blas);
   for (int t = 0; t < kMaxTypes; ++t) {
-    blas_destroy(M->fit_blas[t]);
     if (M->fit_st[t]) (void)hipStreamDestroy(M->fit_st[t]);
     if (M->join_ev[t]) (void)hipEventDestroy(M->join_ev[t]);
   }
@@ -1397,8 +1388,21 @@ int dp_compute_device_noalloc(dp_model* M, int natoms, const double* d_coord, co
                               void* stream) {
   return guarded(M, [&]() {
     DPAMD_HIP(hipSetDevice(M->device));
+    {
+      // the call synchronises and reads back from the host: it cannot be
+      // recorded into a graph, and trying would invalidate the capture
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      DPAMD_HIP(hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs));
+      if (cs != hipStreamCaptureStatusNone)
+        throw ApiError{DP_ERR_ARG,
+                       "dp_compute_device_noalloc is synchronous and cannot run on a stream "
+                       "under graph capture"};
+    }
     settle_async(M);
     if (!M->arena_base) throw ApiError{DP_ERR_NO_GPU, "no static scratch on this device"};
+    // every handle on the device carves from the same scratch: one call at
+    // a time, from the first carve to the restore
+    std::lock_guard<std::mutex> lock(noalloc_device_mutex(M->device));
     std::vector<Buf> saved;
     saved.reserve(M->bufs.size());
     for (Buf* b : M->bufs) {

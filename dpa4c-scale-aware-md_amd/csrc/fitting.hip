@@ -11,7 +11,6 @@
 // e = h.w_head + b_head + bias_atom_e[type]
 // (deepmd-op/overlays/op/pt/graph_fitting.cu:1-25, :614-719); the reference's
 // fused tile analog is deepmd-op/overlays/op/pt/tiled_fitting.cuh:4-60.
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 
@@ -595,6 +594,45 @@ __global__ __launch_bounds__(kDtWaves * 64) void k_dT(int nb, int L3,
   }
 }
 
+// The same dT for any axis (a power of two <= 64; fitting shapes other than
+// axis 16): one wave per atom, T of its position staged in the wave's LDS
+// rows, lane l owning the columns a = l and l + 64. dD[pos] ([L3][axis]
+// row-major) is read straight from memory: the first term walks a row
+// (consecutive b), the second a column (stride axis) of the atom's block.
+template <class T>
+__global__ __launch_bounds__(kDtWaves * 64) void k_dT_any(int nb, int L3, int axis,
+                                                         const int* __restrict__ items,
+                                                         const T* __restrict__ Tt,
+                                                         const T* __restrict__ dD,
+                                                         T* __restrict__ dT) {
+  __shared__ T Ts[kDtWaves][4 * 128];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pos = blockIdx.x * kDtWaves + w;
+  if (pos >= nb) return;  // wave-uniform; no block barrier below
+  for (int a = lane; a < L3; a += 64)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) Ts[w][m * L3 + a] = Tt[(long)a * 4 * nb + 4L * pos + m];
+  wave_lds_sync();
+  const T* Dp = dD + (long)pos * L3 * axis;
+  T* out = dT + (long)items[pos] * 4 * L3;
+  for (int a = lane; a < L3; a += 64) {
+    T acc[4] = {T(0), T(0), T(0), T(0)};
+    for (int b = 0; b < axis; ++b) {
+      const T d = Dp[(long)a * axis + b];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc[m] += d * Ts[w][m * L3 + b];
+    }
+    if (a < axis)
+      for (int a2 = 0; a2 < L3; ++a2) {
+        const T d = Dp[(long)a2 * axis + a];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc[m] += d * Ts[w][m * L3 + a2];
+      }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) out[m * L3 + a] = acc[m];
+  }
+}
+
 // Input gradient of the first fitting layer fused with the descriptor
 // backward (fp64): for the rows (atoms of one type) of a block,
 //   dD[a][b] = sum_k dZ0[k] W0[16a + b][k]         (FP64 MFMA, in registers)
@@ -1072,49 +1110,17 @@ static void gemm_at(hipStream_t st, const GemmArgs<T>& a) {
   else gemm_nt<T, 1, false, true>(st, a);
 }
 
-// dD = dZ0 W0^T (row-major [rows][Dn]; W0 row-major [Dn][F0]) through the
-// vendor BLAS, for fitting shapes the fused dE/dD -> dE/dT kernels do not
-// cover (F0 != 240 or axis != 16): a plain GEMM with no epilogue, where
-// rocBLAS' tuned kernels beat this file's (measured on MI355X for rows
-// 131072, Dn 2048, F0 240: 2.03 vs 2.49 ms in fp64). In column-major terms
-// C' = W0'^T A' with C' = dD^T [Dn x rows], W0' [F0 x Dn], A' = dZ0^T
-// [F0 x rows].
-static void blas_gemm_nt(void* handle, hipStream_t st, int rows, int Dn, int F0, const double* dZ,
-                         const double* W, double* dD) {
-  auto h = static_cast<rocblas_handle>(handle);
-  const double one = 1.0, zero = 0.0;
-  if (rocblas_set_stream(h, st) != rocblas_status_success ||
-      rocblas_dgemm(h, rocblas_operation_transpose, rocblas_operation_none, Dn, rows, F0, &one, W, F0,
-                    dZ, F0, &zero, dD, Dn) != rocblas_status_success)
-    throw HipError{hipErrorLaunchFailure, "rocblas_dgemm (dE/dD)"};
-}
-static void blas_gemm_nt(void* handle, hipStream_t st, int rows, int Dn, int F0, const float* dZ,
-                         const float* W, float* dD) {
-  auto h = static_cast<rocblas_handle>(handle);
-  const float one = 1.0f, zero = 0.0f;
-  if (rocblas_set_stream(h, st) != rocblas_status_success ||
-      rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, Dn, rows, F0, &one, W, F0,
-                    dZ, F0, &zero, dD, Dn) != rocblas_status_success)
-    throw HipError{hipErrorLaunchFailure, "rocblas_sgemm (dE/dD)"};
-}
-
-void* blas_create() {
-  rocblas_handle h = nullptr;
-  if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
-  return h;
-}
-
-void blas_destroy(void* h) {
-  if (h) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(h));
-}
-
 template <class T>
 void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, const T* Tt,
-                    long ldt, int L3, const FitBufs<T>& b, T* dD, double* e_bucket, void* blas,
+                    long ldt, int L3, const FitBufs<T>& b, T* dD, double* e_bucket,
                     const FitDdt* ddt) {
   using G = GemmArgs<T>;
   if (rows <= 0) return;
   const int Dn = net.L[0].in, F0 = net.L[0].out, F1 = net.L[1].out, F2 = net.L[2].out;
+  // the GEMM kernels address A by 32-bit element offsets within a type
+  if ((long)rows * std::max(Dn, F0) > 0x7fffffffL)
+    throw HipError{hipErrorInvalidValue,
+                   "fitting input of one atom type exceeds 2^31 elements (atoms x descriptor width)"};
   G g{};
   // forward
   g = G{};
@@ -1181,10 +1187,8 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
                    ddt->ws);
     return;
   }
-  if (blas) {
-    blas_gemm_nt(blas, st, rows, Dn, F0, b.dZa, net.L[0].W, dD);
-    return;
-  }
+  // fitting shapes the fused kernels do not cover (F0 != 240 or axis != 16):
+  // the plain product dD = dZ0 W0^T, then launch_dT
   g = G{};
   g.M = rows; g.N = Dn; g.K = F0; g.A = b.dZa; g.lda = F0; g.B = net.L[0].W; g.ldb = F0;
   g.epi = 0; g.C = dD; g.ldc = Dn;
@@ -1287,19 +1291,22 @@ template <class T>
 void launch_dT(hipStream_t st, int nloc, int L3, int axis, const int* items, const T* Tt,
                const T* dD, T* dT) {
   if (nloc <= 0) return;
-  if (axis != 16 || L3 > 128 || L3 % 4 != 0)
-    throw HipError{hipErrorInvalidValue, "dE/dT kernel needs axis 16 and L3 <= 128"};
-  hipLaunchKernelGGL(k_dT<T>, dim3((nloc + kDtWaves - 1) / kDtWaves), dim3(kDtWaves * 64), 0, st,
-                     nloc, L3, items, Tt, dD, dT);
+  if (L3 > 128 || axis < 1 || axis > 64 || axis > L3)
+    throw HipError{hipErrorInvalidValue, "dE/dT kernel needs L3 <= 128 and axis <= min(64, L3)"};
+  const dim3 grid((nloc + kDtWaves - 1) / kDtWaves), block(kDtWaves * 64);
+  if (axis == 16 && L3 % 4 == 0)
+    hipLaunchKernelGGL(k_dT<T>, grid, block, 0, st, nloc, L3, items, Tt, dD, dT);
+  else
+    hipLaunchKernelGGL(k_dT_any<T>, grid, block, 0, st, nloc, L3, axis, items, Tt, dD, dT);
   DPAMD_LAUNCH_CHECK();
 }
 
 template void launch_fitting<double>(hipStream_t, const FitNet<double>&, int, const double*,
                                      const double*, long, int, const FitBufs<double>&, double*,
-                                     double*, void*, const FitDdt*);
+                                     double*, const FitDdt*);
 template void launch_fitting<float>(hipStream_t, const FitNet<float>&, int, const float*,
                                     const float*, long, int, const FitBufs<float>&, float*,
-                                    double*, void*, const FitDdt*);
+                                    double*, const FitDdt*);
 template void launch_dT<double>(hipStream_t, int, int, int, const int*, const double*,
                                 const double*, double*);
 template void launch_dT<float>(hipStream_t, int, int, int, const int*, const float*, const float*,

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 #include "emb_shape.h"
@@ -150,6 +151,8 @@ void launch_edges_fill(hipStream_t, int nloc, int nedge, int nnode, const int* e
 // device with hipGetSymbolAddress.
 size_t noalloc_scratch_bytes();
 void* noalloc_scratch_init(int device);
+// The lock dp_compute_device_noalloc holds for a whole call on `device`.
+std::mutex& noalloc_device_mutex(int device);
 
 // Device-wide exclusive int prefix sums (scan.hip): scan_temp_bytes(n) of
 // temporary device memory
@@ -206,8 +209,8 @@ int fit_splits(int rows, int N, int K, int ncu);
 // Tt is given (axis 16), forms D = T^T T[:, :16] on the fly from the
 // column-major copy of T (element (row, a, m) at Tt[a * ldt + 4 row + m]) and
 // D may be null.
-// blas: a rocBLAS handle (blas_create) for the plain input-gradient GEMM, or
-// null for this library's own GEMM kernel.
+// Without the fused kernel (fitting shapes other than F0 = 240, axis 16) the
+// input gradient dD = dZ0 W0^T is a plain product of this library's GEMM.
 // fp64: the first layer's input gradient fused with the descriptor backward
 // (launch_dDdT); when given, launch_fitting computes dE/dT of its rows
 // instead of dE/dD.
@@ -235,10 +238,8 @@ void launch_dDdT3(hipStream_t, int rows, int K, int L3, const float* dZ, const v
                   int ncu, int nsplit, double* ws);
 template <class T>
 void launch_fitting(hipStream_t, const FitNet<T>&, int rows, const T* D, const T* Tt, long ldt,
-                    int L3, const FitBufs<T>&, T* dD, double* e_bucket, void* blas,
+                    int L3, const FitBufs<T>&, T* dD, double* e_bucket,
                     const FitDdt* ddt = nullptr);
-void* blas_create();
-void blas_destroy(void* handle);
 // Tt column-major in bucket order (element (pos, a, m) at Tt[a * 4 nloc +
 // 4 pos + m]), dT in atom order (items maps bucket position to atom).
 template <class T>

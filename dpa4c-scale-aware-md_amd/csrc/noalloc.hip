@@ -21,9 +21,18 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 std::mutex g_mu;
 void* g_ptr[kMaxDevices] = {};
+// held by dp_compute_device_noalloc for a whole call: every handle on a
+// device carves its buffers from the same scratch
+std::mutex g_dev_mu[kMaxDevices];
 }  // namespace
 
 size_t noalloc_scratch_bytes() { return kScratchBytes; }
+
+std::mutex& noalloc_device_mutex(int device) {
+  if (device < 0 || device >= kMaxDevices)
+    throw HipError{hipErrorInvalidDevice, "no-allocation scratch: device index out of range"};
+  return g_dev_mu[device];
+}
 
 void* noalloc_scratch_init(int device) {
   if (device < 0 || device >= kMaxDevices)

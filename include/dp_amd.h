@@ -198,12 +198,16 @@ int dp_compute_device_async(dp_model* model, int natoms, const double* d_coord,
  * The caller passes inputs and outputs; the handle's own buffers are left as
  * they were. A system whose work buffers exceed the scratch is rejected
  * with DP_ERR_CAPACITY (the outputs are then unspecified; the handle keeps
- * working). Every handle on one GPU shares that GPU's scratch: calls that
- * overlap on one GPU (from several host threads, or queued on different
- * streams) race, and must be serialised by the caller. Returns when the
- * outputs are complete. No counterpart in the reference: for callers that
- * cannot allocate device memory (code under HIP graph capture, serving
- * loops and harnesses that forbid hipMalloc).
+ * working). Every handle on one GPU shares that GPU's scratch: the library
+ * serialises the calls of several host threads on one GPU (a per-device
+ * lock held for the whole call), but work the caller queues on other streams
+ * that reads or writes the scratch's contents is not ordered against it.
+ * The call is synchronous: it reads the atom types back to the host and
+ * returns when the outputs are complete, so it cannot be recorded into a
+ * HIP graph; on a stream that is being captured it returns DP_ERR_ARG
+ * without touching the stream. No counterpart in the reference: for
+ * callers that cannot allocate device memory (serving loops and harnesses
+ * that forbid hipMalloc).
  */
 #define DP_NOALLOC_SCRATCH_BYTES (128u << 20)
 int dp_compute_device_noalloc(dp_model* model, int natoms, const double* d_coord,

@@ -61,6 +61,29 @@ CASES = {"water192": water192, "cu864": cu_small, "hea1024": hea_small,
          "cu864_tric": cu_tric, "water24_tric": water_small_tric}
 
 
+# Fitting shapes the fused dE/dD -> dE/dT kernels do not cover: (system, model
+# overrides)
+FALLBACK_SHAPES = {
+    # F0 != 240 with axis 16: D formed inside the first GEMM, dE/dD as a
+    # plain product of the library's GEMM, then the axis-16 dE/dT kernel
+    "water_f160": ("water192", dict(fit=[160, 160, 160])),
+    # axis != 16: D stored by the descriptor kernel, the first layer reads it,
+    # dE/dD plain, then the any-axis dE/dT kernel
+    "water_axis8_f192": ("water192", dict(axis=8, fit=[192, 192, 192])),
+    "cu_axis4_f160": ("cu864", dict(axis=4, fit=[160, 160, 160])),
+    # F0 = 240 but axis 32 (no fused kernel), four centre types
+    "hea_axis32": ("hea1024", dict(axis=32)),
+}
+_KIND_OF = {"water192": "water", "cu864": "cu", "hea1024": "hea"}
+
+
+def fallback_case(name):
+    system, over = FALLBACK_SHAPES[name]
+    (coord, atype, box), _ = CASES[system]()
+    m = dp.model.random_model(_KIND_OF[system], seed=1020, **over)
+    return (coord, atype, box), m
+
+
 def model_bytes(m):
     return dp.model.to_bytes(m)
 

@@ -7,7 +7,7 @@ bit-exact; energy per atom <= 1e-10 eV; forces <= 1e-8 eV/A; virial <= 1e-8 eV
 import numpy as np
 import pytest
 
-from cases import CASES, lammps_inputs, model_bytes
+from cases import CASES, FALLBACK_SHAPES, fallback_case, lammps_inputs, model_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -262,6 +262,32 @@ def test_fitting_shapes(dp, orc, fit):
     ref = orc.Oracle(mb).compute(coord, atype, box)
     e, f, v, ae, av = dp.DeepPot(file_content=mb).compute(coord, atype, box, atomic=True)
     n = len(atype)
+    assert abs(e - ref["energy"]) / n <= E_TOL
+    assert np.abs(ae - ref["atom_energy"]).max() <= E_TOL
+    assert np.abs(f - ref["force"]).max() <= F_TOL
+    assert np.abs(v - ref["virial"]).max() <= V_TOL
+    assert np.abs(av - ref["atom_virial"]).max() <= V_TOL
+
+
+@pytest.mark.parametrize("name", list(FALLBACK_SHAPES))
+@pytest.mark.parametrize("mixed", [False, True])
+def test_fitting_fallback_shapes(dp, orc, name, mixed):
+    """Fitting shapes the fused dE/dD -> dE/dT kernels do not cover (first
+    fitting layer other than 240 wide, or axis other than 16): every output
+    against the oracle, in fp64 to the fp64 bar and in mixed precision to the
+    reference's mixed-precision limits; the library's own kernels only (no
+    vendor BLAS is linked)."""
+    from test_gpu_mixed import _check as mixed_check, _volume
+    (coord, atype, box), m = fallback_case(name)
+    mb = model_bytes(m)
+    ref = orc.Oracle(mb).compute(coord, atype, box)
+    pot = dp.DeepPot(file_content=mb, precision=dp.PREC_MIXED if mixed else dp.PREC_FP64)
+    got = pot.compute(coord, atype, box, atomic=True)
+    n = len(atype)
+    if mixed:
+        mixed_check(n, _volume(box), got, ref, f"{name} mixed")
+        return
+    e, f, v, ae, av = got
     assert abs(e - ref["energy"]) / n <= E_TOL
     assert np.abs(ae - ref["atom_energy"]).max() <= E_TOL
     assert np.abs(f - ref["force"]).max() <= F_TOL

@@ -29,6 +29,17 @@ def test_library_exports_declared_symbols(dp):
     assert set(syms) == set(dp.EXPORTED)
 
 
+def test_library_links_no_vendor_blas(dp):
+    """Every product on the path is this library's own kernel: the shared
+    library needs no BLAS / GEMM library (rocBLAS, hipBLAS, hipBLASLt)."""
+    import subprocess
+    lib_path = dp.lib()._name
+    out = subprocess.run(["readelf", "-d", lib_path], capture_output=True, text=True, check=True).stdout
+    needed = [ln for ln in out.splitlines() if "(NEEDED)" in ln]
+    assert needed, out
+    assert not [ln for ln in needed if "blas" in ln.lower()], needed
+
+
 def test_bad_model_is_reported(dp):
     L = dp.lib()
     h = ctypes.c_void_p()

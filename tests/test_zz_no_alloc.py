@@ -12,7 +12,7 @@ import importlib
 import numpy as np
 import pytest
 
-from cases import CASES, model_bytes
+from cases import CASES, fallback_case, model_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -66,31 +66,43 @@ def _check(got, ref, n):
     assert np.abs(av - av0).max() <= V_TOL
 
 
-@pytest.mark.parametrize("case", ["water192", "hea250", "hea250_mixed"])
+@pytest.mark.parametrize("case", ["water192", "hea250", "hea250_mixed", "water_axis8",
+                                  "water_axis8_mixed", "dpa4c_hea250"])
 def test_noalloc_matches_device_entry_point_twice(dp, case):
     """Two calls in a row on one handle, the second with a smaller system
     (192 water atoms -> 24 in a small box; 250 HEA atoms of four types ->
-    128, in fp64 and in mixed precision), then the first again: each agrees
-    with dp_compute_device. The saved fp64 embedding activations (16 (L2P +
+    128, in fp64 and in mixed precision; the water model with a fitting shape
+    outside the fused kernels; a DPA4C-Nano model on the HEA pair), then the
+    first again: each agrees with dp_compute_device. The saved fp64 embedding activations (16 (L2P +
     L3P) doubles per 16-slot tile: 295 KB per HEA atom, 221 KB per Cu atom)
     bound what fits in 128 MiB; the mixed path saves none."""
     hip = importlib.import_module("dpamd.hip")
     if case == "water192":
         (coord, atype, box), m = CASES[case]()
         small = CASES["water24_smallbox"]()[0]
+    elif case.startswith("water_axis8"):
+        # a fitting shape without the fused input-gradient kernels (axis 8,
+        # first layer 192 wide): stored D, the plain dE/dD GEMM, any-axis dE/dT
+        (coord, atype, box), m = fallback_case("water_axis8_f192")
+        small = CASES["water24_smallbox"]()[0]
+    elif case == "dpa4c_hea250":
+        m = None
+        coord, atype, box = dp.systems.bcc_hea(5, 3.2, seed=8)
+        small = dp.systems.bcc_hea(4, 3.2, seed=36)
     else:
         m = CASES["hea1024"]()[1]
         coord, atype, box = dp.systems.bcc_hea(5, 3.2, seed=35)
         small = dp.systems.bcc_hea(4, 3.2, seed=36)
     prec = dp.PREC_MIXED if case.endswith("_mixed") else dp.PREC_FP64
-    pot = dp.DeepPot(file_content=model_bytes(m), precision=prec)
+    mb = dp.dpa4c.to_bytes(dp.dpa4c.random_model("hea", seed=307)) if m is None else model_bytes(m)
+    pot = dp.DeepPot(file_content=mb, precision=prec)
     bytes0 = pot.device_bytes()
     big = (coord, atype, box)
     for system in (big, small, big):
         got, ref = _both(hip, pot, system)
         _check(got, ref, len(system[1]))
     # the handle's own buffers were only sized by dp_compute_device
-    pot2 = dp.DeepPot(file_content=model_bytes(m), precision=prec)
+    pot2 = dp.DeepPot(file_content=mb, precision=prec)
     n = len(atype)
     dc = hip.DeviceArray(np.ascontiguousarray(coord, np.float64))
     da = hip.DeviceArray(np.ascontiguousarray(atype, np.int32))
@@ -140,3 +152,39 @@ def test_noalloc_rejects_system_beyond_scratch(dp):
         pot.compute_device_noalloc(dc.ptr, da.ptr, nb, bb, *[x.ptr for x in out])
     got, ref = _both(hip, pot, (coord, atype, box))
     _check(got, ref, len(atype))
+
+
+def test_noalloc_refuses_a_capturing_stream(dp):
+    """The call reads the atom types back and synchronises, so on a stream
+    under graph capture it returns an argument error before touching the
+    stream; the capture then ends cleanly (an empty graph) and the handle
+    keeps working."""
+    hip = importlib.import_module("dpamd.hip")
+    h = hip.hip()
+    P = C.c_void_p
+    h.hipStreamCreate.argtypes = [C.POINTER(P)]
+    h.hipStreamDestroy.argtypes = [P]
+    h.hipStreamBeginCapture.argtypes = [P, C.c_int]
+    h.hipStreamEndCapture.argtypes = [P, C.POINTER(P)]
+    h.hipGraphDestroy.argtypes = [P]
+    (coord, atype, box), m = CASES["water192"]()
+    pot = dp.DeepPot(file_content=model_bytes(m))
+    n = len(atype)
+    dc = hip.DeviceArray(np.ascontiguousarray(coord, np.float64))
+    da = hip.DeviceArray(np.ascontiguousarray(atype, np.int32))
+    out = _outputs(hip, n)
+    st = P()
+    hip.check(h.hipStreamCreate(C.byref(st)))
+    try:
+        hip.check(h.hipStreamBeginCapture(st, 2))  # hipStreamCaptureModeRelaxed
+        with pytest.raises(dp.DeepmdException, match="graph capture"):
+            pot.compute_device_noalloc(dc.ptr, da.ptr, n, box, *[b.ptr for b in out],
+                                       stream=st.value)
+        g = P()
+        hip.check(h.hipStreamEndCapture(st, C.byref(g)))
+        if g.value:
+            hip.check(h.hipGraphDestroy(g))
+    finally:
+        hip.check(h.hipStreamDestroy(st))
+    got, ref = _both(hip, pot, (coord, atype, box))
+    _check(got, ref, n)
