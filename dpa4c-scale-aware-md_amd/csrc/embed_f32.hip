@@ -296,7 +296,8 @@ k_embed_fwd32(EmbArgs a) {
   }
 }
 
-template <class S, int WAVES>
+// AV: atom virials asked for (a.vacc non-null), see edge_out
+template <class S, int WAVES, bool AV>
 __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
   static_assert(S::L1 > 2, "layer-1 residual not supported");
   static_assert(S::K3P == S::L2P, "fp32 layout expected");
@@ -526,7 +527,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
         up[m] = add_xor32(add_xor16(up[m]));
         vp[m] = add_xor32(add_xor16(vp[m]));
       }
-      if (valid && g == 0) {
+      // the slot's outputs: lane group 0 alone, or all four groups when atom
+      // virials are asked for (edge_out shares the atomics out)
+      if (valid && (AV || g == 0)) {
         double nd[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) nd[m] = (double)up[m] * a.inv_nnei;
@@ -538,7 +541,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd32(EmbArgs a) {
         double gv[3];
         env_grad(d0, d1, d2, a.rcut_smth, a.rcut, a.inv_sw, sd, nd, gv);
         const double dv[3] = {d0, d1, d2};
-        edge_out(a, ebase + slot, jslot, dv, gv, own_w + 12 * c);
+        edge_out<AV>(a, ebase + slot, jslot, dv, gv, own_w + 12 * c, g);
       }
     }
     own_flush(a, i, tj, nr, ebase, own_w, lane);
@@ -566,7 +569,7 @@ void fwd32_impl(hipStream_t st, const EmbArgs& a, int nblocks) {
 template <class S>
 void bwd32_impl(hipStream_t st, const EmbArgs& a, int nblocks) {
   const size_t bytes = sizeof(float) * bwd_lds_floats<S>(kBwdWaves32);
-  auto kern = k_embed_bwd32<S, kBwdWaves32>;
+  auto kern = a.vacc ? k_embed_bwd32<S, kBwdWaves32, true> : k_embed_bwd32<S, kBwdWaves32, false>;
   DPAMD_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)bytes));
   hipLaunchKernelGGL(kern, dim3(nblocks), dim3(kBwdWaves32 * 64), bytes, st, a);

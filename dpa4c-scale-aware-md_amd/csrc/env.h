@@ -91,44 +91,61 @@ __device__ __forceinline__ void env_grad(double d0, double d1, double d2, double
   }
 }
 
-// Output of one slot of the embedding backward, from the lane that holds the
-// slot's edge gradient g = dE/d(x_j - x_i), d = x_j - x_i, neighbour j
-// (extended-atom index). The centre side (force += g, frame virial -= g (x) d)
-// goes into the lane's private LDS cells own[12], added in tile order; the
-// neighbour side (force -= g, atom virial -= g (x) d, charged to the
-// neighbour as in deepmd-op/overlays/op/pt/edge_force_virial.cu:138-146) is
-// scattered in fixed point onto slot j. g itself is stored only when the
-// caller keeps edge gradients.
+// One slot's outputs. The centre side (force += g, frame virial -= g (x) d)
+// goes into the slot lane's LDS cells own[12], each cell added in tile order
+// by one lane; the neighbour side (force -= g and, when asked for, the atom
+// virial -= g (x) d, charged to the neighbour as in
+// deepmd-op/overlays/op/pt/edge_force_virial.cu:138-146) is scattered in
+// fixed point onto atom j. g = dE/d(x_j - x_i), d = x_j - x_i.
+//   AV false (no atom virials): lane group 0 of the slot's column alone
+//     (three atomics per slot).
+//   AV true: all four lane groups grp (each holds the slot's g, d and j),
+//     three of the twelve values each: group 0 the force, group 1 + c row c
+//     of the virial, so that a wave instruction carries the atomics of 64
+//     lanes instead of 16 (Cu-131k with atom virials: 29.2 -> 28.2 ms per
+//     step). The kernels are instantiated for both: forming the edge
+//     gradient on all 64 lanes, or the branch for both forms in one kernel,
+//     cost the water backward 2-4 % without atom virials.
+// g itself is stored (group 0) only when the caller keeps edge gradients.
+template <bool AV>
 __device__ __forceinline__ void edge_out(const EmbArgs& a, long e, int t, const double d[3],
-                                         const double gv[3], double* own) {
+                                         const double gv[3], double* own, int grp) {
+  if (grp == 0) {
 #pragma unroll
-  for (int c = 0; c < 3; ++c) {
-    __hip_atomic_fetch_add(own + c, gv[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    for (int c = 0; c < 3; ++c) {
+      __hip_atomic_fetch_add(own + c, gv[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+      if constexpr (!AV) {
 #pragma unroll
-    for (int q = 0; q < 3; ++q)
-      __hip_atomic_fetch_add(own + 3 + 3 * c + q, -gv[c] * d[q], __ATOMIC_RELAXED,
+        for (int q = 0; q < 3; ++q)
+          __hip_atomic_fetch_add(own + 3 + 3 * c + q, -gv[c] * d[q], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WAVEFRONT);
+      }
+    }
+    // range guard of the fixed point: a NaN or an out-of-range gradient
+    // would wrap silently in the integer sums
+    const double gm = fmax(fabs(gv[0]), fmax(fabs(gv[1]), fabs(gv[2])));
+    if (!(gm <= a.fix_gmax)) atomicOr(a.status, kStatusFixedRange);
+    unsigned long long* fa = a.facc + 3L * t;
+    fixed_add(fa, gv[0]);
+    fixed_add(fa + 1, gv[1]);
+    fixed_add(fa + 2, gv[2]);
+    if (a.edge_grad) {
+      double* eg = a.edge_grad + e * 3;
+      eg[0] = gv[0];
+      eg[1] = gv[1];
+      eg[2] = gv[2];
+    }
+  } else if constexpr (AV) {
+    const int c = grp - 1;
+    const double gc = grp == 1 ? gv[0] : grp == 2 ? gv[1] : gv[2];
+    unsigned long long* va = a.vacc + 9L * t + 3 * c;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const double v = -gc * d[q];
+      __hip_atomic_fetch_add(own + 3 + 3 * c + q, v, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_WAVEFRONT);
-  }
-  // range guard of the fixed point: a NaN or an out-of-range gradient would
-  // wrap silently in the integer sums
-  const double gm = fmax(fabs(gv[0]), fmax(fabs(gv[1]), fabs(gv[2])));
-  if (!(gm <= a.fix_gmax)) atomicOr(a.status, kStatusFixedRange);
-  unsigned long long* fa = a.facc + 3L * t;
-  fixed_add(fa, gv[0]);
-  fixed_add(fa + 1, gv[1]);
-  fixed_add(fa + 2, gv[2]);
-  if (a.vacc) {
-    unsigned long long* va = a.vacc + 9L * t;
-#pragma unroll
-    for (int c = 0; c < 3; ++c)
-#pragma unroll
-      for (int q = 0; q < 3; ++q) fixed_add(va + 3 * c + q, -gv[c] * d[q]);
-  }
-  if (a.edge_grad) {
-    double* eg = a.edge_grad + e * 3;
-    eg[0] = gv[0];
-    eg[1] = gv[1];
-    eg[2] = gv[2];
+      fixed_add(va + q, v);
+    }
   }
 }
 
