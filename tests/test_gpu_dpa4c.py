@@ -94,6 +94,23 @@ def test_standalone_parity(dp, case):
         assert np.array_equal(np.asarray(a), np.asarray(b))
 
 
+@pytest.mark.parametrize("case", ["cu256", "hea250", "water24_smallbox"])
+def test_forces_with_and_without_atom_virials(dp, case):
+    """The standalone force pass scatters each edge's neighbour side in fixed
+    point, with or without the atom virials: the forces, energy and virial of
+    the two forms agree bit for bit, match the oracle at the reference's
+    limits, and the forces of a periodic system sum to zero."""
+    (coord, atype, box), kind = _systems(dp)[case]
+    m, mb, O = _model(dp, kind, 300)
+    pot = dp.DeepPot(file_content=mb)
+    e, f, v = pot.compute(coord, atype, box)
+    e2, f2, v2, ae, av = pot.compute(coord, atype, box, atomic=True)
+    assert e == e2 and np.array_equal(f, f2) and np.array_equal(v, v2)
+    n = len(atype)
+    _check(O.compute(coord, atype, box), (e, f, v, ae, av), n, _volume(box))
+    assert np.abs(f.sum(0)).max() <= 1e-9 * max(1.0, np.abs(f).max())
+
+
 @pytest.mark.parametrize("case", ["cu256", "hea250"])
 def test_moments_and_cotangents(dp, case):
     """Stage parity: the 44 raw sums per atom and their cotangents dE/d(sums)
