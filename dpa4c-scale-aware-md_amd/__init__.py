@@ -27,7 +27,7 @@ MAX_TYPES = 8
 STAGE_NLIST, STAGE_EXT_COORD, STAGE_MAPPING, STAGE_DESCRPT = 0, 1, 2, 3
 STAGE_ATOM_ENERGY, STAGE_EDGE_GRAD, STAGE_DEDD, STAGE_EXT_TYPE = 4, 5, 6, 7
 STAGE_C4_MOMENTS, STAGE_C4_COTANGENTS = 8, 9
-PREC_FP64, PREC_MIXED = 0, 1
+PREC_FP64, PREC_MIXED, PREC_MODEL = 0, 1, -1
 MODEL_SE_E2_A, MODEL_DPA4C = 0, 1
 
 EXPORTED = ("dp_create", "dp_destroy", "dp_get_info", "dp_last_error", "dp_compute",
@@ -95,12 +95,12 @@ class DeepPot:
     the family is read from the model file."""
 
     def __init__(self, model_path: str | None = None, gpu_rank: int = 0,
-                 file_content: bytes | None = None, precision: int = PREC_FP64):
+                 file_content: bytes | None = None, precision: int = PREC_MODEL):
         self._h = None
         if model_path is not None or file_content is not None:
             self.init(model_path, gpu_rank, file_content, precision)
 
-    def init(self, model_path, gpu_rank=0, file_content=None, precision=PREC_FP64):
+    def init(self, model_path, gpu_rank=0, file_content=None, precision=PREC_MODEL):
         L = lib()
         h = C.c_void_p()
         buf = file_content if file_content else None

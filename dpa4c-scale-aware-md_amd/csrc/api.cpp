@@ -1192,9 +1192,8 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
   *out = nullptr;
   dp_model* M = new dp_model();
   int rc = guarded(M, [&]() {
-    if (precision != DP_PREC_FP64 && precision != DP_PREC_MIXED)
-      throw ApiError{DP_ERR_ARG, "precision must be DP_PREC_FP64 or DP_PREC_MIXED"};
-    M->precision = precision;
+    if (precision != DP_PREC_FP64 && precision != DP_PREC_MIXED && precision != DP_PREC_MODEL)
+      throw ApiError{DP_ERR_ARG, "precision must be DP_PREC_MODEL, DP_PREC_FP64 or DP_PREC_MIXED"};
     std::vector<unsigned char> buf;
     if (file_content && content_len) {
       const auto* b = static_cast<const unsigned char*>(file_content);
@@ -1210,6 +1209,8 @@ int dp_create(const char* path, int gpu_rank, const void* file_content, size_t c
     const std::string perr = c4 ? parse_c4_model(buf.data(), buf.size(), M->host, M->c4)
                                 : parse_model(buf.data(), buf.size(), M->host);
     if (!perr.empty()) throw ApiError{DP_ERR_MODEL, perr};
+    if (precision == DP_PREC_MODEL) precision = M->host.precision;
+    M->precision = precision;
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
       throw ApiError{DP_ERR_NO_GPU, "no HIP device visible"};

@@ -67,7 +67,11 @@ std::string parse_model(const unsigned char* buf, size_t len, ModelHost& m) {
   for (int k = 0; k < 3; ++k) m.emb[k] = (int)r.get<uint32_t>();
   m.axis = (int)r.get<uint32_t>();
   for (int k = 0; k < 3; ++k) m.fit[k] = (int)r.get<uint32_t>();
-  (void)r.get<uint32_t>();
+  // precision the model was written for: 0 fp64 (also every file written
+  // while this word was reserved), 1 mixed
+  const uint32_t prec = r.get<uint32_t>();
+  if (prec > 1) return "model precision field must be 0 (fp64) or 1 (mixed)";
+  m.precision = (int)prec;
   m.type_map.clear();
   for (int t = 0; t < m.ntypes; ++t) {
     char name[17] = {0};

@@ -17,6 +17,7 @@ struct ModelHost {
   int emb[3] = {0, 0, 0};
   int axis = 0;
   int fit[3] = {0, 0, 0};
+  int precision = 0;  // the file's DP_PREC_FP64 / DP_PREC_MIXED
   std::vector<std::string> type_map;
   std::vector<double> davg, dstd;  // [nt][nt][4]
   std::vector<double> emb_params;  // [nt*nt][emb_block]

@@ -10,7 +10,9 @@ File layout (little endian), read by the C++ loader in csrc/model.cpp:
     u32[3]   embedding widths L1, L2, L3
     u32      axis (M2)
     u32[3]   fitting widths F0, F1, F2
-    u32      reserved (0)
+    u32      precision the model is evaluated in: 0 fp64, 1 mixed (fp32
+             nets, fp64 env matrix, forces, virials); files written while
+             this word was reserved read as fp64
     char[nt][16] type_map, NUL padded
     f64[nt][nt][4] davg     (per centre type, per neighbour section)
     f64[nt][nt][4] dstd
@@ -110,7 +112,8 @@ def to_bytes(m: dict) -> bytes:
     nt = len(m["type_map"])
     out = [MAGIC, struct.pack("<II", 1, nt), struct.pack(f"<{nt}I", *m["sel"]),
            struct.pack("<dd", m["rcut"], m["rcut_smth"]), struct.pack("<3I", *m["emb"]),
-           struct.pack("<I", m["axis"]), struct.pack("<3I", *m["fit"]), struct.pack("<I", 0)]
+           struct.pack("<I", m["axis"]), struct.pack("<3I", *m["fit"]),
+           struct.pack("<I", 1 if m.get("precision", "fp64") == "mixed" else 0)]
     for name in m["type_map"]:
         b = name.encode()[:15]
         out.append(b + b"\0" * (16 - len(b)))
@@ -137,7 +140,7 @@ def from_bytes(buf: bytes) -> dict:
     emb = list(struct.unpack_from("<3I", buf, off)); off += 12
     (axis,) = struct.unpack_from("<I", buf, off); off += 4
     fit = list(struct.unpack_from("<3I", buf, off)); off += 12
-    off += 4
+    (prec,) = struct.unpack_from("<I", buf, off); off += 4
     type_map = []
     for _ in range(nt):
         type_map.append(buf[off:off + 16].split(b"\0")[0].decode()); off += 16
@@ -155,7 +158,7 @@ def from_bytes(buf: bytes) -> dict:
     bias = take(nt, (nt,))
     return dict(type_map=type_map, sel=sel, rcut=rcut, rcut_smth=rcut_smth, emb=emb, axis=axis,
                 fit=fit, davg=davg, dstd=dstd, emb_params=emb_params, fit_params=fit_params,
-                bias_atom_e=bias)
+                bias_atom_e=bias, precision="mixed" if prec == 1 else "fp64")
 
 
 def read_model(path: str) -> dict:

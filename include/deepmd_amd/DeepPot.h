@@ -8,11 +8,10 @@
 //
 // Link with -ldpamd. The interface is double precision; the float overloads
 // convert at the boundary, as the reference's compute<float> does. The
-// evaluation precision is chosen at init: DP_PREC_FP64 (default) or
-// DP_PREC_MIXED (fp32 nets, fp64 env matrix / forces / virial). Upstream the
-// precision is a property of the trained model, so init() keeps the
-// reference's three arguments and reads the choice from the environment
-// variable DPAMD_PRECISION ("fp64" or "mixed") unless it is passed explicitly.
+// evaluation precision is a property of the model, as upstream: init() keeps
+// the reference's three arguments and evaluates in the precision the model
+// file records (DP_PREC_FP64, or DP_PREC_MIXED: fp32 nets, fp64 env matrix /
+// forces / virial); a fourth argument overrides it.
 //
 // Frames: the std::vector<ENERGYTYPE> overloads take nframes configurations
 // back to back (coord nframes x natoms x 3, box nframes x 9 or empty) and
@@ -35,17 +34,10 @@ class DeepPot : public DeepBaseModel {
   }
 
   void init(const std::string& model, const int& gpu_rank = 0,
-            const std::string& file_content = "", int precision = -1) {
+            const std::string& file_content = "", int precision = DP_PREC_MODEL) {
     if (h_) {
       dp_destroy(h_);
       h_ = nullptr;
-    }
-    if (precision < 0) {
-      const char* env = std::getenv("DPAMD_PRECISION");
-      precision = DP_PREC_FP64;
-      if (env && std::strcmp(env, "mixed") == 0) precision = DP_PREC_MIXED;
-      else if (env && *env && std::strcmp(env, "fp64") != 0)
-        throw deepmd_exception(std::string("DPAMD_PRECISION must be fp64 or mixed, got ") + env);
     }
     dp_model* h = nullptr;
     const int rc = dp_create(model.c_str(), gpu_rank,

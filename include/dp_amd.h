@@ -47,7 +47,9 @@ enum {
   DP_ERR_NO_GPU = -5    /* no usable gfx950 device */
 };
 
-enum { DP_PREC_FP64 = 0, DP_PREC_MIXED = 1 };
+/* DP_PREC_MODEL: the precision the model file was written for (se_e2_a files
+ * carry it in their header; DPA4C models are mixed by definition). */
+enum { DP_PREC_FP64 = 0, DP_PREC_MIXED = 1, DP_PREC_MODEL = -1 };
 
 /* Model families: se_e2_a (DPAMDSEA files) and the DPA4C compressed
  * degree-wise descriptor in its Nano profile (DPAMDC4N files). */
@@ -93,7 +95,9 @@ enum {
  * (deepmd-op/overlays/api_cc/include/DeepPot.h:475-477; called at
  * lammps-deepmd-plugin/src/pair_deepmd.cpp:668). If `file_content` is non-NULL
  * the model is read from those `content_len` bytes instead of `path`.
- * `precision` DP_PREC_FP64 evaluates everything in fp64; DP_PREC_MIXED
+ * `precision` DP_PREC_MODEL takes the precision recorded in the model file
+ * (upstream, the evaluation precision is a property of the trained model);
+ * DP_PREC_FP64 evaluates everything in fp64; DP_PREC_MIXED
  * evaluates the embedding nets, the descriptor and the fitting net in fp32
  * (FP32 MFMA) and the env matrix, edge gradients, forces, virials and energy
  * sums in fp64 -- the reference's mixed-precision rule (fp32

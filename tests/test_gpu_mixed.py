@@ -144,6 +144,26 @@ def test_mixed_full_size_hea128k(dp, orc):
     assert np.abs(deg).max() > 0.0
 
 
+def test_precision_from_the_model_file(dp):
+    """A model file written for mixed precision is evaluated in mixed
+    precision by default (as upstream, the precision comes with the model),
+    one written for fp64 in fp64, and an explicit precision overrides the
+    file's; the two evaluations differ (the fp32 nets really ran)."""
+    (coord, atype, box), m = CASES["cu864"]()
+    m64 = dict(m, precision="fp64")
+    mmx = dict(m, precision="mixed")
+    p64 = dp.DeepPot(file_content=model_bytes(m64))
+    pmx = dp.DeepPot(file_content=model_bytes(mmx))
+    pov = dp.DeepPot(file_content=model_bytes(mmx), precision=dp.PREC_FP64)
+    assert p64.info.precision == dp.PREC_FP64 and pov.info.precision == dp.PREC_FP64
+    assert pmx.info.precision == dp.PREC_MIXED
+    e64, f64, _ = p64.compute(coord, atype, box)
+    emx, fmx, _ = pmx.compute(coord, atype, box)
+    eov, fov, _ = pov.compute(coord, atype, box)
+    assert eov == e64 and np.array_equal(fov, f64)
+    assert emx != e64 and abs(emx - e64) / len(atype) <= E_ATOM
+
+
 def test_mixed_device_entry_point_and_reproducible(dp):
     import importlib
     hip = importlib.import_module("dpamd.hip")

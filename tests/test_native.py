@@ -52,6 +52,33 @@ def test_bad_model_is_reported(dp):
         dp.DeepPot(file_content=junk)
 
 
+def test_model_precision_field(dp):
+    """The model file records the precision it is evaluated in (the header
+    word after the fitting widths): the Python writer and reader round-trip
+    it, files written before the word was used read as fp64, and the C
+    loader rejects a value other than 0 or 1 before it looks for a GPU."""
+    import struct
+    m = dp.model.random_model("water", seed=3)
+    assert dp.model.from_bytes(dp.model.to_bytes(m))["precision"] == "fp64"
+    m["precision"] = "mixed"
+    b = dp.model.to_bytes(m)
+    assert dp.model.from_bytes(b)["precision"] == "mixed"
+    nt = len(m["type_map"])
+    off = 8 + 8 + 4 * nt + 16 + 12 + 4 + 12  # magic, version/ntypes, sel, rcut, emb, axis, fit
+    assert struct.unpack_from("<I", b, off)[0] == 1
+    bad = bytearray(b)
+    struct.pack_into("<I", bad, off, 2)
+    L = dp.lib()
+    h = ctypes.c_void_p()
+    rc = L.dp_create(None, 0, bytes(bad), len(bad), -1, ctypes.byref(h))
+    assert rc == -2 and b"precision field" in L.dp_last_error(h)
+    L.dp_destroy(h)
+    h = ctypes.c_void_p()
+    rc = L.dp_create(None, 0, b, len(b), 7, ctypes.byref(h))
+    assert rc == -1 and b"DP_PREC_MODEL" in L.dp_last_error(h)
+    L.dp_destroy(h)
+
+
 def test_unsupported_shape_is_reported(dp):
     m = dp.model.random_model("water", seed=1, emb=[8, 16, 32])
     with pytest.raises(dp.DeepmdException, match="not compiled"):
