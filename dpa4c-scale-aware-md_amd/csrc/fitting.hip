@@ -483,14 +483,16 @@ __global__ __launch_bounds__(256) void k_splitk_tanh(int M, int N, int split,
 }
 
 // K slices for the first fitting layer: split only when the row blocks alone
-// leave the device short of work (fewer than two blocks per compute unit),
-// and keep at least 8 K chunks of 16 per slice.
+// leave the device short of work (fewer than four blocks per compute unit),
+// and keep at least 8 K chunks of 16 per slice (12,288-atom water: fitting
+// 0.717 -> 0.694 ms against a two-block target; an eight-block target with
+// 4-chunk slices was slower, 0.72 ms; the large types never split).
 int fit_splits(int rows, int N, int K, int ncu) {
   const int cols = N % 128 == 0 ? N / 128 : N % 80 == 0 ? N / 80 : N % 64 == 0 ? N / 64 : N / 16;
   const long blocks = (long)cols * ((rows + 63) / 64);
   const int nk = K / 16;
   int split = 1;
-  while (blocks * split < 2L * ncu && nk / (2 * split) >= 8) split *= 2;
+  while (blocks * split < 4L * ncu && nk / (2 * split) >= 8) split *= 2;
   return split;
 }
 
