@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from cases import CASES, model_bytes
-from test_native import build_facade, build_pair_shape, write_input
+from test_native import build_backend_shape, build_facade, build_pair_shape, write_input
 
 pytestmark = pytest.mark.gpu
 
@@ -120,6 +120,33 @@ def test_pair_style_shape_on_gpu(dp, orc, tmp_path):
     vs = np.stack([x["virial"] for x in res]) / n
     assert float.fromhex(out["DEVI_V"][0]) == pytest.approx(
         (np.sqrt(((vs - vs.mean(0)) ** 2).mean(0)) / (np.abs(vs.mean(0)) + 0.1)).max(), rel=1e-6)
+
+
+def test_backend_adapter_on_gpu(dp, orc, tmp_path):
+    """Every computew form of the backend adapter, called through the
+    reference's backend interface, against the oracle: standalone in double
+    and float, two frames with per-frame types, and the LAMMPS list."""
+    exe = build_backend_shape(tmp_path)
+    (coord, atype, box), m = CASES["water192"]()
+    mpath = tmp_path / "m.dp"
+    dp.model.write_model(str(mpath), m)
+    write_input(tmp_path / "in.bin", coord, atype, box)
+    r = subprocess.run([str(exe), "run", str(mpath), str(tmp_path / "in.bin")],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    out = {ln.split()[0]: ln.split()[1:] for ln in r.stdout.splitlines()}
+    assert out["META"] == ["O", "H"]
+    n = len(atype)
+    O = orc.Oracle(model_bytes(m))
+    ref = O.compute(coord, atype, box)
+    assert abs(float.fromhex(out["E"][0]) - ref["energy"]) / n <= E_TOL
+    # float coordinates: the configuration rounded to fp32 (energy to 1e-4 eV/atom)
+    assert abs(float.fromhex(out["EF"][0]) - ref["energy"]) / n <= 1e-4
+    e2 = [float.fromhex(x) for x in out["E2"]]
+    assert e2[0] == e2[1] and abs(e2[0] - ref["energy"]) / n <= E_TOL
+    off, cand = O.candidates(n, coord, atype, O.m["rcut"], "brute")
+    ref2 = O.eval_ext(n, coord, atype, O.format_nlist(n, coord, atype, off, cand))
+    assert abs(float.fromhex(out["ENL"][0]) - ref2["energy"]) / n <= E_TOL
 
 
 def _full(dp, orc, cfg):
