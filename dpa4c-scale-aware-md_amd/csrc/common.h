@@ -144,6 +144,23 @@ __device__ __forceinline__ int3 xcd_swizzle() {
   return int3{id % nx, (id / nx) % ny, id / (nx * ny)};
 }
 
+// Chunk walk of a persistent 1-D grid over `nchunks` equal chunks of work in
+// a spatially ordered array: XCD x (the blocks b with b % 8 == x) takes the
+// contiguous x-th eighth of the chunks and its blocks stride over it, so
+// every neighbourhood is gathered through one XCD's L2 instead of all eight
+// (a plain grid stride hands consecutive chunks to consecutive XCDs). Grids
+// that are not a multiple of 8 blocks walk the plain stride.
+struct ChunkWalk {
+  int first, step, end;
+};
+__device__ __forceinline__ ChunkWalk xcd_chunks(int nchunks) {
+  const int nb = gridDim.x, b = blockIdx.x;
+  if (nb % kXcds != 0) return ChunkWalk{b, nb, nchunks};
+  const int x = b % kXcds, q = nchunks / kXcds, r = nchunks % kXcds;
+  const int beg = x * q + (x < r ? x : r);
+  return ChunkWalk{beg + b / kXcds, nb / kXcds, beg + q + (x < r ? 1 : 0)};
+}
+
 // Status word bits raised by kernels and checked by the host after a step.
 enum StatusBit : int {
   kStatusNeighbourOverflow = 1,  // > kMaxCand candidates within rcut of a centre

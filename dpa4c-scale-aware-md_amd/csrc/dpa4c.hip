@@ -253,7 +253,8 @@ struct GraphSrc {
 
 // ---- pass 1: moments --------------------------------------------------------
 // Persistent blocks (grid of a few blocks per CU, the tables staged once):
-// block b serves nodes b*gpb + g, then strides by the grid.
+// the nodes go in chunks of gpb (one node per group of kG lanes), walked
+// XCD by XCD (xcd_chunks) so that neighbouring nodes share one L2.
 template <class Src, bool Lds>
 __global__ __launch_bounds__(kEdgeBlock) void k_c4_moments(C4Params p, Src src, int nnodes,
                                                           float* __restrict__ mom, int* status) {
@@ -261,7 +262,9 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_moments(C4Params p, Src src, 
   stage_tables<Lds>(p, tab, flm);
   const int lane = threadIdx.x & (kG - 1);
   constexpr int gpb = kEdgeBlock / kG;
-  for (int base = blockIdx.x * gpb; base < nnodes; base += gridDim.x * gpb) {
+  const ChunkWalk cw = xcd_chunks((nnodes + gpb - 1) / gpb);
+  for (int ch = cw.first; ch < cw.end; ch += cw.step) {
+  const int base = ch * gpb;
   const int node = base + (int)threadIdx.x / kG;
   float S[8], V[3][4], T[5][4], ms = 0.f, ma = 0.f;
 #pragma unroll
@@ -796,7 +799,9 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_grad(C4Params p, Src src
   stage_tables<Lds>(p, tab, flm);
   const int lane = threadIdx.x & (kG - 1);
   constexpr int gpb = kEdgeBlock / kG;
-  for (int base = blockIdx.x * gpb; base < nnodes; base += gridDim.x * gpb) {
+  const ChunkWalk cw = xcd_chunks((nnodes + gpb - 1) / gpb);
+  for (int ch = cw.first; ch < cw.end; ch += cw.step) {
+  const int base = ch * gpb;
   const int node = base + (int)threadIdx.x / kG;
   if (node >= nnodes) continue;
   const int ti = src.node_type(node);
@@ -852,7 +857,9 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_force(
   stage_tables<Lds>(p, tab, flm);
   const int lane = threadIdx.x & (kG - 1);
   constexpr int gpb = kEdgeBlock / kG;
-  for (int base = blockIdx.x * gpb; base < nnodes; base += gridDim.x * gpb) {
+  const ChunkWalk cw = xcd_chunks((nnodes + gpb - 1) / gpb);
+  for (int ch = cw.first; ch < cw.end; ch += cw.step) {
+  const int base = ch * gpb;
   const int node = base + (int)threadIdx.x / kG;
   double f[3] = {0.0, 0.0, 0.0}, fo[3] = {0.0, 0.0, 0.0};
   double vo[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
