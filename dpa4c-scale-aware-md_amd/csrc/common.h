@@ -77,6 +77,19 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Wait for every vector memory operation the wave has issued. Loads and
+// stores share the vector memory counter, and with stores issued after a
+// load the compiler's wait before the load's first use is vmcnt(0) or close to
+// it (it does not treat stores as completing in order with loads), so that
+// use also waits for the stores. A kernel that prefetches calls this where
+// its loads have had their latency and no store has been issued since; the
+// wait is visible to the compiler, and the later uses need none.
+__device__ __forceinline__ void vmem_wait_all() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt(7), lgkmcnt(15): no wait
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ __forceinline__ double shfl_xor_d(double v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }

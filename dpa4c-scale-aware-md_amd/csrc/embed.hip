@@ -168,6 +168,34 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     double Tacc[S::NU3 * 4];
 #pragma unroll
     for (int q = 0; q < S::NU3 * 4; ++q) Tacc[q] = 0.0;
+    if (a.Tt) {
+      // single neighbour type (T stored whole at the end): the padded slots'
+      // constant share npad * tpad starts in the accumulators of lane group 0
+      // (the tail's in slot lane 0), which the end-of-item sums then carry,
+      // so the stores of T need no load behind the tile's stores
+      // (every lane loads, at a clamped feature, so that the loads issue
+      // together and are waited for once)
+      const double npad = (double)(a.sel[tj] - nr);
+      const double* tp = a.tpad + (long)p * 4 * S::L3;
+      double tv[S::NU3][4];
+#pragma unroll
+      for (int u = 0; u < S::NU3; ++u) {
+        const int f = min(u < U3 ? 16 * u + c : 16 * U3 + g, S::L3 - 1);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) tv[u][m] = tp[m * S::L3 + f];
+      }
+#pragma unroll
+      for (int u = 0; u < U3; ++u) {
+        const bool own = g == 0 && 16 * u + c < S::L3;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] = own ? npad * tv[u][m] : 0.0;
+      }
+      if constexpr (T3V) {
+        const bool own = c == 0 && 16 * U3 + g < S::L3;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) Tacc[4 * U3 + m] = own ? npad * tv[U3][m] : 0.0;
+      }
+    }
     constexpr int BLK = 16 * (S::L2P + S::L3P);
     double* act = static_cast<double*>(a.act) + ((long)i * a.tiles_per_atom + a.tile_off[tj]) * BLK;
     // the layer-3 tail's activation (slot c, feature 16 U3 + g), where the
@@ -181,9 +209,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
     // (measured: 3 % off this kernel on Cu).
     double* act2 = act + c * 4 + g;
     double* act3 = act + 16 * S::L2P + (c >> 2) * 64 + g * 4 + (c & 3);
-    // Neighbour coordinates of tile k+1 are fetched during tile k, from an index
-    // loaded during tile k-1: the memory counter is in order, so no wait on a
-    // load ever has to cover the activation stores issued after it.
+    // Neighbour coordinates of tile k+1 are fetched at the start of tile k,
+    // from an index loaded one tile earlier, and waited for after tile k's
+    // layer-2 products, before its first activation store (vmem_wait_all):
+    // a wait at their use in tile k+1 would also wait for tile k's stores.
+    // The index loads are unconditional, clamped into the section (sel >= 1),
+    // so the index register is written by loads only (a conditional zero
+    // would be a VALU write behind a pending load, which the compiler covers
+    // with a wait on every outstanding memory operation).
+    const int slast = a.sel[tj] - 1;
     double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
     if (c < nr) {
       const long j = row[c];
@@ -191,7 +225,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       nx1 = a.ext[3 * j + 1];
       nx2 = a.ext[3 * j + 2];
     }
-    int jn = 16 + c < nr ? row[16 + c] : 0;
+    int jn = row[min(16 + c, slast)];
+    vmem_wait_all();  // so that no use in the tile loop waits (see above)
     for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK, act3t += BLK) {
       const int slot = tile + c;
       double Rn[4] = {0.0, 0.0, 0.0, 0.0};
@@ -201,7 +236,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
         nx1 = a.ext[3 * (long)jn + 1];
         nx2 = a.ext[3 * (long)jn + 2];
       }
-      jn = slot + 32 < nr ? row[slot + 32] : 0;
+      jn = row[min(slot + 32, slast)];
       if (g == 0) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) Rs[c * 4 + m] = Rn[m];
@@ -255,6 +290,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
         for (int j = 0; j < TL; ++j) pj[j] = add_xor32(add_xor16(pj[j]));
         const int f = 16 * NT2M + g;
         const double th = tanh_tab1(pick(pj, g) + P[S::OFF_B2 + f], Tab);
+        // the next tile's coordinates and index have landed (see the loop
+        // head); this tile's stores start here
+        vmem_wait_all();
         __builtin_nontemporal_store(th, &act2[(4 * NT2M) * 64]);
         double res = 0.0;
         if constexpr (S::RES2 != 0) {
@@ -267,6 +305,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
         }
         x2[NT2M][0] = (f < S::L2) ? res + th : 0.0;
         x2[NT2M][1] = x2[NT2M][2] = x2[NT2M][3] = 0.0;
+      } else {
+        vmem_wait_all();  // as above, before this tile's first store
       }
 #pragma unroll
       for (int t = 0; t < NT2M; ++t) {
@@ -393,12 +433,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       if (c == 0 && g < TL) {
         const int f = 16 * U3 + g;
         if (a.Tt) {
-          const double npad = (double)(a.sel[tj] - nr);
-          const double* tp = a.tpad + (long)p * 4 * S::L3;
           double* Tt = static_cast<double*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
 #pragma unroll
-          for (int m = 0; m < 4; ++m)
-            Tt[f * a.ldt + m] = (double)((Tacc[4 * U3 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
+          for (int m = 0; m < 4; ++m) Tt[f * a.ldt + m] = Tacc[4 * U3 + m] * a.inv_nnei;
         } else {
           double* out = static_cast<double*>(a.Tsec) + ((long)i * a.ntypes + tj) * 4 * S::L3;
 #pragma unroll
@@ -407,18 +444,14 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       }
     }
     if (g == 0 && a.Tt) {
-      // single neighbour type: this section is all of T
-      const double npad = (double)(a.sel[tj] - nr);
-      const double* tp = a.tpad + (long)p * 4 * S::L3;
+      // single neighbour type: this section (padding share included) is all of T
       double* Tt = static_cast<double*>(a.Tt) + 4 * (long)(a.type_off[ti] + item);
 #pragma unroll
       for (int u = 0; u < U3; ++u) {
         const int f = 16 * u + c;
         if (f < S::L3) {
 #pragma unroll
-          for (int m = 0; m < 4; ++m)
-            Tt[f * a.ldt + m] =
-                (double)(((double)Tacc[u * 4 + m] + npad * tp[m * S::L3 + f]) * a.inv_nnei);
+          for (int m = 0; m < 4; ++m) Tt[f * a.ldt + m] = Tacc[u * 4 + m] * a.inv_nnei;
         }
       }
     } else if (g == 0) {
@@ -524,15 +557,23 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
     // tile ahead would need the registers of that second wave.
     // The neighbour index of each slot is parked in LDS (jbuf, by tile
     // parity) when its coordinates are fetched, for the slot's output.
+    // (index loads unconditional and clamped into the section, as in the
+    // forward; jbuf entries of padded slots are never read)
+    const int slast = a.sel[tj] - 1;
     double nx0 = 0.0, nx1 = 0.0, nx2 = 0.0;
-    int jn = c < nr ? row[c] : 0;
+    int jn = row[min(c, slast)];
     if (c < nr) {
       nx0 = a.ext[3 * (long)jn];
       nx1 = a.ext[3 * (long)jn + 1];
       nx2 = a.ext[3 * (long)jn + 2];
     }
     if (g == 0) jbuf[c] = jn;
-    jn = 16 + c < nr ? row[16 + c] : 0;
+    jn = row[min(16 + c, slast)];
+    // The coordinates and index loaded for the next tile are waited for
+    // before the tile's own output atomics (vmem_wait_all), here for the
+    // first tile: a wait at their use would also cover the atomics issued
+    // after them.
+    vmem_wait_all();
 
     for (int tile = 0; tile < nr; tile += 16, act2 += BLK, act3 += BLK) {
       const int par = (tile >> 4) & 1;
@@ -564,7 +605,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         nx2 = a.ext[3 * (long)jn + 2];
         if (g == 0) jbuf[16 * (par ^ 1) + c] = jn;
       }
-      jn = slot + 32 < nr ? row[slot + 32] : 0;
+      jn = row[min(slot + 32, slast)];
       const double s = Rn[0];
 
       // layer 1 (recomputed, elementwise) and its tangent; padded features
@@ -734,7 +775,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         vp[m] = add_xor32(add_xor16(vp[m]));
       }
       // the slot's outputs: lane group 0 alone, or all four groups when atom
-      // virials are asked for (edge_out shares the atomics out)
+      // virials are asked for (edge_out shares the atomics out); the next
+      // tile's coordinates and index have landed by now
+      vmem_wait_all();
       if (valid && (AV || g == 0)) {
         double nd[4];
 #pragma unroll
