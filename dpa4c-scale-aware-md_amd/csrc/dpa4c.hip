@@ -848,29 +848,41 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_grad(C4Params p, Src src
 //   cpart[t]       = (sum_e g(t->j), -sum_e g(t->j) (x) d), the centre-side
 //                    force and frame-virial partials the reduction sums.
 // Sums run in a fixed order (lane stride, then a butterfly): deterministic.
-template <bool Lds>
-__global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_force(
+// Twelve waves per block (three per SIMD, 168 registers): the centre's
+// cotangents sit in LDS (read by every edge of its lane group, not held in
+// registers), and the atom virial is accumulated only when asked for (AV).
+constexpr int kForceBlock = 768;
+template <bool Lds, bool AV>
+__global__ __launch_bounds__(kForceBlock) void k_c4_edge_force(
     C4Params p, NlSrc src, int nnodes, const int* __restrict__ mapping,
     const float* __restrict__ cot, double* __restrict__ force, double* __restrict__ atom_virial,
     double* __restrict__ cpart) {
+  __shared__ f4 cown[kForceBlock / kG][kC4Mom / 4];
   const f4 *tab, *flm;
   stage_tables<Lds>(p, tab, flm);
-  const int lane = threadIdx.x & (kG - 1);
-  constexpr int gpb = kEdgeBlock / kG;
+  const int lane = threadIdx.x & (kG - 1), grp = (int)threadIdx.x / kG;
+  constexpr int gpb = kForceBlock / kG;
   const ChunkWalk cw = xcd_chunks((nnodes + gpb - 1) / gpb);
   for (int ch = cw.first; ch < cw.end; ch += cw.step) {
   const int base = ch * gpb;
-  const int node = base + (int)threadIdx.x / kG;
+  const int node = base + grp;
   double f[3] = {0.0, 0.0, 0.0}, fo[3] = {0.0, 0.0, 0.0};
   double vo[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
   double av[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
   const int ti = node < nnodes ? src.node_type(node) : -1;
+  // the group's cotangents into LDS (the group's lanes are one wave's; its
+  // reads of the previous node's are all done)
+  if (node < nnodes && lane < kC4Mom / 4)
+    cown[grp][lane] = reinterpret_cast<const f4*>(cot + (long)node * kC4Mom)[lane];
+  wave_lds_sync();
   if (ti >= 0 && ti < p.nt) {
     NlSrc::Node nd;
     src.open(p, node, nd);
-    float c[kC4Mom];
-    load_mom(cot + (long)node * kC4Mom, c);
+    const float* c = reinterpret_cast<const float*>(cown[grp]);
     for (int k = lane; k < nd.n; k += kG) {
+      // read the cotangents from LDS on every edge (keeps them out of the
+      // registers: the compiler may not hoist the reads past this)
+      asm volatile("" ::: "memory");
       float d[3];
       int tj, j;
       long slot;
@@ -902,7 +914,7 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_force(
 #pragma unroll
         for (int b = 0; b < 3; ++b) {
           vo[3 * a + b] = fma(-(double)gf[a], dd[b], vo[3 * a + b]);
-          av[3 * a + b] = fma((double)gb[a], dd[b], av[3 * a + b]);
+          if constexpr (AV) av[3 * a + b] = fma((double)gb[a], dd[b], av[3 * a + b]);
         }
       }
     }
@@ -917,7 +929,7 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_force(
 #pragma unroll
     for (int a = 0; a < 9; ++a) {
       vo[a] += __shfl_xor(vo[a], off, kWave);
-      av[a] += __shfl_xor(av[a], off, kWave);
+      if constexpr (AV) av[a] += __shfl_xor(av[a], off, kWave);
     }
   }
   if (node < nnodes && lane == 0) {
@@ -928,7 +940,7 @@ __global__ __launch_bounds__(kEdgeBlock) void k_c4_edge_force(
     }
 #pragma unroll
     for (int a = 0; a < 9; ++a) cpart[12 * (long)node + 3 + a] = vo[a];
-    if (atom_virial)
+    if constexpr (AV)
 #pragma unroll
       for (int a = 0; a < 9; ++a) atom_virial[9 * (long)node + a] = av[a];
   }
@@ -1083,12 +1095,16 @@ void launch_c4_edge_force(hipStream_t st, const C4Params& p, const C4Nlist& s, i
                           double* atom_virial, double* cpart) {
   if (n <= 0) return;
   const size_t lds = table_lds_bytes(p);
+  constexpr int gpb = kForceBlock / kG;
+  const dim3 grid((unsigned)std::max<long>(1, std::min<long>((n + gpb - 1) / gpb, (long)p.ncu)));
+  auto go = [&](auto kern, size_t bytes) {
+    hipLaunchKernelGGL(kern, grid, dim3(kForceBlock), bytes, st, p, NlSrc{s}, n, mapping, cot,
+                       force, atom_virial, cpart);
+  };
   if (lds)
-    hipLaunchKernelGGL(k_c4_edge_force<true>, edge_grid(p, n, 1), dim3(kEdgeBlock), lds, st, p,
-                       NlSrc{s}, n, mapping, cot, force, atom_virial, cpart);
+    atom_virial ? go(k_c4_edge_force<true, true>, lds) : go(k_c4_edge_force<true, false>, lds);
   else
-    hipLaunchKernelGGL(k_c4_edge_force<false>, edge_grid(p, n, 1), dim3(kEdgeBlock), 0, st, p,
-                       NlSrc{s}, n, mapping, cot, force, atom_virial, cpart);
+    atom_virial ? go(k_c4_edge_force<false, true>, 0) : go(k_c4_edge_force<false, false>, 0);
   DPAMD_LAUNCH_CHECK();
 }
 
