@@ -35,6 +35,10 @@ def _systems(dp):
         "water24_smallbox": (dp.systems.water(2, 6.21, seed=44), "water"),
         "cu256_tric": (tilted(dp.systems.fcc(4, 3.615, seed=9), (0.15, -0.2, 0.1)), "cu"),
         "water24_tric": (tilted(dp.systems.water(2, 6.21, seed=46), (-0.3, 0.2, 0.25)), "water"),
+        # 768 atoms: the edge passes' grids (16 force blocks of 48 nodes, 24
+        # moment / gradient blocks of 32) are multiples of the 8 XCDs, so the
+        # nodes are walked XCD by XCD (the smaller systems walk a plain stride)
+        "cuni768": (dp.systems.fcc_alloy((4, 4, 12), 3.56, seed=10), "cuni"),
     }
 
 
@@ -66,7 +70,7 @@ def _model(dp, kind, seed):
 
 
 @pytest.mark.parametrize("case", ["cu256", "hea250", "water192", "water24_smallbox",
-                                  "cu256_tric", "water24_tric"])
+                                  "cu256_tric", "water24_tric", "cuni768"])
 def test_standalone_parity(dp, case):
     (coord, atype, box), kind = _systems(dp)[case]
     m, mb, O = _model(dp, kind, 300)
@@ -94,7 +98,7 @@ def test_standalone_parity(dp, case):
         assert np.array_equal(np.asarray(a), np.asarray(b))
 
 
-@pytest.mark.parametrize("case", ["cu256", "hea250", "water24_smallbox"])
+@pytest.mark.parametrize("case", ["cu256", "hea250", "water24_smallbox", "cuni768"])
 def test_forces_with_and_without_atom_virials(dp, case):
     """The standalone force pass scatters each edge's neighbour side in fixed
     point, with or without the atom virials: the forces, energy and virial of
@@ -111,7 +115,7 @@ def test_forces_with_and_without_atom_virials(dp, case):
     assert np.abs(f.sum(0)).max() <= 1e-9 * max(1.0, np.abs(f).max())
 
 
-@pytest.mark.parametrize("case", ["cu256", "hea250"])
+@pytest.mark.parametrize("case", ["cu256", "hea250", "cuni768"])
 def test_moments_and_cotangents(dp, case):
     """Stage parity: the 44 raw sums per atom and their cotangents dE/d(sums)
     against the oracle (fp32 sums of ~80 edges: relative 2e-5 of the largest
@@ -184,10 +188,11 @@ def test_virtual_atoms(dp):
     assert np.all(ae[atype < 0] == 0.0) and np.all(f[atype < 0] == 0.0)
 
 
-def test_lammps_path(dp, orc):
+@pytest.mark.parametrize("case", ["hea250", "cuni768"])
+def test_lammps_path(dp, orc, case):
     """dp_compute_nlist with a DPA4C model: LAMMPS' full list with skin,
     shuffled rows, ghosts after the locals; ghost forces stay in ghost slots."""
-    (coord, atype, box), kind = _systems(dp)["hea250"]
+    (coord, atype, box), kind = _systems(dp)[case]
     m, mb, O = _model(dp, kind, 303)
     shim = types.SimpleNamespace(ghosts=orc.Oracle.ghosts, candidates=orc.Oracle.candidates,
                                  m={"rcut": m["rcut"]})
