@@ -1085,17 +1085,30 @@ static void gemm_nt(hipStream_t st, const GemmArgs<T>& a) {
   throw HipError{hipErrorInvalidValue, "fitting GEMM: epilogue not available for this operand form"};
 }
 
-static int col_tiles(int N) {
+// Column tile (in MFMA tiles of 16 columns) of a fitting GEMM: the widest of
+// 8, 5, 4 or 1 that divides N; an fp64 GEMM over few rows takes 3 when it
+// divides N, for 5/3 as many blocks (a type of 8,192 rows, N = 240: 384 ->
+// 640 blocks of 64 rows; the layer is too short to fill the GPU otherwise).
+constexpr int kFewRows = 16384;
+template <class T>
+static int col_tiles(int M, int N) {
   const int tiles = N / 16;
+  if (sizeof(T) == 8 && M < kFewRows && tiles % 3 == 0 && tiles % 8 != 0) return 3;
   return tiles % 8 == 0 ? 8 : tiles % 5 == 0 ? 5 : tiles % 4 == 0 ? 4 : 1;
 }
 template <bool TRANSB, class T>
 static void gemm(hipStream_t st, const GemmArgs<T>& a) {
   if (a.M <= 0) return;
-  switch (col_tiles(a.N)) {
+  switch (col_tiles<T>(a.M, a.N)) {
     case 8: gemm_nt<T, 8, TRANSB>(st, a); break;
     case 5: gemm_nt<T, 5, TRANSB>(st, a); break;
     case 4: gemm_nt<T, 4, TRANSB>(st, a); break;
+    case 3:
+      if constexpr (sizeof(T) == 8) {
+        gemm_nt<T, 3, TRANSB>(st, a);
+        break;
+      }
+      [[fallthrough]];
     default: gemm_nt<T, 1, TRANSB>(st, a);
   }
 }
@@ -1159,7 +1172,7 @@ void launch_fitting(hipStream_t st, const FitNet<T>& net, int rows, const T* D, 
   g.epi = 3; g.bias = net.L[2].b; g.idt = net.L[2].idt; g.C = b.dZa; g.ldc = F2;
   g.Bf = net.L[2].Wf; g.Wo = net.Wo; g.epart = b.epart;
   gemm<false>(st, g);
-  const int ncb = F2 / (16 * col_tiles(F2));
+  const int ncb = F2 / (16 * col_tiles<T>(rows, F2));
   hipLaunchKernelGGL(k_head_sum, dim3((rows + 255) / 256), dim3(256), 0, st, rows, ncb, b.epart,
                      net.bo, net.bias, e_bucket);
   DPAMD_LAUNCH_CHECK();
