@@ -758,6 +758,11 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
   const long nf = bp.nshift > 0 ? (long)bp.nshift * nloc : 0;
   if (nloc + nf >= (1L << 31) - 1) throw ApiError{DP_ERR_CAPACITY, "too many ghost candidates"};
   const int nall_cap = nloc + (int)nf;
+  const NlParams np = nl_params_cells(M);
+  // the candidate-order list addresses the cell-sorted records with 32-bit
+  // byte offsets
+  if (np.unsorted && (long)nall_cap * (long)sizeof(CellAtom) >= (1L << 32))
+    throw ApiError{DP_ERR_CAPACITY, "too many atoms and ghosts for the neighbour list"};
   double* sfrac = need<double>(M, M->sfrac, (size_t)nloc * 3);
   double* ext = need<double>(M, M->ext, (size_t)nall_cap * 3);
   int* ext_type = need<int>(M, M->ext_type, (size_t)nall_cap);
@@ -792,7 +797,6 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
     exclusive_scan_int(st, ccount, cstart, ncell + 1, tmp, tb);
   }
   launch_cell_scatter(st, nall, nall_d, cell_of, crank, cstart, ext, ext_type, sorted);
-  const NlParams np = nl_params_cells(M);
   if (np.unsorted) launch_cell_order(st, ncell, cstart, sorted);
   record(M, st, kStGeom + 1);
   int* nlist = need<int>(M, M->nlist, (size_t)std::max(nloc, 1) * m.nnei);

@@ -430,6 +430,145 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells(
   nl_place(np, i, n, lds.k[w], lds.claim[w], nlist, nreal, status);
 }
 
+// Candidate-order list (NlParams::unsorted) over the same 9 runs. A kept
+// candidate goes straight to its type section at its type's running count (one
+// ballot and one masked prefix count per type and batch of 64), written into
+// the wave's row in LDS (nnei ints per wave: no candidate array, so the LDS
+// does not limit residency) and copied out whole at the end; no global store
+// is issued inside the scan, so no candidate load waits behind one (the vector
+// memory counter is in order). The runs' offsets live in a register table
+// (lane k: run k; lanes 9, 10: the end, as sentinels) read with a wave-uniform
+// lane index, and a wave-uniform cursor follows the run that holds each
+// batch's first candidate: a lane then needs one compare and select for the
+// next boundary, and a batch that reaches past a second boundary (a run shorter
+// than the batch, or an empty run) takes the general path over the later
+// boundaries. Lanes past the last candidate load the last one again and are
+// not kept. Output, status bits and section order are those of k_nlist_cells
+// with unsorted set: candidates in concatenation order, at most sel[t] per
+// type, the rest -1. The record offsets are 32-bit (the host limits the
+// extended atoms to 2^27). NT is the model's type count (np.ntypes).
+template <int NT>
+__global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells_seq(
+    int nloc, BoxParams bp, NlParams np, const double* __restrict__ ext,
+    const int* __restrict__ ext_type, const int* __restrict__ cell_of,
+    const int* __restrict__ cell_start, const CellAtom* __restrict__ sorted,
+    int* __restrict__ nlist, int* __restrict__ nreal, int* __restrict__ status) {
+  extern __shared__ int nl_rows[];  // [kNlWaves][nnei]
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = blockIdx.x * kNlWaves + w;
+  if (i >= nloc) return;
+  const int ti = ext_type[i];
+  if (ti < 0 || ti >= NT) {
+    nl_empty_row(np, i, nlist, nreal);
+    return;
+  }
+  const int nnei = np.nnei;
+  int* lrow = nl_rows + w * nnei;
+  for (int s = lane; s < nnei; s += kWave) lrow[s] = -1;
+  const double xi = ext[3 * i], yi = ext[3 * i + 1], zi = ext[3 * i + 2];
+  const int ci = cell_of[i];
+  const int c0 = ci % bp.ncell[0], c1 = (ci / bp.ncell[0]) % bp.ncell[1];
+  const int c2 = ci / (bp.ncell[0] * bp.ncell[1]);
+  int rbeg = 0, rcnt = 0;
+  if (lane < 9) {
+    const int y = c1 + lane % 3 - 1, z = c2 + lane / 3 - 1;
+    if (y >= 0 && y < bp.ncell[1] && z >= 0 && z < bp.ncell[2]) {
+      const int x0 = c0 > 0 ? c0 - 1 : 0, x1 = c0 + 1 < bp.ncell[0] ? c0 + 1 : bp.ncell[0] - 1;
+      const int rowc = (z * bp.ncell[1] + y) * bp.ncell[0];
+      rbeg = cell_start[rowc + x0];
+      rcnt = cell_start[rowc + x1 + 1] - rbeg;
+    }
+  }
+  int incl = rcnt;
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) {
+    const int v = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += v;
+  }
+  const int total = __builtin_amdgcn_readlane(incl, 8);
+  // lane k < 9: run k starts at roffv of the concatenation and its candidate q
+  // is sorted[q + rdelv]; lanes 9 and 10 start at total
+  const int roffv = lane < 9 ? incl - rcnt : total;
+  const int rdelv = rbeg - roffv;
+  int put[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) put[t] = 0;
+  // cursor: run k holds the current batch's first candidate (dcur its offset),
+  // onext / dnext the next run's start and offset
+  int k = 0;
+  int dcur = __builtin_amdgcn_readlane(rdelv, 0);
+  int onext = __builtin_amdgcn_readlane(roffv, 1), dnext = __builtin_amdgcn_readlane(rdelv, 1);
+  // index into sorted of candidate qc (qc in the batch starting at b)
+  auto locate = [&](int b, int qc) {
+    while (onext <= b) {  // wave-uniform; empty runs are passed over here
+      ++k;
+      dcur = dnext;
+      onext = __builtin_amdgcn_readlane(roffv, k + 1);
+      dnext = __builtin_amdgcn_readlane(rdelv, k + 1);
+    }
+    int at = qc + dcur + (qc >= onext ? dnext - dcur : 0);
+    if (__builtin_amdgcn_readlane(roffv, k + 2) < b + kWave) {
+      asm volatile("");  // rare: kept as a branch, not evaluated for every batch
+      for (int kk = k + 2; kk < 9; ++kk) {
+        const int o = __builtin_amdgcn_readlane(roffv, kk);
+        if (o >= b + kWave) break;
+        if (qc >= o) at = qc + __builtin_amdgcn_readlane(rdelv, kk);
+      }
+    }
+    return at;
+  };
+  const char* sbytes = reinterpret_cast<const char*>(sorted);
+  for (int base = 0; base < total; base += 2 * kWave) {
+    CellAtom ca[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int b = base + kWave * u;
+      if (b < total) {  // wave-uniform
+        const int qc = min(b + lane, total - 1);
+        const unsigned at = (unsigned)locate(b, qc);
+        ca[u] = *reinterpret_cast<const CellAtom*>(sbytes + at * (unsigned)sizeof(CellAtom));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int b = base + kWave * u;
+      if (b >= total) break;  // wave-uniform
+      const int j = ca[u].idx, t = ca[u].type;
+      const double dx = ca[u].x - xi;
+      const double dy = ca[u].y - yi;
+      const double dz = ca[u].z - zi;
+      const double r2 = dx * dx + dy * dy + dz * dz;
+      // (bitwise, and ballots of single compares: each compare stays a lane
+      // mask, combined on the scalar unit)
+      const bool keep = (b + lane < total) & (j != i) & (r2 <= np.rc2);
+      const unsigned long long km =
+          __ballot(b + lane < total) & __ballot(j != i) & __ballot(r2 <= np.rc2);
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        const bool mine = keep & (t == tt);
+        const unsigned long long m = __ballot(t == tt) & km;
+        const unsigned pos = __builtin_amdgcn_mbcnt_hi(
+            (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u)) + (unsigned)put[tt];
+        if (mine & (pos < (unsigned)np.sel[tt])) lrow[np.sec[tt] + pos] = j;
+        put[tt] += __popcll(m);
+      }
+    }
+  }
+  wave_lds_sync();
+  int* row = nlist + (long)i * nnei;
+  for (int s = lane; s < nnei; s += kWave) row[s] = lrow[s];
+  int n = 0;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    n += put[t];
+    if (np.sel_strict && put[t] > np.sel[t] && lane == 0) atomicOr(status, kStatusSelOverflow);
+    if (lane == 0) nreal[(long)i * NT + t] = put[t] < np.sel[t] ? put[t] : np.sel[t];
+  }
+  // the LDS form holds at most kMaxCand kept candidates; the same bound is
+  // reported here so both forms fail alike
+  if (n > kMaxCand && lane == 0) atomicOr(status, kStatusNeighbourOverflow);
+}
+
 // LAMMPS front end: candidates come from the caller's full list (CSR by centre).
 __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_csr(
     int nloc, NlParams np, const double* __restrict__ ext, const int* __restrict__ ext_type,
@@ -548,9 +687,26 @@ void launch_nlist_cells(hipStream_t st, int nloc, const BoxParams& bp, const NlP
                         const int* cell_start, const CellAtom* sorted, int* nlist, int* nreal,
                         int* status) {
   if (nloc <= 0) return;
-  hipLaunchKernelGGL(k_nlist_cells, dim3((nloc + kNlWaves - 1) / kNlWaves), dim3(kNlWaves * 64),
-                     0, st, nloc, bp, np, ext, ext_type, cell_of, cell_start, sorted, nlist, nreal,
-                     status);
+  const dim3 grid((nloc + kNlWaves - 1) / kNlWaves), block(kNlWaves * 64);
+  if (np.unsorted) {
+    const size_t lds = kNlWaves * np.nnei * sizeof(int);
+    auto go = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, grid, block, lds, st, nloc, bp, np, ext, ext_type, cell_of,
+                         cell_start, sorted, nlist, nreal, status);
+    };
+    switch (np.ntypes) {
+      case 1: go(k_nlist_cells_seq<1>); break;
+      case 2: go(k_nlist_cells_seq<2>); break;
+      case 3: go(k_nlist_cells_seq<3>); break;
+      case 4: go(k_nlist_cells_seq<4>); break;
+      case 5: go(k_nlist_cells_seq<5>); break;
+      case 6: go(k_nlist_cells_seq<6>); break;
+      case 7: go(k_nlist_cells_seq<7>); break;
+      default: go(k_nlist_cells_seq<kMaxTypes>); break;
+    }
+  } else
+    hipLaunchKernelGGL(k_nlist_cells, grid, block, 0, st, nloc, bp, np, ext, ext_type, cell_of,
+                       cell_start, sorted, nlist, nreal, status);
   DPAMD_LAUNCH_CHECK();
 }
 
