@@ -770,14 +770,15 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
   int* nall_d = need<int>(M, M->nall_d, 1);
   launch_wrap(st, nloc, d_coord, d_atype, bp, ext, ext_type, mapping, sfrac);
   if (nf > 0) {
-    int* flags = need<int>(M, M->flags, (size_t)nf);
-    int* pos = need<int>(M, M->gpos, (size_t)nf);
-    launch_ghost_flags(st, nloc, bp, sfrac, flags);
-    const size_t tb = scan_temp_bytes((int)nf);
+    const long nc = (long)bp.nshift * ghost_tiles(nloc);  // per (shift, tile of atoms)
+    int* count = need<int>(M, M->flags, (size_t)nc);
+    int* first = need<int>(M, M->gpos, (size_t)nc);
+    launch_ghost_count(st, nloc, bp, sfrac, count);
+    const size_t tb = scan_temp_bytes((int)nc);
     void* tmp = need<char>(M, M->scan_tmp, tb);
-    exclusive_scan_int(st, flags, pos, (int)nf, tmp, tb);
-    launch_ghost_total(st, nloc, nf, flags, pos, nall_d);
-    launch_ghost_fill(st, nloc, bp, flags, pos, ext, ext_type, mapping);
+    exclusive_scan_int(st, count, first, (int)nc, tmp, tb);
+    launch_ghost_total(st, nloc, nc, count, first, nall_d);
+    launch_ghost_place(st, nloc, bp, sfrac, first, ext, ext_type, mapping);
   } else {
     launch_fill_int(st, 1, nloc, nall_d);
   }

@@ -111,9 +111,14 @@ struct DescArgs {
 // Neighbour stage
 void launch_wrap(hipStream_t, int nloc, const double* coord, const int* atype, const BoxParams&,
                  double* ext, int* ext_type, int* mapping, double* sfrac);
-void launch_ghost_flags(hipStream_t, int nloc, const BoxParams&, const double* sfrac, int* flags);
-void launch_ghost_fill(hipStream_t, int nloc, const BoxParams&, const int* flags, const int* pos,
-                       double* ext, int* ext_type, int* mapping);
+// Ghost images in (shift, atom) order: per shift, the number of images of each
+// tile of atoms that land in the extended region (count[s * ghost_tiles(nloc)
+// + tile]); then, from the exclusive scan of those counts, the images
+// themselves (coordinates, types and mapping after the nloc local atoms).
+int ghost_tiles(int nloc);
+void launch_ghost_count(hipStream_t, int nloc, const BoxParams&, const double* sfrac, int* count);
+void launch_ghost_place(hipStream_t, int nloc, const BoxParams&, const double* sfrac,
+                        const int* first, double* ext, int* ext_type, int* mapping);
 // Cell kernels over cap atoms, or over *d_count of them when d_count is given
 // (a count produced on the device, at most cap).
 // (cell_rank: an atom's rank within its cell, from the count)
@@ -124,7 +129,7 @@ void launch_cell_scatter(hipStream_t, int cap, const int* d_count, const int* ce
                          const int* ext_type, CellAtom* sorted);
 // atoms of each cell in ascending index order (reproducible candidate order)
 void launch_cell_order(hipStream_t, int ncell, const int* cell_start, CellAtom* sorted);
-// nall = nloc + number of flagged ghost candidates, from the flags and their
+// nall = nloc + number of ghosts, from the per-(shift, tile) counts and their
 // exclusive scan, into device memory
 void launch_ghost_total(hipStream_t, int nloc, long nf, const int* flags, const int* pos,
                         int* nall);

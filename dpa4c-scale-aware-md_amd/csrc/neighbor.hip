@@ -62,37 +62,89 @@ __device__ __forceinline__ void decode_shift(const BoxParams& bp, int s, int* n)
   n[2] = q / (wa * wb) - bp.nrep[2];
 }
 
-// flags[s*nloc + k] = 1 when image s of atom k lies in the extended region.
-__global__ void k_ghost_flags(int nloc, BoxParams bp, const double* __restrict__ sfrac,
-                              int* __restrict__ flags) {
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)bp.nshift * nloc) return;
-  const int s = (int)(idx / nloc), k = (int)(idx % nloc);
-  int n[3];
-  decode_shift(bp, s, n);
+// Whether image s of atom k lies in the extended region.
+__device__ __forceinline__ bool ghost_in(const BoxParams& bp, const double* __restrict__ sfrac,
+                                         int k, const int (&n)[3]) {
   const double f0 = sfrac[3 * k] + (double)n[0];
   const double f1 = sfrac[3 * k + 1] + (double)n[1];
   const double f2 = sfrac[3 * k + 2] + (double)n[2];
-  const bool in = f0 >= -bp.rcf[0] && f0 < bp.hi[0] && f1 >= -bp.rcf[1] && f1 < bp.hi[1] &&
-                  f2 >= -bp.rcf[2] && f2 < bp.hi[2];
-  flags[idx] = in ? 1 : 0;
+  return f0 >= -bp.rcf[0] && f0 < bp.hi[0] && f1 >= -bp.rcf[1] && f1 < bp.hi[1] &&
+         f2 >= -bp.rcf[2] && f2 < bp.hi[2];
 }
 
-__global__ void k_ghost_fill(int nloc, BoxParams bp, const int* __restrict__ flags,
-                             const int* __restrict__ pos, double* __restrict__ ext,
-                             int* __restrict__ ext_type, int* __restrict__ mapping) {
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)bp.nshift * nloc || !flags[idx]) return;
-  const int s = (int)(idx / nloc), k = (int)(idx % nloc);
-  int n[3];
-  decode_shift(bp, s, n);
-  const int o = nloc + pos[idx];
-  const double na = (double)n[0], nb = (double)n[1], nc = (double)n[2];
-  ext[3 * o] = ext[3 * k] + na * bp.h[0] + nb * bp.h[3] + nc * bp.h[6];
-  ext[3 * o + 1] = ext[3 * k + 1] + nb * bp.h[4] + nc * bp.h[7];
-  ext[3 * o + 2] = ext[3 * k + 2] + nc * bp.h[8];
-  ext_type[o] = ext_type[k];
-  mapping[o] = k;
+// Ghost images in (shift, atom) order. Block (b, y) owns images s = y * spb ..
+// y * spb + spb - 1 of the tile of atoms [256 b, 256 b + 256): k_ghost_count
+// writes, per shift, how many of them land in the extended region
+// (count[s * ntiles + b]); an exclusive scan of those counts gives every
+// (shift, tile) its first ghost slot, and k_ghost_place re-tests the images
+// and writes them there in atom order (wave ballots, then the earlier waves'
+// totals through LDS, double-buffered by shift parity so one barrier per
+// shift suffices). The order is that of one flag per (shift, atom) scanned in
+// shift-major order, with nshift * nloc / 256 counts instead of nshift * nloc
+// flags. spb (shifts per block) keeps the grid near a few thousand blocks:
+// one shift per block for small systems, several for large ones.
+constexpr int kGhostTile = 256;
+__global__ __launch_bounds__(kGhostTile) void k_ghost_count(int nloc, int spb, BoxParams bp,
+                                                           const double* __restrict__ sfrac,
+                                                           int* __restrict__ count) {
+  __shared__ int wc[2][kGhostTile / kWave];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int k = blockIdx.x * kGhostTile + threadIdx.x;
+  const int s0 = blockIdx.y * spb, s1 = min(bp.nshift, s0 + spb);
+  for (int s = s0; s < s1; ++s) {
+    int n[3];
+    decode_shift(bp, s, n);
+    const bool in = k < nloc && ghost_in(bp, sfrac, k, n);
+    const int c = __popcll(__ballot(in));  // (every lane votes: outside the lane-0 branch)
+    if (lane == 0) wc[s & 1][w] = c;
+    __syncthreads();  // (the other buffer was last read before the previous barrier)
+    if (threadIdx.x == 0) {
+      int t = 0;
+#pragma unroll
+      for (int q = 0; q < kGhostTile / kWave; ++q) t += wc[s & 1][q];
+      count[(long)s * gridDim.x + blockIdx.x] = t;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kGhostTile) void k_ghost_place(int nloc, int spb, BoxParams bp,
+                                                           const double* __restrict__ sfrac,
+                                                           const int* __restrict__ first,
+                                                           double* __restrict__ ext,
+                                                           int* __restrict__ ext_type,
+                                                           int* __restrict__ mapping) {
+  __shared__ int wc[2][kGhostTile / kWave];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int k = blockIdx.x * kGhostTile + threadIdx.x;
+  const int s0 = blockIdx.y * spb, s1 = min(bp.nshift, s0 + spb);
+  double x0 = 0.0, x1 = 0.0, x2 = 0.0;
+  int tk = 0;
+  if (k < nloc) {
+    x0 = ext[3 * k];
+    x1 = ext[3 * k + 1];
+    x2 = ext[3 * k + 2];
+    tk = ext_type[k];
+  }
+  for (int s = s0; s < s1; ++s) {
+    int n[3];
+    decode_shift(bp, s, n);
+    const bool in = k < nloc && ghost_in(bp, sfrac, k, n);
+    const unsigned long long m = __ballot(in);
+    if (lane == 0) wc[s & 1][w] = __popcll(m);
+    __syncthreads();
+    if (in) {
+      int before = (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+      for (int q = 0; q < w; ++q) before += wc[s & 1][q];
+      const int o = nloc + first[(long)s * gridDim.x + blockIdx.x] + before;
+      const double na = (double)n[0], nb = (double)n[1], nc = (double)n[2];
+      ext[3 * o] = x0 + na * bp.h[0] + nb * bp.h[3] + nc * bp.h[6];
+      ext[3 * o + 1] = x1 + nb * bp.h[4] + nc * bp.h[7];
+      ext[3 * o + 2] = x2 + nc * bp.h[8];
+      ext_type[o] = tk;
+      mapping[o] = k;
+    }
+  }
 }
 
 __device__ __forceinline__ int cell_of_point(const BoxParams& bp, double x0, double x1, double x2) {
@@ -110,9 +162,12 @@ __device__ __forceinline__ int cell_of_point(const BoxParams& bp, double x0, dou
 
 // The atom count is cap, or *d_count when given (ghost count known on the
 // device only; the grid then covers the capacity cap).
-// Each atom's rank among the atoms of its cell is the value its count
-// increment returned, so the scatter needs no second round of atomics (the
-// order within a cell is arbitrary; the neighbour list sorts its candidates).
+// Each atom's rank among the atoms of its cell comes from the count increment,
+// so the scatter needs no second round of atomics (the order within a cell is
+// arbitrary; the neighbour list sorts its candidates, or k_cell_order orders
+// them). The lanes of a wave that fall in one cell (consecutive atoms often
+// do) share one atomic: the first such lane adds the group's size, and each
+// lane's rank is the returned count plus its place in the group.
 __global__ void k_cell_assign(int cap, const int* __restrict__ d_count, BoxParams bp,
                               const double* __restrict__ ext, int* __restrict__ cell_of,
                               int* __restrict__ cell_rank, int* __restrict__ cell_count) {
@@ -120,7 +175,19 @@ __global__ void k_cell_assign(int cap, const int* __restrict__ d_count, BoxParam
   if (n >= (d_count ? *d_count : cap)) return;
   const int c = cell_of_point(bp, ext[3 * n], ext[3 * n + 1], ext[3 * n + 2]);
   cell_of[n] = c;
-  cell_rank[n] = atomicAdd(&cell_count[c], 1);
+  unsigned long long left = __ballot(true);
+  while (left) {  // wave-uniform: one round per distinct cell among the active lanes
+    const int lead = __ffsll((long long)left) - 1;
+    const int cl = __builtin_amdgcn_readlane(c, lead);
+    const unsigned long long m = __ballot(c == cl) & left;
+    int base = 0;
+    if (threadIdx.x % kWave == lead) base = atomicAdd(&cell_count[cl], __popcll(m));
+    base = __builtin_amdgcn_readlane(base, lead);
+    if (c == cl)
+      cell_rank[n] = base + (int)__builtin_amdgcn_mbcnt_hi(
+                                (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+    left &= ~m;
+  }
 }
 
 __global__ void k_cell_scatter(int cap, const int* __restrict__ d_count,
@@ -142,37 +209,50 @@ __global__ void k_cell_scatter(int cap, const int* __restrict__ d_count,
 }
 
 // Atoms of a cell in ascending index order (the scatter's order comes from
-// atomic ranks): one wave per cell reads the cell's records into registers,
-// ranks them by index and writes them back, so candidate order -- and with it
-// an unsorted neighbour list -- is reproducible. Cells of more than
-// kCellSortMax atoms keep the scatter's order (every access stays in bounds).
+// atomic ranks): one wave per cell holds the cell's records in registers (K
+// per lane), ranks them by index against the indices read back from the
+// lanes (no memory access in the rank loop) and writes them back, so candidate
+// order -- and with it an unsorted neighbour list -- is reproducible. Cells of
+// more than kCellSortMax atoms keep the scatter's order (every access stays in
+// bounds).
 constexpr int kCellSortK = 8;
 constexpr int kCellSortMax = 64 * kCellSortK;
-__global__ __launch_bounds__(256) void k_cell_order(int ncell, const int* __restrict__ cell_start,
-                                                   CellAtom* __restrict__ sorted) {
+template <int K>
+__device__ __forceinline__ void cell_order_k(int beg, int cnt, CellAtom* __restrict__ sorted) {
   const int lane = threadIdx.x & 63;
-  const int c = (int)(((long)blockIdx.x * 256 + threadIdx.x) >> 6);
-  if (c >= ncell) return;
-  const int beg = cell_start[c], cnt = cell_start[c + 1] - beg;
-  if (cnt <= 1 || cnt > kCellSortMax) return;
-  CellAtom a[kCellSortK];
-  int rank[kCellSortK];
+  CellAtom a[K];
+  int rank[K];
 #pragma unroll
-  for (int k = 0; k < kCellSortK; ++k) {
+  for (int k = 0; k < K; ++k) {
     rank[k] = 0;
     a[k].idx = 0x7fffffff;
     if (lane + 64 * k < cnt) a[k] = sorted[beg + lane + 64 * k];
   }
-  for (int m = 0; m < cnt; ++m) {
-    const int om = sorted[beg + m].idx;
 #pragma unroll
-    for (int k = 0; k < kCellSortK; ++k) rank[k] += om < a[k].idx ? 1 : 0;
+  for (int k2 = 0; k2 < K; ++k2) {
+    const int m_end = min(cnt - 64 * k2, 64);  // wave-uniform
+    for (int m = 0; m < m_end; ++m) {
+      const int om = __builtin_amdgcn_readlane(a[k2].idx, m);
+#pragma unroll
+      for (int k = 0; k < K; ++k) rank[k] += om < a[k].idx ? 1 : 0;
+    }
   }
-  // the wave's loads above all complete before its stores below (the stores
-  // write the loaded records at addresses computed from loaded indices)
+  // every load above has been consumed (the ranks need all of them) before
+  // the stores below
 #pragma unroll
-  for (int k = 0; k < kCellSortK; ++k)
+  for (int k = 0; k < K; ++k)
     if (lane + 64 * k < cnt) sorted[beg + rank[k]] = a[k];
+}
+
+__global__ __launch_bounds__(256) void k_cell_order(int ncell, const int* __restrict__ cell_start,
+                                                   CellAtom* __restrict__ sorted) {
+  const int c = (int)(((long)blockIdx.x * 256 + threadIdx.x) >> 6);
+  if (c >= ncell) return;
+  const int beg = cell_start[c], cnt = cell_start[c + 1] - beg;
+  if (cnt <= 1 || cnt > kCellSortMax) return;
+  if (cnt <= 64) cell_order_k<1>(beg, cnt, sorted);
+  else if (cnt <= 128) cell_order_k<2>(beg, cnt, sorted);
+  else cell_order_k<kCellSortK>(beg, cnt, sorted);
 }
 
 // ---------------------------------------------------------------------------
@@ -615,21 +695,33 @@ void launch_wrap(hipStream_t st, int nloc, const double* coord, const int* atype
   DPAMD_LAUNCH_CHECK();
 }
 
-void launch_ghost_flags(hipStream_t st, int nloc, const BoxParams& bp, const double* sfrac,
-                        int* flags) {
-  const long n = (long)bp.nshift * nloc;
-  if (n <= 0) return;
-  hipLaunchKernelGGL(k_ghost_flags, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, nloc, bp,
-                     sfrac, flags);
+int ghost_tiles(int nloc) { return (nloc + kGhostTile - 1) / kGhostTile; }
+
+// shifts per block, and the grid: (tiles, shift groups)
+static dim3 ghost_grid(int nloc, const BoxParams& bp, int* spb) {
+  const long tiles = ghost_tiles(nloc), pairs = tiles * bp.nshift;
+  *spb = (int)std::max(1L, (pairs + 4095) / 4096);
+  const int groups = (bp.nshift + *spb - 1) / *spb;
+  if (groups > 65535) throw HipError{hipErrorInvalidValue, "too many periodic images"};
+  return dim3((unsigned)tiles, (unsigned)groups);
+}
+
+void launch_ghost_count(hipStream_t st, int nloc, const BoxParams& bp, const double* sfrac,
+                        int* count) {
+  if (nloc <= 0 || bp.nshift <= 0) return;
+  int spb = 1;
+  const dim3 grid = ghost_grid(nloc, bp, &spb);
+  hipLaunchKernelGGL(k_ghost_count, grid, dim3(kGhostTile), 0, st, nloc, spb, bp, sfrac, count);
   DPAMD_LAUNCH_CHECK();
 }
 
-void launch_ghost_fill(hipStream_t st, int nloc, const BoxParams& bp, const int* flags,
-                       const int* pos, double* ext, int* ext_type, int* mapping) {
-  const long n = (long)bp.nshift * nloc;
-  if (n <= 0) return;
-  hipLaunchKernelGGL(k_ghost_fill, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, nloc, bp,
-                     flags, pos, ext, ext_type, mapping);
+void launch_ghost_place(hipStream_t st, int nloc, const BoxParams& bp, const double* sfrac,
+                        const int* first, double* ext, int* ext_type, int* mapping) {
+  if (nloc <= 0 || bp.nshift <= 0) return;
+  int spb = 1;
+  const dim3 grid = ghost_grid(nloc, bp, &spb);
+  hipLaunchKernelGGL(k_ghost_place, grid, dim3(kGhostTile), 0, st, nloc, spb, bp, sfrac, first,
+                     ext, ext_type, mapping);
   DPAMD_LAUNCH_CHECK();
 }
 
