@@ -633,10 +633,7 @@ void reduce_outputs(dp_model* M, hipStream_t st, int nloc, int ntarget, const do
   const double* cpart = static_cast<const double*>(M->cpart.p);
   double* partials = need<double>(M, M->partials, 256 * 10);
   double* out10 = need<double>(M, M->out10, 10);
-  launch_reduce_ev(st, ne, nloc, e_vals, cpart, partials, out10);
-  if (out.energy) DPAMD_HIP(hipMemcpyAsync(out.energy, out10, 8, hipMemcpyDeviceToDevice, st));
-  if (out.virial)
-    DPAMD_HIP(hipMemcpyAsync(out.virial, out10 + 1, 72, hipMemcpyDeviceToDevice, st));
+  launch_reduce_ev(st, ne, nloc, e_vals, cpart, partials, out10, out.energy, out.virial);
   if (out.atom_energy) {
     launch_fill_int(st, 2L * ntarget, 0, reinterpret_cast<int*>(out.atom_energy));
     if (items) {
@@ -686,10 +683,7 @@ void run_c4(dp_model* M, hipStream_t st, int nloc, const int* d_mapping, int nta
     record(M, st, kStForce + 1);
     double* partials = need<double>(M, M->partials, 256 * 10);
     double* out10 = need<double>(M, M->out10, 10);
-    launch_reduce_ev(st, nloc, nloc, e, cpart, partials, out10);
-    if (out.energy) DPAMD_HIP(hipMemcpyAsync(out.energy, out10, 8, hipMemcpyDeviceToDevice, st));
-    if (out.virial)
-      DPAMD_HIP(hipMemcpyAsync(out.virial, out10 + 1, 72, hipMemcpyDeviceToDevice, st));
+    launch_reduce_ev(st, nloc, nloc, e, cpart, partials, out10, out.energy, out.virial);
     if (out.atom_energy && nloc > 0)
       DPAMD_HIP(hipMemcpyAsync(out.atom_energy, e, sizeof(double) * nloc,
                                hipMemcpyDeviceToDevice, st));
@@ -768,7 +762,17 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
   int* ext_type = need<int>(M, M->ext_type, (size_t)nall_cap);
   int* mapping = need<int>(M, M->mapping, (size_t)nall_cap);
   int* nall_d = need<int>(M, M->nall_d, 1);
-  launch_wrap(st, nloc, d_coord, d_atype, bp, ext, ext_type, mapping, sfrac);
+  const int nall = nall_cap;
+  const int ncell = bp.ncell[0] * bp.ncell[1] * bp.ncell[2];
+  int* cell_of = need<int>(M, M->cell_of, (size_t)nall);
+  int* ccount = need<int>(M, M->cell_count, (size_t)ncell + 1);
+  int* cstart = need<int>(M, M->cell_start, (size_t)ncell + 1);
+  int* crank = need<int>(M, M->cell_rank, (size_t)nall);
+  CellAtom* sorted = need<CellAtom>(M, M->sorted, (size_t)nall);
+  // the wrap also clears the cell counts (and gives nall when there are no
+  // ghosts); the ghost placement gives nall otherwise
+  launch_wrap(st, nloc, d_coord, d_atype, bp, ext, ext_type, mapping, sfrac, ncell + 1, ccount,
+              nf > 0 ? nullptr : nall_d);
   if (nf > 0) {
     const long nc = (long)bp.nshift * ghost_tiles(nloc);  // per (shift, tile of atoms)
     int* count = need<int>(M, M->flags, (size_t)nc);
@@ -777,20 +781,9 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
     const size_t tb = scan_temp_bytes((int)nc);
     void* tmp = need<char>(M, M->scan_tmp, tb);
     exclusive_scan_int(st, count, first, (int)nc, tmp, tb);
-    launch_ghost_total(st, nloc, nc, count, first, nall_d);
-    launch_ghost_place(st, nloc, bp, sfrac, first, ext, ext_type, mapping);
-  } else {
-    launch_fill_int(st, 1, nloc, nall_d);
+    launch_ghost_place(st, nloc, bp, sfrac, count, first, ext, ext_type, mapping, nall_d);
   }
-  const int nall = nall_cap;
   // cells
-  const int ncell = bp.ncell[0] * bp.ncell[1] * bp.ncell[2];
-  int* cell_of = need<int>(M, M->cell_of, (size_t)nall);
-  int* ccount = need<int>(M, M->cell_count, (size_t)ncell + 1);
-  int* cstart = need<int>(M, M->cell_start, (size_t)ncell + 1);
-  int* crank = need<int>(M, M->cell_rank, (size_t)nall);
-  CellAtom* sorted = need<CellAtom>(M, M->sorted, (size_t)nall);
-  launch_fill_int(st, (long)ncell + 1, 0, ccount);
   launch_cell_assign(st, nall, nall_d, bp, ext, cell_of, crank, ccount);
   {
     const size_t tb = scan_temp_bytes(ncell + 1);

@@ -284,7 +284,9 @@ __global__ __launch_bounds__(256) void k_reduce_ev1(int nbucket, int nloc,
 }
 
 __global__ __launch_bounds__(256) void k_reduce_ev2(const double* __restrict__ partials,
-                                                    double* __restrict__ out10) {
+                                                    double* __restrict__ out10,
+                                                    double* __restrict__ energy,
+                                                    double* __restrict__ virial) {
   __shared__ double sm[10][256];
   for (int q = 0; q < 10; ++q) sm[q][threadIdx.x] = partials[threadIdx.x * 10 + q];
   __syncthreads();
@@ -293,7 +295,12 @@ __global__ __launch_bounds__(256) void k_reduce_ev2(const double* __restrict__ p
       for (int q = 0; q < 10; ++q) sm[q][threadIdx.x] += sm[q][threadIdx.x + h];
     __syncthreads();
   }
-  if (threadIdx.x < 10) out10[threadIdx.x] = sm[threadIdx.x][0];
+  if (threadIdx.x < 10) {
+    const double v = sm[threadIdx.x][0];
+    out10[threadIdx.x] = v;
+    if (threadIdx.x == 0 && energy) *energy = v;
+    if (threadIdx.x > 0 && virial) virial[threadIdx.x - 1] = v;
+  }
 }
 
 __global__ void k_scatter_energy(int n, const int* __restrict__ items,
@@ -331,11 +338,12 @@ void launch_force_gather(hipStream_t st, int ntarget, int nloc, int nnei, const 
 }
 
 void launch_reduce_ev(hipStream_t st, int nbucket, int nloc, const double* e_bucket,
-                      const double* cpart, double* partials, double* out10) {
+                      const double* cpart, double* partials, double* out10, double* energy,
+                      double* virial) {
   hipLaunchKernelGGL(k_reduce_ev1, dim3(kRedBlocks), dim3(256), 0, st, nbucket, nloc, e_bucket,
                      cpart, partials);
   DPAMD_LAUNCH_CHECK();
-  hipLaunchKernelGGL(k_reduce_ev2, dim3(1), dim3(256), 0, st, partials, out10);
+  hipLaunchKernelGGL(k_reduce_ev2, dim3(1), dim3(256), 0, st, partials, out10, energy, virial);
   DPAMD_LAUNCH_CHECK();
 }
 

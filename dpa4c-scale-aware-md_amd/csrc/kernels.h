@@ -109,16 +109,20 @@ struct DescArgs {
 };
 
 // Neighbour stage
+// also clears clear[0 .. nclear) and, when nall is given, sets *nall = nloc
 void launch_wrap(hipStream_t, int nloc, const double* coord, const int* atype, const BoxParams&,
-                 double* ext, int* ext_type, int* mapping, double* sfrac);
+                 double* ext, int* ext_type, int* mapping, double* sfrac, int nclear, int* clear,
+                 int* nall);
 // Ghost images in (shift, atom) order: per shift, the number of images of each
 // tile of atoms that land in the extended region (count[s * ghost_tiles(nloc)
 // + tile]); then, from the exclusive scan of those counts, the images
 // themselves (coordinates, types and mapping after the nloc local atoms).
 int ghost_tiles(int nloc);
 void launch_ghost_count(hipStream_t, int nloc, const BoxParams&, const double* sfrac, int* count);
+// (also *nall = nloc + the number of ghosts)
 void launch_ghost_place(hipStream_t, int nloc, const BoxParams&, const double* sfrac,
-                        const int* first, double* ext, int* ext_type, int* mapping);
+                        const int* count, const int* first, double* ext, int* ext_type,
+                        int* mapping, int* nall);
 // Cell kernels over cap atoms, or over *d_count of them when d_count is given
 // (a count produced on the device, at most cap).
 // (cell_rank: an atom's rank within its cell, from the count)
@@ -129,10 +133,6 @@ void launch_cell_scatter(hipStream_t, int cap, const int* d_count, const int* ce
                          const int* ext_type, CellAtom* sorted);
 // atoms of each cell in ascending index order (reproducible candidate order)
 void launch_cell_order(hipStream_t, int ncell, const int* cell_start, CellAtom* sorted);
-// nall = nloc + number of ghosts, from the per-(shift, tile) counts and their
-// exclusive scan, into device memory
-void launch_ghost_total(hipStream_t, int nloc, long nf, const int* flags, const int* pos,
-                        int* nall);
 // p[0 .. n) = v (a kernel rather than a memset node, so it can be captured)
 void launch_fill_int(hipStream_t, long n, int v, int* p);
 void launch_nlist_cells(hipStream_t, int nloc, const BoxParams&, const NlParams&, const double* ext,
@@ -280,8 +280,10 @@ void launch_force_gather(hipStream_t, int ntarget, int nloc, int nnei, const int
                          const int* rev, const int* nlist, const double* ext,
                          const double* edge_grad, double* cpart, double* force,
                          double* atom_virial, int* status);
+// out10 = [energy, virial[9]]; also written to energy / virial when given
 void launch_reduce_ev(hipStream_t, int nbucket, int nloc, const double* atom_energy_bucket,
-                      const double* cpart, double* partials, double* out10);
+                      const double* cpart, double* partials, double* out10, double* energy,
+                      double* virial);
 void launch_scatter_energy(hipStream_t, int nloc, const int* items, const double* e_bucket,
                            double* atom_energy);
 

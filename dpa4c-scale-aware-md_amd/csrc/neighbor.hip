@@ -26,10 +26,15 @@ __device__ __forceinline__ void to_frac(const BoxParams& bp, double x0, double x
   s[0] = (x0 - s[1] * bp.h[3] - s[2] * bp.h[6]) / bp.h[0];
 }
 
+// (also clears clear[0 .. nclear) for the next kernels, and sets *nall = nloc
+// when given: no launches of their own)
 __global__ void k_wrap(int nloc, const double* __restrict__ coord, const int* __restrict__ atype,
                        BoxParams bp, double* __restrict__ ext, int* __restrict__ ext_type,
-                       int* __restrict__ mapping, double* __restrict__ sfrac) {
+                       int* __restrict__ mapping, double* __restrict__ sfrac, int nclear,
+                       int* __restrict__ clear, int* __restrict__ nall) {
   const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < nclear) clear[k] = 0;
+  if (nall && k == 0) *nall = nloc;
   if (k >= nloc) return;
   const double x0 = coord[3 * k], x1 = coord[3 * k + 1], x2 = coord[3 * k + 2];
   double w0 = x0, w1 = x1, w2 = x2;
@@ -109,14 +114,20 @@ __global__ __launch_bounds__(kGhostTile) void k_ghost_count(int nloc, int spb, B
 
 __global__ __launch_bounds__(kGhostTile) void k_ghost_place(int nloc, int spb, BoxParams bp,
                                                            const double* __restrict__ sfrac,
+                                                           const int* __restrict__ count,
                                                            const int* __restrict__ first,
                                                            double* __restrict__ ext,
                                                            int* __restrict__ ext_type,
-                                                           int* __restrict__ mapping) {
+                                                           int* __restrict__ mapping,
+                                                           int* __restrict__ nall) {
   __shared__ int wc[2][kGhostTile / kWave];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int k = blockIdx.x * kGhostTile + threadIdx.x;
   const int s0 = blockIdx.y * spb, s1 = min(bp.nshift, s0 + spb);
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+    const long last = (long)bp.nshift * gridDim.x - 1;  // the last (shift, tile)
+    *nall = nloc + first[last] + count[last];
+  }
   double x0 = 0.0, x1 = 0.0, x2 = 0.0;
   int tk = 0;
   if (k < nloc) {
@@ -688,10 +699,12 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_csr(
 // ---------------------------------------------------------------------------
 // Host launchers
 void launch_wrap(hipStream_t st, int nloc, const double* coord, const int* atype,
-                 const BoxParams& bp, double* ext, int* ext_type, int* mapping, double* sfrac) {
-  if (nloc <= 0) return;
-  hipLaunchKernelGGL(k_wrap, dim3((nloc + 255) / 256), dim3(256), 0, st, nloc, coord, atype, bp,
-                     ext, ext_type, mapping, sfrac);
+                 const BoxParams& bp, double* ext, int* ext_type, int* mapping, double* sfrac,
+                 int nclear, int* clear, int* nall) {
+  const int n = std::max(std::max(nloc, nclear), nall ? 1 : 0);
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_wrap, dim3((n + 255) / 256), dim3(256), 0, st, nloc, coord, atype, bp, ext,
+                     ext_type, mapping, sfrac, nclear, clear, nall);
   DPAMD_LAUNCH_CHECK();
 }
 
@@ -716,12 +729,13 @@ void launch_ghost_count(hipStream_t st, int nloc, const BoxParams& bp, const dou
 }
 
 void launch_ghost_place(hipStream_t st, int nloc, const BoxParams& bp, const double* sfrac,
-                        const int* first, double* ext, int* ext_type, int* mapping) {
+                        const int* count, const int* first, double* ext, int* ext_type,
+                        int* mapping, int* nall) {
   if (nloc <= 0 || bp.nshift <= 0) return;
   int spb = 1;
   const dim3 grid = ghost_grid(nloc, bp, &spb);
-  hipLaunchKernelGGL(k_ghost_place, grid, dim3(kGhostTile), 0, st, nloc, spb, bp, sfrac, first,
-                     ext, ext_type, mapping);
+  hipLaunchKernelGGL(k_ghost_place, grid, dim3(kGhostTile), 0, st, nloc, spb, bp, sfrac, count,
+                     first, ext, ext_type, mapping, nall);
   DPAMD_LAUNCH_CHECK();
 }
 
@@ -746,20 +760,6 @@ void launch_cell_order(hipStream_t st, int ncell, const int* cell_start, CellAto
   if (ncell <= 0) return;
   hipLaunchKernelGGL(k_cell_order, dim3((unsigned)(((long)ncell * 64 + 255) / 256)), dim3(256), 0,
                      st, ncell, cell_start, sorted);
-  DPAMD_LAUNCH_CHECK();
-}
-
-// nall = nloc + (exclusive scan of the ghost flags at the last candidate) +
-// (that candidate's own flag)
-__global__ void k_ghost_total(int nloc, long nf, const int* __restrict__ flags,
-                              const int* __restrict__ pos, int* __restrict__ nall) {
-  if (threadIdx.x == 0) *nall = nloc + pos[nf - 1] + flags[nf - 1];
-}
-
-void launch_ghost_total(hipStream_t st, int nloc, long nf, const int* flags, const int* pos,
-                        int* nall) {
-  if (nf <= 0) return;
-  hipLaunchKernelGGL(k_ghost_total, dim3(1), dim3(64), 0, st, nloc, nf, flags, pos, nall);
   DPAMD_LAUNCH_CHECK();
 }
 

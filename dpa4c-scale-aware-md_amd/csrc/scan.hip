@@ -118,8 +118,10 @@ void exclusive_scan_int(hipStream_t st, const int* in, int* out, int n, void* te
   if (temp_bytes < sizeof(int) * (size_t)nb)
     throw HipError{hipErrorInvalidValue, "exclusive_scan_int: temporary buffer too small"};
   int* part = static_cast<int*>(temp);
-  hipLaunchKernelGGL(k_scan_parts, dim3(nb), dim3(kScanThreads), 0, st, in, n, part);
-  DPAMD_LAUNCH_CHECK();
+  if (nb > 1) {  // (a single tile has no earlier tiles to add up)
+    hipLaunchKernelGGL(k_scan_parts, dim3(nb), dim3(kScanThreads), 0, st, in, n, part);
+    DPAMD_LAUNCH_CHECK();
+  }
   hipLaunchKernelGGL(k_scan_tiles, dim3(nb), dim3(kScanThreads), 0, st, in, n, part, out);
   DPAMD_LAUNCH_CHECK();
 }
