@@ -35,7 +35,8 @@ EXPORTED = ("dp_create", "dp_destroy", "dp_get_info", "dp_last_error", "dp_compu
             "dp_compute_device_noalloc", "dp_sync",
             "dp_graph_stats", "dp_compute_canonical_graph_device", "dp_compute_edges_device",
             "dp_compute_edges_device_f32",
-            "dp_debug_copy", "dp_debug_keep", "dp_stage_times", "dp_device_bytes")
+            "dp_debug_copy", "dp_debug_keep", "dp_debug_fused_rows", "dp_stage_times",
+            "dp_device_bytes")
 
 
 class DeepmdException(RuntimeError):
@@ -78,6 +79,7 @@ def lib():
         L.dp_debug_copy.argtypes = [P, I, P, C.c_size_t]
         L.dp_debug_copy.restype = C.c_long
         L.dp_debug_keep.argtypes = [P, I]
+        L.dp_debug_fused_rows.argtypes = [P, I]
         L.dp_stage_times.argtypes = [P, I, P, I, P, C.c_size_t]
         L.dp_device_bytes.argtypes = [P]
         L.dp_device_bytes.restype = C.c_size_t
@@ -276,6 +278,11 @@ class DeepPot:
         """Store the per-slot edge gradients of the evaluations that follow, so
         stage(STAGE_EDGE_GRAD) can return them (dp_debug_keep)."""
         self._check(lib().dp_debug_keep(self._h, 1 if on else 0))
+
+    def set_fused_rows(self, rows):
+        """fp64 se_e2_a: use the fused dE/dD -> dE/dT kernel when every atom
+        type has at least `rows` atoms (0: always; dp_debug_fused_rows)."""
+        self._check(lib().dp_debug_fused_rows(self._h, int(rows)))
 
     def enable_stage_timing(self, on=True):
         times = (C.c_double * 16)()

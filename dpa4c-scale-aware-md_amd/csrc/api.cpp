@@ -147,6 +147,9 @@ struct dp_model {
   // eg_valid: the last evaluation left them in edge_grad
   bool keep_edge_grad = false;
   bool eg_valid = false;
+  // dp_debug_fused_rows: smallest type (rows) for which the fp64 fitting uses
+  // the fused dE/dD -> dE/dT kernel
+  int fused_ddt_rows = 12288;
   bool dd_valid = false;  // dE/dD of the last evaluation is in dD
   // stage timers
   bool timing = false;
@@ -371,8 +374,20 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   const bool d_from_t = axis == 16;
   E* D = d_from_t ? nullptr : need<E>(M, M->D, (size_t)std::max(nb, 1) * Dn);
   // fp64 with the fused input-gradient kernel: dE/dD is not stored (only
-  // when kept for inspection)
-  const bool fused_ddt = d_from_t && (f32 ? M->fitf_off[0][0][1] >= 0 : M->d_w0t != nullptr);
+  // when kept for inspection). In fp64 a type of few rows gives the fused
+  // kernel too few blocks (it splits its column groups instead), and the
+  // plain product dE/dD = dZ0 W0^T followed by the dE/dT pass is faster:
+  // water-5k 1.09 -> 1.01 ms/step, water-12k 1.96 -> 1.90; equal at 24k and
+  // slower from 98k (queued steps, one box). So fp64 takes the fused kernel
+  // when every type has at least fused_ddt_rows rows.
+  int min_rows = nb;
+  for (int t = 0; t < nt; ++t) {
+    const int rows = M->type_off[t + 1] - M->type_off[t];
+    if (rows > 0) min_rows = std::min(min_rows, rows);
+  }
+  const bool fused_ddt =
+      d_from_t && (f32 ? M->fitf_off[0][0][1] >= 0
+                       : M->d_w0t != nullptr && min_rows >= M->fused_ddt_rows);
   E* dD = (!fused_ddt || M->keep_edge_grad) ? need<E>(M, M->dD, (size_t)std::max(nb, 1) * Dn)
                                             : nullptr;
   E* dT = need<E>(M, M->dT, (size_t)nloc * 4 * L3);
@@ -485,15 +500,30 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   // concurrently)
   E* split_ws = ws_need ? need<E>(M, M->split_ws, ws_need) : nullptr;
   const bool fork = active > 1 && !M->arena_on;
+  // With the plain dE/dD product (few rows per type) the type with the most
+  // rows stays on the evaluation stream, enqueued last, and only the others
+  // wait for the fork event (water-12k 1.95 -> 1.91 ms/step); with the fused
+  // kernel every type runs on a stream of its own (keeping one on the
+  // evaluation stream measured 0.3-0.7 % slower on HEA-128k and water-393k).
+  int tmain = -1;
+  if (fork && !fused_ddt) {
+    tmain = 0;
+    for (int t = 1; t < nt; ++t)
+      if (M->type_off[t + 1] - M->type_off[t] > M->type_off[tmain + 1] - M->type_off[tmain])
+        tmain = t;
+  }
   if (fork) {
     if (!M->fork_ev) DPAMD_HIP(hipEventCreateWithFlags(&M->fork_ev, hipEventDisableTiming));
     DPAMD_HIP(hipEventRecord(M->fork_ev, st));
   }
-  for (int t = 0; t < nt; ++t) {
+  for (int q = 0; q < nt; ++q) {
+    // visiting order: every type but tmain, then tmain
+    const int t = tmain < 0 ? q : (q < tmain ? q : (q + 1 < nt ? q + 1 : tmain));
     const int rows = M->type_off[t + 1] - M->type_off[t];
     if (rows <= 0) continue;
+    const bool side = fork && t != tmain;
     hipStream_t fst = st;
-    if (fork) {
+    if (side) {
       if (!M->fit_st[t]) {
         DPAMD_HIP(hipStreamCreateWithFlags(&M->fit_st[t], hipStreamNonBlocking));
         DPAMD_HIP(hipEventCreateWithFlags(&M->join_ev[t], hipEventDisableTiming));
@@ -549,11 +579,12 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
     launch_fitting(fst, net, rows, d_from_t ? nullptr : D + r0 * Dn,
                    d_from_t ? Tt + r0 * 4 : nullptr, 4L * nb, L3, fb, dD ? dD + r0 * Dn : nullptr,
                    e_bucket + r0, fused_ddt ? &ddt : nullptr);
-    if (fork) {
-      DPAMD_HIP(hipEventRecord(M->join_ev[t], fst));
-      DPAMD_HIP(hipStreamWaitEvent(st, M->join_ev[t], 0));
-    }
+    if (side) DPAMD_HIP(hipEventRecord(M->join_ev[t], fst));
   }
+  if (fork)
+    for (int t = 0; t < nt; ++t)
+      if (t != tmain && M->type_off[t + 1] > M->type_off[t])
+        DPAMD_HIP(hipStreamWaitEvent(st, M->join_ev[t], 0));
   record(M, st, kStFit + 1);
 
   if (!fused_ddt) launch_dT(st, nb, L3, axis, items, Tt, dD, dT);
@@ -1762,6 +1793,12 @@ size_t dp_device_bytes(const dp_model* M) { return M ? M->bytes_peak : 0; }
 int dp_debug_keep(dp_model* M, int keep) {
   if (!M) return DP_ERR_ARG;
   M->keep_edge_grad = keep != 0;
+  return DP_OK;
+}
+
+int dp_debug_fused_rows(dp_model* M, int rows) {
+  if (!M || rows < 0) return DP_ERR_ARG;
+  M->fused_ddt_rows = rows;
   return DP_OK;
 }
 

@@ -305,6 +305,15 @@ long dp_debug_copy(dp_model* model, int stage, void* dst, size_t capacity);
  * reference: a parity-test hook, like dp_debug_copy. */
 int dp_debug_keep(dp_model* model, int keep);
 
+/* se_e2_a in fp64 forms dE/dT from the fitting's input gradient with a fused
+ * kernel (dE/dD never stored) when every atom type has at least `rows` atoms
+ * (default 12288; 0: always), and otherwise as the plain product
+ * dE/dD = dZ0 W0^T followed by a separate dE/dT pass, which is faster for
+ * few atoms per type. Both forms give the same results to rounding. No
+ * counterpart in the reference: a parity-test hook, so that both forms are
+ * checked at the sizes the oracle evaluates. */
+int dp_debug_fused_rows(dp_model* model, int rows);
+
 /* Per-stage GPU time in milliseconds (hipEvent pairs) of the last synchronous
  * evaluation, or the mean over the evaluations queued by
  * dp_compute_device_async up to the last dp_sync, filled into times[0..n-1] in

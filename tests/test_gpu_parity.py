@@ -16,7 +16,7 @@ F_TOL = 1e-8    # eV/A
 V_TOL = 1e-8    # eV
 
 
-def _run(dp, orc, case, keep=False):
+def _run(dp, orc, case, keep=False, fused=False):
     (coord, atype, box), m = CASES[case]()
     mb = model_bytes(m)
     O = orc.Oracle(mb)
@@ -24,6 +24,10 @@ def _run(dp, orc, case, keep=False):
     pot = dp.DeepPot(file_content=mb)
     if keep:
         pot.keep_stages(True)
+    if fused:
+        # the fused dE/dD -> dE/dT kernel at this size too (by default a
+        # system this small takes the plain product and the dE/dT pass)
+        pot.set_fused_rows(0)
     e, f, v, ae, av = pot.compute(coord, atype, box, atomic=True)
     return O, ref, pot, (e, f, v, ae, av), (coord, atype, box)
 
@@ -42,9 +46,10 @@ def test_nlist_bit_exact(dp, orc, case):
     assert np.array_equal(nl, ref["nlist"])
 
 
+@pytest.mark.parametrize("fused", [False, True], ids=["plain_dD", "fused_dDdT"])
 @pytest.mark.parametrize("case", list(CASES))
-def test_energy_force_virial(dp, orc, case):
-    O, ref, pot, (e, f, v, ae, av), (coord, atype, box) = _run(dp, orc, case)
+def test_energy_force_virial(dp, orc, case, fused):
+    O, ref, pot, (e, f, v, ae, av), (coord, atype, box) = _run(dp, orc, case, fused=fused)
     n = len(atype)
     assert abs(e - ref["energy"]) / n <= E_TOL
     assert np.abs(ae - ref["atom_energy"]).max() <= E_TOL
@@ -53,9 +58,11 @@ def test_energy_force_virial(dp, orc, case):
     assert np.abs(av - ref["atom_virial"]).max() <= V_TOL
 
 
+@pytest.mark.parametrize("fused", [False, True], ids=["plain_dD", "fused_dDdT"])
 @pytest.mark.parametrize("case", ["water192", "cu864"])
-def test_stage_parity(dp, orc, case):
-    O, ref, pot, (e, f, v, ae, av), (coord, atype, box) = _run(dp, orc, case, keep=True)
+def test_stage_parity(dp, orc, case, fused):
+    O, ref, pot, (e, f, v, ae, av), (coord, atype, box) = _run(dp, orc, case, keep=True,
+                                                                fused=fused)
     n = len(atype)
     d = pot.stage(dp.STAGE_DESCRPT, np.float64, (n, O.ndescrpt))
     np.testing.assert_allclose(d, ref["descrpt"], rtol=0, atol=1e-12)
@@ -65,6 +72,8 @@ def test_stage_parity(dp, orc, case):
     np.testing.assert_allclose(eg, ref["edge_grad"], rtol=0, atol=1e-11)
     # keeping the edge gradients changes no output
     pot2 = dp.DeepPot(file_content=model_bytes(CASES[case]()[1]))
+    if fused:
+        pot2.set_fused_rows(0)
     e2, f2, v2, ae2, av2 = pot2.compute(coord, atype, box, atomic=True)
     assert e2 == e and np.array_equal(f2, f) and np.array_equal(v2, v)
     assert np.array_equal(av2, av)
