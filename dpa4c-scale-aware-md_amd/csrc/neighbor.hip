@@ -67,6 +67,22 @@ __device__ __forceinline__ void decode_shift(const BoxParams& bp, int s, int* n)
   n[2] = q / (wa * wb) - bp.nrep[2];
 }
 
+// The shift after n in decode_shift's order (an odometer over the image
+// vectors that skips the zero vector): a block walking consecutive shifts
+// decodes only its first.
+__device__ __forceinline__ void next_shift(const BoxParams& bp, int* n) {
+  for (int rep = 0; rep < 2; ++rep) {
+    if (++n[0] > bp.nrep[0]) {
+      n[0] = -bp.nrep[0];
+      if (++n[1] > bp.nrep[1]) {
+        n[1] = -bp.nrep[1];
+        ++n[2];
+      }
+    }
+    if (n[0] != 0 || n[1] != 0 || n[2] != 0) return;
+  }
+}
+
 // Whether image s of atom k lies in the extended region.
 __device__ __forceinline__ bool ghost_in(const BoxParams& bp, const double* __restrict__ sfrac,
                                          int k, const int (&n)[3]) {
@@ -96,9 +112,9 @@ __global__ __launch_bounds__(kGhostTile) void k_ghost_count(int nloc, int spb, B
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int k = blockIdx.x * kGhostTile + threadIdx.x;
   const int s0 = blockIdx.y * spb, s1 = min(bp.nshift, s0 + spb);
-  for (int s = s0; s < s1; ++s) {
-    int n[3];
-    decode_shift(bp, s, n);
+  int n[3];
+  decode_shift(bp, s0, n);
+  for (int s = s0; s < s1; ++s, next_shift(bp, n)) {
     const bool in = k < nloc && ghost_in(bp, sfrac, k, n);
     const int c = __popcll(__ballot(in));  // (every lane votes: outside the lane-0 branch)
     if (lane == 0) wc[s & 1][w] = c;
@@ -136,9 +152,9 @@ __global__ __launch_bounds__(kGhostTile) void k_ghost_place(int nloc, int spb, B
     x2 = ext[3 * k + 2];
     tk = ext_type[k];
   }
-  for (int s = s0; s < s1; ++s) {
-    int n[3];
-    decode_shift(bp, s, n);
+  int n[3];
+  decode_shift(bp, s0, n);
+  for (int s = s0; s < s1; ++s, next_shift(bp, n)) {
     const bool in = k < nloc && ghost_in(bp, sfrac, k, n);
     const unsigned long long m = __ballot(in);
     if (lane == 0) wc[s & 1][w] = __popcll(m);
