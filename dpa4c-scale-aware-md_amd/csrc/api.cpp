@@ -784,10 +784,6 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
   if (nloc + nf >= (1L << 31) - 1) throw ApiError{DP_ERR_CAPACITY, "too many ghost candidates"};
   const int nall_cap = nloc + (int)nf;
   const NlParams np = nl_params_cells(M);
-  // the candidate-order list addresses the cell-sorted records with 32-bit
-  // byte offsets
-  if (np.unsorted && (long)nall_cap * (long)sizeof(CellAtom) >= (1L << 32))
-    throw ApiError{DP_ERR_CAPACITY, "too many atoms and ghosts for the neighbour list"};
   double* sfrac = need<double>(M, M->sfrac, (size_t)nloc * 3);
   double* ext = need<double>(M, M->ext, (size_t)nall_cap * 3);
   int* ext_type = need<int>(M, M->ext_type, (size_t)nall_cap);
@@ -826,7 +822,7 @@ int build_standalone_nlist(dp_model* M, hipStream_t st, int nloc, const double* 
   record(M, st, kStGeom + 1);
   int* nlist = need<int>(M, M->nlist, (size_t)std::max(nloc, 1) * m.nnei);
   int* nreal = need<int>(M, M->nreal, (size_t)std::max(nloc, 1) * m.ntypes);
-  launch_nlist_cells(st, nloc, bp, np, ext, ext_type, cell_of, cstart, sorted, nlist, nreal,
+  launch_nlist_cells(st, nloc, bp, np, ext, ext_type, cell_of, cstart, sorted, nall, nlist, nreal,
                      static_cast<int*>(M->status.p));
   record(M, st, kStNlist + 1);
   return nall;

@@ -135,9 +135,11 @@ void launch_cell_scatter(hipStream_t, int cap, const int* d_count, const int* ce
 void launch_cell_order(hipStream_t, int ncell, const int* cell_start, CellAtom* sorted);
 // p[0 .. n) = v (a kernel rather than a memset node, so it can be captured)
 void launch_fill_int(hipStream_t, long n, int v, int* p);
+// (sorted_cap: the capacity of `sorted` in records)
 void launch_nlist_cells(hipStream_t, int nloc, const BoxParams&, const NlParams&, const double* ext,
                         const int* ext_type, const int* cell_of, const int* cell_start,
-                        const CellAtom* sorted, int* nlist, int* nreal, int* status);
+                        const CellAtom* sorted, long sorted_cap, int* nlist, int* nreal,
+                        int* status);
 void launch_nlist_csr(hipStream_t, int nloc, const NlParams&, const double* ext, const int* ext_type,
                       const long* cand_off, const int* cand, int* nlist, int* nreal, int* status);
 

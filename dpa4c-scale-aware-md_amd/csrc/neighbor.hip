@@ -17,6 +17,8 @@
 // first sel[t] of type t fill section t, the rest -1.
 #include "kernels.h"
 
+#include <type_traits>
+
 namespace dpamd {
 
 __device__ __forceinline__ void to_frac(const BoxParams& bp, double x0, double x1, double x2,
@@ -328,6 +330,24 @@ __device__ __forceinline__ void nl_push(bool keep, double r2, int j, int t, int&
   n += __popcll(m);
 }
 
+// nl_push with the wave's keep mask given (the ballot of keep, formed by the
+// caller from single compares)
+__device__ __forceinline__ void nl_push_mask(unsigned long long m, bool keep, double r2, int j,
+                                             int t, int& n, NlKey* s) {
+  if (keep) {
+    const int q = n + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+    if (q < kMaxCand) {
+      NlKey e;
+      e.key = nl_pack(t, r2);
+      e.j = j;
+      e.t = t;
+      s[q] = e;
+    }
+  }
+  n += __popcll(m);
+}
+
 // Rank = #{keys below} + #{equal keys with a smaller index}. The first pass
 // counts keys below only; equal keys are rare (exact r^2 ties), so each
 // candidate then claims the LDS slot of its rank, and only if two candidates
@@ -458,12 +478,93 @@ __device__ __forceinline__ void nl_empty_row(const NlParams& np, int i, int* __r
   if (lane < np.ntypes) nreal[(long)i * np.ntypes + lane] = 0;
 }
 
+// The stencil runs of centre cell ci: lane k < 9 gets run k's first sorted
+// index (rbeg) and length (rcnt), and every lane the inclusive prefix of the
+// lengths over lanes 0..lane (incl).
+__device__ __forceinline__ void stencil_runs(const BoxParams& bp, int ci, int lane,
+                                             const int* __restrict__ cell_start, int& rbeg,
+                                             int& rcnt, int& incl) {
+  const int c0 = ci % bp.ncell[0], c1 = (ci / bp.ncell[0]) % bp.ncell[1];
+  const int c2 = ci / (bp.ncell[0] * bp.ncell[1]);
+  rbeg = 0;
+  rcnt = 0;
+  if (lane < 9) {
+    const int y = c1 + lane % 3 - 1, z = c2 + lane / 3 - 1;
+    if (y >= 0 && y < bp.ncell[1] && z >= 0 && z < bp.ncell[2]) {
+      const int x0 = c0 > 0 ? c0 - 1 : 0, x1 = c0 + 1 < bp.ncell[0] ? c0 + 1 : bp.ncell[0] - 1;
+      const int rowc = (z * bp.ncell[1] + y) * bp.ncell[0];
+      rbeg = cell_start[rowc + x0];
+      rcnt = cell_start[rowc + x1 + 1] - rbeg;
+    }
+  }
+  incl = rcnt;
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) {
+    const int v = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += v;
+  }
+}
+
+// Where candidate q of the concatenated runs lies in the cell-sorted array.
+// The runs' offsets live in a register table (lane k: run k; lanes 9, 10: the
+// end, as sentinels) read with a wave-uniform lane index, and a wave-uniform
+// cursor follows the run that holds each batch's first candidate: a lane
+// then needs one compare and select for the next boundary, and a batch that
+// reaches past a second boundary (a run shorter than the batch, or an empty
+// run) takes the general path over the later boundaries. Batches must be
+// visited in increasing order.
+struct RunCursor {
+  int roffv, rdelv;  // lane k < 9: run k starts at roffv; candidate q is sorted[q + rdelv]
+  int k, dcur, onext, dnext;
+  __device__ __forceinline__ RunCursor(int lane, int incl, int rcnt, int rbeg, int total) {
+    roffv = lane < 9 ? incl - rcnt : total;
+    rdelv = rbeg - roffv;
+    k = 0;
+    dcur = __builtin_amdgcn_readlane(rdelv, 0);
+    onext = __builtin_amdgcn_readlane(roffv, 1);
+    dnext = __builtin_amdgcn_readlane(rdelv, 1);
+  }
+  // sorted index of candidate qc of the batch starting at b (qc < total)
+  __device__ __forceinline__ int locate(int b, int qc) {
+    while (onext <= b) {  // wave-uniform; empty runs are passed over here
+      ++k;
+      dcur = dnext;
+      onext = __builtin_amdgcn_readlane(roffv, k + 1);
+      dnext = __builtin_amdgcn_readlane(rdelv, k + 1);
+    }
+    int at = qc + dcur + (qc >= onext ? dnext - dcur : 0);
+    if (__builtin_amdgcn_readlane(roffv, k + 2) < b + kWave) {
+      asm volatile("");  // rare: kept as a branch, not evaluated for every batch
+      for (int kk = k + 2; kk < 9; ++kk) {
+        const int o = __builtin_amdgcn_readlane(roffv, kk);
+        if (o >= b + kWave) break;
+        if (qc >= o) at = qc + __builtin_amdgcn_readlane(rdelv, kk);
+      }
+    }
+    return at;
+  }
+};
+
+// Record `at` of the cell-sorted array: by a 32-bit byte offset from the
+// array's (wave-uniform) base, one address instruction per lane, unless the
+// array's capacity reaches 2^32 bytes (Wide).
+template <bool Wide>
+__device__ __forceinline__ CellAtom load_cand(const CellAtom* __restrict__ sorted, int at) {
+  if constexpr (Wide) return sorted[at];
+  return *reinterpret_cast<const CellAtom*>(reinterpret_cast<const char*>(sorted) +
+                                            (unsigned)at * (unsigned)sizeof(CellAtom));
+}
+
 // The 27-cell stencil as 9 contiguous runs of the cell-sorted atoms (cells
 // x-1..x+1 of one (y, z) row are adjacent in cell order). Lanes 0..8 read the
-// run bounds at once; candidate q of the concatenated runs is then found by
-// counting run offsets <= q, so the candidates of a wave-wide batch are loaded
-// independently (four rounds of 64 in flight) instead of cell after cell.
-// Candidate order does not matter: the rank pass orders by (type, r^2, j).
+// run bounds at once (stencil_runs); candidate q of the concatenated runs is
+// then found through RunCursor, so the candidates of a wave-wide batch are
+// loaded independently (four rounds of 64 in flight) instead of cell after
+// cell. The keep test is a set of single compares whose lane masks are ANDed
+// on the scalar unit (a ballot of a combined boolean costs two instructions
+// to rebuild the mask). Candidate order does not matter: the rank pass orders
+// by (type, r^2, j).
+template <bool Wide>
 __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells(
     int nloc, BoxParams bp, NlParams np, const double* __restrict__ ext,
     const int* __restrict__ ext_type, const int* __restrict__ cell_of,
@@ -479,59 +580,37 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells(
     return;
   }
   const double xi = ext[3 * i], yi = ext[3 * i + 1], zi = ext[3 * i + 2];
-  const int ci = cell_of[i];
-  const int c0 = ci % bp.ncell[0], c1 = (ci / bp.ncell[0]) % bp.ncell[1];
-  const int c2 = ci / (bp.ncell[0] * bp.ncell[1]);
-  int rbeg = 0, rcnt = 0;
-  if (lane < 9) {
-    const int y = c1 + lane % 3 - 1, z = c2 + lane / 3 - 1;
-    if (y >= 0 && y < bp.ncell[1] && z >= 0 && z < bp.ncell[2]) {
-      const int x0 = c0 > 0 ? c0 - 1 : 0, x1 = c0 + 1 < bp.ncell[0] ? c0 + 1 : bp.ncell[0] - 1;
-      const int rowc = (z * bp.ncell[1] + y) * bp.ncell[0];
-      rbeg = cell_start[rowc + x0];
-      rcnt = cell_start[rowc + x1 + 1] - rbeg;
-    }
-  }
-  int incl = rcnt;
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) {
-    const int v = __shfl_up(incl, off, kWave);
-    if (lane >= off) incl += v;
-  }
-  const int total = __shfl(incl, 8, kWave);
-  int roff[9], rdel[9];  // run start in the concatenation, and sorted index - q
-#pragma unroll
-  for (int k = 0; k < 9; ++k) {
-    roff[k] = __shfl(incl - rcnt, k, kWave);
-    rdel[k] = __shfl(rbeg, k, kWave) - roff[k];
-  }
+  int rbeg, rcnt, incl;
+  stencil_runs(bp, cell_of[i], lane, cell_start, rbeg, rcnt, incl);
+  const int total = __builtin_amdgcn_readlane(incl, 8);
+  RunCursor rc(lane, incl, rcnt, rbeg, total);
+  const unsigned nt = (unsigned)np.ntypes;
   int n = 0;
   for (int base = 0; base < total; base += 4 * kWave) {
     CellAtom ca[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int q = base + kWave * u + lane;
-      ca[u].idx = -1;
-      if (q < total) {
-        int del = rdel[0];
-#pragma unroll
-        for (int k = 1; k < 9; ++k) del = roff[k] <= q ? rdel[k] : del;
-        ca[u] = sorted[q + del];
+      const int b = base + kWave * u;
+      if (b < total) {  // wave-uniform
+        const int qc = min(b + lane, total - 1);
+        ca[u] = load_cand<Wide>(sorted, rc.locate(b, qc));
       }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      bool keep = false;
-      double r2 = 0.0;
+      const int b = base + kWave * u;
+      if (b >= total) break;  // wave-uniform
       const int j = ca[u].idx, t = ca[u].type;
-      if (j >= 0) {
-        const double dx = ca[u].x - xi;
-        const double dy = ca[u].y - yi;
-        const double dz = ca[u].z - zi;
-        r2 = dx * dx + dy * dy + dz * dz;
-        keep = (j != i) && t >= 0 && t < np.ntypes && r2 <= np.rc2;
-      }
-      nl_push(keep, r2, j, t, n, lds.k[w]);
+      const double dx = ca[u].x - xi;
+      const double dy = ca[u].y - yi;
+      const double dz = ca[u].z - zi;
+      const double r2 = dx * dx + dy * dy + dz * dz;
+      // (bitwise, and ballots of single compares: each compare stays a lane
+      // mask, combined on the scalar unit)
+      const bool keep = (b + lane < total) & (j != i) & ((unsigned)t < nt) & (r2 <= np.rc2);
+      const unsigned long long m = __ballot(b + lane < total) & __ballot(j != i) &
+                                   __ballot((unsigned)t < nt) & __ballot(r2 <= np.rc2);
+      nl_push_mask(m, keep, r2, j, t, n, lds.k[w]);
     }
   }
   nl_place(np, i, n, lds.k[w], lds.claim[w], nlist, nreal, status);
@@ -543,18 +622,11 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells(
 // the wave's row in LDS (nnei ints per wave: no candidate array, so the LDS
 // does not limit residency) and copied out whole at the end; no global store
 // is issued inside the scan, so no candidate load waits behind one (the vector
-// memory counter is in order). The runs' offsets live in a register table
-// (lane k: run k; lanes 9, 10: the end, as sentinels) read with a wave-uniform
-// lane index, and a wave-uniform cursor follows the run that holds each
-// batch's first candidate: a lane then needs one compare and select for the
-// next boundary, and a batch that reaches past a second boundary (a run shorter
-// than the batch, or an empty run) takes the general path over the later
-// boundaries. Lanes past the last candidate load the last one again and are
-// not kept. Output, status bits and section order are those of k_nlist_cells
+// memory counter is in order). Candidates are found through RunCursor;
+// lanes past the last candidate load the last one again and are not kept. Output, status bits and section order are those of k_nlist_cells
 // with unsorted set: candidates in concatenation order, at most sel[t] per
-// type, the rest -1. The record offsets are 32-bit (the host limits the
-// extended atoms to 2^27). NT is the model's type count (np.ntypes).
-template <int NT>
+// type, the rest -1. NT is the model's type count (np.ntypes).
+template <int NT, bool Wide>
 __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells_seq(
     int nloc, BoxParams bp, NlParams np, const double* __restrict__ ext,
     const int* __restrict__ ext_type, const int* __restrict__ cell_of,
@@ -573,58 +645,13 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells_seq(
   int* lrow = nl_rows + w * nnei;
   for (int s = lane; s < nnei; s += kWave) lrow[s] = -1;
   const double xi = ext[3 * i], yi = ext[3 * i + 1], zi = ext[3 * i + 2];
-  const int ci = cell_of[i];
-  const int c0 = ci % bp.ncell[0], c1 = (ci / bp.ncell[0]) % bp.ncell[1];
-  const int c2 = ci / (bp.ncell[0] * bp.ncell[1]);
-  int rbeg = 0, rcnt = 0;
-  if (lane < 9) {
-    const int y = c1 + lane % 3 - 1, z = c2 + lane / 3 - 1;
-    if (y >= 0 && y < bp.ncell[1] && z >= 0 && z < bp.ncell[2]) {
-      const int x0 = c0 > 0 ? c0 - 1 : 0, x1 = c0 + 1 < bp.ncell[0] ? c0 + 1 : bp.ncell[0] - 1;
-      const int rowc = (z * bp.ncell[1] + y) * bp.ncell[0];
-      rbeg = cell_start[rowc + x0];
-      rcnt = cell_start[rowc + x1 + 1] - rbeg;
-    }
-  }
-  int incl = rcnt;
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) {
-    const int v = __shfl_up(incl, off, kWave);
-    if (lane >= off) incl += v;
-  }
+  int rbeg, rcnt, incl;
+  stencil_runs(bp, cell_of[i], lane, cell_start, rbeg, rcnt, incl);
   const int total = __builtin_amdgcn_readlane(incl, 8);
-  // lane k < 9: run k starts at roffv of the concatenation and its candidate q
-  // is sorted[q + rdelv]; lanes 9 and 10 start at total
-  const int roffv = lane < 9 ? incl - rcnt : total;
-  const int rdelv = rbeg - roffv;
+  RunCursor rc(lane, incl, rcnt, rbeg, total);
   int put[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) put[t] = 0;
-  // cursor: run k holds the current batch's first candidate (dcur its offset),
-  // onext / dnext the next run's start and offset
-  int k = 0;
-  int dcur = __builtin_amdgcn_readlane(rdelv, 0);
-  int onext = __builtin_amdgcn_readlane(roffv, 1), dnext = __builtin_amdgcn_readlane(rdelv, 1);
-  // index into sorted of candidate qc (qc in the batch starting at b)
-  auto locate = [&](int b, int qc) {
-    while (onext <= b) {  // wave-uniform; empty runs are passed over here
-      ++k;
-      dcur = dnext;
-      onext = __builtin_amdgcn_readlane(roffv, k + 1);
-      dnext = __builtin_amdgcn_readlane(rdelv, k + 1);
-    }
-    int at = qc + dcur + (qc >= onext ? dnext - dcur : 0);
-    if (__builtin_amdgcn_readlane(roffv, k + 2) < b + kWave) {
-      asm volatile("");  // rare: kept as a branch, not evaluated for every batch
-      for (int kk = k + 2; kk < 9; ++kk) {
-        const int o = __builtin_amdgcn_readlane(roffv, kk);
-        if (o >= b + kWave) break;
-        if (qc >= o) at = qc + __builtin_amdgcn_readlane(rdelv, kk);
-      }
-    }
-    return at;
-  };
-  const char* sbytes = reinterpret_cast<const char*>(sorted);
   for (int base = 0; base < total; base += 2 * kWave) {
     CellAtom ca[2];
 #pragma unroll
@@ -632,8 +659,7 @@ __global__ __launch_bounds__(kNlWaves * 64) void k_nlist_cells_seq(
       const int b = base + kWave * u;
       if (b < total) {  // wave-uniform
         const int qc = min(b + lane, total - 1);
-        const unsigned at = (unsigned)locate(b, qc);
-        ca[u] = *reinterpret_cast<const CellAtom*>(sbytes + at * (unsigned)sizeof(CellAtom));
+        ca[u] = load_cand<Wide>(sorted, rc.locate(b, qc));
       }
     }
 #pragma unroll
@@ -792,29 +818,36 @@ void launch_fill_int(hipStream_t st, long n, int v, int* p) {
 
 void launch_nlist_cells(hipStream_t st, int nloc, const BoxParams& bp, const NlParams& np,
                         const double* ext, const int* ext_type, const int* cell_of,
-                        const int* cell_start, const CellAtom* sorted, int* nlist, int* nreal,
-                        int* status) {
+                        const int* cell_start, const CellAtom* sorted, long sorted_cap,
+                        int* nlist, int* nreal, int* status) {
   if (nloc <= 0) return;
   const dim3 grid((nloc + kNlWaves - 1) / kNlWaves), block(kNlWaves * 64);
-  if (np.unsorted) {
-    const size_t lds = kNlWaves * np.nnei * sizeof(int);
-    auto go = [&](auto kernel) {
-      hipLaunchKernelGGL(kernel, grid, block, lds, st, nloc, bp, np, ext, ext_type, cell_of,
-                         cell_start, sorted, nlist, nreal, status);
-    };
-    switch (np.ntypes) {
-      case 1: go(k_nlist_cells_seq<1>); break;
-      case 2: go(k_nlist_cells_seq<2>); break;
-      case 3: go(k_nlist_cells_seq<3>); break;
-      case 4: go(k_nlist_cells_seq<4>); break;
-      case 5: go(k_nlist_cells_seq<5>); break;
-      case 6: go(k_nlist_cells_seq<6>); break;
-      case 7: go(k_nlist_cells_seq<7>); break;
-      default: go(k_nlist_cells_seq<kMaxTypes>); break;
-    }
-  } else
-    hipLaunchKernelGGL(k_nlist_cells, grid, block, 0, st, nloc, bp, np, ext, ext_type, cell_of,
+  const bool wide = sorted_cap * (long)sizeof(CellAtom) >= (1L << 32);
+  const size_t lds = np.unsorted ? kNlWaves * np.nnei * sizeof(int) : 0;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, nloc, bp, np, ext, ext_type, cell_of,
                        cell_start, sorted, nlist, nreal, status);
+  };
+  auto seq = [&](auto wide_tag) {
+    constexpr bool W = decltype(wide_tag)::value;
+    switch (np.ntypes) {
+      case 1: go(k_nlist_cells_seq<1, W>); break;
+      case 2: go(k_nlist_cells_seq<2, W>); break;
+      case 3: go(k_nlist_cells_seq<3, W>); break;
+      case 4: go(k_nlist_cells_seq<4, W>); break;
+      case 5: go(k_nlist_cells_seq<5, W>); break;
+      case 6: go(k_nlist_cells_seq<6, W>); break;
+      case 7: go(k_nlist_cells_seq<7, W>); break;
+      default: go(k_nlist_cells_seq<kMaxTypes, W>); break;
+    }
+  };
+  if (np.unsorted) {
+    if (wide) seq(std::true_type{});
+    else seq(std::false_type{});
+  } else {
+    if (wide) go(k_nlist_cells<true>);
+    else go(k_nlist_cells<false>);
+  }
   DPAMD_LAUNCH_CHECK();
 }
 
