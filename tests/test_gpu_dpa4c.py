@@ -98,6 +98,42 @@ def test_standalone_parity(dp, case):
         assert np.array_equal(np.asarray(a), np.asarray(b))
 
 
+@pytest.mark.parametrize("ncell,rcut,min_big", [(6, 9.0, 65), (8, 10.5, 129)])
+def test_large_cells(dp, ncell, rcut, min_big):
+    """Cells of more than 64 and more than 128 atoms (cutoffs of 9 and 10.5 A
+    on Cu-Ni, 4 cells per side of 9.8 and 12.4 A): the cell order then ranks
+    two or eight records per lane, and the neighbour list walks runs longer
+    than a batch. Parity with the oracle, exact edge sets, and a fresh handle
+    reproducing the list and every output bit for bit."""
+    coord, atype, box = dp.systems.fcc_alloy((ncell, ncell, ncell), 3.56, seed=31)
+    m = dp.dpa4c.random_model("cuni", seed=330, rcut=rcut, sel=[300, 300])
+    mb = dp.dpa4c.to_bytes(m)
+    ref = C4.Dpa4cOracle(mb).compute(coord, atype, box)
+    pot = dp.DeepPot(file_content=mb)
+    got = pot.compute(coord, atype, box, atomic=True)
+    n = len(atype)
+    _check(ref, got, n, _volume(box))
+    # the cells really are that large: bin the extended atoms as the library
+    # does (orthorhombic box: cells of (L + 2 rcut) / floor((L + 2 rcut) / rcut))
+    nall = len(ref["ext_type"])
+    ext = pot.stage(dp.STAGE_EXT_COORD, np.float64, (nall, 3))
+    L = np.diag(np.asarray(box, np.float64).reshape(3, 3))
+    nc = np.floor((L + 2 * rcut) / (rcut * (1 + 1e-6))).astype(int)
+    cell = np.floor((ext + rcut) / ((L + 2 * rcut) / nc)).astype(int)
+    cell = np.clip(cell, 0, nc - 1)
+    counts = np.bincount((cell[:, 2] * nc[1] + cell[:, 1]) * nc[0] + cell[:, 0])
+    assert counts.max() >= min_big, counts.max()
+    nl = pot.stage(dp.STAGE_NLIST, np.int32, (n, pot.nnei))
+    for i in range(0, n, 7):
+        row = nl[i][nl[i] >= 0]
+        assert sorted(row.tolist()) == sorted(ref["src"][ref["dst"] == i].tolist()), i
+    pot2 = dp.DeepPot(file_content=mb)
+    got2 = pot2.compute(coord, atype, box, atomic=True)
+    assert np.array_equal(pot2.stage(dp.STAGE_NLIST, np.int32, (n, pot.nnei)), nl)
+    for a, b in zip(got, got2):
+        assert np.array_equal(np.asarray(a), np.asarray(b))
+
+
 @pytest.mark.parametrize("case", ["cu256", "hea250", "water24_smallbox", "cuni768"])
 def test_forces_with_and_without_atom_virials(dp, case):
     """The standalone force pass scatters each edge's neighbour side in fixed
