@@ -627,15 +627,29 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
         for (int q = 0; q < S::NQ2; ++q) X1s[c * X1LD + 4 * q + g] = x1[q];
         wave_lds_sync();
       }
-      // layer 2: tangent product only; tanh of the primal comes from the forward
+      // layer 2: tangent product only; tanh of the primal comes from the forward.
+      // The weight fragments are read from LDS one k-step ahead of their
+      // MFMAs, held there by scheduling fences (compiled freely, each pair of
+      // MFMAs waited for its own reads).
       d4 acc2t[S::NT2];
 #pragma unroll
       for (int t = 0; t < S::NT2; ++t) acc2t[t] = d4{0.0, 0.0, 0.0, 0.0};
+      {
+        double w2b[2][NT2M > 0 ? NT2M : 1];
+        const double* W2 = P + S::OFF_W2 + g * S::L2P + c;
 #pragma unroll
-      for (int q = 0; q < S::NQ2; ++q) {
+        for (int t = 0; t < NT2M; ++t) w2b[0][t] = W2[16 * t];
 #pragma unroll
-        for (int t = 0; t < NT2M; ++t)
-          acc2t[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1t[q], acc2t[t]);
+        for (int q = 0; q < S::NQ2; ++q) {
+          if (q + 1 < S::NQ2) {
+#pragma unroll
+            for (int t = 0; t < NT2M; ++t) w2b[(q + 1) & 1][t] = W2[4 * (q + 1) * S::L2P + 16 * t];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int t = 0; t < NT2M; ++t) acc2t[t] = mfma_f64(w2b[q & 1][t], x1t[q], acc2t[t]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
       if constexpr (T2V) {
         // tangent of the tail features 16 NT2M + j (lane group g: j = g, register 0)
