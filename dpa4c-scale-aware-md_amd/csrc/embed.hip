@@ -730,9 +730,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
             for (int uu = 0; uu < kU3B; ++uu)
               wnxt[uu] = u0 + uu < U3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
           }
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int uu = 0; uu < kU3B; ++uu)
             if (u0 + uu < U3) acc3t[uu] = mfma_f64(wcur[uu], x2t[q / 4][q % 4], acc3t[uu]);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = wnxt[uu];
         }
