@@ -710,33 +710,48 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
             }
           }
       }
-      // layer 3 tangent, transposed; tanh part of G from the forward
+      // layer 3 tangent, transposed; tanh part of G from the forward.
+      // The weight fragments stream one k-step ahead of their MFMAs across
+      // the output tile groups too (the next group's first fragment is read
+      // during this group's last product), held there by scheduling fences.
+      const double* W3 = P + S::OFF_W3 + g * S::L3P + c;
+      double w3b[2][kU3B];
+#pragma unroll
+      for (int uu = 0; uu < kU3B; ++uu) w3b[0][uu] = uu < U3 ? W3[16 * uu] : 0.0;
 #pragma unroll
       for (int u0 = 0; u0 < U3; u0 += kU3B) {
-        // keep the scheduler from hoisting later tile groups' weight loads
-        __builtin_amdgcn_sched_barrier(0);
         d4 acc3t[kU3B];
+        double dtv[kU3B][4][4];
 #pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) acc3t[uu] = d4{0.0, 0.0, 0.0, 0.0};
-        // weight fragments double-buffered one k-step ahead of the MFMAs
-        double wcur[kU3B], wnxt[kU3B];
-        const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
-#pragma unroll
-        for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = u0 + uu < U3 ? W3[16 * uu] : 0.0;
 #pragma unroll
         for (int q = 0; q < S::NQ3; ++q) {
+          const int st = (u0 / kU3B) * S::NQ3 + q;  // fragment step (compile time)
           if (q + 1 < S::NQ3) {
 #pragma unroll
             for (int uu = 0; uu < kU3B; ++uu)
-              wnxt[uu] = u0 + uu < U3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
+              w3b[(st + 1) & 1][uu] =
+                  u0 + uu < U3 ? W3[4 * (q + 1) * S::L3P + 16 * (u0 + uu)] : 0.0;
+          } else if (u0 + kU3B < U3) {
+#pragma unroll
+            for (int uu = 0; uu < kU3B; ++uu)
+              w3b[(st + 1) & 1][uu] = u0 + kU3B + uu < U3 ? W3[16 * (u0 + kU3B + uu)] : 0.0;
+          }
+          if (q + 1 == S::NQ3) {
+            // the group's dT values, read during its last product
+#pragma unroll
+            for (int uu = 0; uu < kU3B; ++uu)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                  dtv[uu][r][m] = u0 + uu < U3 ? dTs[m * S::L3P + 16 * (u0 + uu) + 4 * r + g] : 0.0;
           }
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int uu = 0; uu < kU3B; ++uu)
-            if (u0 + uu < U3) acc3t[uu] = mfma_f64(wcur[uu], x2t[q / 4][q % 4], acc3t[uu]);
+            if (u0 + uu < U3) acc3t[uu] = mfma_f64(w3b[st & 1][uu], x2t[q / 4][q % 4], acc3t[uu]);
           __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int uu = 0; uu < kU3B; ++uu) wcur[uu] = wnxt[uu];
         }
 #pragma unroll
         for (int uu = 0; uu < kU3B; ++uu) {
@@ -745,12 +760,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               if (16 * u + 4 * r >= S::L3) continue;
-              const int f = 16 * u + 4 * r + g;
               const double th = th3[u][r];
               const double tt = (1.0 - th * th) * acc3t[uu][r];
 #pragma unroll
               for (int m = 0; m < 4; ++m) {
-                const double wv = dTs[m * S::L3P + f];
+                const double wv = dtv[uu][r][m];
                 up[m] += wv * th;
                 vp[m] += wv * tt;
               }
