@@ -352,6 +352,8 @@ void gather_and_reduce(dp_model* M, hipStream_t st, int nloc, int ntarget, const
                        const double* e_vals, int ne, const int* items, const Outputs& out);
 void reduce_outputs(dp_model* M, hipStream_t st, int nloc, int ntarget, const double* e_vals,
                     int ne, const int* items, const Outputs& out);
+void atom_energy_out(dp_model* M, hipStream_t st, int ntarget, const double* e_vals, int ne,
+                     const int* items, const Outputs& out);
 
 // nall: extended atoms, or (d_nall non-null, standalone path) their
 // capacity with the count itself on the device.
@@ -401,9 +403,11 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   double* edge_grad = M->keep_edge_grad
                           ? need<double>(M, M->edge_grad, (size_t)std::max(nloc, 1) * nnei * 3)
                           : nullptr;
-  const size_t nfix = (size_t)std::max(std::max(nall, ntarget), 1);
-  auto* facc = need<unsigned long long>(M, M->facc, nfix * 3);
-  auto* vacc = out.atom_virial ? need<unsigned long long>(M, M->vacc, nfix * 9) : nullptr;
+  const long nfix = std::max(nall, ntarget);
+  auto* facc = need<unsigned long long>(M, M->facc, (size_t)std::max(nfix, 1L) * 3);
+  auto* vacc = out.atom_virial
+                   ? need<unsigned long long>(M, M->vacc, (size_t)std::max(nfix, 1L) * 9)
+                   : nullptr;
   double* cpsec = need<double>(M, M->cpsec, (size_t)std::max(nloc, 1) * nt * 12);
 
   EmbArgs ea{};
@@ -434,6 +438,11 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   ea.facc = facc;
   ea.vacc = vacc;
   ea.cpsec = cpsec;
+  // the fixed-point sums are cleared by the forward (no kernel of their own;
+  // stores, not a memset, so the step can be captured in a graph); on the
+  // standalone path over the ghosts counted on the device
+  ea.zero_n = nfix;
+  ea.zero_count = d_nall;
   ea.Tt = nt == 1 ? static_cast<void*>(Tt) : nullptr;
   ea.ldt = 4L * nb;
   ea.tpad = M->d_tpad;
@@ -479,6 +488,11 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
 
   int nblk = block_table(embed_waves_fwd(M->el, f32));
   launch_embed_fwd(st, M->el, ea, nblk, f32);
+  if (nblk <= 0) {
+    // no forward grid to clear the fixed-point sums (no centres)
+    launch_zero_u64(st, ea.zero_n, ea.zero_count, 3, facc);
+    if (vacc) launch_zero_u64(st, ea.zero_n, ea.zero_count, 9, vacc);
+  }
   record(M, st, kStEmbFwd + 1);
 
   if (nt > 1 || D) launch_descriptor(st, desc_args(M, Tt, D), f32);
@@ -591,18 +605,12 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
   M->dd_valid = dD != nullptr;
   record(M, st, kStDT + 1);
 
-  // the fixed-point sums start at zero (a kernel, so that the step can be
-  // captured in a graph); on the standalone path over the ghosts counted on
-  // the device
-  const long nzero = std::max(nall, ntarget);
-  launch_zero_u64(st, nzero, d_nall, 3, facc);
-  if (vacc) launch_zero_u64(st, nzero, d_nall, 9, vacc);
+  // (the fixed-point sums were cleared by the forward)
   nblk = block_table(embed_waves_bwd(M->el, f32));
   launch_embed_bwd(st, M->el, ea, nblk, f32);
   M->eg_valid = edge_grad != nullptr;
   record(M, st, kStEmbBwd + 1);
   const int nsec = nt;
-  double* cpart = need<double>(M, M->cpart, (size_t)std::max(nloc, 1) * 12);
   const unsigned long long *fsum = facc, *vsum = vacc;
   if (d_mapping && ntarget == nloc) {
     // every owner is local: ghost sums folded in place
@@ -618,11 +626,16 @@ void run_model_t(dp_model* M, hipStream_t st, int nloc, int nall, const int* d_n
     fsum = ft;
     vsum = vt;
   }
-  launch_force_finalize(st, ntarget, nloc, nsec, static_cast<const int*>(M->ext_type.p), cpsec,
-                        fsum, vsum, out.force, out.atom_virial, cpart);
+  // forces and atom virials, then energy and frame virial (both stages of the
+  // reduction under the force timer)
+  double* partials =
+      need<double>(M, M->partials, (size_t)finalize_ev_blocks(ntarget, nloc, nb) * 10);
+  double* out10 = need<double>(M, M->out10, 10);
+  launch_finalize_ev(st, ntarget, nloc, nb, nsec, static_cast<const int*>(M->ext_type.p), cpsec,
+                     fsum, vsum, e_bucket, out.force, out.atom_virial, partials, out10, out.energy,
+                     out.virial);
   record(M, st, kStForce + 1);
-  reduce_outputs(M, st, nloc, ntarget, e_bucket, nb, items, out);
-  (void)nall;
+  atom_energy_out(M, st, ntarget, e_bucket, nb, items, out);
 }
 
 // Reverse list + force / atom-virial gather from stored edge gradients (the
@@ -665,6 +678,14 @@ void reduce_outputs(dp_model* M, hipStream_t st, int nloc, int ntarget, const do
   double* partials = need<double>(M, M->partials, 256 * 10);
   double* out10 = need<double>(M, M->out10, 10);
   launch_reduce_ev(st, ne, nloc, e_vals, cpart, partials, out10, out.energy, out.virial);
+  atom_energy_out(M, st, ntarget, e_vals, ne, items, out);
+}
+
+// Atom energies (when asked for) from e_vals[0..ne), in bucket order (items
+// maps a position to its atom) or, with items null, in atom order; the
+// reduce stage timer.
+void atom_energy_out(dp_model* M, hipStream_t st, int ntarget, const double* e_vals, int ne,
+                     const int* items, const Outputs& out) {
   if (out.atom_energy) {
     launch_fill_int(st, 2L * ntarget, 0, reinterpret_cast<int*>(out.atom_energy));
     if (items) {

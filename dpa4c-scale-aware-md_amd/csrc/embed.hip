@@ -466,6 +466,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       }
     }
   }
+  clear_fixed(a);
 }
 
 // AV: atom virials asked for (a.vacc non-null), see edge_out

@@ -294,6 +294,7 @@ k_embed_fwd32(EmbArgs a) {
       }
     }
   }
+  clear_fixed(a);
 }
 
 // AV: atom virials asked for (a.vacc non-null), see edge_out

@@ -173,6 +173,18 @@ __device__ __forceinline__ void own_flush(const EmbArgs& a, int i, int tj, int n
   }
 }
 
+// The backward's fixed-point sums set to zero, spread over the forward's
+// whole grid and issued as each block ends (no load of the block waits
+// behind these stores), so the step needs no clearing kernel of its own.
+__device__ __forceinline__ void clear_fixed(const EmbArgs& a) {
+  const long n = a.zero_count ? (long)*a.zero_count : a.zero_n;
+  const long stride = (long)gridDim.x * blockDim.x;
+  const long q0 = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  for (long q = q0; q < 3 * n; q += stride) a.facc[q] = 0ull;
+  if (a.vacc)
+    for (long q = q0; q < 9 * n; q += stride) a.vacc[q] = 0ull;
+}
+
 __device__ __forceinline__ int find_pair(const EmbArgs& a) {
   int p = 0;
   while (p + 1 < a.npair && (int)blockIdx.x >= a.block_off[p + 1]) ++p;

@@ -19,22 +19,26 @@
 namespace dpamd {
 
 // se_e2_a: the embedding backward leaves each centre's own-row sums per
-// neighbour section in cpsec [nloc][nsec][12] (fp64) and scatters every
-// edge's target side into fixed-point sums facc / vacc. One thread per target
-// atom: force = own sums (sections in order) - incoming sum; atom virial =
-// the incoming sum (charged to the neighbour); cpart = the own sums, which
-// the reduction turns into the frame virial. Centres of a negative type
-// (absent, "virtual" atoms) have no sections.
-__global__ __launch_bounds__(256) void k_force_finalize(int ntarget, int nloc, int nsec,
-                                                        const int* __restrict__ type,
-                                                        const double* __restrict__ cpsec,
-                                                        const unsigned long long* __restrict__ facc,
-                                                        const unsigned long long* __restrict__ vacc,
-                                                        double* __restrict__ force,
-                                                        double* __restrict__ atom_virial,
-                                                        double* __restrict__ cpart) {
+// neighbour section in cpsec [nloc][nsec][12] (fp64) and adds every edge's
+// target side to fixed-point sums facc / vacc. One thread per target atom:
+// force = own sums (sections in order) - incoming sum; atom virial = the
+// incoming sum (charged to the neighbour). Centres of a negative type
+// (absent, "virtual" atoms) have no sections. The same pass forms the first
+// stage of the energy / virial reduction: block b sums the bucket energies
+// e_bucket[p] and the centres' frame virials (the own sums' last nine) of
+// its 256 indices into partials[b][10], which k_reduce_ev2 adds in block
+// order.
+__global__ __launch_bounds__(256) void k_finalize_ev(int ntarget, int nloc, int nbucket, int nsec,
+                                                     const int* __restrict__ type,
+                                                     const double* __restrict__ cpsec,
+                                                     const unsigned long long* __restrict__ facc,
+                                                     const unsigned long long* __restrict__ vacc,
+                                                     const double* __restrict__ e_bucket,
+                                                     double* __restrict__ force,
+                                                     double* __restrict__ atom_virial,
+                                                     double* __restrict__ partials) {
+  __shared__ double sm[10][4];
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= ntarget) return;
   double own[12];
 #pragma unroll
   for (int q = 0; q < 12; ++q) own[q] = 0.0;
@@ -45,14 +49,35 @@ __global__ __launch_bounds__(256) void k_force_finalize(int ntarget, int nloc, i
 #pragma unroll
       for (int q = 0; q < 12; ++q) own[q] += cp[q];
     }
-#pragma unroll
-    for (int q = 0; q < 12; ++q) cpart[(long)t * 12 + q] = own[q];
   }
+  if (t < ntarget) {
 #pragma unroll
-  for (int c = 0; c < 3; ++c) force[3L * t + c] = own[c] - from_fixed(facc[3L * t + c]);
-  if (atom_virial) {
+    for (int c = 0; c < 3; ++c) force[3L * t + c] = own[c] - from_fixed(facc[3L * t + c]);
+    if (atom_virial) {
 #pragma unroll
-    for (int q = 0; q < 9; ++q) atom_virial[9L * t + q] = from_fixed(vacc[9L * t + q]);
+      for (int q = 0; q < 9; ++q) atom_virial[9L * t + q] = from_fixed(vacc[9L * t + q]);
+    }
+  }
+  double part[10];
+  part[0] = t < nbucket ? e_bucket[t] : 0.0;
+#pragma unroll
+  for (int q = 0; q < 9; ++q) part[1 + q] = own[3 + q];
+  // ten block sums; each wave's partial in its own LDS row
+#pragma unroll
+  for (int q = 0; q < 10; ++q) {
+    double v = part[q];
+    v += __shfl_xor(v, 32, 64);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 1, 64);
+    if ((threadIdx.x & 63) == 0) sm[q][threadIdx.x >> 6] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 10) {
+    const double* r = sm[threadIdx.x];
+    partials[(long)blockIdx.x * 10 + threadIdx.x] = (r[0] + r[1]) + (r[2] + r[3]);
   }
 }
 
@@ -96,16 +121,6 @@ void launch_zero_u64(hipStream_t st, long cap, const int* d_count, int per, unsi
   if (cap <= 0) return;
   const long blocks = std::min<long>((cap * per + 255) / 256, 2048);
   hipLaunchKernelGGL(k_zero_u64, dim3((unsigned)blocks), dim3(256), 0, st, cap, d_count, per, p);
-  DPAMD_LAUNCH_CHECK();
-}
-
-void launch_force_finalize(hipStream_t st, int ntarget, int nloc, int nsec, const int* type,
-                           const double* cpsec, const unsigned long long* facc,
-                           const unsigned long long* vacc, double* force, double* atom_virial,
-                           double* cpart) {
-  if (ntarget <= 0) return;
-  hipLaunchKernelGGL(k_force_finalize, dim3((ntarget + 255) / 256), dim3(256), 0, st, ntarget,
-                     nloc, nsec, type, cpsec, facc, vacc, force, atom_virial, cpart);
   DPAMD_LAUNCH_CHECK();
 }
 
@@ -283,12 +298,17 @@ __global__ __launch_bounds__(256) void k_reduce_ev1(int nbucket, int nloc,
   if (threadIdx.x < 10) partials[blockIdx.x * 10 + threadIdx.x] = sm[threadIdx.x][0];
 }
 
-__global__ __launch_bounds__(256) void k_reduce_ev2(const double* __restrict__ partials,
+// (nparts partials: thread k adds partials k, k + 256, ... in order first)
+__global__ __launch_bounds__(256) void k_reduce_ev2(int nparts, const double* __restrict__ partials,
                                                     double* __restrict__ out10,
                                                     double* __restrict__ energy,
                                                     double* __restrict__ virial) {
   __shared__ double sm[10][256];
-  for (int q = 0; q < 10; ++q) sm[q][threadIdx.x] = partials[threadIdx.x * 10 + q];
+  for (int q = 0; q < 10; ++q) {
+    double v = 0.0;
+    for (int k = threadIdx.x; k < nparts; k += 256) v += partials[(long)k * 10 + q];
+    sm[q][threadIdx.x] = v;
+  }
   __syncthreads();
   for (int h = 128; h > 0; h >>= 1) {
     if ((int)threadIdx.x < h)
@@ -343,7 +363,26 @@ void launch_reduce_ev(hipStream_t st, int nbucket, int nloc, const double* e_buc
   hipLaunchKernelGGL(k_reduce_ev1, dim3(kRedBlocks), dim3(256), 0, st, nbucket, nloc, e_bucket,
                      cpart, partials);
   DPAMD_LAUNCH_CHECK();
-  hipLaunchKernelGGL(k_reduce_ev2, dim3(1), dim3(256), 0, st, partials, out10, energy, virial);
+  hipLaunchKernelGGL(k_reduce_ev2, dim3(1), dim3(256), 0, st, kRedBlocks, partials, out10, energy,
+                     virial);
+  DPAMD_LAUNCH_CHECK();
+}
+
+int finalize_ev_blocks(int ntarget, int nloc, int nbucket) {
+  return (std::max(std::max(ntarget, nloc), std::max(nbucket, 1)) + 255) / 256;
+}
+
+void launch_finalize_ev(hipStream_t st, int ntarget, int nloc, int nbucket, int nsec,
+                        const int* type, const double* cpsec, const unsigned long long* facc,
+                        const unsigned long long* vacc, const double* e_bucket, double* force,
+                        double* atom_virial, double* partials, double* out10, double* energy,
+                        double* virial) {
+  const int nparts = finalize_ev_blocks(ntarget, nloc, nbucket);
+  hipLaunchKernelGGL(k_finalize_ev, dim3(nparts), dim3(256), 0, st, ntarget, nloc, nbucket, nsec,
+                     type, cpsec, facc, vacc, e_bucket, force, atom_virial, partials);
+  DPAMD_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_reduce_ev2, dim3(1), dim3(256), 0, st, nparts, partials, out10, energy,
+                     virial);
   DPAMD_LAUNCH_CHECK();
 }
 

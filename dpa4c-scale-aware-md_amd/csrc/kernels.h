@@ -64,14 +64,18 @@ struct EmbArgs {
   // Backward outputs. Each slot's edge gradient goes to its centre's
   // section sums cpsec [nloc][ntypes][12] (force 3, frame virial 9, fp64)
   // and, in fixed point (fixed.h), to its neighbour's extended-atom slot j:
-  // facc [nall][3] and, when non-null, vacc [nall][9]; both must start at
-  // zero (launch_fold_fixed then moves ghost sums onto their owners).
+  // facc [nall][3] and, when non-null, vacc [nall][9] (launch_fold_fixed
+  // then moves ghost sums onto their owners). The forward clears both sums
+  // at its end for the backward: zero_n atoms, or *zero_count when
+  // zero_count is non-null.
   // edge_grad [nloc][nnei][3] is written only when non-null (kept for
   // inspection).
   double* edge_grad;
   unsigned long long* facc;
   unsigned long long* vacc;
   double* cpsec;
+  long zero_n;
+  const int* zero_count;
   // status word, and the largest |component| of an edge gradient the fixed
   // point accepts (raising kStatusFixedRange above it or on NaN)
   int* status;
@@ -268,14 +272,20 @@ void launch_fold_fixed(hipStream_t, int j0, int cap, const int* d_count, const i
                        unsigned long long* dst_f, unsigned long long* dst_v);
 // p[0 .. per * n) = 0 for 64-bit words, n = *d_count (at most cap) or cap
 void launch_zero_u64(hipStream_t, long cap, const int* d_count, int per, unsigned long long* p);
-// se_e2_a: forces, atom virials and the centre partials cpart [nloc][12]
-// from the embedding backward's section sums cpsec [nloc][nsec][12] and the
+// se_e2_a: forces, atom virials, energy and frame virial from the
+// embedding backward's section sums cpsec [nloc][nsec][12] and the
 // fixed-point target sums facc [ntarget][3], vacc [ntarget][9] (or null);
-// type [nloc]: centres of a negative type have no sections.
-void launch_force_finalize(hipStream_t, int ntarget, int nloc, int nsec, const int* type,
-                           const double* cpsec, const unsigned long long* facc,
-                           const unsigned long long* vacc, double* force, double* atom_virial,
-                           double* cpart);
+// type [nloc]: centres of a negative type have no sections. Per block of 256
+// indices the bucket energies e_bucket [nbucket] and the centres' frame
+// virials are summed into partials [finalize_ev_blocks(...)][10], then added
+// in block order into out10 = [energy, virial[9]] (also written to energy /
+// virial when given).
+int finalize_ev_blocks(int ntarget, int nloc, int nbucket);
+void launch_finalize_ev(hipStream_t, int ntarget, int nloc, int nbucket, int nsec, const int* type,
+                        const double* cpsec, const unsigned long long* facc,
+                        const unsigned long long* vacc, const double* e_bucket, double* force,
+                        double* atom_virial, double* partials, double* out10, double* energy,
+                        double* virial);
 // cpart [nloc][12]: each centre's own-row force (3) and frame virial (9),
 // written by the gather and summed by the reduction.
 void launch_force_gather(hipStream_t, int ntarget, int nloc, int nnei, const int* rev_off,
