@@ -211,6 +211,28 @@ def test_edge_cases(dp, orc):
     assert ref["nlist"][0, 0] == 1 and ref["nlist"][1, 0] == 0
 
 
+def test_lammps_path_ghosts_only(dp, orc):
+    """A LAMMPS call with no local atoms, only ghosts (a rank whose domain
+    is empty), after a full evaluation on the same handle: there are no
+    centres, so the embedding forward (which otherwise clears the fixed-point
+    sums) does not run, and the ghost slots' forces and atom virials must
+    still come back zero, not the previous step's sums."""
+    (coord, atype, box), m = CASES["water192"]()
+    mb = model_bytes(m)
+    O = orc.Oracle(mb)
+    ext, et, mp, ilist, numneigh, firstneigh = lammps_inputs(O, coord, atype, box)
+    nloc, nall = len(atype), len(et)
+    pot = dp.DeepPot(file_content=mb)
+    e, f, v, ae, av = pot.compute_nlist(ext, et, box, nall - nloc, ilist, numneigh, firstneigh,
+                                        ago=0, atomic=True)
+    assert np.any(f[nloc:] != 0.0) and np.any(av[nloc:] != 0.0)
+    empty = np.zeros(0, np.int32)
+    e0, f0, v0, ae0, av0 = pot.compute_nlist(ext, et, box, nall, empty, empty, [], ago=0,
+                                             atomic=True)
+    assert e0 == 0.0 and f0.shape == (nall, 3) and av0.shape == (nall, 9)
+    assert not np.any(f0) and not np.any(v0) and not np.any(ae0) and not np.any(av0)
+
+
 def test_virtual_atoms(dp, orc):
     (coord, atype, box), m = CASES["water192"]()
     atype = atype.copy()
