@@ -40,11 +40,11 @@ namespace dpamd {
 // Layer-3 output tiles per group: MFMA accumulation chains in flight. Both
 // kernels run two waves per SIMD (LDS holds one block of eight waves per CU);
 // an accumulation chain into one register issues back to back, so fewer
-// chains cost no matrix throughput and free registers: with 4 chains the
-// forward spilled 192 bytes per lane (25-50-100) and 116 (32-64-128), with 2
-// it spills 52 / 36 and with 1 none, but 2 measured fastest. Measured on
-// 12,288-atom water: forward 0.672 -> 0.634 ms, backward 0.616 -> 0.603 ms;
-// Cu unchanged.
+// chains cost no matrix throughput and free registers. Two measure fastest
+// in the forward: 12,288-atom water 0.634 ms against 0.672 with four (which
+// then spilled); with the forward at 232 registers three and four chains fit
+// without spilling (244-254), and still run 2-3 % slower on water, 0.3 % on
+// Cu. The backward keeps one (two spill 20-30 registers).
 constexpr int kU3 = 2;
 constexpr int kU3B = 1;
 
