@@ -16,10 +16,15 @@
 //                                              deepmd_exception> {
 //     using DeepPotBackendAMD::DeepPotBackendAMD;
 //   };
-// and lets DeepPot::init choose it for this library's model files (magic
-// "DPAMDSEA" / "DPAMDC4N"), as it chooses DeepPotPTExpt for ".pt2"; see
-// INTEGRATION.md of this repository for the few lines. The pair style and the
-// rest of the reference stay unchanged.
+// and lets DeepPot::init choose it for this library's model files, as it
+// chooses DeepPotPTExpt for ".pt2": before the choice by file extension,
+//   std::string head = file_content.substr(0, 8);  // else the file's first 8 bytes
+//   if (head == "DPAMDSEA" || head == "DPAMDC4N") {
+//     dp = std::make_shared<deepmd::DeepPotAMD>(model, gpu_rank, file_content);
+//     inited = true;
+//     return;
+//   }
+// The pair style and the rest of the reference stay unchanged.
 //
 // Conventions are the reference's: coord [nframes][natoms][3], box
 // [nframes][9] (LAMMPS-shaped, lower-triangular) or empty (open system),
