@@ -681,6 +681,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_bwd(EmbArgs a) {
               const int q1 = (S::RES2 == 2 ? 4 * (t % (S::L1 / 16)) : 4 * t) + r;
               res = x1[q1];
               rest = x1t[q1];
+            } else if (16 * t + 4 * r + 3 < S::L1) {
+              // feature f < L1 in every lane group: the lane's own registers
+              const int q1 = min(4 * t + r, S::NQ2 - 1);
+              res = x1[q1];
+              rest = x1t[q1];
             } else {
               const int f1 = (S::RES2 == 2) ? f % S::L1 : f;
               if (f1 < S::L1) {
