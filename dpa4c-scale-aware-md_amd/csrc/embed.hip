@@ -349,17 +349,36 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
         const double* W3 = P + S::OFF_W3 + g * S::L3P + 16 * u0 + c;
 #pragma unroll
         for (int uu = 0; uu < kU3; ++uu) wcur[uu] = u0 + uu < U3 ? W3[16 * uu] : 0.0;
+        double b3v[kU3], resv[kU3][4];
 #pragma unroll
         for (int q = 0; q < S::NQ3; ++q) {
           if (q + 1 < S::NQ3) {
 #pragma unroll
             for (int uu = 0; uu < kU3; ++uu)
               wnxt[uu] = u0 + uu < U3 ? W3[4 * (q + 1) * S::L3P + 16 * uu] : 0.0;
+          } else {
+            // the epilogue's bias and residual values, read during the last product
+#pragma unroll
+            for (int uu = 0; uu < kU3; ++uu) {
+              const int f = 16 * (u0 + uu) + c;
+              b3v[uu] = u0 + uu < U3 ? P[S::OFF_B3 + f] : 0.0;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int sl = g + 4 * r;
+                resv[uu][r] = 0.0;
+                if (u0 + uu < U3) {
+                  if constexpr (S::RES3 == 2) resv[uu][r] = X2s[sl * X2LD + f % S::L2];
+                  if constexpr (S::RES3 == 1) resv[uu][r] = X2s[sl * X2LD + f];
+                }
+              }
+            }
           }
           const double av = x2[q / 4][q % 4];
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int uu = 0; uu < kU3; ++uu)
             if (u0 + uu < U3) acc3[uu] = mfma_f64(av, wcur[uu], acc3[uu]);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int uu = 0; uu < kU3; ++uu) wcur[uu] = wnxt[uu];
         }
@@ -367,9 +386,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
         for (int uu = 0; uu < kU3; ++uu) {
           const int u = u0 + uu;
           if (u < U3) {
-            const int f = 16 * u + c;
             double z3[4], th3v[4];
-            const double b3 = P[S::OFF_B3 + f];
+            const double b3 = b3v[uu];
 #pragma unroll
             for (int r = 0; r < 4; ++r) z3[r] = acc3[uu][r] + b3;
             tanh_tab4(z3, th3v, Tab);
@@ -379,9 +397,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
               const double th = th3v[r];
               // backward order: feature 16u + 4(c>>2) + (c&3) of slot sl
               __builtin_nontemporal_store(th, &act3[256 * u + 16 * r]);
-              double G = th;
-              if constexpr (S::RES3 == 2) G += X2s[sl * X2LD + f % S::L2];
-              if constexpr (S::RES3 == 1) G += X2s[sl * X2LD + f];
+              const double G = th + resv[uu][r];
 #pragma unroll
               for (int m = 0; m < 4; ++m) Tacc[u * 4 + m] += Rs[sl * 4 + m] * G;
             }
