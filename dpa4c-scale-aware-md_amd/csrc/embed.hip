@@ -267,8 +267,17 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       d4 acc2[S::NT2];
 #pragma unroll
       for (int t = 0; t < S::NT2; ++t) acc2[t] = d4{0.0, 0.0, 0.0, 0.0};
+      // (the epilogue's biases are read before the last k-step's products)
+      double b2v[NT2M > 0 ? NT2M : 1][4];
 #pragma unroll
       for (int q = 0; q < S::NQ2; ++q) {
+        if (q + 1 == S::NQ2) {
+#pragma unroll
+          for (int t = 0; t < NT2M; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) b2v[t][r] = P[S::OFF_B2 + 16 * t + 4 * r + g];
+          __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int t = 0; t < NT2M; ++t)
           acc2[t] = mfma_f64(P[S::OFF_W2 + (4 * q + g) * S::L2P + 16 * t + c], x1[q], acc2[t]);
@@ -312,7 +321,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_embed_fwd(EmbArgs a) {
       for (int t = 0; t < NT2M; ++t) {
         double z2[4], th2v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) z2[r] = acc2[t][r] + P[S::OFF_B2 + 16 * t + 4 * r + g];
+        for (int r = 0; r < 4; ++r) z2[r] = acc2[t][r] + b2v[t][r];
         tanh_tab4(z2, th2v, Tab);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
